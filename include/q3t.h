@@ -1,0 +1,138 @@
+/*
+ * q3t — MI355X-native Qwen3-TTS token loop (Talker decode step + 15-group CodePredictor).
+ *
+ * C ABI.  Plain pointers and sizes; no C++ or torch types cross this boundary.
+ * Each entry point replaces one piece of the reference crate's public API
+ * (piedshag/qwen3-tts-hip, src/generation.rs) and is cited below.
+ *
+ * Conventions (mirroring the reference's Result<T, Error>, src/error.rs:3-44):
+ *   - every call returns an int status: Q3T_OK (0) or one of the Q3T_ERR_* codes;
+ *   - the message of the last failure on the calling thread is q3t_last_error();
+ *   - the engine owns all device memory; the caller owns host arrays and nothing is
+ *     retained after a call returns;
+ *   - one host thread drives an engine (the reference engine is neither Send nor Sync);
+ *     a stream must not outlive its engine.
+ */
+#ifndef Q3T_H
+#define Q3T_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q3T_OK 0
+#define Q3T_ERR_INVALID 1   /* Error::InvalidInput (src/error.rs) */
+#define Q3T_ERR_HIP 2       /* Error::Hip{call,status,message} */
+#define Q3T_ERR_CAPACITY 3  /* P + max_frames exceeds max_cache_steps (generation.rs:608-617) */
+#define Q3T_ERR_NOT_FOUND 4 /* missing file / tensor (Error::InvalidInput in the reference loader) */
+#define Q3T_ERR_BUSY 5      /* every stream slot of the engine is in use */
+
+typedef struct q3t_engine q3t_engine;
+typedef struct q3t_stream q3t_stream;
+
+/* EngineOptions (generation.rs:25-38) plus the model directory the reference passes to
+ * HipTtsEngine::load_with_options (generation.rs:255-315).  max_streams is new: the
+ * reference engine owns a single Talker KV cache. */
+typedef struct {
+  const char *model_dir;   /* holds config.json + model.safetensors */
+  int32_t device;          /* HIP device ordinal */
+  int32_t max_cache_steps; /* Talker KV capacity per stream (default 512) */
+  int32_t max_streams;     /* stream slots (KV caches) to allocate (default 1) */
+  int32_t use_graph;       /* 1 = replay each frame as one captured hipGraph (default) */
+  int32_t kv_dtype;        /* KV cache element: 0 = fp32 (default, as the reference),
+                              1 = bf16 (half the KV bytes, rounded once at the store) */
+} q3t_engine_options;
+
+/* GenerateOptions (generation.rs:40-77), field for field.  speaker / language / decode_audio
+ * are carried for API parity; the token loop does not read them (the speaker and language
+ * are already encoded in the prefill rows, and waveform decoding is outside this library). */
+typedef struct {
+  int32_t speaker;
+  int32_t language;
+  int32_t max_frames;
+  int32_t decode_audio;
+  int32_t do_sample;
+  int32_t top_k;
+  float top_p;
+  float temperature;
+  float repetition_penalty;
+  int32_t subtalker_dosample;
+  int32_t subtalker_top_k;
+  float subtalker_top_p;
+  float subtalker_temperature;
+  uint64_t seed;
+} q3t_generate_options;
+
+/* Shapes read from config.json (src/model/config.rs:8-43). */
+typedef struct {
+  int32_t talker_hidden, talker_intermediate, talker_layers, talker_vocab;
+  int32_t cp_hidden, cp_intermediate, cp_layers, cp_vocab;
+  int32_t q_heads, kv_heads, head_dim, num_code_groups;
+  int32_t codec_eos, max_cache_steps, max_streams;
+  int64_t device_bytes; /* device memory held by the engine */
+} q3t_engine_info;
+
+/* GeneratedCodesChunk (generation.rs:876-963). */
+typedef struct {
+  int32_t frames;       /* frames in this chunk (0 = the stream had nothing left: None) */
+  int32_t total_frames; /* frames produced by the stream so far */
+  int32_t ended_by_eos;
+} q3t_chunk_info;
+
+/* Fills *opts with the reference defaults (GenerateOptions::default, generation.rs:60-77). */
+void q3t_generate_options_default(q3t_generate_options *opts);
+
+/* HipTtsEngine::validate_generate_options (generation.rs:569-583) and
+ * SamplingConfig::validate (src/model/sampling.rs:11-26): max_frames > 0,
+ * repetition_penalty > 0, top_p in (0, 1], temperature > 0, top_k >= 0, for both the Talker
+ * and the subtalker.  q3t_stream_start applies the same checks. */
+int q3t_generate_options_validate(const q3t_generate_options *opts);
+
+/* HipTtsEngine::load_with_options (generation.rs:255-315). */
+int q3t_engine_create(const q3t_engine_options *opts, q3t_engine **out);
+int q3t_engine_destroy(q3t_engine *engine);
+int q3t_engine_get_info(const q3t_engine *engine, q3t_engine_info *out);
+
+/* HipTtsEngine::start_stream_with_inputs (generation.rs:513-567): validates options
+ * (generation.rs:569-606), checks P + max_frames <= max_cache_steps, uploads the prefill
+ * [P, H], trailing text rows [T, H] and tts_pad [H], runs the Talker prefill and draws the
+ * first semantic token.  Host arrays are float32 row-major. */
+int q3t_stream_start(q3t_engine *engine, const float *prefill, int32_t prefill_steps,
+                     const float *trailing, int32_t trailing_steps, const float *tts_pad,
+                     const q3t_generate_options *opts, q3t_stream **out);
+
+/* HipTtsStream::next_codes_chunk (generation.rs:876-963): runs up to max_chunk_frames
+ * frames and copies their codes ([frames, num_code_groups] int32, frame-major
+ * [semantic, a1..a15]) into codes, which must hold max_chunk_frames * num_code_groups. */
+int q3t_stream_next_codes(q3t_stream *stream, int32_t max_chunk_frames, int32_t *codes,
+                          q3t_chunk_info *info);
+
+/* Drops the stream and frees its slot (HipTtsStream's Drop). */
+int q3t_stream_destroy(q3t_stream *stream);
+
+/* HipTtsEngine::generate_codes (generation.rs:356-371, rollout 657-749): start + drain.
+ * codes must hold max_frames * num_code_groups int32. */
+int q3t_generate_codes(q3t_engine *engine, const float *prefill, int32_t prefill_steps,
+                       const float *trailing, int32_t trailing_steps, const float *tts_pad,
+                       const q3t_generate_options *opts, int32_t *codes, int32_t *frames,
+                       int32_t *ended_by_eos);
+
+/* Parity hook (the reference's fixture dump, python-reference/qwen3_tts_reference.py:487-523):
+ * raw Talker logits of every Talker evaluation so far ([rows, talker_vocab]: row 0 is the
+ * prefill, row f+1 follows frame f).  Recording is on when the stream was started after
+ * q3t_engine_set_trace(engine, 1).  *rows receives the number of rows written. */
+int q3t_engine_set_trace(q3t_engine *engine, int32_t enabled);
+int q3t_stream_read_talker_logits(q3t_stream *stream, float *out, int32_t capacity_rows,
+                                  int32_t *rows);
+/* CodePredictor logits of the frames so far ([frames, num_code_groups - 1, cp_vocab]). */
+int q3t_stream_read_cp_logits(q3t_stream *stream, float *out, int32_t capacity_frames,
+                              int32_t *frames);
+
+const char *q3t_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* Q3T_H */

@@ -1,0 +1,120 @@
+// Types shared by the host engine and the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q3t {
+
+// Per-stream loop state, resident in device memory so that one captured frame graph can
+// be replayed frame after frame without host round trips.  Written only by the kernels
+// that end a frame (select + frame_end) and by the host at stream start.
+struct SlotState {
+  int32_t frame;          // frames completed so far
+  int32_t semantic;       // semantic token that starts the next frame
+  int32_t done;           // 0 running, 1 ended by codec_eos, 2 reached max_frames
+  int32_t prefill_steps;  // P: the Talker decodes frame f at position P + f
+  int32_t max_frames;
+  int32_t trailing_rows;  // trailing text rows held on device (the next row is tts_pad)
+  int32_t pad0, pad1;
+};
+
+struct SamplingParams {
+  int32_t do_sample;
+  int32_t top_k;       // 0 keeps every finite candidate
+  float top_p;
+  float temperature;
+};
+
+// Per-stream options, also device resident (read by the select kernels).
+struct SlotParams {
+  SamplingParams talker;
+  SamplingParams cp;
+  float repetition_penalty;
+  int32_t use_history;  // repetition penalty applies (penalty != 1 or talker sampling on)
+  uint32_t seed_lo, seed_hi;
+  int32_t trace;        // record raw logits
+  int32_t codec_eos;
+  int32_t pad0, pad1;
+};
+
+enum SkipMode : int32_t {
+  SKIP_NEVER = 0,   // host-driven work (prefill)
+  SKIP_DONE = 1,    // frame work: skipped once the stream has ended
+  SKIP_TALKER = 2,  // the Talker step that follows a frame: also skipped after the last frame
+};
+
+enum PosMode : int32_t {
+  POS_CONST = 0,        // position given by the launch
+  POS_TALKER_FRAME = 1, // position = prefill_steps + frame
+};
+
+enum Epilogue : int32_t {
+  EPI_STORE = 0,     // out[n] = acc
+  EPI_RESIDUAL = 1,  // out[n] = res[n] + acc
+  EPI_SWIGLU = 2,    // out[j] = silu(acc_gate_j) * acc_up_j; W holds gate rows then up rows
+  EPI_BIAS = 3,      // out[n] = acc + bias[n]
+};
+
+struct GemvArgs {
+  const uint16_t *W;  // [rows, K] bf16, row-major (the checkpoint's [out, in] layout)
+  const float *x;     // [K]
+  const float *gamma; // RMSNorm gain over x (prologue variants)
+  const float *res;   // residual (EPI_RESIDUAL)
+  const float *bias;  // bias (EPI_BIAS)
+  float *out;
+  int32_t N;          // outputs (EPI_SWIGLU: I, with 2I weight rows)
+  int32_t K;
+  float eps;
+  int32_t skip;
+  const SlotState *st;
+};
+
+struct AttnArgs {
+  const float *qkv;     // [q_heads*d + 2*kv_heads*d] raw projections
+  const float *gq;      // [d] q_norm gain
+  const float *gk;      // [d] k_norm gain
+  const float2 *rope;   // [cap][d/2] (cos, sin)
+  void *kcache;         // [kv_heads][cap][d], fp32 or bf16 (kv_bf16)
+  void *vcache;         // [kv_heads][cap][d]
+  float *out;           // [q_heads*d]
+  int32_t q_heads, kv_heads, cap;
+  float eps, scale;
+  int32_t pos_mode, pos_const;
+  int32_t skip;
+  int32_t kv_bf16;
+  const SlotState *st;
+};
+
+struct SelectTalkerArgs {
+  const float *logits;      // [V] raw codec-head logits
+  const float *x;           // [H] Talker output before the final norm
+  const float *gamma;       // [H] talker.model.norm
+  const uint16_t *codec_emb;// [V][H] bf16
+  float *cp_prefix;         // [2][H]: normed hidden ; codec_emb[token]
+  int32_t *codes;           // [max_frames][groups]
+  float *trace;             // [max_frames + 1][V] or null
+  SlotState *st;
+  const SlotParams *prm;
+  int32_t V, H, groups;
+  float eps;
+  int32_t after_frame;      // 0: token drawn after the prefill; 1: after the current frame
+};
+
+struct SelectCpArgs {
+  const float *logits;        // [Vc]
+  const uint16_t *emb;        // [Vc][Ht] codec_embedding.g (bf16)
+  float *cur;                 // [Ht] embedding of the chosen token (next CP input)
+  float *emb_sum;             // [Ht]
+  int32_t *codes;
+  float *trace;               // [max_frames][groups-1][Vc] or null
+  // last group only: next Talker input = (codec_emb[semantic] + emb_sum) + trailing row
+  float *talker_in;
+  const uint16_t *codec_emb;  // [Vt][Ht]
+  const float *trailing;      // [trailing_rows + 1][Ht], last row = tts_pad
+  SlotState *st;
+  const SlotParams *prm;
+  int32_t Vc, Ht, groups, group;
+};
+
+}  // namespace q3t

@@ -1,0 +1,856 @@
+// Host engine behind the C ABI in include/q3t.h.
+//
+// Mirrors the reference crate's engine (piedshag/qwen3-tts-hip src/generation.rs,
+// src/model/{talker,code_predictor,decode}.rs) with a MI355X-first execution model:
+//   * bf16 weights kept in the checkpoint's [out, in] layout (rows contiguous along K),
+//     packed per layer as [q | k | v], [o], [gate | up], [down];
+//   * per-stream slots, each with its own bf16 KV caches, workspace and loop state;
+//   * the whole frame (15 CodePredictor groups + the next Talker step + token selection)
+//     enqueued as one sequence of kernels whose varying inputs (frame index, position,
+//     tokens, EOS) live in device memory, so it is captured once as a hipGraph and
+//     replayed; the host synchronises once per chunk.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <memory>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include "../../include/q3t.h"
+#include "q3t_device.h"
+#include "q3t_json.h"
+#include "q3t_kernels.h"
+
+namespace q3t {
+namespace {
+
+thread_local std::string g_last_error;
+
+struct Failure {
+  int code;
+  std::string msg;
+};
+
+[[noreturn]] void fail(int code, const char *fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  throw Failure{code, buf};
+}
+
+void hip_check(hipError_t e, const char *call) {
+  if (e != hipSuccess) fail(Q3T_ERR_HIP, "%s failed: %s (%d)", call, hipGetErrorString(e), (int)e);
+}
+#define HIPC(x) ::q3t::hip_check((x), #x)
+
+template <typename F>
+int guarded(F &&f) {
+  try {
+    f();
+    return Q3T_OK;
+  } catch (const Failure &e) {
+    g_last_error = e.msg;
+    return e.code;
+  } catch (const std::exception &e) {
+    g_last_error = e.what();
+    return Q3T_ERR_INVALID;
+  }
+}
+
+uint16_t f32_to_bf16_host(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+float bf16_to_f32_host(uint16_t b) {
+  const uint32_t u = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+// ------------------------------------------------------------------------------------
+// safetensors (BF16 or F32 tensors; F32 is rounded to bf16 on load)
+// ------------------------------------------------------------------------------------
+class SafeTensors {
+ public:
+  explicit SafeTensors(const std::string &path) : path_(path) {
+    fd_ = open(path.c_str(), O_RDONLY);
+    if (fd_ < 0) fail(Q3T_ERR_NOT_FOUND, "cannot open %s", path.c_str());
+    struct stat sb;
+    fstat(fd_, &sb);
+    size_ = (size_t)sb.st_size;
+    if (size_ < 8) fail(Q3T_ERR_INVALID, "%s is not a safetensors file", path.c_str());
+    base_ = (const uint8_t *)mmap(nullptr, size_, PROT_READ, MAP_PRIVATE, fd_, 0);
+    if (base_ == MAP_FAILED) fail(Q3T_ERR_INVALID, "mmap of %s failed", path.c_str());
+    uint64_t hlen;
+    memcpy(&hlen, base_, 8);
+    if (8 + hlen > size_) fail(Q3T_ERR_INVALID, "%s: header length out of range", path.c_str());
+    header_ = json::parse(std::string((const char *)base_ + 8, hlen));
+    data_ = base_ + 8 + hlen;
+    data_size_ = size_ - 8 - hlen;
+  }
+  ~SafeTensors() {
+    if (base_ && base_ != MAP_FAILED) munmap((void *)base_, size_);
+    if (fd_ >= 0) close(fd_);
+  }
+
+  // Appends the tensor (as bf16) to out, checking its shape.
+  void append_bf16(const std::string &name, const std::vector<int64_t> &shape, std::vector<uint16_t> &out) const {
+    const auto [ptr, dtype, n] = view(name, shape);
+    const size_t at = out.size();
+    out.resize(at + n);
+    if (dtype == "BF16") {
+      memcpy(out.data() + at, ptr, n * 2);
+    } else {
+      const float *f = (const float *)ptr;
+      for (size_t i = 0; i < n; ++i) out[at + i] = f32_to_bf16_host(f[i]);
+    }
+  }
+  std::vector<float> f32(const std::string &name, const std::vector<int64_t> &shape) const {
+    const auto [ptr, dtype, n] = view(name, shape);
+    std::vector<float> out(n);
+    if (dtype == "BF16") {
+      const uint16_t *b = (const uint16_t *)ptr;
+      for (size_t i = 0; i < n; ++i) out[i] = bf16_to_f32_host(b[i]);
+    } else {
+      memcpy(out.data(), ptr, n * 4);
+    }
+    return out;
+  }
+  bool has(const std::string &name) const { return header_.has(name); }
+
+ private:
+  struct View {
+    const uint8_t *ptr;
+    std::string dtype;
+    size_t n;
+  };
+  View view(const std::string &name, const std::vector<int64_t> &shape) const {
+    if (!header_.has(name)) fail(Q3T_ERR_NOT_FOUND, "tensor %s not found in %s", name.c_str(), path_.c_str());
+    const json::Value &t = header_.at(name);
+    const std::string dtype = t.at("dtype").str;
+    if (dtype != "BF16" && dtype != "F32")
+      fail(Q3T_ERR_INVALID, "%s has dtype %s, expected BF16 or F32", name.c_str(), dtype.c_str());
+    const auto &sh = t.at("shape").arr;
+    bool ok = sh.size() == shape.size();
+    size_t n = 1;
+    for (size_t i = 0; ok && i < sh.size(); ++i) {
+      ok = sh[i].integer() == shape[i];
+      n *= (size_t)shape[i];
+    }
+    if (!ok) {
+      std::string want, got;
+      for (auto d : shape) want += std::to_string(d) + ",";
+      for (auto &d : sh) got += std::to_string(d.integer()) + ",";
+      fail(Q3T_ERR_INVALID, "%s shape [%s] does not match expected [%s]", name.c_str(), got.c_str(), want.c_str());
+    }
+    const auto &off = t.at("data_offsets").arr;
+    const size_t b = (size_t)off[0].integer(), e = (size_t)off[1].integer();
+    const size_t esz = dtype == "BF16" ? 2 : 4;
+    if (e > data_size_ || e - b != n * esz) fail(Q3T_ERR_INVALID, "%s: data offsets out of range", name.c_str());
+    return {data_ + b, dtype, n};
+  }
+
+  std::string path_;
+  int fd_ = -1;
+  size_t size_ = 0;
+  const uint8_t *base_ = nullptr;
+  const uint8_t *data_ = nullptr;
+  size_t data_size_ = 0;
+  json::Value header_;
+};
+
+// ------------------------------------------------------------------------------------
+// model
+// ------------------------------------------------------------------------------------
+struct Dims {
+  int hidden, intermediate, layers, q_heads, kv_heads, head_dim, vocab;
+  float eps, theta;
+  int q_out() const { return q_heads * head_dim; }
+  int kv_out() const { return kv_heads * head_dim; }
+  int qkv_rows() const { return q_out() + 2 * kv_out(); }
+  size_t layer_elems() const {
+    return (size_t)qkv_rows() * hidden + (size_t)hidden * q_out() + 2 * (size_t)intermediate * hidden +
+           (size_t)hidden * intermediate;
+  }
+};
+
+Dims dims_from(const json::Value &c) {
+  Dims d;
+  d.hidden = (int)c.at("hidden_size").integer();
+  d.intermediate = (int)c.at("intermediate_size").integer();
+  d.layers = (int)c.at("num_hidden_layers").integer();
+  d.q_heads = (int)c.at("num_attention_heads").integer();
+  d.kv_heads = (int)c.at("num_key_value_heads").integer();
+  d.head_dim = (int)c.at("head_dim").integer();
+  d.vocab = (int)c.at("vocab_size").integer();
+  d.eps = (float)c.at("rms_norm_eps").number();
+  d.theta = (float)c.at("rope_theta").number();
+  return d;
+}
+
+template <typename T>
+T *dev_alloc(size_t n, int64_t &tally) {
+  void *p = nullptr;
+  if (n == 0) n = 1;
+  HIPC(hipMalloc(&p, n * sizeof(T)));
+  tally += (int64_t)(n * sizeof(T));
+  return (T *)p;
+}
+
+struct LayerW {
+  const uint16_t *qkv, *o, *gu, *down;
+  const float *g_in, *g_post, *gq, *gk;
+};
+
+struct StackW {
+  Dims d;
+  std::vector<LayerW> layers;
+  uint16_t *mats = nullptr;
+  float *gains = nullptr;
+  float2 *rope = nullptr;  // [cap][head_dim / 2]
+  int cap = 0;
+};
+
+void load_stack(const SafeTensors &st, const std::string &prefix, const Dims &d, int cap, StackW &w,
+                int64_t &tally) {
+  w.d = d;
+  w.cap = cap;
+  std::vector<uint16_t> mats;
+  mats.reserve(d.layer_elems() * d.layers);
+  std::vector<float> gains;
+  const int64_t H = d.hidden, I = d.intermediate, Q = d.q_out(), KV = d.kv_out(), D = d.head_dim;
+  struct Off {
+    size_t qkv, o, gu, down, g_in, g_post, gq, gk;
+  };
+  std::vector<Off> offs;
+  for (int l = 0; l < d.layers; ++l) {
+    const std::string p = prefix + ".layers." + std::to_string(l);
+    Off o;
+    o.qkv = mats.size();
+    st.append_bf16(p + ".self_attn.q_proj.weight", {Q, H}, mats);
+    st.append_bf16(p + ".self_attn.k_proj.weight", {KV, H}, mats);
+    st.append_bf16(p + ".self_attn.v_proj.weight", {KV, H}, mats);
+    o.o = mats.size();
+    st.append_bf16(p + ".self_attn.o_proj.weight", {H, Q}, mats);
+    o.gu = mats.size();
+    st.append_bf16(p + ".mlp.gate_proj.weight", {I, H}, mats);
+    st.append_bf16(p + ".mlp.up_proj.weight", {I, H}, mats);
+    o.down = mats.size();
+    st.append_bf16(p + ".mlp.down_proj.weight", {H, I}, mats);
+    auto add = [&](const std::string &n, int64_t len) {
+      const size_t at = gains.size();
+      auto v = st.f32(n, {len});
+      gains.insert(gains.end(), v.begin(), v.end());
+      return at;
+    };
+    o.g_in = add(p + ".input_layernorm.weight", H);
+    o.g_post = add(p + ".post_attention_layernorm.weight", H);
+    o.gq = add(p + ".self_attn.q_norm.weight", D);
+    o.gk = add(p + ".self_attn.k_norm.weight", D);
+    offs.push_back(o);
+  }
+  w.mats = dev_alloc<uint16_t>(mats.size(), tally);
+  HIPC(hipMemcpy(w.mats, mats.data(), mats.size() * 2, hipMemcpyHostToDevice));
+  w.gains = dev_alloc<float>(gains.size(), tally);
+  HIPC(hipMemcpy(w.gains, gains.data(), gains.size() * 4, hipMemcpyHostToDevice));
+  for (auto &o : offs)
+    w.layers.push_back(LayerW{w.mats + o.qkv, w.mats + o.o, w.mats + o.gu, w.mats + o.down, w.gains + o.g_in,
+                              w.gains + o.g_post, w.gains + o.gq, w.gains + o.gk});
+  // RoPE table: angle = pos * theta^(-2i/d), evaluated in double and stored as float.
+  const int half = d.head_dim / 2;
+  std::vector<float2> rope((size_t)cap * half);
+  for (int p = 0; p < cap; ++p)
+    for (int i = 0; i < half; ++i) {
+      const double inv = std::pow((double)d.theta, -(2.0 * i) / (double)d.head_dim);
+      const double ang = (double)p * inv;
+      rope[(size_t)p * half + i] = make_float2((float)std::cos(ang), (float)std::sin(ang));
+    }
+  w.rope = dev_alloc<float2>(rope.size(), tally);
+  HIPC(hipMemcpy(w.rope, rope.data(), rope.size() * sizeof(float2), hipMemcpyHostToDevice));
+}
+
+struct Slot {
+  bool in_use = false;
+  char *t_k = nullptr, *t_v = nullptr, *c_k = nullptr, *c_v = nullptr;  // KV caches (fp32 or bf16)
+  float *x_t, *t_in, *qkv, *attn, *act, *logits_t, *logits_c, *x_c, *cp_prefix, *cp_in, *cur, *emb_sum;
+  float *trailing, *prefill;
+  int32_t *codes;
+  SlotState *st;
+  SlotParams *prm;
+  float *trace_t = nullptr, *trace_c = nullptr;
+  hipStream_t stream = nullptr;
+  hipGraphExec_t graph = nullptr;
+  bool graph_traced = false;
+  SlotState *h_state = nullptr;  // pinned host mirror
+};
+
+}  // namespace
+
+struct Engine {
+  int device = 0;
+  int cap = 512;
+  int use_graph = 1;
+  int kv_bf16 = 0;
+  int trace = 0;
+  int groups = 16;
+  int codec_eos = 2150;
+  Dims td{}, cd{};
+  int talker_hidden = 0;
+  bool has_proj = false;
+  StackW talker, cp;
+  uint16_t *codec_head = nullptr, *codec_emb = nullptr;  // [Vt][Ht]
+  float *t_norm = nullptr, *c_norm = nullptr;
+  uint16_t *lm_heads = nullptr;  // [groups-1][Vc][Hc]
+  uint16_t *cp_emb = nullptr;    // [groups-1][Vc][Ht]
+  uint16_t *proj_w = nullptr;    // [Hc][Ht]
+  float *proj_b = nullptr;
+  std::vector<Slot> slots;
+  int64_t device_bytes = 0;
+
+  void gemv(int epi, bool norm, const uint16_t *W, const float *x, const float *gamma, float eps,
+            const float *res, const float *bias, float *out, int N, int K, int skip, const SlotState *st,
+            hipStream_t s) {
+    GemvArgs a{W, x, gamma, res, bias, out, N, K, eps, skip, st};
+    hip_check(launch_gemv(epi, norm, a, s), "launch_gemv");
+  }
+
+  // One decoder-stack step for one position (decode.rs:951-1001 / 1300-1475).
+  void stack_step(const StackW &w, char *kc, char *vc, const float *in, float *x, Slot &sl, int pos_mode,
+                  int pos_const, int skip, hipStream_t s) {
+    const Dims &d = w.d;
+    const size_t cache_layer = (size_t)d.kv_heads * w.cap * d.head_dim * (kv_bf16 ? 2 : 4);
+    for (int l = 0; l < d.layers; ++l) {
+      const LayerW &L = w.layers[l];
+      const float *src = l == 0 ? in : x;
+      gemv(EPI_STORE, true, L.qkv, src, L.g_in, d.eps, nullptr, nullptr, sl.qkv, d.qkv_rows(), d.hidden, skip,
+           sl.st, s);
+      AttnArgs aa{sl.qkv,   L.gq,    L.gk,     w.rope,  kc + l * cache_layer, vc + l * cache_layer,
+                  sl.attn,  d.q_heads, d.kv_heads, w.cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
+                  pos_mode, pos_const, skip,    kv_bf16, sl.st};
+      hip_check(launch_attn_decode(aa, d.head_dim, s), "launch_attn_decode");
+      gemv(EPI_RESIDUAL, false, L.o, sl.attn, nullptr, 0.f, src, nullptr, x, d.hidden, d.q_out(), skip, sl.st, s);
+      gemv(EPI_SWIGLU, true, L.gu, x, L.g_post, d.eps, nullptr, nullptr, sl.act, d.intermediate, d.hidden, skip,
+           sl.st, s);
+      gemv(EPI_RESIDUAL, false, L.down, sl.act, nullptr, 0.f, x, nullptr, x, d.hidden, d.intermediate, skip, sl.st,
+           s);
+    }
+  }
+
+  void select_talker(Slot &sl, int after_frame, hipStream_t s) {
+    SelectTalkerArgs a{sl.logits_t, sl.x_t, t_norm, codec_emb, sl.cp_prefix, sl.codes,
+                       trace ? sl.trace_t : nullptr, sl.st, sl.prm, td.vocab, td.hidden, groups, td.eps,
+                       after_frame};
+    hip_check(launch_select_talker(a, s), "launch_select_talker");
+  }
+
+  // Everything one frame does after its semantic token is known (generation.rs:697-741):
+  // CodePredictor groups 0..14, the next Talker step, token selection, frame bookkeeping.
+  void enqueue_frame(Slot &sl, hipStream_t s) {
+    const int Ht = talker_hidden, Hc = cd.hidden, Vc = cd.vocab, nac = groups - 1;
+    const float *in0 = sl.cp_prefix, *in1 = sl.cp_prefix + Ht;
+    if (has_proj) {
+      gemv(EPI_BIAS, false, proj_w, sl.cp_prefix, nullptr, 0.f, nullptr, proj_b, sl.cp_in, Hc, Ht, SKIP_DONE,
+           sl.st, s);
+      gemv(EPI_BIAS, false, proj_w, sl.cp_prefix + Ht, nullptr, 0.f, nullptr, proj_b, sl.cp_in + Hc, Hc, Ht,
+           SKIP_DONE, sl.st, s);
+      in0 = sl.cp_in;
+      in1 = sl.cp_in + Hc;
+    }
+    stack_step(cp, sl.c_k, sl.c_v, in0, sl.x_c, sl, POS_CONST, 0, SKIP_DONE, s);
+    stack_step(cp, sl.c_k, sl.c_v, in1, sl.x_c, sl, POS_CONST, 1, SKIP_DONE, s);
+    for (int g = 0; g < nac; ++g) {
+      if (g > 0) {
+        const float *in = sl.cur;
+        if (has_proj) {
+          gemv(EPI_BIAS, false, proj_w, sl.cur, nullptr, 0.f, nullptr, proj_b, sl.cp_in + 2 * Hc, Hc, Ht,
+               SKIP_DONE, sl.st, s);
+          in = sl.cp_in + 2 * Hc;
+        }
+        stack_step(cp, sl.c_k, sl.c_v, in, sl.x_c, sl, POS_CONST, g + 1, SKIP_DONE, s);
+      }
+      gemv(EPI_STORE, true, lm_heads + (size_t)g * Vc * Hc, sl.x_c, c_norm, cd.eps, nullptr, nullptr, sl.logits_c,
+           Vc, Hc, SKIP_DONE, sl.st, s);
+      SelectCpArgs a{sl.logits_c, cp_emb + (size_t)g * Vc * Ht, sl.cur, sl.emb_sum, sl.codes,
+                     trace ? sl.trace_c : nullptr, sl.t_in, codec_emb, sl.trailing, sl.st, sl.prm, Vc, Ht, groups,
+                     g};
+      hip_check(launch_select_cp(a, s), "launch_select_cp");
+    }
+    stack_step(talker, sl.t_k, sl.t_v, sl.t_in, sl.x_t, sl, POS_TALKER_FRAME, 0, SKIP_TALKER, s);
+    gemv(EPI_STORE, true, codec_head, sl.x_t, t_norm, td.eps, nullptr, nullptr, sl.logits_t, td.vocab, td.hidden,
+         SKIP_TALKER, sl.st, s);
+    select_talker(sl, 1, s);
+    hip_check(launch_frame_end(sl.st, sl.prm, 1, s), "launch_frame_end");
+  }
+};
+
+struct Stream {
+  Engine *engine;
+  int slot;
+  int host_frame = 0;  // frames already handed to the caller
+  int done = 0;
+  int max_frames = 0;
+};
+
+namespace {
+
+void validate_sampling(int do_sample, int top_k, float top_p, float temperature, const char *name) {
+  (void)do_sample;
+  if (!(top_p > 0.0f && top_p <= 1.0f)) fail(Q3T_ERR_INVALID, "%s.top_p must be in (0, 1], got %g", name, top_p);
+  if (!(temperature > 0.0f)) fail(Q3T_ERR_INVALID, "%s.temperature must be positive, got %g", name, temperature);
+  if (top_k < 0) fail(Q3T_ERR_INVALID, "%s.top_k must be non-negative, got %d", name, top_k);
+}
+
+void validate_options(const q3t_generate_options *o) {
+  if (!o) fail(Q3T_ERR_INVALID, "options must not be null");
+  if (o->max_frames <= 0) fail(Q3T_ERR_INVALID, "max_frames must be non-zero");
+  if (!(o->repetition_penalty > 0.0f)) fail(Q3T_ERR_INVALID, "repetition_penalty must be positive");
+  validate_sampling(o->do_sample, o->top_k, o->top_p, o->temperature, "talker");
+  validate_sampling(o->subtalker_dosample, o->subtalker_top_k, o->subtalker_top_p, o->subtalker_temperature,
+                    "subtalker");
+}
+
+std::string read_file(const std::string &path) {
+  std::ifstream f(path, std::ios::binary);
+  if (!f) fail(Q3T_ERR_NOT_FOUND, "cannot open %s", path.c_str());
+  std::stringstream ss;
+  ss << f.rdbuf();
+  return ss.str();
+}
+
+void alloc_slot(Engine &e, Slot &s) {
+  int64_t &t = e.device_bytes;
+  const Dims &td = e.td, &cd = e.cd;
+  const size_t tcache = (size_t)td.layers * td.kv_heads * e.cap * td.head_dim;
+  const size_t ccache = (size_t)cd.layers * cd.kv_heads * e.cp.cap * cd.head_dim;
+  const size_t esz = e.kv_bf16 ? 2 : 4;
+  s.t_k = dev_alloc<char>(tcache * esz, t);
+  s.t_v = dev_alloc<char>(tcache * esz, t);
+  s.c_k = dev_alloc<char>(ccache * esz, t);
+  s.c_v = dev_alloc<char>(ccache * esz, t);
+  HIPC(hipMemset(s.t_k, 0, tcache * esz));
+  HIPC(hipMemset(s.t_v, 0, tcache * esz));
+  HIPC(hipMemset(s.c_k, 0, ccache * esz));
+  HIPC(hipMemset(s.c_v, 0, ccache * esz));
+  const int Ht = e.talker_hidden, Hc = cd.hidden;
+  const int qkv = std::max(td.qkv_rows(), cd.qkv_rows());
+  s.x_t = dev_alloc<float>(Ht, t);
+  s.t_in = dev_alloc<float>(Ht, t);
+  s.qkv = dev_alloc<float>(qkv, t);
+  s.attn = dev_alloc<float>(std::max(td.q_out(), cd.q_out()), t);
+  s.act = dev_alloc<float>(std::max(td.intermediate, cd.intermediate), t);
+  s.logits_t = dev_alloc<float>(td.vocab, t);
+  s.logits_c = dev_alloc<float>(cd.vocab, t);
+  s.x_c = dev_alloc<float>(Hc, t);
+  s.cp_prefix = dev_alloc<float>(2 * (size_t)Ht, t);
+  s.cp_in = dev_alloc<float>(3 * (size_t)Hc, t);
+  s.cur = dev_alloc<float>(Ht, t);
+  s.emb_sum = dev_alloc<float>(Ht, t);
+  s.trailing = dev_alloc<float>((size_t)(e.cap + 1) * Ht, t);
+  s.prefill = dev_alloc<float>((size_t)e.cap * Ht, t);
+  s.codes = dev_alloc<int32_t>((size_t)e.cap * e.groups, t);
+  s.st = dev_alloc<SlotState>(1, t);
+  s.prm = dev_alloc<SlotParams>(1, t);
+  HIPC(hipMemset(s.st, 0, sizeof(SlotState)));
+  HIPC(hipMemset(s.prm, 0, sizeof(SlotParams)));
+  HIPC(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking));
+  HIPC(hipHostMalloc((void **)&s.h_state, sizeof(SlotState), hipHostMallocDefault));
+}
+
+void free_slot(Slot &s) {
+  if (s.graph) (void)hipGraphExecDestroy(s.graph);
+  void *ptrs[] = {s.t_k,    s.t_v,   s.c_k,       s.c_v,   s.x_t,     s.t_in,     s.qkv,      s.attn,
+                  s.act,    s.logits_t, s.logits_c, s.x_c, s.cp_prefix, s.cp_in, s.cur,      s.emb_sum,
+                  s.trailing, s.prefill, s.codes,   s.st,    s.prm,     s.trace_t,  s.trace_c};
+  for (void *p : ptrs)
+    if (p) (void)hipFree(p);
+  if (s.stream) (void)hipStreamDestroy(s.stream);
+  if (s.h_state) (void)hipHostFree(s.h_state);
+  s = Slot();
+}
+
+void ensure_trace(Engine &e, Slot &s) {
+  if (!e.trace || s.trace_t) return;
+  s.trace_t = dev_alloc<float>((size_t)(e.cap + 1) * e.td.vocab, e.device_bytes);
+  s.trace_c = dev_alloc<float>((size_t)e.cap * (e.groups - 1) * e.cd.vocab, e.device_bytes);
+}
+
+void sync_state(Slot &s) {
+  HIPC(hipMemcpyAsync(s.h_state, s.st, sizeof(SlotState), hipMemcpyDeviceToHost, s.stream));
+  HIPC(hipStreamSynchronize(s.stream));
+}
+
+void run_frames(Engine &e, Slot &s, int n) {
+  if (e.use_graph) {
+    if (!s.graph || s.graph_traced != (bool)e.trace) {
+      if (s.graph) {
+        HIPC(hipGraphExecDestroy(s.graph));
+        s.graph = nullptr;
+      }
+      hipGraph_t g;
+      HIPC(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal));
+      try {
+        e.enqueue_frame(s, s.stream);
+      } catch (...) {
+        (void)hipStreamEndCapture(s.stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      HIPC(hipStreamEndCapture(s.stream, &g));
+      const hipError_t err = hipGraphInstantiate(&s.graph, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      hip_check(err, "hipGraphInstantiate");
+      s.graph_traced = (bool)e.trace;
+    }
+    for (int i = 0; i < n; ++i) HIPC(hipGraphLaunch(s.graph, s.stream));
+  } else {
+    for (int i = 0; i < n; ++i) e.enqueue_frame(s, s.stream);
+  }
+}
+
+}  // namespace
+}  // namespace q3t
+
+using q3t::Engine;
+using q3t::fail;
+using q3t::guarded;
+
+struct q3t_engine : Engine {};
+struct q3t_stream : q3t::Stream {};
+
+extern "C" {
+
+void q3t_generate_options_default(q3t_generate_options *o) {
+  if (!o) return;
+  o->speaker = 3;   // Speaker::Ryan
+  o->language = 1;  // Language::English
+  o->max_frames = 240;
+  o->decode_audio = 1;
+  o->do_sample = 1;
+  o->top_k = 50;
+  o->top_p = 1.0f;
+  o->temperature = 0.9f;
+  o->repetition_penalty = 1.05f;
+  o->subtalker_dosample = 1;
+  o->subtalker_top_k = 50;
+  o->subtalker_top_p = 1.0f;
+  o->subtalker_temperature = 0.9f;
+  o->seed = 0;
+}
+
+const char *q3t_last_error(void) { return q3t::g_last_error.c_str(); }
+
+int q3t_generate_options_validate(const q3t_generate_options *o) {
+  return guarded([&] { q3t::validate_options(o); });
+}
+
+int q3t_engine_create(const q3t_engine_options *opts, q3t_engine **out) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!opts || !out || !opts->model_dir) fail(Q3T_ERR_INVALID, "engine options and output must not be null");
+    *out = nullptr;
+    auto e = std::make_unique<q3t_engine>();
+    e->device = opts->device;
+    e->cap = opts->max_cache_steps > 0 ? opts->max_cache_steps : 512;
+    e->use_graph = opts->use_graph;
+    if (opts->kv_dtype != 0 && opts->kv_dtype != 1) fail(Q3T_ERR_INVALID, "kv_dtype must be 0 (fp32) or 1 (bf16)");
+    e->kv_bf16 = opts->kv_dtype;
+    const int nslots = opts->max_streams > 0 ? opts->max_streams : 1;
+    const std::string dir = opts->model_dir;
+    const json::Value cfg = json::parse(read_file(dir + "/config.json"));
+    const json::Value &tc = cfg.at("talker_config");
+    const json::Value &cc = tc.at("code_predictor_config");
+    e->td = dims_from(tc);
+    e->cd = dims_from(cc);
+    e->groups = (int)tc.at("num_code_groups").integer();
+    e->codec_eos = (int)tc.at("codec_eos_token_id").integer();
+    e->talker_hidden = e->td.hidden;
+    e->has_proj = e->td.hidden != e->cd.hidden;
+    const Dims &td = e->td, &cd = e->cd;
+    // Shape limits of the kernels (checked here so that no launch can index outside).
+    for (const Dims *d : {&td, &cd}) {
+      if (d->head_dim != 128) fail(Q3T_ERR_INVALID, "head_dim %d unsupported (kernels are built for 128)", d->head_dim);
+      if (d->kv_heads <= 0 || d->q_heads % d->kv_heads || d->q_heads / d->kv_heads > 4 ||
+          d->q_heads / d->kv_heads == 3)
+        fail(Q3T_ERR_INVALID, "q_heads %d / kv_heads %d unsupported", d->q_heads, d->kv_heads);
+      if (!gemv_supports_k(d->hidden) || !gemv_supports_k(d->intermediate) || !gemv_supports_k(d->q_out()))
+        fail(Q3T_ERR_INVALID, "hidden %d / intermediate %d / q_out %d must be 512 x {1,2,3,4,6,8,12}", d->hidden,
+             d->intermediate, d->q_out());
+    }
+    if (td.vocab > kMaxVocab || td.vocab < 1024 || cd.vocab > kMaxVocab)
+      fail(Q3T_ERR_INVALID, "vocab sizes %d / %d unsupported", td.vocab, cd.vocab);
+    if (e->groups < 2) fail(Q3T_ERR_INVALID, "CodePredictor needs at least one semantic and one acoustic group");
+    if (e->cap > attn_max_cache_steps(td.q_heads, td.kv_heads))
+      fail(Q3T_ERR_INVALID, "max_cache_steps %d exceeds the attention kernel limit %d", e->cap,
+           attn_max_cache_steps(td.q_heads, td.kv_heads));
+    if (e->codec_eos < 0 || e->codec_eos >= td.vocab) fail(Q3T_ERR_INVALID, "codec_eos out of range");
+
+    SafeTensors st(dir + "/model.safetensors");
+    HIPC(hipSetDevice(e->device));
+    int64_t &tally = e->device_bytes;
+    load_stack(st, "talker.model", td, e->cap, e->talker, tally);
+    load_stack(st, "talker.code_predictor.model", cd, e->groups, e->cp, tally);
+    const int64_t Ht = td.hidden, Vt = td.vocab, Hc = cd.hidden, Vc = cd.vocab, nac = e->groups - 1;
+    auto upload_bf16 = [&](const std::vector<std::string> &names, const std::vector<int64_t> &shape) {
+      std::vector<uint16_t> host;
+      for (auto &n : names) st.append_bf16(n, shape, host);
+      uint16_t *d = dev_alloc<uint16_t>(host.size(), tally);
+      HIPC(hipMemcpy(d, host.data(), host.size() * 2, hipMemcpyHostToDevice));
+      return d;
+    };
+    auto upload_f32 = [&](const std::string &n, int64_t len) {
+      auto v = st.f32(n, {len});
+      float *d = dev_alloc<float>(v.size(), tally);
+      HIPC(hipMemcpy(d, v.data(), v.size() * 4, hipMemcpyHostToDevice));
+      return d;
+    };
+    e->codec_head = upload_bf16({"talker.codec_head.weight"}, {Vt, Ht});
+    e->codec_emb = upload_bf16({"talker.model.codec_embedding.weight"}, {Vt, Ht});
+    e->t_norm = upload_f32("talker.model.norm.weight", Ht);
+    e->c_norm = upload_f32("talker.code_predictor.model.norm.weight", Hc);
+    std::vector<std::string> heads, embs;
+    for (int g = 0; g < nac; ++g) {
+      heads.push_back("talker.code_predictor.lm_head." + std::to_string(g) + ".weight");
+      embs.push_back("talker.code_predictor.model.codec_embedding." + std::to_string(g) + ".weight");
+    }
+    e->lm_heads = upload_bf16(heads, {Vc, Hc});
+    e->cp_emb = upload_bf16(embs, {Vc, Ht});
+    if (e->has_proj) {
+      if (!gemv_supports_k((int)Ht)) fail(Q3T_ERR_INVALID, "projection width %d unsupported", (int)Ht);
+      e->proj_w = upload_bf16({"talker.code_predictor.small_to_mtp_projection.weight"}, {Hc, Ht});
+      e->proj_b = upload_f32("talker.code_predictor.small_to_mtp_projection.bias", Hc);
+    }
+    e->slots.resize(nslots);
+    for (auto &s : e->slots) alloc_slot(*e, s);
+    HIPC(hipDeviceSynchronize());
+    *out = e.release();
+  });
+}
+
+int q3t_engine_destroy(q3t_engine *e) {
+  return guarded([&] {
+    if (!e) return;
+    (void)hipSetDevice(e->device);
+    (void)hipDeviceSynchronize();
+    for (auto &s : e->slots) q3t::free_slot(s);
+    void *ptrs[] = {e->talker.mats, e->talker.gains, e->talker.rope, e->cp.mats,    e->cp.gains,
+                    e->cp.rope,     e->codec_head,   e->codec_emb,   e->t_norm,     e->c_norm,
+                    e->lm_heads,    e->cp_emb,       e->proj_w,      e->proj_b};
+    for (void *p : ptrs)
+      if (p) (void)hipFree(p);
+    delete e;
+  });
+}
+
+int q3t_engine_get_info(const q3t_engine *e, q3t_engine_info *o) {
+  return guarded([&] {
+    if (!e || !o) fail(Q3T_ERR_INVALID, "null argument");
+    o->talker_hidden = e->td.hidden;
+    o->talker_intermediate = e->td.intermediate;
+    o->talker_layers = e->td.layers;
+    o->talker_vocab = e->td.vocab;
+    o->cp_hidden = e->cd.hidden;
+    o->cp_intermediate = e->cd.intermediate;
+    o->cp_layers = e->cd.layers;
+    o->cp_vocab = e->cd.vocab;
+    o->q_heads = e->td.q_heads;
+    o->kv_heads = e->td.kv_heads;
+    o->head_dim = e->td.head_dim;
+    o->num_code_groups = e->groups;
+    o->codec_eos = e->codec_eos;
+    o->max_cache_steps = e->cap;
+    o->max_streams = (int32_t)e->slots.size();
+    o->device_bytes = e->device_bytes;
+  });
+}
+
+int q3t_engine_set_trace(q3t_engine *e, int32_t enabled) {
+  return guarded([&] {
+    if (!e) fail(Q3T_ERR_INVALID, "null engine");
+    e->trace = enabled ? 1 : 0;
+  });
+}
+
+int q3t_stream_start(q3t_engine *e, const float *prefill, int32_t P, const float *trailing, int32_t T,
+                     const float *tts_pad, const q3t_generate_options *o, q3t_stream **out) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || !out) fail(Q3T_ERR_INVALID, "null engine or output");
+    *out = nullptr;
+    validate_options(o);
+    if (P <= 0) fail(Q3T_ERR_INVALID, "prefill steps must be non-zero");
+    if (!prefill || !tts_pad || (T > 0 && !trailing) || T < 0) fail(Q3T_ERR_INVALID, "null input array");
+    if ((int64_t)P + o->max_frames > e->cap)
+      fail(Q3T_ERR_CAPACITY,
+           "requested %lld cache steps but engine was loaded for %d; call load_with_max_frames with a larger "
+           "max_frames",
+           (long long)P + o->max_frames, e->cap);
+    int slot = -1;
+    for (size_t i = 0; i < e->slots.size(); ++i)
+      if (!e->slots[i].in_use) {
+        slot = (int)i;
+        break;
+      }
+    if (slot < 0) fail(Q3T_ERR_BUSY, "all %zu stream slots are in use", e->slots.size());
+    HIPC(hipSetDevice(e->device));
+    Slot &s = e->slots[slot];
+    ensure_trace(*e, s);
+    const int Ht = e->talker_hidden;
+    const int rows = std::min<int>(T, e->cap);
+    // Inputs: prefill rows, trailing rows then tts_pad as the row after the last.
+    HIPC(hipMemcpyAsync(s.prefill, prefill, (size_t)P * Ht * 4, hipMemcpyHostToDevice, s.stream));
+    if (rows > 0)
+      HIPC(hipMemcpyAsync(s.trailing, trailing, (size_t)rows * Ht * 4, hipMemcpyHostToDevice, s.stream));
+    HIPC(hipMemcpyAsync(s.trailing + (size_t)rows * Ht, tts_pad, (size_t)Ht * 4, hipMemcpyHostToDevice, s.stream));
+    SlotState st0{};
+    st0.frame = 0;
+    st0.semantic = -1;
+    st0.done = 0;
+    st0.prefill_steps = P;
+    st0.max_frames = o->max_frames;
+    st0.trailing_rows = rows;
+    SlotParams pr{};
+    pr.talker = SamplingParams{o->do_sample ? 1 : 0, o->top_k, o->top_p, o->temperature};
+    pr.cp = SamplingParams{o->subtalker_dosample ? 1 : 0, o->subtalker_top_k, o->subtalker_top_p,
+                           o->subtalker_temperature};
+    pr.repetition_penalty = o->repetition_penalty;
+    pr.use_history = (o->repetition_penalty != 1.0f || o->do_sample) ? 1 : 0;
+    pr.seed_lo = (uint32_t)(o->seed & 0xffffffffu);
+    pr.seed_hi = (uint32_t)(o->seed >> 32);
+    pr.trace = e->trace;
+    pr.codec_eos = e->codec_eos;
+    *s.h_state = st0;
+    HIPC(hipMemcpyAsync(s.st, s.h_state, sizeof(SlotState), hipMemcpyHostToDevice, s.stream));
+    HIPC(hipStreamSynchronize(s.stream));  // h_state is reused below
+    HIPC(hipMemcpyAsync(s.prm, &pr, sizeof(SlotParams), hipMemcpyHostToDevice, s.stream));
+    HIPC(hipStreamSynchronize(s.stream));
+    // Talker prefill: positions 0..P-1, then the head and the first semantic token
+    // (talker.rs:207-233).
+    for (int p = 0; p < P; ++p)
+      e->stack_step(e->talker, s.t_k, s.t_v, s.prefill + (size_t)p * Ht, s.x_t, s, POS_CONST, p, SKIP_NEVER,
+                    s.stream);
+    e->gemv(EPI_STORE, true, e->codec_head, s.x_t, e->t_norm, e->td.eps, nullptr, nullptr, s.logits_t, e->td.vocab,
+            e->td.hidden, SKIP_NEVER, s.st, s.stream);
+    e->select_talker(s, 0, s.stream);
+    hip_check(launch_frame_end(s.st, s.prm, 0, s.stream), "launch_frame_end");
+    sync_state(s);
+    s.in_use = true;
+    auto *stream = new q3t_stream();
+    stream->engine = e;
+    stream->slot = slot;
+    stream->max_frames = o->max_frames;
+    stream->done = s.h_state->done;
+    *out = stream;
+  });
+}
+
+int q3t_stream_next_codes(q3t_stream *sp, int32_t max_chunk, int32_t *codes, q3t_chunk_info *info) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!sp || !info || (max_chunk > 0 && !codes)) fail(Q3T_ERR_INVALID, "null argument");
+    if (max_chunk <= 0) fail(Q3T_ERR_INVALID, "max_chunk_frames must be non-zero");
+    Engine &e = *sp->engine;
+    Slot &s = e.slots[sp->slot];
+    info->frames = 0;
+    info->total_frames = sp->host_frame;
+    info->ended_by_eos = sp->done == 1;
+    if (sp->done || sp->host_frame >= sp->max_frames) return;
+    HIPC(hipSetDevice(e.device));
+    const int n = std::min(max_chunk, sp->max_frames - sp->host_frame);
+    run_frames(e, s, n);
+    sync_state(s);
+    const int produced = s.h_state->frame - sp->host_frame;
+    if (produced < 0 || produced > n) fail(Q3T_ERR_HIP, "device loop state is inconsistent");
+    if (produced > 0)
+      HIPC(hipMemcpy(codes, s.codes + (size_t)sp->host_frame * e.groups, (size_t)produced * e.groups * 4,
+                     hipMemcpyDeviceToHost));
+    sp->host_frame += produced;
+    sp->done = s.h_state->done;
+    info->frames = produced;
+    info->total_frames = sp->host_frame;
+    info->ended_by_eos = sp->done == 1;
+  });
+}
+
+int q3t_stream_destroy(q3t_stream *sp) {
+  return guarded([&] {
+    if (!sp) return;
+    Engine &e = *sp->engine;
+    (void)hipSetDevice(e.device);
+    (void)hipStreamSynchronize(e.slots[sp->slot].stream);
+    e.slots[sp->slot].in_use = false;
+    delete sp;
+  });
+}
+
+int q3t_stream_read_talker_logits(q3t_stream *sp, float *out, int32_t capacity, int32_t *rows) {
+  return guarded([&] {
+    if (!sp || !rows) fail(Q3T_ERR_INVALID, "null argument");
+    Engine &e = *sp->engine;
+    auto &s = e.slots[sp->slot];
+    if (!s.trace_t) fail(Q3T_ERR_INVALID, "logit tracing was off when the stream started");
+    // Row 0: prefill; row f + 1: after frame f (only frames followed by a Talker step).
+    int n = sp->host_frame + 1;
+    if (sp->host_frame >= sp->max_frames) n = sp->max_frames;  // the last frame has no Talker step
+    n = std::min(n, capacity);
+    if (n > 0 && out)
+      HIPC(hipMemcpy(out, s.trace_t, (size_t)n * e.td.vocab * 4, hipMemcpyDeviceToHost));
+    *rows = n;
+  });
+}
+
+int q3t_stream_read_cp_logits(q3t_stream *sp, float *out, int32_t capacity, int32_t *frames) {
+  return guarded([&] {
+    if (!sp || !frames) fail(Q3T_ERR_INVALID, "null argument");
+    Engine &e = *sp->engine;
+    auto &s = e.slots[sp->slot];
+    if (!s.trace_c) fail(Q3T_ERR_INVALID, "logit tracing was off when the stream started");
+    const int n = std::min(sp->host_frame, capacity);
+    if (n > 0 && out)
+      HIPC(hipMemcpy(out, s.trace_c, (size_t)n * (e.groups - 1) * e.cd.vocab * 4, hipMemcpyDeviceToHost));
+    *frames = n;
+  });
+}
+
+int q3t_generate_codes(q3t_engine *e, const float *prefill, int32_t P, const float *trailing, int32_t T,
+                       const float *tts_pad, const q3t_generate_options *o, int32_t *codes, int32_t *frames,
+                       int32_t *ended_by_eos) {
+  q3t_stream *sp = nullptr;
+  int rc = q3t_stream_start(e, prefill, P, trailing, T, tts_pad, o, &sp);
+  if (rc != Q3T_OK) return rc;
+  rc = guarded([&] {
+    if (!codes || !frames || !ended_by_eos) fail(Q3T_ERR_INVALID, "null output");
+  });
+  int total = 0;
+  q3t_chunk_info info{};
+  while (rc == Q3T_OK) {
+    const int chunk = o->max_frames - total;
+    if (chunk <= 0) break;
+    rc = q3t_stream_next_codes(sp, chunk, codes + (size_t)total * e->groups, &info);
+    if (rc != Q3T_OK || info.frames == 0) break;
+    total = info.total_frames;
+  }
+  if (rc == Q3T_OK) {
+    *frames = total;
+    *ended_by_eos = info.ended_by_eos;
+  }
+  const int rc2 = q3t_stream_destroy(sp);
+  return rc != Q3T_OK ? rc : rc2;
+}
+
+}  // extern "C"

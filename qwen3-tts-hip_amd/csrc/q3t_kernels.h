@@ -1,0 +1,25 @@
+// Host-side launchers for the gfx950 kernels in q3t_kernels.hip.
+#pragma once
+
+#include "q3t_device.h"
+
+namespace q3t {
+
+// y = W x (optionally x := RMSNorm(x) * gamma first) with the epilogue `epi`.
+// Requires K = 512 * c for c in {1, 2, 3, 4, 6, 8, 12}; returns hipErrorInvalidValue otherwise.
+hipError_t launch_gemv(int epi, bool norm, const GemvArgs &a, hipStream_t stream);
+bool gemv_supports_k(int K);
+
+// Fused q/k head RMSNorm + RoPE + bf16 KV-cache write + GQA decode attention.
+// One workgroup per KV head; LDS holds the scores of one position range.
+hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t stream);
+int attn_max_cache_steps(int q_heads, int kv_heads);
+
+hipError_t launch_select_talker(const SelectTalkerArgs &a, hipStream_t stream);
+hipError_t launch_select_cp(const SelectCpArgs &a, hipStream_t stream);
+hipError_t launch_frame_end(SlotState *st, const SlotParams *prm, int advance, hipStream_t stream);
+
+// Largest vocabulary the select kernels hold in LDS.
+constexpr int kMaxVocab = 4096;
+
+}  // namespace q3t

@@ -1,0 +1,411 @@
+"""Python mirror of the reference crate's engine API, over the q3t C ABI (include/q3t.h).
+
+Names, defaults, argument meaning and error behaviour follow src/generation.rs of
+piedshag/qwen3-tts-hip:
+
+=========================================  =============================================
+reference (Rust)                            here
+=========================================  =============================================
+``HipTtsEngine::load`` / ``load_with_max_   ``HipTtsEngine.load`` / ``load_with_max_frames``
+frames`` / ``load_with_options`` (255-315)  / ``load_with_options``
+``generate_codes`` (356-371)                ``HipTtsEngine.generate_codes``
+``start_stream`` (421-440)                  ``HipTtsEngine.start_stream``
+``HipTtsStream::next_codes_chunk`` (876-)   ``HipTtsStream.next_codes_chunk``
+``HipTtsStream::finish_codes`` (991-997)    ``HipTtsStream.finish_codes``
+``GenerateOptions`` / ``StreamOptions``     same names, same defaults (40-92)
+``Error::InvalidInput`` / ``Error::Hip``    ``InvalidInputError`` / ``HipError``
+=========================================  =============================================
+
+The reference takes text and tokenizes it; no tokenizer ships offline, so these calls
+take a :class:`q3t.textprep.PreparedInputs` (the reference's ``TtsPreparedInputs``) or a
+sequence of content token ids together with a :class:`q3t.textprep.TextPrep`.
+
+There is no CPU fallback: if ``libq3t.so`` is missing or the GPU call fails, the call
+raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+import os
+from typing import Optional, Sequence, Union
+
+import numpy as np
+
+from .textprep import PreparedInputs, TextPrep
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libq3t.so")
+
+DEFAULT_MAX_CACHE_STEPS = 512          # generation.rs:20
+DEFAULT_PREFILL_HEADROOM = 256         # generation.rs:21
+DEFAULT_STREAM_LEFT_CONTEXT_FRAMES = 25
+DEFAULT_TEXT_LOOKAHEAD_TOKENS = 8
+SAMPLE_RATE = 24_000
+SAMPLES_PER_FRAME = 1920               # 80 ms per codec frame
+
+Q3T_OK, Q3T_ERR_INVALID, Q3T_ERR_HIP, Q3T_ERR_CAPACITY, Q3T_ERR_NOT_FOUND, Q3T_ERR_BUSY = range(6)
+
+SPEAKERS = ["serena", "vivian", "uncle_fu", "ryan", "aiden", "ono_anna", "sohee", "eric", "dylan"]
+LANGUAGES = ["chinese", "english", "japanese", "korean", "german", "french", "russian",
+             "portuguese", "spanish", "italian"]
+
+
+class Q3tError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(message)
+        self.code = code
+
+
+class InvalidInputError(Q3tError, ValueError):
+    pass
+
+
+class HipError(Q3tError):
+    pass
+
+
+class CapacityError(InvalidInputError):
+    pass
+
+
+class NotFoundError(InvalidInputError):
+    pass
+
+
+class BusyError(Q3tError):
+    pass
+
+
+_ERRORS = {Q3T_ERR_INVALID: InvalidInputError, Q3T_ERR_HIP: HipError, Q3T_ERR_CAPACITY: CapacityError,
+           Q3T_ERR_NOT_FOUND: NotFoundError, Q3T_ERR_BUSY: BusyError}
+
+
+class _EngineOptions(ctypes.Structure):
+    _fields_ = [("model_dir", ctypes.c_char_p), ("device", ctypes.c_int32),
+                ("max_cache_steps", ctypes.c_int32), ("max_streams", ctypes.c_int32),
+                ("use_graph", ctypes.c_int32), ("kv_dtype", ctypes.c_int32)]
+
+
+class _GenerateOptions(ctypes.Structure):
+    _fields_ = [("speaker", ctypes.c_int32), ("language", ctypes.c_int32),
+                ("max_frames", ctypes.c_int32), ("decode_audio", ctypes.c_int32),
+                ("do_sample", ctypes.c_int32), ("top_k", ctypes.c_int32),
+                ("top_p", ctypes.c_float), ("temperature", ctypes.c_float),
+                ("repetition_penalty", ctypes.c_float), ("subtalker_dosample", ctypes.c_int32),
+                ("subtalker_top_k", ctypes.c_int32), ("subtalker_top_p", ctypes.c_float),
+                ("subtalker_temperature", ctypes.c_float), ("seed", ctypes.c_uint64)]
+
+
+class _EngineInfo(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in (
+        "talker_hidden", "talker_intermediate", "talker_layers", "talker_vocab",
+        "cp_hidden", "cp_intermediate", "cp_layers", "cp_vocab",
+        "q_heads", "kv_heads", "head_dim", "num_code_groups",
+        "codec_eos", "max_cache_steps", "max_streams")] + [("device_bytes", ctypes.c_int64)]
+
+
+class _ChunkInfo(ctypes.Structure):
+    _fields_ = [("frames", ctypes.c_int32), ("total_frames", ctypes.c_int32),
+                ("ended_by_eos", ctypes.c_int32)]
+
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load libq3t.so (built by ``__graft_entry__.build()``); raise if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`")
+    lib = ctypes.CDLL(path)
+    P = ctypes.POINTER
+    f32p, i32p = P(ctypes.c_float), P(ctypes.c_int32)
+    sigs = {
+        "q3t_generate_options_default": (None, [P(_GenerateOptions)]),
+        "q3t_generate_options_validate": (ctypes.c_int, [P(_GenerateOptions)]),
+        "q3t_engine_create": (ctypes.c_int, [P(_EngineOptions), P(ctypes.c_void_p)]),
+        "q3t_engine_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+        "q3t_engine_get_info": (ctypes.c_int, [ctypes.c_void_p, P(_EngineInfo)]),
+        "q3t_engine_set_trace": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32]),
+        "q3t_stream_start": (ctypes.c_int, [ctypes.c_void_p, f32p, ctypes.c_int32, f32p, ctypes.c_int32,
+                                            f32p, P(_GenerateOptions), P(ctypes.c_void_p)]),
+        "q3t_stream_next_codes": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, i32p, P(_ChunkInfo)]),
+        "q3t_stream_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+        "q3t_generate_codes": (ctypes.c_int, [ctypes.c_void_p, f32p, ctypes.c_int32, f32p, ctypes.c_int32,
+                                              f32p, P(_GenerateOptions), i32p, i32p, i32p]),
+        "q3t_stream_read_talker_logits": (ctypes.c_int, [ctypes.c_void_p, f32p, ctypes.c_int32, i32p]),
+        "q3t_stream_read_cp_logits": (ctypes.c_int, [ctypes.c_void_p, f32p, ctypes.c_int32, i32p]),
+        "q3t_last_error": (ctypes.c_char_p, []),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _check(rc: int) -> None:
+    if rc != Q3T_OK:
+        msg = _lib.q3t_last_error().decode(errors="replace")
+        raise _ERRORS.get(rc, Q3tError)(rc, msg)
+
+
+def _f32(a: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _fptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def _iptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))
+
+
+@dataclasses.dataclass
+class EngineOptions:
+    """``EngineOptions`` (generation.rs:25-38) + stream slots and graph replay."""
+    device: int = 0
+    max_cache_steps: int = DEFAULT_MAX_CACHE_STEPS
+    max_streams: int = 1
+    use_graph: bool = True
+    kv_bf16: bool = False   # KV cache in bf16 instead of fp32
+
+
+@dataclasses.dataclass
+class GenerateOptions:
+    """``GenerateOptions`` (generation.rs:40-77), same defaults."""
+    speaker: str = "ryan"
+    language: str = "english"
+    max_frames: int = 240
+    decode_audio: bool = True
+    do_sample: bool = True
+    top_k: int = 50
+    top_p: float = 1.0
+    temperature: float = 0.9
+    repetition_penalty: float = 1.05
+    subtalker_dosample: bool = True
+    subtalker_top_k: int = 50
+    subtalker_top_p: float = 1.0
+    subtalker_temperature: float = 0.9
+    seed: int = 0
+
+    @classmethod
+    def greedy(cls, max_frames: int = 240, **kw) -> "GenerateOptions":
+        """The reference's parity setting (scripts/qwen3-hip-parity.sh:51-70)."""
+        return cls(max_frames=max_frames, do_sample=False, repetition_penalty=1.0,
+                   subtalker_dosample=False, decode_audio=False, **kw)
+
+    def _c(self) -> _GenerateOptions:
+        o = _GenerateOptions()
+        o.speaker = SPEAKERS.index(self.speaker.lower()) if self.speaker.lower() in SPEAKERS else -1
+        o.language = LANGUAGES.index(self.language.lower()) if self.language.lower() in LANGUAGES else -1
+        o.max_frames = int(self.max_frames)
+        o.decode_audio = int(bool(self.decode_audio))
+        o.do_sample = int(bool(self.do_sample))
+        o.top_k = int(self.top_k)
+        o.top_p = float(self.top_p)
+        o.temperature = float(self.temperature)
+        o.repetition_penalty = float(self.repetition_penalty)
+        o.subtalker_dosample = int(bool(self.subtalker_dosample))
+        o.subtalker_top_k = int(self.subtalker_top_k)
+        o.subtalker_top_p = float(self.subtalker_top_p)
+        o.subtalker_temperature = float(self.subtalker_temperature)
+        o.seed = int(self.seed) & 0xFFFFFFFFFFFFFFFF
+        return o
+
+    def validate(self) -> None:
+        """``validate_generate_options`` (generation.rs:569-583), through the C ABI."""
+        load_library()
+        o = self._c()
+        _check(_lib.q3t_generate_options_validate(ctypes.byref(o)))
+
+
+@dataclasses.dataclass
+class StreamOptions:
+    """``StreamOptions`` (generation.rs:79-92)."""
+    text_lookahead_tokens: int = DEFAULT_TEXT_LOOKAHEAD_TOKENS
+    left_context_frames: int = DEFAULT_STREAM_LEFT_CONTEXT_FRAMES
+
+    def validate(self) -> None:
+        if self.text_lookahead_tokens == 0:
+            raise InvalidInputError(Q3T_ERR_INVALID, "text_lookahead_tokens must be non-zero")
+
+
+@dataclasses.dataclass
+class GeneratedCodes:
+    codes: np.ndarray        # [frames, num_code_groups] int32
+    frames: int
+    ended_by_eos: bool
+
+
+@dataclasses.dataclass
+class GeneratedCodesChunk:
+    codes: np.ndarray        # [frames, num_code_groups] int32
+    frames: int
+    total_frames: int
+    ended_by_eos: bool
+
+
+Inputs = Union[PreparedInputs, Sequence[int]]
+
+
+class HipTtsEngine:
+    def __init__(self, model_dir: str, options: EngineOptions = EngineOptions(),
+                 text_prep: Optional[TextPrep] = None):
+        load_library()
+        o = _EngineOptions(model_dir.encode(), options.device, options.max_cache_steps,
+                           options.max_streams, int(options.use_graph), int(options.kv_bf16))
+        handle = ctypes.c_void_p()
+        _check(_lib.q3t_engine_create(ctypes.byref(o), ctypes.byref(handle)))
+        self._h = handle
+        info = _EngineInfo()
+        _check(_lib.q3t_engine_get_info(self._h, ctypes.byref(info)))
+        self.info = {n: getattr(info, n) for n, _ in _EngineInfo._fields_}
+        self.code_groups = info.num_code_groups
+        self.codec_eos_token = info.codec_eos
+        self.max_cache_steps = info.max_cache_steps
+        self.hidden = info.talker_hidden
+        self.text_prep = text_prep
+        self._streams = 0
+
+    # -- constructors (generation.rs:255-315) ------------------------------------------
+    @classmethod
+    def load(cls, model_dir: str, device: int = 0, **kw) -> "HipTtsEngine":
+        return cls(model_dir, EngineOptions(device=device), **kw)
+
+    @classmethod
+    def load_with_max_frames(cls, model_dir: str, device: int, max_frames: int, **kw) -> "HipTtsEngine":
+        return cls(model_dir, EngineOptions(device=device,
+                                            max_cache_steps=DEFAULT_PREFILL_HEADROOM + max_frames), **kw)
+
+    @classmethod
+    def load_with_options(cls, model_dir: str, options: EngineOptions, **kw) -> "HipTtsEngine":
+        return cls(model_dir, options, **kw)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            _check(_lib.q3t_engine_destroy(self._h))
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_trace(self, enabled: bool) -> None:
+        """Record raw logits of every step (parity checks)."""
+        _check(_lib.q3t_engine_set_trace(self._h, int(bool(enabled))))
+
+    # -- generation ----------------------------------------------------------------------
+    def _prepare(self, inputs: Inputs, options: GenerateOptions, lookahead: int) -> PreparedInputs:
+        if isinstance(inputs, PreparedInputs):
+            return inputs
+        if self.text_prep is None:
+            raise InvalidInputError(Q3T_ERR_INVALID, "content ids need a TextPrep; pass PreparedInputs instead")
+        return self.text_prep.prepare(inputs, options.speaker, options.language, lookahead)
+
+    def generate_codes(self, inputs: Inputs, options: GenerateOptions = GenerateOptions()) -> GeneratedCodes:
+        """``generate_codes`` (generation.rs:356-371): all text in the prefill, then the rollout."""
+        inp = self._prepare(inputs, options, 1 << 30)
+        o = options._c()
+        pre, trail, pad = _f32(inp.prefill), _f32(inp.trailing_text), _f32(inp.tts_pad_embed)
+        codes = np.zeros((max(options.max_frames, 0), self.code_groups), dtype=np.int32)
+        frames, eos = ctypes.c_int32(), ctypes.c_int32()
+        _check(_lib.q3t_generate_codes(self._h, _fptr(pre), pre.shape[0], _fptr(trail), trail.shape[0],
+                                       _fptr(pad), ctypes.byref(o), _iptr(codes), ctypes.byref(frames),
+                                       ctypes.byref(eos)))
+        return GeneratedCodes(codes[:frames.value].copy(), frames.value, bool(eos.value))
+
+    def start_stream(self, inputs: Inputs, options: GenerateOptions = GenerateOptions(),
+                     stream_options: StreamOptions = StreamOptions()) -> "HipTtsStream":
+        """``start_stream`` (generation.rs:421-440)."""
+        stream_options.validate()
+        inp = self._prepare(inputs, options, stream_options.text_lookahead_tokens)
+        return HipTtsStream(self, inp, options, stream_options)
+
+
+class HipTtsStream:
+    """``HipTtsStream`` (generation.rs:145-163, 876-997).  Must not outlive its engine."""
+
+    def __init__(self, engine: HipTtsEngine, inputs: PreparedInputs, options: GenerateOptions,
+                 stream_options: StreamOptions):
+        self.engine = engine
+        self.inputs = inputs
+        self.options = options
+        self.stream_options = stream_options
+        o = options._c()
+        pre, trail, pad = _f32(inputs.prefill), _f32(inputs.trailing_text), _f32(inputs.tts_pad_embed)
+        h = ctypes.c_void_p()
+        _check(_lib.q3t_stream_start(engine._h, _fptr(pre), pre.shape[0], _fptr(trail), trail.shape[0],
+                                     _fptr(pad), ctypes.byref(o), ctypes.byref(h)))
+        self._h = h
+        self.prefill_steps = inputs.prefill_steps
+        self._codes = []
+        self.frame = 0
+        self.ended_by_eos = False
+
+    def next_codes_chunk(self, max_chunk_frames: int) -> Optional[GeneratedCodesChunk]:
+        if max_chunk_frames <= 0:
+            raise InvalidInputError(Q3T_ERR_INVALID, "max_chunk_frames must be non-zero")
+        buf = np.zeros((max_chunk_frames, self.engine.code_groups), dtype=np.int32)
+        info = _ChunkInfo()
+        _check(_lib.q3t_stream_next_codes(self._h, max_chunk_frames, _iptr(buf), ctypes.byref(info)))
+        self.frame = info.total_frames
+        self.ended_by_eos = bool(info.ended_by_eos)
+        if info.frames == 0:
+            return None
+        codes = buf[:info.frames].copy()
+        self._codes.append(codes)
+        return GeneratedCodesChunk(codes, info.frames, info.total_frames, bool(info.ended_by_eos))
+
+    def finish_codes(self) -> GeneratedCodes:
+        codes = (np.concatenate(self._codes) if self._codes
+                 else np.zeros((0, self.engine.code_groups), dtype=np.int32))
+        self.close()
+        return GeneratedCodes(codes, int(codes.shape[0]), self.ended_by_eos)
+
+    def talker_logits(self) -> np.ndarray:
+        """Raw Talker logits of every Talker evaluation so far ([rows, V])."""
+        V = self.engine.info["talker_vocab"]
+        cap = self.frame + 1
+        out = np.zeros((cap, V), dtype=np.float32)
+        rows = ctypes.c_int32()
+        _check(_lib.q3t_stream_read_talker_logits(self._h, _fptr(out), cap, ctypes.byref(rows)))
+        return out[:rows.value]
+
+    def cp_logits(self) -> np.ndarray:
+        """CodePredictor logits of the frames so far ([frames, groups - 1, V_cp])."""
+        e = self.engine.info
+        out = np.zeros((max(self.frame, 1), e["num_code_groups"] - 1, e["cp_vocab"]), dtype=np.float32)
+        n = ctypes.c_int32()
+        _check(_lib.q3t_stream_read_cp_logits(self._h, _fptr(out), self.frame, ctypes.byref(n)))
+        return out[:n.value]
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            _check(_lib.q3t_stream_destroy(self._h))
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

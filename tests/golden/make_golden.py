@@ -1,0 +1,60 @@
+"""Writes the golden fixtures under tests/golden/ from the float64 CPU oracle.
+
+    python tests/golden/make_golden.py [workload ...]
+
+Each fixture holds one oracle rollout of a workload from q3t/workloads.py: the codes,
+the raw Talker logits (float16; the parity tolerance is 2e-2), the top-2 margins of every
+argmax (for the near-tie policy) and the first frames' CodePredictor logits, plus the
+weight checksum so a test can tell that it rebuilt the same synthetic model.
+"""
+from __future__ import annotations
+
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "qwen3-tts-hip_amd"))
+
+from oracle.model import GenerateOptions, Oracle  # noqa: E402
+from q3t import synth  # noqa: E402
+from q3t.workloads import WORKLOADS  # noqa: E402
+
+# Talker-logit rows kept per fixture (the codes and margins are always complete).
+MAX_LOGIT_ROWS = 256
+CP_LOGIT_FRAMES = 2
+
+
+def make(name: str) -> str:
+    w = WORKLOADS[name]
+    t0 = time.time()
+    model = synth.SyntheticModel.build(w.spec, w.weight_seed)
+    inputs = w.inputs(model)
+    oracle = Oracle(model.tensors, model.config(), max_cache_steps=w.max_cache_steps, dtype=np.float64)
+    opts = GenerateOptions(**w.options_kwargs())
+    tr = oracle.rollout(inputs.prefill, inputs.trailing_text, inputs.tts_pad_embed, opts,
+                        keep_cp_logits=CP_LOGIT_FRAMES)
+    meta = dict(workload=name, spec=w.spec, weight_seed=w.weight_seed, checksum=model.checksum(),
+                prefill_steps=inputs.prefill_steps, trailing_steps=inputs.trailing_steps,
+                frames=tr.frames, ended_by_eos=tr.ended_by_eos, options=w.options_kwargs(),
+                oracle_dtype="float64", seconds=round(time.time() - t0, 1))
+    path = os.path.join(HERE, f"{name}.npz")
+    np.savez_compressed(
+        path, meta=np.array(json.dumps(meta)), codes=tr.codes,
+        talker_logits=tr.talker_logits[:MAX_LOGIT_ROWS].astype(np.float16),
+        talker_margins=tr.talker_margins, cp_margins=tr.cp_margins,
+        cp_logits=np.asarray(tr.cp_logits, dtype=np.float16),
+        prefill_sum=np.array([float(np.sum(inputs.prefill, dtype=np.float64))]))
+    print(f"{name}: {tr.frames} frames, eos={tr.ended_by_eos}, {meta['seconds']} s -> {path}", flush=True)
+    return path
+
+
+if __name__ == "__main__":
+    names = sys.argv[1:] or [n for n in WORKLOADS if not n.startswith("cfg1")]
+    for n in names:
+        make(n)
