@@ -130,6 +130,15 @@ int q3t_stream_read_talker_logits(q3t_stream *stream, float *out, int32_t capaci
 int q3t_stream_read_cp_logits(q3t_stream *stream, float *out, int32_t capacity_frames,
                               int32_t *frames);
 
+/* The fused token sampler on its own: n draws from one logit row [V] (host array), draw i
+ * using Philox4x32-10 counter (i, kind, 0, 0) and key seed.  This is the code path of the
+ * frame loop's select kernels, exposed the way the reference exposes its sample_topk_f32
+ * kernel (src/gpu/kernels.rs:265-334) for statistical checks.  do_sample = 0 returns the
+ * argmax (ties to the lowest index, kernels.rs:176-221). */
+int q3t_sampler_draw(q3t_engine *engine, const float *logits, int32_t vocab, int32_t do_sample,
+                     int32_t top_k, float top_p, float temperature, uint64_t seed, int32_t kind,
+                     int32_t n, int32_t *tokens);
+
 const char *q3t_last_error(void);
 
 #ifdef __cplusplus

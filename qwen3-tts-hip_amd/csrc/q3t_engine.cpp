@@ -827,6 +827,34 @@ int q3t_stream_read_cp_logits(q3t_stream *sp, float *out, int32_t capacity, int3
   });
 }
 
+int q3t_sampler_draw(q3t_engine *e, const float *logits, int32_t V, int32_t do_sample, int32_t top_k, float top_p,
+                     float temperature, uint64_t seed, int32_t kind, int32_t n, int32_t *tokens) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || !logits || !tokens) fail(Q3T_ERR_INVALID, "null argument");
+    if (V <= 0 || V > kMaxVocab) fail(Q3T_ERR_INVALID, "vocabulary %d outside 1..%d", V, kMaxVocab);
+    if (n <= 0) fail(Q3T_ERR_INVALID, "draw count must be positive");
+    validate_sampling(do_sample, top_k, top_p, temperature, "sampler");
+    HIPC(hipSetDevice(e->device));
+    int64_t scratch = 0;
+    float *d_logits = dev_alloc<float>(V, scratch);
+    int32_t *d_out = nullptr;
+    try {
+      d_out = dev_alloc<int32_t>(n, scratch);
+      HIPC(hipMemcpy(d_logits, logits, (size_t)V * 4, hipMemcpyHostToDevice));
+      const SamplingParams sp{do_sample ? 1 : 0, top_k, top_p, temperature};
+      hip_check(launch_sample_draws(d_logits, V, sp, seed, kind, n, d_out, nullptr), "launch_sample_draws");
+      HIPC(hipMemcpy(tokens, d_out, (size_t)n * 4, hipMemcpyDeviceToHost));
+    } catch (...) {
+      (void)hipFree(d_logits);
+      if (d_out) (void)hipFree(d_out);
+      throw;
+    }
+    (void)hipFree(d_logits);
+    (void)hipFree(d_out);
+  });
+}
+
 int q3t_generate_codes(q3t_engine *e, const float *prefill, int32_t P, const float *trailing, int32_t T,
                        const float *tts_pad, const q3t_generate_options *o, int32_t *codes, int32_t *frames,
                        int32_t *ended_by_eos) {

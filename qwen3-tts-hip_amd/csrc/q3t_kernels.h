@@ -17,6 +17,9 @@ int attn_max_cache_steps(int q_heads, int kv_heads);
 
 hipError_t launch_select_talker(const SelectTalkerArgs &a, hipStream_t stream);
 hipError_t launch_select_cp(const SelectCpArgs &a, hipStream_t stream);
+// n independent draws from one logit row (draw i uses Philox counter (i, kind, 0, 0)).
+hipError_t launch_sample_draws(const float *logits, int V, const SamplingParams &sp, uint64_t seed, int kind, int n,
+                               int32_t *out, hipStream_t stream);
 hipError_t launch_frame_end(SlotState *st, const SlotParams *prm, int advance, hipStream_t stream);
 
 // Largest vocabulary the select kernels hold in LDS.

@@ -595,6 +595,19 @@ __global__ __launch_bounds__(1024) void k_select_cp(SelectCpArgs a) {
   }
 }
 
+// Standalone draws from one logit row: block b draws with Philox counter (b, kind, 0, 0).
+__global__ __launch_bounds__(1024) void k_sample_draws(const float *logits, int V, SamplingParams sp, uint32_t seed_lo,
+                                                       uint32_t seed_hi, int kind, int32_t *out) {
+  __shared__ SelectShared sh;
+  for (int i = threadIdx.x; i < V; i += 1024) sh.lg[i] = logits[i];
+  __syncthreads();
+  SlotParams p{};
+  p.seed_lo = seed_lo;
+  p.seed_hi = seed_hi;
+  const int tok = sp.do_sample ? block_sample(sh, V, sp, sampler_uniform(p, blockIdx.x, kind)) : block_argmax(sh, V);
+  if (threadIdx.x == 0) out[blockIdx.x] = tok;
+}
+
 // Ends a frame (advance = 1) or checks the token drawn after the prefill (advance = 0).
 __global__ void k_frame_end(SlotState *st, const SlotParams *prm, int advance) {
   if (threadIdx.x != 0 || st->done) return;
@@ -712,6 +725,14 @@ hipError_t launch_select_talker(const SelectTalkerArgs &a, hipStream_t s) {
 hipError_t launch_select_cp(const SelectCpArgs &a, hipStream_t s) {
   if (a.Vc > kMaxVocab) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_select_cp, dim3(1), dim3(1024), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_sample_draws(const float *logits, int V, const SamplingParams &sp, uint64_t seed, int kind, int n,
+                               int32_t *out, hipStream_t s) {
+  if (V <= 0 || V > kMaxVocab || n <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_sample_draws, dim3(n), dim3(1024), 0, s, logits, V, sp, (uint32_t)(seed & 0xffffffffu),
+                     (uint32_t)(seed >> 32), kind, out);
   return hipGetLastError();
 }
 

@@ -138,6 +138,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                                               f32p, P(_GenerateOptions), i32p, i32p, i32p]),
         "q3t_stream_read_talker_logits": (ctypes.c_int, [ctypes.c_void_p, f32p, ctypes.c_int32, i32p]),
         "q3t_stream_read_cp_logits": (ctypes.c_int, [ctypes.c_void_p, f32p, ctypes.c_int32, i32p]),
+        "q3t_sampler_draw": (ctypes.c_int, [ctypes.c_void_p, f32p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                            ctypes.c_float, ctypes.c_float, ctypes.c_uint64, ctypes.c_int32,
+                                            ctypes.c_int32, i32p]),
         "q3t_last_error": (ctypes.c_char_p, []),
     }
     for name, (res, args) in sigs.items():
@@ -197,8 +200,10 @@ class GenerateOptions:
     @classmethod
     def greedy(cls, max_frames: int = 240, **kw) -> "GenerateOptions":
         """The reference's parity setting (scripts/qwen3-hip-parity.sh:51-70)."""
-        return cls(max_frames=max_frames, do_sample=False, repetition_penalty=1.0,
-                   subtalker_dosample=False, decode_audio=False, **kw)
+        base = dict(max_frames=max_frames, do_sample=False, repetition_penalty=1.0,
+                    subtalker_dosample=False, decode_audio=False)
+        base.update(kw)
+        return cls(**base)
 
     def _c(self) -> _GenerateOptions:
         o = _GenerateOptions()
@@ -307,6 +312,16 @@ class HipTtsEngine:
     def set_trace(self, enabled: bool) -> None:
         """Record raw logits of every step (parity checks)."""
         _check(_lib.q3t_engine_set_trace(self._h, int(bool(enabled))))
+
+    def sampler_draw(self, logits: np.ndarray, n: int, do_sample: bool = True, top_k: int = 50,
+                     top_p: float = 1.0, temperature: float = 0.9, seed: int = 0, kind: int = 0) -> np.ndarray:
+        """n draws of the fused sampler from one logit row (draw i uses Philox counter (i, kind))."""
+        l = _f32(logits)
+        out = np.zeros(n, dtype=np.int32)
+        _check(_lib.q3t_sampler_draw(self._h, _fptr(l), l.shape[0], int(bool(do_sample)), int(top_k),
+                                     float(top_p), float(temperature), int(seed) & 0xFFFFFFFFFFFFFFFF,
+                                     int(kind), int(n), _iptr(out)))
+        return out
 
     # -- generation ----------------------------------------------------------------------
     def _prepare(self, inputs: Inputs, options: GenerateOptions, lookahead: int) -> PreparedInputs:

@@ -1,0 +1,207 @@
+"""GPU parity: the gfx950 token loop, through the C ABI, against the CPU oracle.
+
+Fixtures (tests/golden/*.npz) hold float64-oracle rollouts of the workloads in
+q3t/workloads.py; small variants are recomputed here with the oracle directly.
+"""
+import numpy as np
+import pytest
+
+from oracle.model import GenerateOptions as OracleOptions
+from oracle.model import Oracle
+from q3t import engine as E
+from q3t import synth
+from q3t.workloads import WORKLOADS
+
+from parity import LOGIT_TOL, check_codes, check_talker_logits, fixture_exists, load_fixture
+
+pytestmark = pytest.mark.gpu
+
+
+def run(models, name, chunk=None, use_graph=True, kv_bf16=False, trace=True, options=None, inputs=None,
+        model_dir=None, cap=None):
+    w = WORKLOADS[name]
+    model, d = models.get(w.spec, w.weight_seed)
+    inputs = inputs if inputs is not None else w.inputs(model)
+    opts = options or E.GenerateOptions(**w.options_kwargs())
+    print(f"[gpu] {name} chunk={chunk} graph={use_graph} kv_bf16={kv_bf16}", flush=True)
+    eng = E.HipTtsEngine(model_dir or d, E.EngineOptions(max_cache_steps=cap or w.max_cache_steps,
+                                                         use_graph=use_graph, kv_bf16=kv_bf16))
+    try:
+        eng.set_trace(trace)
+        st = eng.start_stream(inputs, opts)
+        chunks = []
+        while True:
+            c = st.next_codes_chunk(chunk or w.chunk_frames)
+            if c is None:
+                break
+            chunks.append(c)
+        tl = st.talker_logits() if trace else None
+        cl = st.cp_logits() if trace else None
+        eos = st.ended_by_eos
+        st.close()
+    finally:
+        eng.close()
+    codes = np.concatenate([c.codes for c in chunks]) if chunks else np.zeros((0, 16), np.int32)
+    return dict(codes=codes, eos=eos, talker_logits=tl, cp_logits=cl, chunks=chunks)
+
+
+@pytest.mark.parametrize("name", ["tiny_greedy", "tiny_sampled", "tinyproj_greedy"])
+def test_small_workloads_match_fixture(models, name):
+    fx = load_fixture(name)
+    model, _ = models.get(fx["meta"]["spec"], fx["meta"]["weight_seed"])
+    assert model.checksum() == fx["meta"]["checksum"]
+    r = run(models, name)
+    same = check_codes(r["codes"], r["eos"], fx, allow_ties=not WORKLOADS[name].do_sample)
+    err = check_talker_logits(r["talker_logits"], fx, same)
+    cp_err = float(np.abs(r["cp_logits"][:len(fx["cp_logits"])] - fx["cp_logits"].astype(np.float32)).max())
+    print(f"{name}: {same} frames identical, talker logit err {err:.2e}, cp logit err {cp_err:.2e}")
+    assert cp_err <= LOGIT_TOL
+
+
+def test_chunking_and_generate_codes_agree(models):
+    ref = run(models, "tiny_greedy", chunk=24)["codes"]
+    for chunk in (1, 5, 7):
+        r = run(models, "tiny_greedy", chunk=chunk, trace=False)
+        np.testing.assert_array_equal(r["codes"], ref)
+        sizes = [c.frames for c in r["chunks"]]
+        assert all(s == chunk for s in sizes[:-1]) and 0 < sizes[-1] <= chunk
+        assert [c.total_frames for c in r["chunks"]] == list(np.cumsum(sizes))
+    w = WORKLOADS["tiny_greedy"]
+    model, d = models.get(w.spec)
+    with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=w.max_cache_steps)) as eng:
+        g = eng.generate_codes(w.inputs(model), E.GenerateOptions(**w.options_kwargs()))
+    np.testing.assert_array_equal(g.codes, ref)
+    assert g.frames == len(ref) and not g.ended_by_eos
+
+
+def test_graph_replay_is_bitwise_equal_to_eager(models):
+    a = run(models, "tiny_sampled", use_graph=True)
+    b = run(models, "tiny_sampled", use_graph=False)
+    np.testing.assert_array_equal(a["codes"], b["codes"])
+    np.testing.assert_array_equal(a["talker_logits"], b["talker_logits"])
+    np.testing.assert_array_equal(a["cp_logits"], b["cp_logits"])
+
+
+def test_runs_are_deterministic(models):
+    a = run(models, "tiny_greedy")
+    b = run(models, "tiny_greedy")
+    np.testing.assert_array_equal(a["talker_logits"], b["talker_logits"])
+    np.testing.assert_array_equal(a["codes"], b["codes"])
+
+
+def _oracle_rollout(model, inputs, opts: E.GenerateOptions, cap, kv_bf16=False, keep_cp=0):
+    o = Oracle(model.tensors, model.config(), max_cache_steps=cap, kv_bf16=kv_bf16)
+    oo = OracleOptions(**{k: getattr(opts, k) for k in OracleOptions.__dataclass_fields__})
+    return o.rollout(inputs.prefill, inputs.trailing_text, inputs.tts_pad_embed, oo, keep_cp_logits=keep_cp)
+
+
+def _as_fixture(tr):
+    return dict(codes=tr.codes, talker_logits=tr.talker_logits, talker_margins=tr.talker_margins,
+                cp_margins=tr.cp_margins, meta=dict(ended_by_eos=tr.ended_by_eos))
+
+
+def test_greedy_repetition_penalty_matches_oracle(models):
+    w = WORKLOADS["tiny_greedy"]
+    model, _ = models.get(w.spec)
+    inputs = w.inputs(model)
+    opts = E.GenerateOptions.greedy(16, repetition_penalty=1.3)
+    r = run(models, "tiny_greedy", options=opts)
+    fx = _as_fixture(_oracle_rollout(model, inputs, opts, w.max_cache_steps))
+    same = check_codes(r["codes"], r["eos"], fx)
+    check_talker_logits(r["talker_logits"], fx, same)
+
+
+def test_bf16_kv_cache_matches_bf16_oracle(models):
+    """KV stored as bf16 (rounded once at the store), against the oracle's bf16-KV model."""
+    w = WORKLOADS["tiny_greedy"]
+    model, _ = models.get(w.spec)
+    tr = _oracle_rollout(model, w.inputs(model), E.GenerateOptions(**w.options_kwargs()), w.max_cache_steps,
+                         kv_bf16=True)
+    r = run(models, "tiny_greedy", kv_bf16=True)
+    fx = _as_fixture(tr)
+    same = check_codes(r["codes"], r["eos"], fx)
+    check_talker_logits(r["talker_logits"], fx, same)
+
+
+def test_eos_ends_stream_like_the_reference(models, tmp_path):
+    """A model whose EOS row copies (and slightly beats) a token the baseline emits."""
+    w = WORKLOADS["tiny_greedy"]
+    base, _ = models.get(w.spec)
+    inputs = w.inputs(base)
+    ref = _oracle_rollout(base, inputs, E.GenerateOptions.greedy(12), w.max_cache_steps)
+    sem = ref.codes[:, 0].tolist()
+    # the first semantic token that first appears at frame >= 2: EOS takes its place there
+    target = next(t for f, t in enumerate(sem) if f >= 2 and t not in sem[:f])
+    tensors = dict(base.tensors)
+    head = synth.bf16_bits_to_f32(tensors["talker.codec_head.weight"]).copy()
+    head[2150] = head[target] * 1.01
+    tensors["talker.codec_head.weight"] = synth.f32_to_bf16_bits(head)
+    model = synth.SyntheticModel(base.spec, base.seed, tensors)
+    model.write(str(tmp_path))
+    tr = _oracle_rollout(model, inputs, E.GenerateOptions.greedy(12), w.max_cache_steps)
+    assert tr.ended_by_eos and 0 < tr.frames < 12
+    r = run(models, "tiny_greedy", options=E.GenerateOptions.greedy(12), model_dir=str(tmp_path), chunk=2)
+    np.testing.assert_array_equal(r["codes"], tr.codes)
+    assert r["eos"] and r["chunks"][-1].ended_by_eos
+
+
+def test_capacity_busy_and_exhausted_streams(models):
+    w = WORKLOADS["tiny_greedy"]
+    model, d = models.get(w.spec)
+    inputs = w.inputs(model)
+    with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=64, max_streams=1)) as eng:
+        with pytest.raises(E.CapacityError):
+            eng.start_stream(inputs, E.GenerateOptions.greedy(64 - inputs.prefill_steps + 1))
+        st = eng.start_stream(inputs, E.GenerateOptions.greedy(3))
+        with pytest.raises(E.BusyError):
+            eng.start_stream(inputs, E.GenerateOptions.greedy(3))
+        assert st.next_codes_chunk(6).frames == 3
+        assert st.next_codes_chunk(6) is None
+        with pytest.raises(E.InvalidInputError):
+            st.next_codes_chunk(0)
+        st.close()
+        st2 = eng.start_stream(inputs, E.GenerateOptions.greedy(2))   # the slot is free again
+        assert st2.next_codes_chunk(1).frames == 1
+        # finish_codes returns what was produced so far, without draining (generation.rs:991-997)
+        assert st2.finish_codes().frames == 1
+        with pytest.raises(E.InvalidInputError):
+            eng.start_stream(inputs, E.GenerateOptions(top_p=0.0))
+
+
+def test_two_stream_slots_are_independent(models):
+    w = WORKLOADS["tiny_greedy"]
+    model, d = models.get(w.spec)
+    inputs = w.inputs(model)
+    ref = run(models, "tiny_greedy", trace=False)["codes"]
+    with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=w.max_cache_steps, max_streams=2)) as eng:
+        opts = E.GenerateOptions(**w.options_kwargs())
+        a = eng.start_stream(inputs, opts)
+        b = eng.start_stream(inputs, opts)
+        out_a, out_b = [], []
+        while True:
+            ca, cb = a.next_codes_chunk(5), b.next_codes_chunk(3)
+            if ca:
+                out_a.append(ca.codes)
+            if cb:
+                out_b.append(cb.codes)
+            if ca is None and cb is None:
+                break
+        a.close()
+        b.close()
+    np.testing.assert_array_equal(np.concatenate(out_a), ref)
+    np.testing.assert_array_equal(np.concatenate(out_b), ref)
+
+
+@pytest.mark.parametrize("name", ["cfg2_0.6b_greedy", "cfg3_0.6b_sampled", "cfg4_1.7b_greedy"])
+def test_baseline_workloads_match_fixture(models, name):
+    if not fixture_exists(name):
+        pytest.skip(f"fixture {name} not generated")
+    fx = load_fixture(name)
+    model, _ = models.get(fx["meta"]["spec"], fx["meta"]["weight_seed"])
+    assert model.checksum() == fx["meta"]["checksum"]
+    r = run(models, name)
+    same = check_codes(r["codes"], r["eos"], fx, allow_ties=not WORKLOADS[name].do_sample)
+    err = check_talker_logits(r["talker_logits"], fx, same)
+    print(f"{name}: {same}/{len(fx['codes'])} frames identical, talker logit max err {err:.2e}")
+    if name.startswith("cfg4"):
+        models.drop(fx["meta"]["spec"], fx["meta"]["weight_seed"])
