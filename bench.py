@@ -1,0 +1,185 @@
+"""Benchmark: codec frames/s and RTF of the Qwen3-TTS token loop on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2_0.6b_greedy]
+
+A step is one full generation of the workload (BASELINE config 2 by default: 0.6B shape,
+bf16 weights, greedy, batch 1, 64-token prompt, 240 frames pulled in chunks of 6, KV
+capacity 256): Talker prefill, then every frame's CodePredictor groups and Talker step.
+Inputs (weights, prefill rows) are resident in HBM before the timed region; the timed
+region is K steps bracketed by device synchronisation.  RTF = seconds / (frames * 0.080).
+
+Prints one JSON line.  Besides the contract fields it carries:
+  rtf, frame_ms                  per-frame latency view of the same run
+  frame_algorithmic_GBps         bytes one frame must move (weights + KV) / frame time
+  roofline                       the dominant kernel, timed live with HIP events
+  cpu_baseline                   the float32 CPU oracle on BASELINE config 1 (bounded sample)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "qwen3-tts-hip_amd"))
+
+HBM_PEAK_GBPS = 8000.0
+FRAME_SECONDS = 0.080
+
+
+def frame_bytes(spec, active_steps_mean: float, kv_elem: int) -> float:
+    """Algorithmic bytes of one frame: every bf16 weight the frame reads once per pass
+    (Talker stack + codec head + final norm, then 15 CodePredictor passes of stack + one
+    LM head (+ projection)), plus the KV cache rows attention reads and writes."""
+    t, c = spec.talker, spec.code_predictor
+
+    def stack_params(s):
+        q, kv = s.q_heads * s.head_dim, s.kv_heads * s.head_dim
+        return s.layers * ((q + 2 * kv) * s.hidden + s.hidden * q + 3 * s.intermediate * s.hidden)
+
+    talker = 2 * (stack_params(t) + t.vocab * t.hidden + t.hidden)
+    proj = c.hidden * t.hidden if spec.has_projection else 0
+    cp_pass = 2 * (stack_params(c) + c.vocab * c.hidden + c.hidden + proj)
+    groups = spec.num_code_groups - 1
+    kv_row_t = t.layers * 2 * t.kv_heads * t.head_dim * kv_elem
+    kv_row_c = c.layers * 2 * c.kv_heads * c.head_dim * kv_elem
+    kv = kv_row_t * active_steps_mean + kv_row_c * sum(range(1, spec.num_code_groups + 1))
+    return talker + groups * cp_pass + kv
+
+
+def cpu_baseline(seconds_budget: float) -> dict:
+    """BASELINE config 1 on the host CPU: float32 oracle, 0.6B shape, 32-token prompt,
+    greedy; as many frames as fit the time budget (bounded sample)."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+
+    sys.path.insert(0, ROOT)
+    from oracle.model import GenerateOptions as OO
+    from oracle.model import Oracle
+    from q3t import synth
+    from q3t.workloads import WORKLOADS
+
+    w = WORKLOADS["cfg1_cpu_0.6b"]
+    model = synth.SyntheticModel.build(w.spec, w.weight_seed)
+    inputs = w.inputs(model)
+    o = Oracle(model.tensors, model.config(), max_cache_steps=w.max_cache_steps, dtype=np.float32)
+    del model
+    # size the sample: one 2-frame probe, then as many frames as the budget allows (<= 40)
+    t0 = time.perf_counter()
+    o.rollout(inputs.prefill, inputs.trailing_text, inputs.tts_pad_embed, OO.greedy(2))
+    probe = time.perf_counter() - t0
+    frames = int(max(2, min(w.frames, 2 * seconds_budget / max(probe, 1e-3) - 2)))
+    t0 = time.perf_counter()
+    tr = o.rollout(inputs.prefill, inputs.trailing_text, inputs.tts_pad_embed, OO.greedy(frames))
+    el = time.perf_counter() - t0
+    blas = [i for i in threadpool_info() if i.get("user_api") == "blas"]
+    cores = int(blas[0]["num_threads"]) if blas else 1
+    try:
+        model_name = next(l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo") if l.startswith("model name"))
+    except Exception:
+        model_name = "unknown"
+    return {"value": round(tr.frames / el, 3), "unit": "frames/s", "cores": cores, "kind": "port",
+            "rtf": round(el / (tr.frames * FRAME_SECONDS), 3),
+            "sample": f"config 1: 0.6B float32 oracle (numpy/BLAS), 32-token prompt (P=41), greedy, "
+                      f"prefill + {tr.frames} frames in {el:.1f} s; cpu '{model_name}', os.cpu_count()="
+                      f"{os.cpu_count()}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--workload", default="cfg2_0.6b_greedy")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--eager", action="store_true", help="launch every kernel from the host (no graph)")
+    ap.add_argument("--kv-bf16", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "streams shard across GPUs by data parallelism with no exchange step, so N GPUs = N x one GPU.",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    from q3t import engine as E
+    from q3t import synth
+    from q3t.workloads import WORKLOADS
+
+    w = WORKLOADS[args.workload]
+    model = synth.SyntheticModel.build(w.spec, w.weight_seed)
+    inputs = w.inputs(model)
+    tmp = tempfile.mkdtemp(prefix="q3t_bench_")
+    model.write(tmp)
+    spec = model.spec
+    del model
+    eng = E.HipTtsEngine(tmp, E.EngineOptions(max_cache_steps=w.max_cache_steps, use_graph=not args.eager,
+                                              kv_bf16=args.kv_bf16))
+    opts = E.GenerateOptions(**w.options_kwargs())
+
+    def one_step():
+        st = eng.start_stream(inputs, opts)
+        n = 0
+        while True:
+            c = st.next_codes_chunk(w.chunk_frames)
+            if c is None:
+                break
+            n += c.frames
+        st.close()
+        return n
+
+    for _ in range(args.warmup):
+        one_step()
+    eng.synchronize()
+    t0 = time.perf_counter()
+    frames = 0
+    for _ in range(args.steps):
+        frames += one_step()
+    eng.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    P = inputs.prefill_steps
+    per_gen = frames / max(args.steps, 1)
+    active_mean = P + (per_gen - 1) / 2.0
+    fb = frame_bytes(spec, active_mean, 2 if args.kv_bf16 else 4)
+    frame_s = elapsed / frames
+    roofline = eng.dominant_kernel_roofline(HBM_PEAK_GBPS)
+    eng.close()
+    import shutil
+    shutil.rmtree(tmp, ignore_errors=True)
+
+    out = {
+        "metric": "codec frames/sec + RTF, 0.6B bs=1 greedy; decode HBM GB/s vs peak",
+        "value": round(frames / elapsed, 2),
+        "unit": "frames/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1000 * elapsed / args.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init N(0,0.02) bf16 weights, seed 0; random prompt ids, seed 1)",
+        "config": {"workload": w.name, "spec": w.spec, "batch": 1, "prompt_tokens": w.prompt_tokens,
+                   "prefill_steps": P, "frames_per_step": per_gen, "chunk_frames": w.chunk_frames,
+                   "kv_capacity": w.max_cache_steps, "greedy": not w.do_sample,
+                   "graph": not args.eager, "kv_cache": "bf16" if args.kv_bf16 else "fp32"},
+        "rtf": round(frame_s / FRAME_SECONDS, 5),
+        "frame_ms": round(1000 * frame_s, 4),
+        "frame_algorithmic_GBps": round(fb / frame_s / 1e9, 1),
+        "frame_algorithmic_bytes": int(fb),
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -130,6 +130,22 @@ int q3t_stream_read_talker_logits(q3t_stream *stream, float *out, int32_t capaci
 int q3t_stream_read_cp_logits(q3t_stream *stream, float *out, int32_t capacity_frames,
                               int32_t *frames);
 
+/* Waits until every stream slot of the engine is idle. */
+int q3t_engine_synchronize(q3t_engine *engine);
+
+/* Kernel timing for the roofline report (no counterpart in the reference, whose profiler is
+ * external rocprofv3 + ROCTx ranges, src/gpu/profile.rs:20-72).  Captures `iters` kernels of
+ * one class, in the order a frame issues them (Talker layers, then the CodePredictor layers of
+ * its 15 passes), as one hipGraph on stream slot 0's stream -- the way frames run -- and times
+ * one replay with hipEvents.  Returns the average time per launch (us; the gap between
+ * dependent launches included) and the algorithmic bytes one launch moves.
+ *   kernel 0: QKV GEMV (+ input RMSNorm)    1: O GEMV (+ residual)
+ *          2: gate/up GEMV (+ RMSNorm, SwiGLU)    3: down GEMV (+ residual)
+ *          4: Talker attention over a full cache
+ * Slot 0 must not hold a stream. */
+int q3t_bench_kernel(q3t_engine *engine, int32_t kernel, int32_t iters, double *avg_us,
+                     double *bytes_per_launch);
+
 /* The fused token sampler on its own: n draws from one logit row [V] (host array), draw i
  * using Philox4x32-10 counter (i, kind, 0, 0) and key seed.  This is the code path of the
  * frame loop's select kernels, exposed the way the reference exposes its sample_topk_f32

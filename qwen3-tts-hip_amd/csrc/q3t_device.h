@@ -68,6 +68,9 @@ struct GemvArgs {
   float eps;
   int32_t skip;
   const SlotState *st;
+  // Input = merge of attention partials (O projection after split attention), when set.
+  const float *attn_part;
+  int32_t attn_part_chunks, attn_chunk, attn_pos_mode, attn_pos_const, attn_q_heads, attn_kv_heads;
 };
 
 struct AttnArgs {
@@ -84,6 +87,10 @@ struct AttnArgs {
   int32_t skip;
   int32_t kv_bf16;
   const SlotState *st;
+  float *part;          // [kv_heads][part_chunks][G][2 + d] per-chunk (max, sum, P.V)
+  int32_t part_chunks;
+  int32_t chunk;        // key rows per workgroup (attn_chunk_len(cap))
+  int32_t partial_out;  // 1: write partials for the O projection to merge; 0: write `out`
 };
 
 struct SelectTalkerArgs {

@@ -290,6 +290,8 @@ struct Slot {
   char *t_k = nullptr, *t_v = nullptr, *c_k = nullptr, *c_v = nullptr;  // KV caches (fp32 or bf16)
   float *x_t, *t_in, *qkv, *attn, *act, *logits_t, *logits_c, *x_c, *cp_prefix, *cp_in, *cur, *emb_sum;
   float *trailing, *prefill;
+  float *attn_part;      // attention partials [kv_heads][chunks][G][2 + head_dim]
+  int attn_part_chunks = 0;
   int32_t *codes;
   SlotState *st;
   SlotParams *prm;
@@ -323,32 +325,49 @@ struct Engine {
   std::vector<Slot> slots;
   int64_t device_bytes = 0;
 
+  // nt: stream the weights with non-temporal loads (Talker weights are read once per frame).
   void gemv(int epi, bool norm, const uint16_t *W, const float *x, const float *gamma, float eps,
             const float *res, const float *bias, float *out, int N, int K, int skip, const SlotState *st,
-            hipStream_t s) {
+            hipStream_t s, bool nt = false, const LaunchTiming *timing = nullptr) {
     GemvArgs a{W, x, gamma, res, bias, out, N, K, eps, skip, st};
-    hip_check(launch_gemv(epi, norm, a, s), "launch_gemv");
+    hip_check(launch_gemv(epi, norm, nt, a, s, timing), "launch_gemv");
   }
 
   // One decoder-stack step for one position (decode.rs:951-1001 / 1300-1475).
   void stack_step(const StackW &w, char *kc, char *vc, const float *in, float *x, Slot &sl, int pos_mode,
                   int pos_const, int skip, hipStream_t s) {
     const Dims &d = w.d;
+    const bool nt = &w == &talker;
     const size_t cache_layer = (size_t)d.kv_heads * w.cap * d.head_dim * (kv_bf16 ? 2 : 4);
     for (int l = 0; l < d.layers; ++l) {
       const LayerW &L = w.layers[l];
       const float *src = l == 0 ? in : x;
       gemv(EPI_STORE, true, L.qkv, src, L.g_in, d.eps, nullptr, nullptr, sl.qkv, d.qkv_rows(), d.hidden, skip,
-           sl.st, s);
+           sl.st, s, nt);
+      // The Talker's attention spans many chunks: partials, merged by the O projection.  The
+      // CodePredictor's 16-row cache is one chunk: direct output.
+      const int partial = attn_chunks(w.cap) > 1 ? 1 : 0;
       AttnArgs aa{sl.qkv,   L.gq,    L.gk,     w.rope,  kc + l * cache_layer, vc + l * cache_layer,
                   sl.attn,  d.q_heads, d.kv_heads, w.cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
-                  pos_mode, pos_const, skip,    kv_bf16, sl.st};
+                  pos_mode, pos_const, skip,    kv_bf16, sl.st,  sl.attn_part, sl.attn_part_chunks,
+                  attn_chunk_len(w.cap), partial};
       hip_check(launch_attn_decode(aa, d.head_dim, s), "launch_attn_decode");
-      gemv(EPI_RESIDUAL, false, L.o, sl.attn, nullptr, 0.f, src, nullptr, x, d.hidden, d.q_out(), skip, sl.st, s);
+      GemvArgs og{L.o, sl.attn, nullptr, src, nullptr, x, d.hidden, d.q_out(), 0.f, skip, sl.st};
+      if (partial) {
+        og.x = nullptr;
+        og.attn_part = sl.attn_part;
+        og.attn_part_chunks = sl.attn_part_chunks;
+        og.attn_chunk = attn_chunk_len(w.cap);
+        og.attn_pos_mode = pos_mode;
+        og.attn_pos_const = pos_const;
+        og.attn_q_heads = d.q_heads;
+        og.attn_kv_heads = d.kv_heads;
+      }
+      hip_check(launch_gemv(EPI_RESIDUAL, false, nt, og, s), "launch_gemv");
       gemv(EPI_SWIGLU, true, L.gu, x, L.g_post, d.eps, nullptr, nullptr, sl.act, d.intermediate, d.hidden, skip,
-           sl.st, s);
+           sl.st, s, nt);
       gemv(EPI_RESIDUAL, false, L.down, sl.act, nullptr, 0.f, x, nullptr, x, d.hidden, d.intermediate, skip, sl.st,
-           s);
+           s, nt);
     }
   }
 
@@ -393,7 +412,7 @@ struct Engine {
     }
     stack_step(talker, sl.t_k, sl.t_v, sl.t_in, sl.x_t, sl, POS_TALKER_FRAME, 0, SKIP_TALKER, s);
     gemv(EPI_STORE, true, codec_head, sl.x_t, t_norm, td.eps, nullptr, nullptr, sl.logits_t, td.vocab, td.hidden,
-         SKIP_TALKER, sl.st, s);
+         SKIP_TALKER, sl.st, s, true);
     select_talker(sl, 1, s);
     hip_check(launch_frame_end(sl.st, sl.prm, 1, s), "launch_frame_end");
   }
@@ -464,6 +483,17 @@ void alloc_slot(Engine &e, Slot &s) {
   s.trailing = dev_alloc<float>((size_t)(e.cap + 1) * Ht, t);
   s.prefill = dev_alloc<float>((size_t)e.cap * Ht, t);
   s.codes = dev_alloc<int32_t>((size_t)e.cap * e.groups, t);
+  s.attn_part_chunks = std::max(attn_chunks(e.cap), attn_chunks(e.cp.cap));
+  const int kvh = std::max(td.kv_heads, cd.kv_heads);
+  const int gq = std::max(td.q_heads / td.kv_heads, cd.q_heads / cd.kv_heads);
+  s.attn_part = dev_alloc<float>((size_t)kvh * s.attn_part_chunks * gq * (td.head_dim + 2), t);
+  HIPC(hipMemset(s.attn_part, 0, (size_t)kvh * s.attn_part_chunks * gq * (td.head_dim + 2) * 4));
+  for (auto [p, n] : std::initializer_list<std::pair<float *, size_t>>{
+           {s.x_t, (size_t)Ht}, {s.t_in, (size_t)Ht}, {s.qkv, (size_t)qkv},
+           {s.attn, (size_t)std::max(td.q_out(), cd.q_out())},
+           {s.act, (size_t)std::max(td.intermediate, cd.intermediate)}, {s.x_c, (size_t)Hc},
+           {s.cp_prefix, 2 * (size_t)Ht}, {s.cp_in, 3 * (size_t)Hc}, {s.cur, (size_t)Ht}, {s.emb_sum, (size_t)Ht}})
+    HIPC(hipMemset(p, 0, n * 4));
   s.st = dev_alloc<SlotState>(1, t);
   s.prm = dev_alloc<SlotParams>(1, t);
   HIPC(hipMemset(s.st, 0, sizeof(SlotState)));
@@ -476,7 +506,8 @@ void free_slot(Slot &s) {
   if (s.graph) (void)hipGraphExecDestroy(s.graph);
   void *ptrs[] = {s.t_k,    s.t_v,   s.c_k,       s.c_v,   s.x_t,     s.t_in,     s.qkv,      s.attn,
                   s.act,    s.logits_t, s.logits_c, s.x_c, s.cp_prefix, s.cp_in, s.cur,      s.emb_sum,
-                  s.trailing, s.prefill, s.codes,   s.st,    s.prm,     s.trace_t,  s.trace_c};
+                  s.trailing, s.prefill, s.codes,   s.st,    s.prm,     s.trace_t,  s.trace_c,
+                  s.attn_part};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (s.stream) (void)hipStreamDestroy(s.stream);
@@ -585,8 +616,7 @@ int q3t_engine_create(const q3t_engine_options *opts, q3t_engine **out) {
     // Shape limits of the kernels (checked here so that no launch can index outside).
     for (const Dims *d : {&td, &cd}) {
       if (d->head_dim != 128) fail(Q3T_ERR_INVALID, "head_dim %d unsupported (kernels are built for 128)", d->head_dim);
-      if (d->kv_heads <= 0 || d->q_heads % d->kv_heads || d->q_heads / d->kv_heads > 4 ||
-          d->q_heads / d->kv_heads == 3)
+      if (d->kv_heads <= 0 || d->q_heads % d->kv_heads || d->q_heads / d->kv_heads > 2)
         fail(Q3T_ERR_INVALID, "q_heads %d / kv_heads %d unsupported", d->q_heads, d->kv_heads);
       if (!gemv_supports_k(d->hidden) || !gemv_supports_k(d->intermediate) || !gemv_supports_k(d->q_out()))
         fail(Q3T_ERR_INVALID, "hidden %d / intermediate %d / q_out %d must be 512 x {1,2,3,4,6,8,12}", d->hidden,
@@ -824,6 +854,132 @@ int q3t_stream_read_cp_logits(q3t_stream *sp, float *out, int32_t capacity, int3
     if (n > 0 && out)
       HIPC(hipMemcpy(out, s.trace_c, (size_t)n * (e.groups - 1) * e.cd.vocab * 4, hipMemcpyDeviceToHost));
     *frames = n;
+  });
+}
+
+int q3t_engine_synchronize(q3t_engine *e) {
+  return guarded([&] {
+    if (!e) fail(Q3T_ERR_INVALID, "null engine");
+    HIPC(hipSetDevice(e->device));
+    for (auto &s : e->slots) HIPC(hipStreamSynchronize(s.stream));
+  });
+}
+
+int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_us, double *bytes) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || !avg_us || !bytes) fail(Q3T_ERR_INVALID, "null argument");
+    if (iters <= 0 || iters > 8192) fail(Q3T_ERR_INVALID, "iters must be in 1..8192");
+    if (kernel < 0 || kernel > 4) fail(Q3T_ERR_INVALID, "unknown kernel class %d", kernel);
+    Slot &s = e->slots[0];
+    if (s.in_use) fail(Q3T_ERR_BUSY, "stream slot 0 is in use");
+    HIPC(hipSetDevice(e->device));
+    const Dims &td = e->td, &cd = e->cd;
+    // The launch sequence one frame issues for this kernel class: Talker layers first, then
+    // the CodePredictor layers of its 15 passes (the order enqueue_frame uses).
+    struct L {
+      const StackW *w;
+      int layer;
+    };
+    std::vector<L> seq;
+    if (kernel <= 3) {
+      for (int l = 0; l < td.layers; ++l) seq.push_back({&e->talker, l});
+      for (int g = 0; g < e->groups - 1; ++g)
+        for (int l = 0; l < cd.layers; ++l) seq.push_back({&e->cp, l});
+    } else {
+      for (int l = 0; l < td.layers; ++l) seq.push_back({&e->talker, l});
+    }
+    double total_bytes = 0.0;
+    auto enqueue = [&](int i, bool count) {
+      const L &l = seq[(size_t)i % seq.size()];
+      const Dims &d = l.w->d;
+      const LayerW &W = l.w->layers[l.layer];
+      const float *xin = l.w == &e->talker ? s.x_t : s.x_c;
+      const bool nt = l.w == &e->talker;
+      double b = 0.0;
+      switch (kernel) {
+        case 0:  // QKV projection with the input RMSNorm prologue
+          e->gemv(EPI_STORE, true, W.qkv, xin, W.g_in, d.eps, nullptr, nullptr, s.qkv, d.qkv_rows(), d.hidden,
+                  SKIP_NEVER, s.st, s.stream, nt);
+          b = 2.0 * d.qkv_rows() * d.hidden + 4.0 * (d.hidden * 2 + d.qkv_rows());
+          break;
+        case 1: {  // O projection + residual (Talker layers merge attention partials first)
+          GemvArgs og{W.o, s.attn, nullptr, s.act, nullptr, s.act, d.hidden, d.q_out(), 0.f, SKIP_NEVER, s.st};
+          if (nt) {
+            og.x = nullptr;
+            og.attn_part = s.attn_part;
+            og.attn_part_chunks = s.attn_part_chunks;
+            og.attn_chunk = attn_chunk_len(l.w->cap);
+            og.attn_pos_mode = POS_CONST;
+            og.attn_pos_const = l.w->cap / 2;
+            og.attn_q_heads = d.q_heads;
+            og.attn_kv_heads = d.kv_heads;
+          }
+          hip_check(launch_gemv(EPI_RESIDUAL, false, nt, og, s.stream), "launch_gemv");
+          b = 2.0 * d.hidden * d.q_out() + 4.0 * (d.q_out() + 2 * d.hidden);
+          break;
+        }
+        case 2:  // gate/up projection with the post-attention RMSNorm prologue and SwiGLU
+          e->gemv(EPI_SWIGLU, true, W.gu, xin, W.g_post, d.eps, nullptr, nullptr, s.act, d.intermediate, d.hidden,
+                  SKIP_NEVER, s.st, s.stream, nt);
+          b = 2.0 * 2 * d.intermediate * d.hidden + 4.0 * (2 * d.hidden + d.intermediate);
+          break;
+        case 3:  // down projection + residual
+          e->gemv(EPI_RESIDUAL, false, W.down, s.act, nullptr, 0.f, s.attn, nullptr, s.attn, d.hidden,
+                  d.intermediate, SKIP_NEVER, s.st, s.stream, nt);
+          b = 2.0 * d.hidden * d.intermediate + 4.0 * (d.intermediate + 2 * d.hidden);
+          break;
+        case 4: {  // Talker attention over a full cache (L = max_cache_steps)
+          const size_t esz = e->kv_bf16 ? 2 : 4;
+          const size_t layer_bytes = (size_t)d.kv_heads * l.w->cap * d.head_dim * esz;
+          AttnArgs aa{s.qkv, W.gq, W.gk, l.w->rope, s.t_k + layer_bytes * l.layer, s.t_v + layer_bytes * l.layer,
+                      s.attn, d.q_heads, d.kv_heads, l.w->cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
+                      POS_CONST, l.w->cap - 1, SKIP_NEVER, e->kv_bf16, s.st, s.attn_part, s.attn_part_chunks,
+                      attn_chunk_len(l.w->cap), attn_chunks(l.w->cap) > 1 ? 1 : 0};
+          hip_check(launch_attn_decode(aa, d.head_dim, s.stream), "launch_attn_decode");
+          b = 2.0 * esz * d.kv_heads * d.head_dim * l.w->cap + 4.0 * (d.qkv_rows() + d.q_out());
+          break;
+        }
+      }
+      if (count) total_bytes += b;
+    };
+    // Capture the launches as one graph (the way frames run), replay once to warm, then
+    // time one replay: average = elapsed / iters, inter-launch gaps included.
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    auto cleanup = [&] {
+      if (ge) (void)hipGraphExecDestroy(ge);
+      if (g) (void)hipGraphDestroy(g);
+      if (ev0) (void)hipEventDestroy(ev0);
+      if (ev1) (void)hipEventDestroy(ev1);
+    };
+    try {
+      HIPC(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal));
+      try {
+        for (int i = 0; i < iters; ++i) enqueue(i, true);
+      } catch (...) {
+        (void)hipStreamEndCapture(s.stream, &g);
+        throw;
+      }
+      HIPC(hipStreamEndCapture(s.stream, &g));
+      HIPC(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+      HIPC(hipEventCreate(&ev0));
+      HIPC(hipEventCreate(&ev1));
+      HIPC(hipGraphLaunch(ge, s.stream));
+      HIPC(hipEventRecord(ev0, s.stream));
+      HIPC(hipGraphLaunch(ge, s.stream));
+      HIPC(hipEventRecord(ev1, s.stream));
+      HIPC(hipStreamSynchronize(s.stream));
+      float ms = 0.f;
+      HIPC(hipEventElapsedTime(&ms, ev0, ev1));
+      *avg_us = 1000.0 * ms / iters;
+      *bytes = total_bytes / iters;
+    } catch (...) {
+      cleanup();
+      throw;
+    }
+    cleanup();
   });
 }
 

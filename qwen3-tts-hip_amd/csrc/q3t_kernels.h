@@ -5,15 +5,27 @@
 
 namespace q3t {
 
-// y = W x (optionally x := RMSNorm(x) * gamma first) with the epilogue `epi`.
-// Requires K = 512 * c for c in {1, 2, 3, 4, 6, 8, 12}; returns hipErrorInvalidValue otherwise.
-hipError_t launch_gemv(int epi, bool norm, const GemvArgs &a, hipStream_t stream);
+// Optional hardware timestamps of one launch (hipExtLaunchKernelGGL start/stop events).
+struct LaunchTiming {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+
+// y = W x (optionally x := RMSNorm(x) * gamma first) with the epilogue `epi`.  `streaming`
+// selects non-temporal weight loads.  Requires K = 512 * c for c in {1, 2, 3, 4, 6, 8, 12};
+// returns hipErrorInvalidValue otherwise.
+hipError_t launch_gemv(int epi, bool norm, bool streaming, const GemvArgs &a, hipStream_t stream,
+                       const LaunchTiming *timing = nullptr);
 bool gemv_supports_k(int K);
 
-// Fused q/k head RMSNorm + RoPE + bf16 KV-cache write + GQA decode attention.
-// One workgroup per KV head; LDS holds the scores of one position range.
-hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t stream);
+// Fused q/k head RMSNorm + RoPE + KV-cache write + GQA decode attention, split over key
+// positions in chunks (one workgroup per (KV head, chunk)); the last chunk merges.
+hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t stream,
+                              const LaunchTiming *timing = nullptr);
 int attn_max_cache_steps(int q_heads, int kv_heads);
+// Key rows per attention workgroup for a cache of `cap` rows, and the resulting number of
+// chunks (partials the workspace must hold per head).
+int attn_chunk_len(int cap);
+int attn_chunks(int cap);
 
 hipError_t launch_select_talker(const SelectTalkerArgs &a, hipStream_t stream);
 hipError_t launch_select_cp(const SelectCpArgs &a, hipStream_t stream);

@@ -8,6 +8,10 @@
 #include <float.h>
 #include <math.h>
 
+#include <algorithm>
+
+#include <hip/hip_ext.h>
+
 namespace q3t {
 namespace {
 
@@ -59,7 +63,25 @@ __device__ __forceinline__ float dot8(uint4 w, const float *x) {
 // 512-wide chunk, so a wave streams 1 KiB of a row per 16-byte load.  All RW x KC loads
 // of a wave are issued before any arithmetic.
 // ---------------------------------------------------------------------------------------
-template <int EPI, bool NORM, int KC, int RW>
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__device__ __forceinline__ uint4 load_w(const u32x4 *p) {
+  u32x4 v;
+  if constexpr (NT)
+    v = __builtin_nontemporal_load(p);
+  else
+    v = *p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// NT = streaming (non-temporal) weight loads: used for the Talker, whose weights are read once
+// per frame, so that they do not displace the CodePredictor weights that every frame rereads
+// 15 times from the last-level cache.
+__device__ void merge_attention(const GemvArgs &a, float *xs);
+
+// ATTN = the input vector is the merge of attention partials (see merge_attention).
+template <int EPI, bool NORM, int KC, int RW, bool NT, bool ATTN = false>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   if (skip_work(a.st, a.skip)) return;
   constexpr int K = KC * 512;
@@ -67,26 +89,48 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int unit0 = (blockIdx.x * 4 + wave) * RW;
+  __shared__ float xs[ATTN ? K : 1];
 
-  uint4 w[NR][KC];
-#pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    const int unit = unit0 + (EPI == EPI_SWIGLU ? (r >> 1) : r);
-    const int row = (EPI == EPI_SWIGLU && (r & 1)) ? a.N + unit : unit;
-    const bool ok = unit < a.N;
-    const uint4 *pw = reinterpret_cast<const uint4 *>(a.W + (size_t)(ok ? row : 0) * K) + lane;
-#pragma unroll
-    for (int c = 0; c < KC; ++c) w[r][c] = ok ? pw[c * 64] : make_uint4(0, 0, 0, 0);
-  }
-
+  // Load order: activations (and the norm gain), then every weight row of this wave, then
+  // nothing else until the arithmetic.  The norm then only waits for the small activation
+  // loads while the whole launch's weights are in flight (one DRAM round trip per launch).
   float xv[KC][8];
+  float gv[NORM ? KC : 1][8];
 #pragma unroll
   for (int c = 0; c < KC; ++c) {
+    if constexpr (ATTN) break;
     const float4 *px = reinterpret_cast<const float4 *>(a.x + c * 512 + lane * 8);
     const float4 p0 = px[0], p1 = px[1];
     xv[c][0] = p0.x; xv[c][1] = p0.y; xv[c][2] = p0.z; xv[c][3] = p0.w;
     xv[c][4] = p1.x; xv[c][5] = p1.y; xv[c][6] = p1.z; xv[c][7] = p1.w;
+    if constexpr (NORM) {
+      const float4 *pg = reinterpret_cast<const float4 *>(a.gamma + c * 512 + lane * 8);
+      const float4 g0 = pg[0], g1 = pg[1];
+      gv[c][0] = g0.x; gv[c][1] = g0.y; gv[c][2] = g0.z; gv[c][3] = g0.w;
+      gv[c][4] = g1.x; gv[c][5] = g1.y; gv[c][6] = g1.z; gv[c][7] = g1.w;
+    }
   }
+  // Rows past the end (a partial last workgroup) load the last row instead of branching;
+  // their results are never stored.
+  uint4 w[NR][KC];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int unit = min(unit0 + (EPI == EPI_SWIGLU ? (r >> 1) : r), a.N - 1);
+    const int row = (EPI == EPI_SWIGLU && (r & 1)) ? a.N + unit : unit;
+    const u32x4 *pw = reinterpret_cast<const u32x4 *>(a.W + (size_t)row * K) + lane;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) w[r][c] = load_w<NT>(pw + c * 64);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (ATTN) {
+    merge_attention(a, xs);
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xv[c][j] = xs[c * 512 + lane * 8 + j];
+  }
+
   if constexpr (NORM) {
     float ss = 0.f;
 #pragma unroll
@@ -96,13 +140,9 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     ss = wave_sum(ss);
     const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
 #pragma unroll
-    for (int c = 0; c < KC; ++c) {
-      const float4 *pg = reinterpret_cast<const float4 *>(a.gamma + c * 512 + lane * 8);
-      const float4 g0 = pg[0], g1 = pg[1];
-      const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    for (int c = 0; c < KC; ++c)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) xv[c][j] = (xv[c][j] * inv) * g[j];
-    }
+      for (int j = 0; j < 8; ++j) xv[c][j] = (xv[c][j] * inv) * gv[c][j];
   }
 
   float acc[NR];
@@ -173,22 +213,37 @@ struct KvIo<uint16_t> {
 };
 
 // ---------------------------------------------------------------------------------------
-// Decode attention for one KV head (head_dim D = 128) and its G query heads.
-//   1. q/k head RMSNorm and rotate-half RoPE at `pos` (wave per vector, lane owns the
-//      RoPE pair (i, i + 64));
-//   2. K and V stored at cache row `pos` (rounded to the cache type);
-//   3. scores over rows 0..pos (16 lanes per row, 8 dims per lane), softmax, P.V.
-// The row at `pos` is taken from LDS (the values just stored), older rows from the cache.
+// Decode attention, split over the key positions (flash-decoding).
+// Grid (kv_heads, max_chunks); workgroup (h, c) owns key rows [c * chunk, min(L, (c+1) * chunk))
+// of KV head h and its G query heads.
+//   1. q head RMSNorm + rotate-half RoPE at `pos` (every workgroup, wave per head); the
+//      workgroup whose chunk holds `pos` also normalises/rotates k, stores K and V at row
+//      `pos` (rounded to the cache type) and keeps them in LDS;
+//   2. scores (16 lanes per row, 8 dims per lane), chunk max m, p = exp(s - m), l = sum p,
+//      acc = sum p * V;
+//   3. partial_out = 0 (one chunk by construction): out = acc / l.  partial_out = 1: the
+//      chunk's (m, l, acc) go to `part`; the consumer (the O-projection GEMV) merges the
+//      chunks in chunk order after the kernel boundary, so no workgroup fences or waits.
 // ---------------------------------------------------------------------------------------
+constexpr int kAttnMaxChunk = 128;
+constexpr int kAttnMaxChunks = 8;
+
 template <int D, int G, typename KVT>
-__global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
+__global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   static_assert(D == 128, "lane layout assumes head_dim 128");
-  static_assert(G >= 1 && G <= 4, "query heads per KV head");
+  static_assert(G >= 1 && G <= 2, "query heads per KV head");
   if (skip_work(a.st, a.skip)) return;
   const int h = blockIdx.x;
+  const int c = blockIdx.y;
   const int pos = (a.pos_mode == POS_TALKER_FRAME) ? a.st->prefill_steps + a.st->frame : a.pos_const;
   if (pos < 0 || pos >= a.cap) return;  // host validates; never index outside the cache
   const int L = pos + 1;
+  const int chunk = a.chunk;
+  const int nchunks = (L + chunk - 1) / chunk;
+  if (c >= nchunks) return;
+  const int t0 = c * chunk;
+  const int t1 = min(L, t0 + chunk);
+  const bool owns_pos = (c == nchunks - 1);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int q_out = a.q_heads * D;
@@ -196,29 +251,19 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
   KVT *kcache = reinterpret_cast<KVT *>(a.kcache);
   KVT *vcache = reinterpret_cast<KVT *>(a.vcache);
 
-  extern __shared__ float smem[];
-  float *qs = smem;               // [G][D]
-  float *ks = qs + G * D;         // [D]  K row at pos, as stored
-  float *vs = ks + D;             // [D]  V row at pos, as stored
-  float *red = vs + D;            // [4][G][D] cross-wave partials
-  float *stat = red + 4 * G * D;  // [2][G][4] max / sum partials
-  float *sc = stat + 8 * G;       // [G][L]
+  __shared__ float qs[G * D];
+  __shared__ float ks[D], vs[D];
+  __shared__ float sc[G][kAttnMaxChunk];
+  __shared__ float red[4][G][D];
+  __shared__ float stat[G][2];
 
-  // 1 + 2: norm, rope, cache write.  Vectors: q_0..q_{G-1}, k, v.
+  // 1: q heads (waves 0..G-1); k and v (waves G, G+1) only where row `pos` is stored.
   const float2 cs = a.rope[(size_t)pos * (D / 2) + lane];
-  for (int vec = wave; vec < G + 2; vec += 4) {
-    const float *src;
-    const float *gain;
-    if (vec < G) {
-      src = a.qkv + (h * G + vec) * D;
-      gain = a.gq;
-    } else if (vec == G) {
-      src = a.qkv + q_out + h * D;
-      gain = a.gk;
-    } else {
-      src = a.qkv + q_out + kv_out + h * D;
-      gain = nullptr;
-    }
+  if (wave < G + 2 && (wave < G || owns_pos)) {
+    const int vec = wave;
+    const float *src = vec < G ? a.qkv + (h * G + vec) * D
+                               : (vec == G ? a.qkv + q_out + h * D : a.qkv + q_out + kv_out + h * D);
+    const float *gain = vec < G ? a.gq : (vec == G ? a.gk : nullptr);
     float x0 = src[lane], x1 = src[lane + 64];
     if (gain) {
       const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
@@ -243,11 +288,11 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
   }
   __syncthreads();
 
-  // 3a: scores.  Lane group of 16 per row, 8 dims per lane.
+  // 2a: scores of this chunk.
   const int sub = lane & 15;
   const int grp = lane >> 4;
   const KVT *kbase = kcache + (size_t)h * a.cap * D;
-  for (int base = wave * 4; base < L; base += 16) {
+  for (int base = t0 + wave * 4; base < t1; base += 16) {
     const int t = base + grp;
     float kv[8];
     if (t < pos) {
@@ -258,69 +303,101 @@ __global__ __launch_bounds__(256) void k_attn_decode(AttnArgs a) {
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      float s = 0.f;
+      float sacc = 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) s = fmaf(qs[g * D + sub * 8 + j], kv[j], s);
-      s += __shfl_xor(s, 8, 16);
-      s += __shfl_xor(s, 4, 16);
-      s += __shfl_xor(s, 2, 16);
-      s += __shfl_xor(s, 1, 16);
-      if (sub == 0 && t < L) sc[g * L + t] = s * a.scale;
+      for (int j = 0; j < 8; ++j) sacc = fmaf(qs[g * D + sub * 8 + j], kv[j], sacc);
+      sacc += __shfl_xor(sacc, 8, 16);
+      sacc += __shfl_xor(sacc, 4, 16);
+      sacc += __shfl_xor(sacc, 2, 16);
+      sacc += __shfl_xor(sacc, 1, 16);
+      if (sub == 0 && t < t1) sc[g][t - t0] = sacc * a.scale;
     }
   }
   __syncthreads();
 
-  // 3b: softmax statistics per query head (fixed-order block reduction).
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
+  // 2b: chunk max and exp (wave g handles query head g, 64 rows per pass).
+  const int n = t1 - t0;
+  if (wave < G) {
     float m = -FLT_MAX;
-    for (int t = threadIdx.x; t < L; t += 256) m = fmaxf(m, sc[g * L + t]);
+    for (int i = lane; i < n; i += 64) m = fmaxf(m, sc[wave][i]);
     m = wave_max(m);
-    if (lane == 0) stat[g * 4 + wave] = m;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float m = fmaxf(fmaxf(stat[g * 4 + 0], stat[g * 4 + 1]), fmaxf(stat[g * 4 + 2], stat[g * 4 + 3]));
-    float s = 0.f;
-    for (int t = threadIdx.x; t < L; t += 256) {
-      const float p = expf(sc[g * L + t] - m);
-      sc[g * L + t] = p;
-      s += p;
+    float l = 0.f;
+    for (int i = lane; i < n; i += 64) {
+      const float p = expf(sc[wave][i] - m);
+      sc[wave][i] = p;
+      l += p;
     }
-    s = wave_sum(s);
-    if (lane == 0) stat[4 * G + g * 4 + wave] = s;
+    l = wave_sum(l);
+    if (lane == 0) {
+      stat[wave][0] = m;
+      stat[wave][1] = l;
+    }
   }
   __syncthreads();
 
-  // 3c: P.V.  Wave w takes rows t = w (mod 4); lane owns dims 2*lane, 2*lane + 1.
+  // 2c: acc = sum_t p_t V_t.  Wave w takes rows t0 + w (mod 4); lane owns dims 2l, 2l+1.
   float acc[G][2];
 #pragma unroll
   for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.f;
   const KVT *vbase = vcache + (size_t)h * a.cap * D;
-  for (int t = wave; t < L; t += 4) {
+  for (int t = t0 + wave; t < t1; t += 4) {
     const float2 v = (t < pos) ? KvIo<KVT>::load2(vbase + (size_t)t * D + 2 * lane)
                                : make_float2(vs[2 * lane], vs[2 * lane + 1]);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float p = sc[g * L + t];
+      const float p = sc[g][t - t0];
       acc[g][0] = fmaf(p, v.x, acc[g][0]);
       acc[g][1] = fmaf(p, v.y, acc[g][1]);
     }
   }
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    red[(wave * G + g) * D + 2 * lane] = acc[g][0];
-    red[(wave * G + g) * D + 2 * lane + 1] = acc[g][1];
+    red[wave][g][2 * lane] = acc[g][0];
+    red[wave][g][2 * lane + 1] = acc[g][1];
   }
   __syncthreads();
-  for (int o = threadIdx.x; o < G * D; o += 256) {
-    const int g = o / D, dd = o % D;
-    const float sum = ((stat[4 * G + g * 4 + 0] + stat[4 * G + g * 4 + 1]) + stat[4 * G + g * 4 + 2]) +
-                      stat[4 * G + g * 4 + 3];
-    const float v = ((red[(0 * G + g) * D + dd] + red[(1 * G + g) * D + dd]) + red[(2 * G + g) * D + dd]) +
-                    red[(3 * G + g) * D + dd];
-    a.out[(h * G + g) * D + dd] = v / sum;
+
+  // 3: final output (single chunk) or this chunk's partial.
+  const int o = threadIdx.x;  // G * D <= 256 outputs
+  if (o >= G * D) return;
+  const int g_o = o / D, d_o = o % D;
+  const float v_o = ((red[0][g_o][d_o] + red[1][g_o][d_o]) + red[2][g_o][d_o]) + red[3][g_o][d_o];
+  if (!a.partial_out) {
+    a.out[(h * G + g_o) * D + d_o] = v_o / stat[g_o][1];
+    return;
+  }
+  float *my = a.part + (((size_t)h * a.part_chunks + c) * G + g_o) * (D + 2);
+  my[2 + d_o] = v_o;
+  if (d_o == 0) {
+    my[0] = stat[g_o][0];
+    my[1] = stat[g_o][1];
+  }
+}
+
+// Merges the attention partials of all query heads into xs[q_heads * D] (LDS), in chunk
+// order: out = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c.  256 threads, 8 dims each.
+__device__ void merge_attention(const GemvArgs &a, float *xs) {
+  constexpr int D = 128;
+  const int pos = (a.attn_pos_mode == POS_TALKER_FRAME) ? a.st->prefill_steps + a.st->frame : a.attn_pos_const;
+  const int nchunks = (pos + a.attn_chunk) / a.attn_chunk;  // ceil((pos + 1) / chunk)
+  const int G = a.attn_q_heads / a.attn_kv_heads;
+  for (int base = threadIdx.x * 8; base < a.K; base += 256 * 8) {
+    const int hq = base / D, d0 = base % D;
+    const int h = hq / G, g = hq % G;
+    const float *p0 = a.attn_part + (((size_t)h * a.attn_part_chunks) * G + g) * (D + 2);
+    const size_t stride = (size_t)G * (D + 2);
+    float M = -FLT_MAX;
+    for (int c = 0; c < nchunks; ++c) M = fmaxf(M, p0[c * stride]);
+    float den = 0.f, num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < nchunks; ++c) {
+      const float *pc = p0 + c * stride;
+      const float w = expf(pc[0] - M);
+      den = fmaf(w, pc[1], den);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) num[j] = fmaf(w, pc[2 + d0 + j], num[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xs[base + j] = num[j] / den;
   }
 }
 
@@ -630,86 +707,122 @@ bool gemv_supports_k(int K) {
   return c == 1 || c == 2 || c == 3 || c == 4 || c == 6 || c == 8 || c == 12;
 }
 
-template <int EPI, bool NORM, int KC, int RW>
-static void gemv_launch(const GemvArgs &a, hipStream_t s) {
-  const int units = 4 * RW;
-  hipLaunchKernelGGL((k_gemv<EPI, NORM, KC, RW>), dim3((a.N + units - 1) / units), dim3(256), 0, s, a);
+template <typename K, typename... Args>
+static void launch_timed(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, const LaunchTiming *t,
+                         Args... args) {
+  if (t && t->start)
+    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, s, t->start, t->stop, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
 }
 
-template <int EPI, bool NORM, int KC>
-static hipError_t gemv_rw(const GemvArgs &a, hipStream_t s) {
-  // Rows per wave: as many as keep >= 256 workgroups, with at most 16 outstanding
-  // 16-byte weight loads per lane.
-  constexpr int per_unit = (EPI == EPI_SWIGLU) ? 2 : 1;
-  constexpr bool can4 = 4 * per_unit * KC <= 16;
-  constexpr bool can2 = 2 * per_unit * KC <= 16;
-  if (can4 && a.N >= 256 * 4 * 4) {
-    if constexpr (can4) gemv_launch<EPI, NORM, KC, 4>(a, s);
-  } else if (can2 && a.N >= 256 * 4 * 2) {
-    if constexpr (can2) gemv_launch<EPI, NORM, KC, 2>(a, s);
-  } else {
-    gemv_launch<EPI, NORM, KC, 1>(a, s);
+// Weight loads in flight per lane are capped at kMaxLoads (4 VGPRs each).
+constexpr int kMaxLoads = 24;
+
+template <int EPI, bool NORM, int KC, int RW, bool NT>
+static void gemv_launch(const GemvArgs &a, hipStream_t s, const LaunchTiming *t) {
+  const int units = 4 * RW;
+  const dim3 grid((a.N + units - 1) / units);
+  if constexpr (EPI == EPI_RESIDUAL && !NORM && KC <= 8) {
+    if (a.attn_part) {
+      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, true>, grid, dim3(256), 0, s, t, a);
+      return;
+    }
+  }
+  launch_timed(k_gemv<EPI, NORM, KC, RW, NT, false>, grid, dim3(256), 0, s, t, a);
+}
+
+template <int EPI, bool NORM, int KC, bool NT>
+static hipError_t gemv_rw(const GemvArgs &a, hipStream_t s, const LaunchTiming *t) {
+  // Rows per wave: spread the matrix over ~256 workgroups (one per CU, one wave per SIMD)
+  // with every weight load of the launch issued up front; when that needs more than
+  // kMaxLoads loads per lane, use more workgroups instead.
+  constexpr int pu = (EPI == EPI_SWIGLU) ? 2 : 1;
+  int rw = (a.N + 1023) / 1024;
+  const int cap_rw = kMaxLoads / (pu * KC);
+  if (rw > cap_rw) rw = std::max(1, cap_rw);
+  if (rw == 5) rw = 6;
+  if (rw > 6) rw = 6;
+  switch (rw) {
+    case 6:
+      if constexpr (6 * pu * KC <= kMaxLoads) { gemv_launch<EPI, NORM, KC, 6, NT>(a, s, t); break; }
+      [[fallthrough]];
+    case 4:
+      if constexpr (4 * pu * KC <= kMaxLoads) { gemv_launch<EPI, NORM, KC, 4, NT>(a, s, t); break; }
+      [[fallthrough]];
+    case 3:
+      if constexpr (3 * pu * KC <= kMaxLoads) { gemv_launch<EPI, NORM, KC, 3, NT>(a, s, t); break; }
+      [[fallthrough]];
+    case 2:
+      if constexpr (2 * pu * KC <= kMaxLoads) { gemv_launch<EPI, NORM, KC, 2, NT>(a, s, t); break; }
+      [[fallthrough]];
+    default:
+      gemv_launch<EPI, NORM, KC, 1, NT>(a, s, t);
   }
   return hipGetLastError();
 }
 
-template <int EPI, bool NORM>
-static hipError_t gemv_k(const GemvArgs &a, hipStream_t s) {
+template <int EPI, bool NORM, bool NT>
+static hipError_t gemv_k(const GemvArgs &a, hipStream_t s, const LaunchTiming *t) {
   switch (a.K / 512) {
-    case 1: return gemv_rw<EPI, NORM, 1>(a, s);
-    case 2: return gemv_rw<EPI, NORM, 2>(a, s);
-    case 3: return gemv_rw<EPI, NORM, 3>(a, s);
-    case 4: return gemv_rw<EPI, NORM, 4>(a, s);
-    case 6: return gemv_rw<EPI, NORM, 6>(a, s);
-    case 8: return gemv_rw<EPI, NORM, 8>(a, s);
-    case 12: return gemv_rw<EPI, NORM, 12>(a, s);
+    case 1: return gemv_rw<EPI, NORM, 1, NT>(a, s, t);
+    case 2: return gemv_rw<EPI, NORM, 2, NT>(a, s, t);
+    case 3: return gemv_rw<EPI, NORM, 3, NT>(a, s, t);
+    case 4: return gemv_rw<EPI, NORM, 4, NT>(a, s, t);
+    case 6: return gemv_rw<EPI, NORM, 6, NT>(a, s, t);
+    case 8: return gemv_rw<EPI, NORM, 8, NT>(a, s, t);
+    case 12: return gemv_rw<EPI, NORM, 12, NT>(a, s, t);
   }
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemv(int epi, bool norm, const GemvArgs &a, hipStream_t s) {
-  if (!gemv_supports_k(a.K) || a.N <= 0) return hipErrorInvalidValue;
+template <bool NT>
+static hipError_t gemv_epi(int epi, bool norm, const GemvArgs &a, hipStream_t s, const LaunchTiming *t) {
   switch (epi) {
-    case EPI_STORE: return norm ? gemv_k<EPI_STORE, true>(a, s) : gemv_k<EPI_STORE, false>(a, s);
-    case EPI_RESIDUAL: return norm ? hipErrorInvalidValue : gemv_k<EPI_RESIDUAL, false>(a, s);
-    case EPI_SWIGLU: return norm ? gemv_k<EPI_SWIGLU, true>(a, s) : hipErrorInvalidValue;
-    case EPI_BIAS: return norm ? hipErrorInvalidValue : gemv_k<EPI_BIAS, false>(a, s);
+    case EPI_STORE: return norm ? gemv_k<EPI_STORE, true, NT>(a, s, t) : gemv_k<EPI_STORE, false, NT>(a, s, t);
+    case EPI_RESIDUAL: return norm ? hipErrorInvalidValue : gemv_k<EPI_RESIDUAL, false, NT>(a, s, t);
+    case EPI_SWIGLU: return norm ? gemv_k<EPI_SWIGLU, true, NT>(a, s, t) : hipErrorInvalidValue;
+    case EPI_BIAS: return norm ? hipErrorInvalidValue : gemv_k<EPI_BIAS, false, NT>(a, s, t);
   }
   return hipErrorInvalidValue;
 }
 
-static size_t attn_lds_bytes(int G, int L) {
-  return sizeof(float) * ((size_t)G * 128 + 2 * 128 + 4 * (size_t)G * 128 + 8 * (size_t)G + (size_t)G * L);
+hipError_t launch_gemv(int epi, bool norm, bool streaming, const GemvArgs &a, hipStream_t s,
+                       const LaunchTiming *t) {
+  if (!gemv_supports_k(a.K) || a.N <= 0) return hipErrorInvalidValue;
+  return streaming ? gemv_epi<true>(epi, norm, a, s, t) : gemv_epi<false>(epi, norm, a, s, t);
 }
+
+int attn_chunk_len(int cap) {
+  int c = (cap + kAttnMaxChunks - 1) / kAttnMaxChunks;
+  c = ((c + 31) / 32) * 32;
+  return std::min(std::max(c, 32), kAttnMaxChunk);
+}
+
+int attn_chunks(int cap) { return (cap + attn_chunk_len(cap) - 1) / attn_chunk_len(cap); }
 
 int attn_max_cache_steps(int q_heads, int kv_heads) {
-  const int G = q_heads / kv_heads;
-  const size_t fixed = attn_lds_bytes(G, 0);
-  const size_t budget = 128 * 1024;
-  return fixed >= budget ? 0 : (int)((budget - fixed) / (sizeof(float) * G));
+  (void)q_heads;
+  (void)kv_heads;
+  return kAttnMaxChunk * 64;  // at most 64 partial chunks per head
 }
 
-hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t s) {
-  if (head_dim != 128 || a.kv_heads <= 0 || a.q_heads % a.kv_heads || a.q_heads / a.kv_heads > 4 ||
-      a.q_heads / a.kv_heads == 3)
-    return hipErrorInvalidValue;
-  if (a.cap > attn_max_cache_steps(a.q_heads, a.kv_heads)) return hipErrorInvalidValue;
+hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t s, const LaunchTiming *t) {
+  if (head_dim != 128 || a.kv_heads <= 0 || a.q_heads % a.kv_heads) return hipErrorInvalidValue;
   const int G = a.q_heads / a.kv_heads;
-  // LDS sized for the longest row range this cache can hold.
-  const size_t lds = attn_lds_bytes(G, a.cap);
-  const dim3 grid(a.kv_heads), block(256);
+  if (a.cap > attn_max_cache_steps(a.q_heads, a.kv_heads) || a.chunk != attn_chunk_len(a.cap)) return hipErrorInvalidValue;
+  if (a.partial_out ? a.part_chunks < attn_chunks(a.cap) : attn_chunks(a.cap) != 1) return hipErrorInvalidValue;
+  const dim3 grid(a.kv_heads, attn_chunks(a.cap)), block(256);
   if (a.kv_bf16) {
     switch (G) {
-      case 1: hipLaunchKernelGGL((k_attn_decode<128, 1, uint16_t>), grid, block, lds, s, a); break;
-      case 2: hipLaunchKernelGGL((k_attn_decode<128, 2, uint16_t>), grid, block, lds, s, a); break;
-      case 4: hipLaunchKernelGGL((k_attn_decode<128, 4, uint16_t>), grid, block, lds, s, a); break;
+      case 1: launch_timed(k_attn_split<128, 1, uint16_t>, grid, block, 0, s, t, a); break;
+      case 2: launch_timed(k_attn_split<128, 2, uint16_t>, grid, block, 0, s, t, a); break;
       default: return hipErrorInvalidValue;
     }
   } else {
     switch (G) {
-      case 1: hipLaunchKernelGGL((k_attn_decode<128, 1, float>), grid, block, lds, s, a); break;
-      case 2: hipLaunchKernelGGL((k_attn_decode<128, 2, float>), grid, block, lds, s, a); break;
-      case 4: hipLaunchKernelGGL((k_attn_decode<128, 4, float>), grid, block, lds, s, a); break;
+      case 1: launch_timed(k_attn_split<128, 1, float>, grid, block, 0, s, t, a); break;
+      case 2: launch_timed(k_attn_split<128, 2, float>, grid, block, 0, s, t, a); break;
       default: return hipErrorInvalidValue;
     }
   }

@@ -141,6 +141,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "q3t_sampler_draw": (ctypes.c_int, [ctypes.c_void_p, f32p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                             ctypes.c_float, ctypes.c_float, ctypes.c_uint64, ctypes.c_int32,
                                             ctypes.c_int32, i32p]),
+        "q3t_engine_synchronize": (ctypes.c_int, [ctypes.c_void_p]),
+        "q3t_bench_kernel": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                            P(ctypes.c_double), P(ctypes.c_double)]),
         "q3t_last_error": (ctypes.c_char_p, []),
     }
     for name, (res, args) in sigs.items():
@@ -312,6 +315,27 @@ class HipTtsEngine:
     def set_trace(self, enabled: bool) -> None:
         """Record raw logits of every step (parity checks)."""
         _check(_lib.q3t_engine_set_trace(self._h, int(bool(enabled))))
+
+    def synchronize(self) -> None:
+        _check(_lib.q3t_engine_synchronize(self._h))
+
+    KERNELS = {0: "gemv_qkv_rmsnorm", 1: "gemv_o_residual", 2: "gemv_gate_up_swiglu", 3: "gemv_down_residual",
+               4: "attention_decode_full_cache"}
+
+    def bench_kernel(self, kernel: int, iters: int = 1030):
+        """(average launch microseconds, algorithmic bytes per launch) of one kernel class."""
+        us, b = ctypes.c_double(), ctypes.c_double()
+        _check(_lib.q3t_bench_kernel(self._h, int(kernel), int(iters), ctypes.byref(us), ctypes.byref(b)))
+        return us.value, b.value
+
+    def dominant_kernel_roofline(self, peak_gbps: float, kernel: int = 2, iters: int = 1030) -> dict:
+        """Roofline entry for the kernel class that dominates a frame's time (the gate/up GEMV)."""
+        self.bench_kernel(kernel, 103)   # warm
+        us, b = self.bench_kernel(kernel, iters)
+        achieved = b / (us * 1e-6) / 1e9
+        return {"kernel": self.KERNELS[kernel], "bound": "hbm", "achieved": round(achieved, 1),
+                "peak": peak_gbps, "unit": "GB/s", "frac": round(achieved / peak_gbps, 4), "traffic": None,
+                "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": int(b), "launches_timed": iters}
 
     def sampler_draw(self, logits: np.ndarray, n: int, do_sample: bool = True, top_k: int = 50,
                      top_p: float = 1.0, temperature: float = 0.9, seed: int = 0, kind: int = 0) -> np.ndarray:
