@@ -50,6 +50,21 @@ def frame_bytes(spec, active_steps_mean: float, kv_elem: int) -> float:
     return talker + groups * cp_pass + kv
 
 
+def measured_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary of this
+    workload (FETCH_SIZE and WRITE_SIZE, each scaled by its copy-kernel calibration)."""
+    path = os.path.join(ROOT, "profiles", f"pmc_traffic_{workload.split('_', 1)[1]}.json")
+    path = path if os.path.exists(path) else os.path.join(ROOT, "profiles", "pmc_traffic_cfg2_0.6b.json")
+    try:
+        d = json.load(open(path))
+    except (OSError, ValueError):
+        return None
+    if d.get("workload") != workload or kernel not in d.get("kernels", {}):
+        return None
+    k, c = d["kernels"][kernel], d["calibration"]
+    return int(1024 * (k["fetch_kib"] * c["fetch_scale"] + k["write_kib"] * c["write_scale"]))
+
+
 def cpu_baseline(seconds_budget: float) -> dict:
     """BASELINE config 1 on the host CPU: float32 oracle, 0.6B shape, 32-token prompt,
     greedy; as many frames as fit the time budget (bounded sample)."""
@@ -98,6 +113,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--eager", action="store_true", help="launch every kernel from the host (no graph)")
     ap.add_argument("--kv-bf16", action="store_true")
+    ap.add_argument("--frames", type=int, default=0, help="override the workload's frame count (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -111,6 +127,9 @@ def main() -> int:
     from q3t.workloads import WORKLOADS
 
     w = WORKLOADS[args.workload]
+    if args.frames > 0:
+        import dataclasses
+        w = dataclasses.replace(w, frames=min(args.frames, w.frames))
     model = synth.SyntheticModel.build(w.spec, w.weight_seed)
     inputs = w.inputs(model)
     tmp = tempfile.mkdtemp(prefix="q3t_bench_")
@@ -148,6 +167,7 @@ def main() -> int:
     fb = frame_bytes(spec, active_mean, 2 if args.kv_bf16 else 4)
     frame_s = elapsed / frames
     roofline = eng.dominant_kernel_roofline(HBM_PEAK_GBPS)
+    roofline["traffic"] = measured_traffic(w.name, roofline["kernel"])
     eng.close()
     import shutil
     shutil.rmtree(tmp, ignore_errors=True)
