@@ -185,6 +185,7 @@ struct KvIo<float> {
     *p = x;
     return x;
   }
+
   __device__ static void load8(const float *p, float *o) {
     const float4 a = reinterpret_cast<const float4 *>(p)[0];
     const float4 b = reinterpret_cast<const float4 *>(p)[1];
@@ -201,6 +202,7 @@ struct KvIo<uint16_t> {
     *p = b;
     return bf16_to_f32(b);
   }
+
   __device__ static void load8(const uint16_t *p, float *o) {
     const uint4 w = *reinterpret_cast<const uint4 *>(p);
     o[0] = bf_lo(w.x); o[1] = bf_hi(w.x); o[2] = bf_lo(w.y); o[3] = bf_hi(w.y);
@@ -228,43 +230,71 @@ struct KvIo<uint16_t> {
 constexpr int kAttnMaxChunk = 128;
 constexpr int kAttnMaxChunks = 8;
 
-template <int D, int G, typename KVT>
+template <int D, int G, typename KVT, int CH>
 __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   static_assert(D == 128, "lane layout assumes head_dim 128");
   static_assert(G >= 1 && G <= 2, "query heads per KV head");
+  static_assert(CH % 16 == 0 && CH <= kAttnMaxChunk, "chunk length");
   if (skip_work(a.st, a.skip)) return;
   const int h = blockIdx.x;
   const int c = blockIdx.y;
   const int pos = (a.pos_mode == POS_TALKER_FRAME) ? a.st->prefill_steps + a.st->frame : a.pos_const;
   if (pos < 0 || pos >= a.cap) return;  // host validates; never index outside the cache
   const int L = pos + 1;
-  const int chunk = a.chunk;
-  const int nchunks = (L + chunk - 1) / chunk;
+  const int nchunks = (L + CH - 1) / CH;
   if (c >= nchunks) return;
-  const int t0 = c * chunk;
-  const int t1 = min(L, t0 + chunk);
+  const int t0 = c * CH;
+  const int t1 = min(L, t0 + CH);
+  const int tpast = min(t1, pos);  // rows [t0, tpast) come from the cache
   const bool owns_pos = (c == nchunks - 1);
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int sub = lane & 15;
+  const int grp = lane >> 4;
   const int q_out = a.q_heads * D;
   const int kv_out = a.kv_heads * D;
   KVT *kcache = reinterpret_cast<KVT *>(a.kcache);
   KVT *vcache = reinterpret_cast<KVT *>(a.vcache);
+  const KVT *kbase = kcache + (size_t)h * a.cap * D;
+  const KVT *vbase = vcache + (size_t)h * a.cap * D;
 
   __shared__ float qs[G * D];
   __shared__ float ks[D], vs[D];
-  __shared__ float sc[G][kAttnMaxChunk];
+  __shared__ float sc[G][CH];
   __shared__ float red[4][G][D];
   __shared__ float stat[G][2];
 
-  // 1: q heads (waves 0..G-1); k and v (waves G, G+1) only where row `pos` is stored.
-  const float2 cs = a.rope[(size_t)pos * (D / 2) + lane];
-  if (wave < G + 2 && (wave < G || owns_pos)) {
-    const int vec = wave;
+  // Loads first: this wave's head vector, then every cached K and V row the workgroup needs
+  // (addresses clamped into the cache instead of branching), so the kernel waits on one
+  // memory round trip.  Rows at or past `pos` are never used from these registers.
+  const int vec = wave;
+  const bool has_vec = wave < G + 2 && (wave < G || owns_pos);
+  float x0 = 0.f, x1 = 0.f;
+  if (has_vec) {
     const float *src = vec < G ? a.qkv + (h * G + vec) * D
                                : (vec == G ? a.qkv + q_out + h * D : a.qkv + q_out + kv_out + h * D);
+    x0 = src[lane];
+    x1 = src[lane + 64];
+  }
+  const int tmax = max(pos - 1, 0);
+  float kpre[CH / 16][8];
+#pragma unroll
+  for (int i = 0; i < CH / 16; ++i) {
+    const int t = min(t0 + wave * 4 + grp + 16 * i, tmax);
+    KvIo<KVT>::load8(kbase + (size_t)t * D + sub * 8, kpre[i]);
+  }
+  float2 vpre[CH / 4];
+#pragma unroll
+  for (int i = 0; i < CH / 4; ++i) {
+    const int t = min(t0 + wave + 4 * i, tmax);
+    vpre[i] = KvIo<KVT>::load2(vbase + (size_t)t * D + 2 * lane);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 1: q heads (waves 0..G-1); k and v (waves G, G+1) only where row `pos` is stored.
+  if (has_vec) {
+    const float2 cs = a.rope[(size_t)pos * (D / 2) + lane];
     const float *gain = vec < G ? a.gq : (vec == G ? a.gk : nullptr);
-    float x0 = src[lane], x1 = src[lane + 64];
     if (gain) {
       const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
       const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
@@ -289,18 +319,13 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   __syncthreads();
 
   // 2a: scores of this chunk.
-  const int sub = lane & 15;
-  const int grp = lane >> 4;
-  const KVT *kbase = kcache + (size_t)h * a.cap * D;
-  for (int base = t0 + wave * 4; base < t1; base += 16) {
-    const int t = base + grp;
-    float kv[8];
-    if (t < pos) {
-      KvIo<KVT>::load8(kbase + (size_t)t * D + sub * 8, kv);
-    } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) kv[j] = (t == pos) ? ks[sub * 8 + j] : 0.f;
-    }
+  for (int i = 0; i < CH / 16; ++i) {
+    const int t = t0 + wave * 4 + grp + 16 * i;
+    if (t0 + wave * 4 + 16 * i >= t1) break;  // wave-uniform
+    float kv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) kv[j] = (t < tpast) ? kpre[i][j] : ((t == pos) ? ks[sub * 8 + j] : 0.f);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float sacc = 0.f;
@@ -339,10 +364,11 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   float acc[G][2];
 #pragma unroll
   for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.f;
-  const KVT *vbase = vcache + (size_t)h * a.cap * D;
-  for (int t = t0 + wave; t < t1; t += 4) {
-    const float2 v = (t < pos) ? KvIo<KVT>::load2(vbase + (size_t)t * D + 2 * lane)
-                               : make_float2(vs[2 * lane], vs[2 * lane + 1]);
+#pragma unroll
+  for (int i = 0; i < CH / 4; ++i) {
+    const int t = t0 + wave + 4 * i;
+    if (t >= t1) break;  // wave-uniform
+    const float2 v = (t < tpast) ? vpre[i] : make_float2(vs[2 * lane], vs[2 * lane + 1]);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       const float p = sc[g][t - t0];
@@ -794,9 +820,10 @@ hipError_t launch_gemv(int epi, bool norm, bool streaming, const GemvArgs &a, hi
 }
 
 int attn_chunk_len(int cap) {
-  int c = (cap + kAttnMaxChunks - 1) / kAttnMaxChunks;
-  c = ((c + 31) / 32) * 32;
-  return std::min(std::max(c, 32), kAttnMaxChunk);
+  // 32, 64 or 128 rows: at most kAttnMaxChunks chunks up to a 1024-row cache
+  int c = 32;
+  while (c < kAttnMaxChunk && c * kAttnMaxChunks < cap) c *= 2;
+  return c;
 }
 
 int attn_chunks(int cap) { return (cap + attn_chunk_len(cap) - 1) / attn_chunk_len(cap); }
@@ -813,20 +840,20 @@ hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t s, co
   if (a.cap > attn_max_cache_steps(a.q_heads, a.kv_heads) || a.chunk != attn_chunk_len(a.cap)) return hipErrorInvalidValue;
   if (a.partial_out ? a.part_chunks < attn_chunks(a.cap) : attn_chunks(a.cap) != 1) return hipErrorInvalidValue;
   const dim3 grid(a.kv_heads, attn_chunks(a.cap)), block(256);
-  if (a.kv_bf16) {
-    switch (G) {
-      case 1: launch_timed(k_attn_split<128, 1, uint16_t>, grid, block, 0, s, t, a); break;
-      case 2: launch_timed(k_attn_split<128, 2, uint16_t>, grid, block, 0, s, t, a); break;
-      default: return hipErrorInvalidValue;
-    }
-  } else {
-    switch (G) {
-      case 1: launch_timed(k_attn_split<128, 1, float>, grid, block, 0, s, t, a); break;
-      case 2: launch_timed(k_attn_split<128, 2, float>, grid, block, 0, s, t, a); break;
-      default: return hipErrorInvalidValue;
-    }
+#define Q3T_ATTN_CASE(GG, TT, CC) \
+  if (G == GG && a.chunk == CC) {  \
+    launch_timed(k_attn_split<128, GG, TT, CC>, grid, block, 0, s, t, a); \
+    return hipGetLastError();     \
   }
-  return hipGetLastError();
+  if (a.kv_bf16) {
+    Q3T_ATTN_CASE(1, uint16_t, 32) Q3T_ATTN_CASE(1, uint16_t, 64) Q3T_ATTN_CASE(1, uint16_t, 128)
+    Q3T_ATTN_CASE(2, uint16_t, 32) Q3T_ATTN_CASE(2, uint16_t, 64) Q3T_ATTN_CASE(2, uint16_t, 128)
+  } else {
+    Q3T_ATTN_CASE(1, float, 32) Q3T_ATTN_CASE(1, float, 64) Q3T_ATTN_CASE(1, float, 128)
+    Q3T_ATTN_CASE(2, float, 32) Q3T_ATTN_CASE(2, float, 64) Q3T_ATTN_CASE(2, float, 128)
+  }
+#undef Q3T_ATTN_CASE
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_select_talker(const SelectTalkerArgs &a, hipStream_t s) {
