@@ -93,6 +93,30 @@ struct AttnArgs {
   int32_t partial_out;  // 1: write partials for the O projection to merge; 0: write `out`
 };
 
+// Y[M][N] = X[M][K] . W[N][K]^T with the GEMV epilogues (matrix-core path for many rows).
+struct GemmArgs {
+  const float *X;          // [M][ldx] fp32
+  const float *row_scale;  // [M] per-row multiplier on X (RMSNorm 1/rms) or null
+  const float *gamma;      // [K] per-column multiplier on X (RMSNorm gain) or null
+  const uint16_t *W;       // [N][K] bf16 (EPI_SWIGLU: [2N][K], gate rows then up rows)
+  float *Y;                // [M][ldy]
+  const float *res;        // EPI_RESIDUAL: [M][ldr]
+  const float *bias;       // EPI_BIAS: [N]
+  int32_t M, N, K, ldx, ldy, ldr;
+};
+
+// Prompt prefill attention over rows at positions pos0 .. pos0 + P - 1.
+struct PrefillAttnArgs {
+  float *qkv;           // [P][ldq] raw projections (q normalised + rotated in place)
+  const float *gq, *gk; // q_norm / k_norm gains
+  const float2 *rope;   // [cap][d/2]
+  void *kcache, *vcache;// [kv_heads][cap][d]
+  float *out;           // [P][ldo] attention output
+  int32_t P, pos0, ldq, ldo, q_heads, kv_heads, cap;
+  float eps, scale;
+  int32_t kv_bf16;
+};
+
 struct SelectTalkerArgs {
   const float *logits;      // [V] raw codec-head logits
   const float *x;           // [H] Talker output before the final norm

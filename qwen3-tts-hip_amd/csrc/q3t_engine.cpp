@@ -290,6 +290,7 @@ struct Slot {
   char *t_k = nullptr, *t_v = nullptr, *c_k = nullptr, *c_v = nullptr;  // KV caches (fp32 or bf16)
   float *x_t, *t_in, *qkv, *attn, *act, *logits_t, *logits_c, *x_c, *cp_prefix, *cp_in, *cur, *emb_sum;
   float *trailing, *prefill;
+  float *px, *pqkv, *pattn, *pact, *pinv;  // prefill rows: [cap][H], [cap][qkv], [cap][q_out], [cap][I], [cap]
   float *attn_part;      // attention partials [kv_heads][chunks][G][2 + head_dim]
   int attn_part_chunks = 0;
   int32_t *codes;
@@ -369,6 +370,41 @@ struct Engine {
       gemv(EPI_RESIDUAL, false, L.down, sl.act, nullptr, 0.f, x, nullptr, x, d.hidden, d.intermediate, skip, sl.st,
            s, nt);
     }
+  }
+
+  // Talker prompt prefill on the matrix cores: every layer runs over all P rows at once
+  // (decode.rs:845-880, 1077-1298); the last row's output lands in x_t.
+  void prefill_rows(Slot &sl, int P, hipStream_t s) {
+    const Dims &d = td;
+    const int H = d.hidden, Q = d.qkv_rows(), O = d.q_out(), I = d.intermediate;
+    HIPC(hipMemcpyAsync(sl.px, sl.prefill, (size_t)P * H * 4, hipMemcpyDeviceToDevice, s));
+    const size_t cache_layer = (size_t)d.kv_heads * talker.cap * d.head_dim * (kv_bf16 ? 2 : 4);
+    for (int l = 0; l < d.layers; ++l) {
+      const LayerW &L = talker.layers[l];
+      hip_check(launch_row_rms(sl.px, H, P, H, d.eps, sl.pinv, s), "launch_row_rms");
+      GemmArgs g{};
+      g.X = sl.px; g.ldx = H; g.row_scale = sl.pinv; g.gamma = L.g_in;
+      g.W = L.qkv; g.Y = sl.pqkv; g.ldy = Q; g.M = P; g.N = Q; g.K = H;
+      hip_check(launch_gemm(EPI_STORE, g, s), "launch_gemm(qkv)");
+      PrefillAttnArgs pa{sl.pqkv, L.gq, L.gk, talker.rope, sl.t_k + l * cache_layer, sl.t_v + l * cache_layer,
+                         sl.pattn, P, 0, Q, O, d.q_heads, d.kv_heads, talker.cap, d.eps,
+                         1.0f / std::sqrt((float)d.head_dim), kv_bf16};
+      hip_check(launch_prefill_attention(pa, s), "launch_prefill_attention");
+      g = GemmArgs{};
+      g.X = sl.pattn; g.ldx = O; g.W = L.o; g.res = sl.px; g.ldr = H; g.Y = sl.px; g.ldy = H;
+      g.M = P; g.N = H; g.K = O;
+      hip_check(launch_gemm(EPI_RESIDUAL, g, s), "launch_gemm(o)");
+      hip_check(launch_row_rms(sl.px, H, P, H, d.eps, sl.pinv, s), "launch_row_rms");
+      g = GemmArgs{};
+      g.X = sl.px; g.ldx = H; g.row_scale = sl.pinv; g.gamma = L.g_post;
+      g.W = L.gu; g.Y = sl.pact; g.ldy = I; g.M = P; g.N = I; g.K = H;
+      hip_check(launch_gemm(EPI_SWIGLU, g, s), "launch_gemm(gate_up)");
+      g = GemmArgs{};
+      g.X = sl.pact; g.ldx = I; g.W = L.down; g.res = sl.px; g.ldr = H; g.Y = sl.px; g.ldy = H;
+      g.M = P; g.N = H; g.K = I;
+      hip_check(launch_gemm(EPI_RESIDUAL, g, s), "launch_gemm(down)");
+    }
+    HIPC(hipMemcpyAsync(sl.x_t, sl.px + (size_t)(P - 1) * H, (size_t)H * 4, hipMemcpyDeviceToDevice, s));
   }
 
   void select_talker(Slot &sl, int after_frame, hipStream_t s) {
@@ -483,6 +519,11 @@ void alloc_slot(Engine &e, Slot &s) {
   s.trailing = dev_alloc<float>((size_t)(e.cap + 1) * Ht, t);
   s.prefill = dev_alloc<float>((size_t)e.cap * Ht, t);
   s.codes = dev_alloc<int32_t>((size_t)e.cap * e.groups, t);
+  s.px = dev_alloc<float>((size_t)e.cap * Ht, t);
+  s.pqkv = dev_alloc<float>((size_t)e.cap * td.qkv_rows(), t);
+  s.pattn = dev_alloc<float>((size_t)e.cap * td.q_out(), t);
+  s.pact = dev_alloc<float>((size_t)e.cap * td.intermediate, t);
+  s.pinv = dev_alloc<float>((size_t)e.cap, t);
   s.attn_part_chunks = std::max(attn_chunks(e.cap), attn_chunks(e.cp.cap));
   const int kvh = std::max(td.kv_heads, cd.kv_heads);
   const int gq = std::max(td.q_heads / td.kv_heads, cd.q_heads / cd.kv_heads);
@@ -507,7 +548,7 @@ void free_slot(Slot &s) {
   void *ptrs[] = {s.t_k,    s.t_v,   s.c_k,       s.c_v,   s.x_t,     s.t_in,     s.qkv,      s.attn,
                   s.act,    s.logits_t, s.logits_c, s.x_c, s.cp_prefix, s.cp_in, s.cur,      s.emb_sum,
                   s.trailing, s.prefill, s.codes,   s.st,    s.prm,     s.trace_t,  s.trace_c,
-                  s.attn_part};
+                  s.attn_part, s.px,  s.pqkv,  s.pattn, s.pact,  s.pinv};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (s.stream) (void)hipStreamDestroy(s.stream);
@@ -771,9 +812,7 @@ int q3t_stream_start(q3t_engine *e, const float *prefill, int32_t P, const float
     HIPC(hipStreamSynchronize(s.stream));
     // Talker prefill: positions 0..P-1, then the head and the first semantic token
     // (talker.rs:207-233).
-    for (int p = 0; p < P; ++p)
-      e->stack_step(e->talker, s.t_k, s.t_v, s.prefill + (size_t)p * Ht, s.x_t, s, POS_CONST, p, SKIP_NEVER,
-                    s.stream);
+    e->prefill_rows(s, P, s.stream);
     e->gemv(EPI_STORE, true, e->codec_head, s.x_t, e->t_norm, e->td.eps, nullptr, nullptr, s.logits_t, e->td.vocab,
             e->td.hidden, SKIP_NEVER, s.st, s.stream);
     e->select_talker(s, 0, s.stream);
@@ -980,6 +1019,53 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
       throw;
     }
     cleanup();
+  });
+}
+
+int q3t_debug_gemm(q3t_engine *e, int32_t epi, const float *X, int32_t M, int32_t K, const uint16_t *W, int32_t N,
+                   const float *gamma, float eps, const float *res, const float *bias, float *Y) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || !X || !W || !Y) fail(Q3T_ERR_INVALID, "null argument");
+    if (M <= 0 || N <= 0 || K <= 0 || K % 32) fail(Q3T_ERR_INVALID, "need M, N > 0 and K a positive multiple of 32");
+    if (epi < EPI_STORE || epi > EPI_BIAS) fail(Q3T_ERR_INVALID, "unknown epilogue %d", epi);
+    if ((epi == EPI_RESIDUAL && !res) || (epi == EPI_BIAS && !bias)) fail(Q3T_ERR_INVALID, "missing operand");
+    HIPC(hipSetDevice(e->device));
+    const size_t wrows = (size_t)(epi == EPI_SWIGLU ? 2 : 1) * N;
+    std::vector<void *> owned;
+    auto up = [&](const void *h, size_t bytes) {
+      void *d = nullptr;
+      HIPC(hipMalloc(&d, bytes));
+      owned.push_back(d);
+      if (h) HIPC(hipMemcpy(d, h, bytes, hipMemcpyHostToDevice));
+      return d;
+    };
+    try {
+      GemmArgs g{};
+      g.X = (const float *)up(X, (size_t)M * K * 4);
+      g.W = (const uint16_t *)up(W, wrows * K * 2);
+      g.Y = (float *)up(nullptr, (size_t)M * N * 4);
+      g.M = M;
+      g.N = N;
+      g.K = K;
+      g.ldx = K;
+      g.ldy = N;
+      g.ldr = N;
+      if (res) g.res = (const float *)up(res, (size_t)M * N * 4);
+      if (bias) g.bias = (const float *)up(bias, (size_t)N * 4);
+      if (gamma) {
+        g.gamma = (const float *)up(gamma, (size_t)K * 4);
+        float *inv = (float *)up(nullptr, (size_t)M * 4);
+        hip_check(launch_row_rms(g.X, K, M, K, eps, inv, nullptr), "launch_row_rms");
+        g.row_scale = inv;
+      }
+      hip_check(launch_gemm(epi, g, nullptr), "launch_gemm");
+      HIPC(hipMemcpy(Y, g.Y, (size_t)M * N * 4, hipMemcpyDeviceToHost));
+    } catch (...) {
+      for (void *p : owned) (void)hipFree(p);
+      throw;
+    }
+    for (void *p : owned) (void)hipFree(p);
   });
 }
 

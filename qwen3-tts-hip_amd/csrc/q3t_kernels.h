@@ -27,6 +27,15 @@ int attn_max_cache_steps(int q_heads, int kv_heads);
 int attn_chunk_len(int cap);
 int attn_chunks(int cap);
 
+// Matrix-core GEMM (bf16 weights, fp32 activations split into two bf16 terms, fp32 accumulate)
+// for many rows: prompt prefill and batched decode.  Requires K % 32 == 0.
+hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t stream);
+// inv_rms[m] = 1 / sqrt(mean(X[m]^2) + eps).
+hipError_t launch_row_rms(const float *X, int ldx, int M, int K, float eps, float *inv_rms, hipStream_t stream);
+
+// Prefill attention: q/k norm + RoPE + KV store for P rows, then causal attention.
+hipError_t launch_prefill_attention(const PrefillAttnArgs &a, hipStream_t stream);
+
 hipError_t launch_select_talker(const SelectTalkerArgs &a, hipStream_t stream);
 hipError_t launch_select_cp(const SelectCpArgs &a, hipStream_t stream);
 // n independent draws from one logit row (draw i uses Philox counter (i, kind, 0, 0)).

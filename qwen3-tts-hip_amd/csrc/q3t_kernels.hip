@@ -428,6 +428,286 @@ __device__ void merge_attention(const GemvArgs &a, float *xs) {
 }
 
 // ---------------------------------------------------------------------------------------
+// Y[M][N] = X[M][K] . W[N][K]^T on the bf16 matrix cores (v_mfma_f32_16x16x32_bf16).
+// W is the bf16 weight as stored; X is fp32 and enters the matrix cores as three bf16 terms
+// (three MFMAs per k-block, smallest term first, fp32 accumulation).  Optional per-row scale
+// and per-column gain on X (the RMSNorm of the rows) are applied while converting.
+// Wave tile: (16 * MB) rows x (16 * NB) columns, no LDS: every lane loads its own A fragment
+// (8 consecutive k of one row, fp32) and B fragment (8 consecutive k of one weight row, bf16).
+// Operand layouts of the 16x16x32 instruction: A[i][k] in lane i + 16 (k / 8), element k % 8;
+// B[k][j] in lane j + 16 (k / 8), element k % 8; C[i][j] in lane j + 16 (i / 4), element i % 4.
+// SwiGLU: the first NB/2 column tiles are gate rows, the last NB/2 the matching up rows.
+// ---------------------------------------------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// x = hi + mid + lo, each a bf16: 24 significant bits, so every product with a bf16 weight
+// is exact and the GEMM matches an fp32 GEMV up to the order of the fp32 additions.
+__device__ __forceinline__ void split_bf16x8(const float *x, bf16x8_t &hi, bf16x8_t &mid, bf16x8_t &lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint16_t h = f32_to_bf16(x[e]);
+    const float r1 = x[e] - bf16_to_f32(h);
+    const uint16_t m = f32_to_bf16(r1);
+    const uint16_t l = f32_to_bf16(r1 - bf16_to_f32(m));
+    hi[e] = __builtin_bit_cast(__bf16, h);
+    mid[e] = __builtin_bit_cast(__bf16, m);
+    lo[e] = __builtin_bit_cast(__bf16, l);
+  }
+}
+
+template <int EPI, int MB, int NB>
+__global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = lane & 15;   // row (A) / column (B, C) within a 16-tile
+  const int kb = lane >> 4;   // k-block of 8 within the 32-wide k step
+  constexpr int NTILE = (EPI == EPI_SWIGLU) ? NB / 2 : NB;  // output column tiles
+  const int m0 = blockIdx.y * 16 * MB;
+  const int n0 = (blockIdx.x * 4 + wave) * 16 * NTILE;  // first output column of this wave
+  if (n0 >= a.N) return;
+
+  f32x4_t acc[MB][NB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // rows / weight rows this lane feeds (clamped into range; padding results are not stored)
+  int arow[MB];
+  float rscale[MB];
+#pragma unroll
+  for (int i = 0; i < MB; ++i) {
+    arow[i] = min(m0 + 16 * i + li, a.M - 1);
+    rscale[i] = a.row_scale ? a.row_scale[arow[i]] : 1.f;
+  }
+  int wrow[NB];
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    int col;
+    if constexpr (EPI == EPI_SWIGLU)
+      col = (j < NTILE) ? n0 + 16 * j + li : a.N + n0 + 16 * (j - NTILE) + li;
+    else
+      col = n0 + 16 * j + li;
+    const int lim = (EPI == EPI_SWIGLU) ? 2 * a.N : a.N;
+    wrow[j] = min(col, lim - 1);
+  }
+
+  for (int k0 = 0; k0 < a.K; k0 += 32) {
+    const int k = k0 + 8 * kb;
+    float xa[MB][8];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      const float4 *px = reinterpret_cast<const float4 *>(a.X + (size_t)arow[i] * a.ldx + k);
+      const float4 p0 = px[0], p1 = px[1];
+      xa[i][0] = p0.x; xa[i][1] = p0.y; xa[i][2] = p0.z; xa[i][3] = p0.w;
+      xa[i][4] = p1.x; xa[i][5] = p1.y; xa[i][6] = p1.z; xa[i][7] = p1.w;
+    }
+    uint4 wb[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) wb[j] = *reinterpret_cast<const uint4 *>(a.W + (size_t)wrow[j] * a.K + k);
+    float g[8];
+    if (a.gamma) {
+      const float4 *pg = reinterpret_cast<const float4 *>(a.gamma + k);
+      const float4 g0 = pg[0], g1 = pg[1];
+      g[0] = g0.x; g[1] = g0.y; g[2] = g0.z; g[3] = g0.w; g[4] = g1.x; g[5] = g1.y; g[6] = g1.z; g[7] = g1.w;
+    }
+    bf16x8_t ahi[MB], amid[MB], alo[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+      if (a.gamma) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xa[i][e] = (xa[i][e] * rscale[i]) * g[e];
+      } else if (a.row_scale) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xa[i][e] = xa[i][e] * rscale[i];
+      }
+      split_bf16x8(xa[i], ahi[i], amid[i], alo[i]);
+    }
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+      const bf16x8_t b = __builtin_bit_cast(bf16x8_t, wb[j]);
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo[i], b, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(amid[i], b, acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi[i], b, acc[i][j], 0, 0, 0);
+      }
+    }
+  }
+
+  // epilogue: lane holds C[4 * kb + e][li] of every tile
+#pragma unroll
+  for (int i = 0; i < MB; ++i)
+#pragma unroll
+    for (int j = 0; j < NTILE; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + 16 * i + 4 * kb + e;
+        const int n = n0 + 16 * j + li;
+        if (m >= a.M || n >= a.N) continue;
+        float v = acc[i][j][e];
+        if constexpr (EPI == EPI_SWIGLU) {
+          const float u = acc[i][j + NTILE][e];
+          v = v / (1.0f + expf(-v)) * u;
+        } else if constexpr (EPI == EPI_RESIDUAL) {
+          v = a.res[(size_t)m * a.ldr + n] + v;
+        } else if constexpr (EPI == EPI_BIAS) {
+          v = v + a.bias[n];
+        }
+        a.Y[(size_t)m * a.ldy + n] = v;
+      }
+}
+
+// inv_rms[m] = 1 / sqrt(mean(X[m]^2) + eps), one wave per row.
+__global__ __launch_bounds__(256) void k_row_rms(const float *X, int ldx, int M, int K, float eps, float *inv_rms) {
+  const int lane = threadIdx.x & 63;
+  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (m >= M) return;
+  float ss = 0.f;
+  for (int k = lane; k < K; k += 64) ss = fmaf(X[(size_t)m * ldx + k], X[(size_t)m * ldx + k], ss);
+  ss = wave_sum(ss);
+  if (lane == 0) inv_rms[m] = 1.0f / sqrtf(ss / (float)K + eps);
+}
+
+// ---------------------------------------------------------------------------------------
+// Prompt prefill attention, rows at positions 0..P-1 (decode.rs:1077-1298 with the cache
+// written first and read back, the same values the decode steps read).
+//   k_prefill_qkv: per (row, head vector): q/k head RMSNorm + RoPE at the row's position
+//     (q written back in place), K and V stored into the cache row.  One wave per vector.
+//   k_attn_prefill: per (KV head, row): causal attention of the row's G query heads over
+//     cache rows 0..p with an online softmax over 64-row chunks.
+// ---------------------------------------------------------------------------------------
+template <typename KVT>
+__global__ __launch_bounds__(256) void k_prefill_qkv(PrefillAttnArgs a) {
+  constexpr int D = 128;
+  const int lane = threadIdx.x & 63;
+  const int vec = blockIdx.x * 4 + (threadIdx.x >> 6);  // q heads, then k heads, then v heads
+  const int p = blockIdx.y;
+  const int nvec = a.q_heads + 2 * a.kv_heads;
+  if (vec >= nvec || p >= a.P) return;
+  const int pos = a.pos0 + p;
+  float *row = a.qkv + (size_t)p * a.ldq;
+  float *v = row + vec * D;
+  float x0 = v[lane], x1 = v[lane + 64];
+  if (vec < a.q_heads + a.kv_heads) {
+    const float *gain = vec < a.q_heads ? a.gq : a.gk;
+    const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
+    const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+    x0 = (x0 * inv) * gain[lane];
+    x1 = (x1 * inv) * gain[lane + 64];
+    const float2 cs = a.rope[(size_t)pos * (D / 2) + lane];
+    const float r0 = x0 * cs.x - x1 * cs.y, r1 = x1 * cs.x + x0 * cs.y;
+    x0 = r0;
+    x1 = r1;
+  }
+  if (vec < a.q_heads) {
+    v[lane] = x0;
+    v[lane + 64] = x1;
+  } else {
+    const bool is_k = vec < a.q_heads + a.kv_heads;
+    const int h = is_k ? vec - a.q_heads : vec - a.q_heads - a.kv_heads;
+    KVT *cache = reinterpret_cast<KVT *>(is_k ? a.kcache : a.vcache) + ((size_t)h * a.cap + pos) * D;
+    KvIo<KVT>::store(cache + lane, x0);
+    KvIo<KVT>::store(cache + lane + 64, x1);
+  }
+}
+
+template <int G, typename KVT>
+__global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs a) {
+  constexpr int D = 128, CH = 64;
+  const int h = blockIdx.x;
+  const int p = blockIdx.y;
+  if (p >= a.P) return;
+  const int L = a.pos0 + p + 1;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int sub = lane & 15, grp = lane >> 4;
+  const KVT *kb = reinterpret_cast<const KVT *>(a.kcache) + (size_t)h * a.cap * D;
+  const KVT *vb = reinterpret_cast<const KVT *>(a.vcache) + (size_t)h * a.cap * D;
+  __shared__ float qs[G * D];
+  __shared__ float sc[G][CH];
+  __shared__ float red[4][G][D];
+  __shared__ float mstat[G];
+  const float *row = a.qkv + (size_t)p * a.ldq;
+  for (int i = threadIdx.x; i < G * D; i += 256) qs[i] = row[h * G * D + i];
+  float m_run[G], l_run[G], acc[G][2];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m_run[g] = -FLT_MAX;
+    l_run[g] = 0.f;
+    acc[g][0] = acc[g][1] = 0.f;
+  }
+  __syncthreads();
+  for (int t0 = 0; t0 < L; t0 += CH) {
+    const int t1 = min(L, t0 + CH);
+    for (int base = t0 + wave * 4; base < t1; base += 16) {
+      const int t = base + grp;
+      float kv[8];
+      KvIo<KVT>::load8(kb + (size_t)min(t, L - 1) * D + sub * 8, kv);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float sacc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sacc = fmaf(qs[g * D + sub * 8 + j], kv[j], sacc);
+        sacc += __shfl_xor(sacc, 8, 16);
+        sacc += __shfl_xor(sacc, 4, 16);
+        sacc += __shfl_xor(sacc, 2, 16);
+        sacc += __shfl_xor(sacc, 1, 16);
+        if (sub == 0 && t < t1) sc[g][t - t0] = sacc * a.scale;
+      }
+    }
+    __syncthreads();
+    const int n = t1 - t0;
+    if (wave < G) {
+      const float sv = lane < n ? sc[wave][lane] : -FLT_MAX;
+      const float mc = wave_max(sv);
+      if (lane == 0) mstat[wave] = mc;
+    }
+    __syncthreads();
+    float scale_old[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float m_new = fmaxf(m_run[g], mstat[g]);
+      scale_old[g] = expf(m_run[g] - m_new);
+      m_run[g] = m_new;
+    }
+    __syncthreads();
+    if (wave < G && lane < n) sc[wave][lane] = expf(sc[wave][lane] - m_run[wave]);
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float ls = 0.f;
+      for (int i = 0; i < n; ++i) ls += sc[g][i];
+      l_run[g] = l_run[g] * scale_old[g] + ls;
+      acc[g][0] *= scale_old[g];
+      acc[g][1] *= scale_old[g];
+    }
+    for (int t = t0 + wave; t < t1; t += 4) {
+      const float2 v = KvIo<KVT>::load2(vb + (size_t)t * D + 2 * lane);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float pr = sc[g][t - t0];
+        acc[g][0] = fmaf(pr, v.x, acc[g][0]);
+        acc[g][1] = fmaf(pr, v.y, acc[g][1]);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    red[wave][g][2 * lane] = acc[g][0];
+    red[wave][g][2 * lane + 1] = acc[g][1];
+  }
+  __syncthreads();
+  const int o = threadIdx.x;
+  if (o >= G * D) return;
+  const int g_o = o / D, d_o = o % D;
+  const float v_o = ((red[0][g_o][d_o] + red[1][g_o][d_o]) + red[2][g_o][d_o]) + red[3][g_o][d_o];
+  a.out[(size_t)p * a.ldo + (h * G + g_o) * D + d_o] = v_o / l_run[g_o];
+}
+
+// ---------------------------------------------------------------------------------------
 // Token selection (one 1024-thread workgroup).
 // ---------------------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t mulhi32(uint32_t a, uint32_t b) {
@@ -854,6 +1134,58 @@ hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t s, co
   }
 #undef Q3T_ATTN_CASE
   return hipErrorInvalidValue;
+}
+
+template <int EPI>
+static hipError_t gemm_epi(const GemmArgs &a, hipStream_t s) {
+  // 16-row tiles for short M (batched decode), 32-row tiles otherwise; 64 output columns
+  // per wave (2 x 32 for SwiGLU gate/up pairs).
+  constexpr int NB = 4;
+  constexpr int NT = (EPI == EPI_SWIGLU) ? NB / 2 : NB;
+  const int cols_per_wg = 4 * 16 * NT;
+  if (a.M <= 16) {
+    hipLaunchKernelGGL((k_gemm_mfma<EPI, 1, NB>), dim3((a.N + cols_per_wg - 1) / cols_per_wg, (a.M + 15) / 16),
+                       dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((k_gemm_mfma<EPI, 2, NB>), dim3((a.N + cols_per_wg - 1) / cols_per_wg, (a.M + 31) / 32),
+                       dim3(256), 0, s, a);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
+  if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.K % 32 || a.ldx % 4) return hipErrorInvalidValue;
+  switch (epi) {
+    case EPI_STORE: return gemm_epi<EPI_STORE>(a, s);
+    case EPI_RESIDUAL: return gemm_epi<EPI_RESIDUAL>(a, s);
+    case EPI_SWIGLU: return gemm_epi<EPI_SWIGLU>(a, s);
+    case EPI_BIAS: return gemm_epi<EPI_BIAS>(a, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_row_rms(const float *X, int ldx, int M, int K, float eps, float *inv_rms, hipStream_t s) {
+  if (M <= 0 || K <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_row_rms, dim3((M + 3) / 4), dim3(256), 0, s, X, ldx, M, K, eps, inv_rms);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_attention(const PrefillAttnArgs &a, hipStream_t s) {
+  if (a.P <= 0 || a.kv_heads <= 0 || a.q_heads % a.kv_heads || a.pos0 < 0 || a.pos0 + a.P > a.cap)
+    return hipErrorInvalidValue;
+  const int G = a.q_heads / a.kv_heads;
+  if (G != 1 && G != 2) return hipErrorInvalidValue;
+  const dim3 g1((a.q_heads + 2 * a.kv_heads + 3) / 4, a.P), g2(a.kv_heads, a.P), block(256);
+  if (a.kv_bf16) {
+    hipLaunchKernelGGL(k_prefill_qkv<uint16_t>, g1, block, 0, s, a);
+    if (G == 1) hipLaunchKernelGGL((k_attn_prefill<1, uint16_t>), g2, block, 0, s, a);
+    else hipLaunchKernelGGL((k_attn_prefill<2, uint16_t>), g2, block, 0, s, a);
+  } else {
+    hipLaunchKernelGGL(k_prefill_qkv<float>, g1, block, 0, s, a);
+    if (G == 1) hipLaunchKernelGGL((k_attn_prefill<1, float>), g2, block, 0, s, a);
+    else hipLaunchKernelGGL((k_attn_prefill<2, float>), g2, block, 0, s, a);
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_select_talker(const SelectTalkerArgs &a, hipStream_t s) {

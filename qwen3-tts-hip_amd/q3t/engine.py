@@ -144,6 +144,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "q3t_engine_synchronize": (ctypes.c_int, [ctypes.c_void_p]),
         "q3t_bench_kernel": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
                                             P(ctypes.c_double), P(ctypes.c_double)]),
+        "q3t_debug_gemm": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, f32p, ctypes.c_int32, ctypes.c_int32,
+                                          P(ctypes.c_uint16), ctypes.c_int32, f32p, ctypes.c_float, f32p, f32p,
+                                          f32p]),
         "q3t_last_error": (ctypes.c_char_p, []),
     }
     for name, (res, args) in sigs.items():
@@ -336,6 +339,25 @@ class HipTtsEngine:
         return {"kernel": self.KERNELS[kernel], "bound": "hbm", "achieved": round(achieved, 1),
                 "peak": peak_gbps, "unit": "GB/s", "frac": round(achieved / peak_gbps, 4), "traffic": None,
                 "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": int(b), "launches_timed": iters}
+
+    def debug_gemm(self, epi: int, X: np.ndarray, W_bits: np.ndarray, N: int, gamma=None, eps: float = 1e-6,
+                   res=None, bias=None) -> np.ndarray:
+        """The matrix-core GEMM on host arrays (test hook)."""
+        X = _f32(X)
+        M, K = X.shape
+        Wb = np.ascontiguousarray(W_bits, dtype=np.uint16)
+        Y = np.zeros((M, N), dtype=np.float32)
+        opt = lambda a: _fptr(_f32(a)) if a is not None else None
+        keep = [_f32(a) for a in (gamma, res, bias) if a is not None]  # noqa: F841 (lifetime)
+        g = _f32(gamma) if gamma is not None else None
+        r = _f32(res) if res is not None else None
+        b = _f32(bias) if bias is not None else None
+        _check(_lib.q3t_debug_gemm(self._h, int(epi), _fptr(X), M, K,
+                                   Wb.ctypes.data_as(ctypes.POINTER(ctypes.c_uint16)), int(N),
+                                   _fptr(g) if g is not None else None, float(eps),
+                                   _fptr(r) if r is not None else None, _fptr(b) if b is not None else None,
+                                   _fptr(Y)))
+        return Y
 
     def sampler_draw(self, logits: np.ndarray, n: int, do_sample: bool = True, top_k: int = 50,
                      top_p: float = 1.0, temperature: float = 0.9, seed: int = 0, kind: int = 0) -> np.ndarray:

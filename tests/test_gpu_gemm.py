@@ -1,0 +1,70 @@
+"""The matrix-core GEMM (bf16 weights, fp32 activations as two bf16 terms, fp32 accumulate)
+against a float64 numpy product, through the C ABI test hook q3t_debug_gemm."""
+import numpy as np
+import pytest
+
+from q3t import engine as E
+from q3t import synth
+from q3t.workloads import WORKLOADS
+
+pytestmark = pytest.mark.gpu
+
+# Activations enter as three bf16 terms (24 significant bits), so every product with a bf16
+# weight is exact; what remains is fp32 accumulation (~1e-7 relative over these K).
+REL_TOL = 2e-6
+
+
+@pytest.fixture(scope="module")
+def eng(models):
+    w = WORKLOADS["tiny_greedy"]
+    _, d = models.get(w.spec)
+    e = E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=64))
+    yield e
+    e.close()
+
+
+def _weights(rows, K, seed):
+    return synth.f32_to_bf16_bits((np.random.default_rng(seed).standard_normal((rows, K)) * 0.02).astype(np.float32))
+
+
+def _close(got, want):
+    scale = np.abs(want).max()
+    err = np.abs(got - want).max() / scale
+    assert err < REL_TOL, f"max error {err:.3g} of scale {scale:.3g}"
+    return err
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 32), (16, 1024, 1024), (17, 300, 64), (73, 4096, 1024),
+                                   (521, 1024, 3072), (5, 2048, 2048)])
+def test_store(eng, M, N, K):
+    print(f"[gpu] gemm store M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M * 7 + N)
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    Wb = _weights(N, K, N + K)
+    W = synth.bf16_bits_to_f32(Wb).astype(np.float64)
+    got = eng.debug_gemm(0, X, Wb, N)
+    _close(got, X.astype(np.float64) @ W.T)
+
+
+def test_epilogues_and_norm(eng):
+    M, N, K = 37, 384, 1024
+    rng = np.random.default_rng(3)
+    X = (rng.standard_normal((M, K)) * 3).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    Xn = X.astype(np.float64) / np.sqrt((X.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6) * g
+    Wb = _weights(2 * N, K, 11)
+    W = synth.bf16_bits_to_f32(Wb).astype(np.float64)
+    res = rng.standard_normal((M, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    # residual (+ RMSNorm prologue)
+    _close(eng.debug_gemm(1, X, Wb[:N], N, gamma=g, res=res), res + Xn @ W[:N].T)
+    # bias
+    _close(eng.debug_gemm(3, X, Wb[:N], N, bias=bias), X.astype(np.float64) @ W[:N].T + bias)
+    # SwiGLU over gate rows [0, N) and up rows [N, 2N)
+    gate, up = Xn @ W[:N].T, Xn @ W[N:].T
+    _close(eng.debug_gemm(2, X, Wb, N, gamma=g), gate / (1 + np.exp(-gate)) * up)
+
+
+def test_rejects_bad_shapes(eng):
+    with pytest.raises(E.InvalidInputError):
+        eng.debug_gemm(0, np.zeros((4, 48), np.float32), np.zeros((8, 48), np.uint16), 8)
