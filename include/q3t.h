@@ -159,7 +159,9 @@ int q3t_sampler_draw(q3t_engine *engine, const float *logits, int32_t vocab, int
  * rocblas_sgemm call sites this kernel replaces, src/gpu/blas.rs:99-154):
  * Y[M][N] = f(X[M][K]) . W[N][K]^T with epilogue epi (0 store, 1 + res[M][N], 2 SwiGLU with
  * W = [gate rows; up rows] ([2N][K]), 3 + bias[N]).  gamma != NULL applies RMSNorm(eps) with
- * gain gamma[K] to each row of X first.  W is bf16 bits; X, Y, res, bias fp32 host arrays. */
+ * gain gamma[K] to each row of X first.  W is bf16 bits; X, Y, res, bias fp32 host arrays.
+ * M <= 16 with K = 512 * {1,2,3,4,6,8,12} runs the batched-decode (skinny) kernel, other
+ * shapes the prefill kernel. */
 int q3t_debug_gemm(q3t_engine *engine, int32_t epi, const float *X, int32_t M, int32_t K,
                    const uint16_t *W, int32_t N, const float *gamma, float eps, const float *res,
                    const float *bias, float *Y);

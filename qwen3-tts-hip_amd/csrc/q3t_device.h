@@ -103,6 +103,7 @@ struct GemmArgs {
   const float *res;        // EPI_RESIDUAL: [M][ldr]
   const float *bias;       // EPI_BIAS: [N]
   int32_t M, N, K, ldx, ldy, ldr;
+  float eps;               // skinny GEMM with a fused RMSNorm
 };
 
 // Prompt prefill attention over rows at positions pos0 .. pos0 + P - 1.

@@ -1053,13 +1053,19 @@ int q3t_debug_gemm(q3t_engine *e, int32_t epi, const float *X, int32_t M, int32_
       g.ldr = N;
       if (res) g.res = (const float *)up(res, (size_t)M * N * 4);
       if (bias) g.bias = (const float *)up(bias, (size_t)N * 4);
-      if (gamma) {
-        g.gamma = (const float *)up(gamma, (size_t)K * 4);
-        float *inv = (float *)up(nullptr, (size_t)M * 4);
-        hip_check(launch_row_rms(g.X, K, M, K, eps, inv, nullptr), "launch_row_rms");
-        g.row_scale = inv;
+      if (gemm_skinny_supports(M, K)) {  // the batched-decode kernel (fused RMSNorm)
+        if (gamma) g.gamma = (const float *)up(gamma, (size_t)K * 4);
+        g.eps = eps;
+        hip_check(launch_gemm_skinny(epi, gamma != nullptr, g, nullptr), "launch_gemm_skinny");
+      } else {
+        if (gamma) {
+          g.gamma = (const float *)up(gamma, (size_t)K * 4);
+          float *inv = (float *)up(nullptr, (size_t)M * 4);
+          hip_check(launch_row_rms(g.X, K, M, K, eps, inv, nullptr), "launch_row_rms");
+          g.row_scale = inv;
+        }
+        hip_check(launch_gemm(epi, g, nullptr), "launch_gemm");
       }
-      hip_check(launch_gemm(epi, g, nullptr), "launch_gemm");
       HIPC(hipMemcpy(Y, g.Y, (size_t)M * N * 4, hipMemcpyDeviceToHost));
     } catch (...) {
       for (void *p : owned) (void)hipFree(p);

@@ -30,6 +30,10 @@ int attn_chunks(int cap);
 // Matrix-core GEMM (bf16 weights, fp32 activations split into two bf16 terms, fp32 accumulate)
 // for many rows: prompt prefill and batched decode.  Requires K % 32 == 0.
 hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t stream);
+// The same product for M <= 16 rows (batched decode); norm = fused RMSNorm of the rows with
+// gain gamma (row_scale must be null).  Requires K = 512 * c, c in {1, 2, 3, 4, 6, 8, 12}.
+bool gemm_skinny_supports(int M, int K);
+hipError_t launch_gemm_skinny(int epi, bool norm, const GemmArgs &a, hipStream_t stream);
 // inv_rms[m] = 1 / sqrt(mean(X[m]^2) + eps).
 hipError_t launch_row_rms(const float *X, int ldx, int M, int K, float eps, float *inv_rms, hipStream_t stream);
 

@@ -559,6 +559,115 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
       }
 }
 
+// ---------------------------------------------------------------------------------------
+// Skinny GEMM for M <= 16 rows (one row per stream in batched decode): one 1024-thread
+// workgroup per 16-column output tile (a gate tile + up tile pair for SwiGLU); its 16 waves
+// split K into contiguous ranges, issue every load of their range up front, run the three
+// bf16-term MFMAs, and the 16 partial tiles are summed in wave order through LDS.  With
+// NORM the rows' RMSNorm is computed from the same loads (sum of squares reduced across the
+// workgroup) and applied before the split.
+// ---------------------------------------------------------------------------------------
+template <int EPI, bool NORM, int KS>  // KS = 32-wide k steps per wave = K / (16 * 32)
+__global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
+  constexpr int T = (EPI == EPI_SWIGLU) ? 2 : 1;
+  constexpr int KW = KS * 32;  // k range per wave
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;  // 0..15
+  const int li = lane & 15, kb = lane >> 4;
+  const int n0 = blockIdx.x * 16;
+  const int kbase = wave * KW;
+  const int arow = min(li, a.M - 1);
+  __shared__ f32x4_t part[16][T][64];
+  __shared__ float ssq[16][16];
+  __shared__ float inv_rms[16];
+
+  float xa[KS][8];
+  uint4 wb[KS][T];
+#pragma unroll
+  for (int st = 0; st < KS; ++st) {
+    const int k = kbase + st * 32 + 8 * kb;
+    const float4 *px = reinterpret_cast<const float4 *>(a.X + (size_t)arow * a.ldx + k);
+    const float4 p0 = px[0], p1 = px[1];
+    xa[st][0] = p0.x; xa[st][1] = p0.y; xa[st][2] = p0.z; xa[st][3] = p0.w;
+    xa[st][4] = p1.x; xa[st][5] = p1.y; xa[st][6] = p1.z; xa[st][7] = p1.w;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int col = min(n0 + li, a.N - 1) + t * a.N;
+      wb[st][t] = *reinterpret_cast<const uint4 *>(a.W + (size_t)col * a.K + k);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  if constexpr (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int st = 0; st < KS; ++st)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(xa[st][e], xa[st][e], ss);
+    ss += __shfl_xor(ss, 16, 64);  // the four lanes of a row (kb = 0..3)
+    ss += __shfl_xor(ss, 32, 64);
+    if (kb == 0) ssq[wave][li] = ss;
+    __syncthreads();
+    if (threadIdx.x < 16) {
+      float tot = 0.f;
+      for (int w = 0; w < 16; ++w) tot += ssq[w][threadIdx.x];
+      inv_rms[threadIdx.x] = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+    }
+    __syncthreads();
+    const float r = inv_rms[li];
+#pragma unroll
+    for (int st = 0; st < KS; ++st) {
+      const int k = kbase + st * 32 + 8 * kb;
+      const float4 *pg = reinterpret_cast<const float4 *>(a.gamma + k);
+      const float4 g0 = pg[0], g1 = pg[1];
+      const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xa[st][e] = (xa[st][e] * r) * g[e];
+    }
+  }
+
+  f32x4_t acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < KS; ++st) {
+    bf16x8_t hi, mid, lo;
+    split_bf16x8(xa[st], hi, mid, lo);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const bf16x8_t b = __builtin_bit_cast(bf16x8_t, wb[st][t]);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, b, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b, acc[t], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < T; ++t) part[wave][t][lane] = acc[t];
+  __syncthreads();
+  if (wave != 0) return;
+  f32x4_t sum[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    sum[t] = part[0][t][lane];
+    for (int w = 1; w < 16; ++w) sum[t] += part[w][t][lane];
+  }
+  const int n = n0 + li;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int m = 4 * kb + e;
+    if (m >= a.M || n >= a.N) continue;
+    float v = sum[0][e];
+    if constexpr (EPI == EPI_SWIGLU) {
+      v = v / (1.0f + expf(-v)) * sum[T - 1][e];
+    } else if constexpr (EPI == EPI_RESIDUAL) {
+      v = a.res[(size_t)m * a.ldr + n] + v;
+    } else if constexpr (EPI == EPI_BIAS) {
+      v = v + a.bias[n];
+    }
+    a.Y[(size_t)m * a.ldy + n] = v;
+  }
+}
+
 // inv_rms[m] = 1 / sqrt(mean(X[m]^2) + eps), one wave per row.
 __global__ __launch_bounds__(256) void k_row_rms(const float *X, int ldx, int M, int K, float eps, float *inv_rms) {
   const int lane = threadIdx.x & 63;
@@ -1151,6 +1260,36 @@ static hipError_t gemm_epi(const GemmArgs &a, hipStream_t s) {
                        dim3(256), 0, s, a);
   }
   return hipGetLastError();
+}
+
+template <int EPI, bool NORM>
+static hipError_t skinny_ks(const GemmArgs &a, hipStream_t s) {
+  const dim3 grid((a.N + 15) / 16), block(1024);
+  switch (a.K / 512) {
+    case 1: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 1>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 2>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 3>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 4>), grid, block, 0, s, a); break;
+    case 6: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 6>), grid, block, 0, s, a); break;
+    case 8: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 8>), grid, block, 0, s, a); break;
+    case 12: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 12>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+bool gemm_skinny_supports(int M, int K) { return M >= 1 && M <= 16 && gemv_supports_k(K); }
+
+hipError_t launch_gemm_skinny(int epi, bool norm, const GemmArgs &a, hipStream_t s) {
+  if (!gemm_skinny_supports(a.M, a.K) || a.N <= 0 || a.ldx % 4 || (norm && (!a.gamma || a.row_scale)))
+    return hipErrorInvalidValue;
+  switch (epi) {
+    case EPI_STORE: return norm ? skinny_ks<EPI_STORE, true>(a, s) : skinny_ks<EPI_STORE, false>(a, s);
+    case EPI_RESIDUAL: return norm ? hipErrorInvalidValue : skinny_ks<EPI_RESIDUAL, false>(a, s);
+    case EPI_SWIGLU: return norm ? skinny_ks<EPI_SWIGLU, true>(a, s) : skinny_ks<EPI_SWIGLU, false>(a, s);
+    case EPI_BIAS: return norm ? hipErrorInvalidValue : skinny_ks<EPI_BIAS, false>(a, s);
+  }
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {

@@ -35,7 +35,8 @@ def _close(got, want):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 64, 32), (16, 1024, 1024), (17, 300, 64), (73, 4096, 1024),
-                                   (521, 1024, 3072), (5, 2048, 2048)])
+                                   (521, 1024, 3072), (5, 2048, 2048), (16, 1024, 3072), (1, 3072, 1024),
+                                   (9, 100, 6144)])
 def test_store(eng, M, N, K):
     print(f"[gpu] gemm store M={M} N={N} K={K}", flush=True)
     rng = np.random.default_rng(M * 7 + N)
@@ -61,6 +62,23 @@ def test_epilogues_and_norm(eng):
     # bias
     _close(eng.debug_gemm(3, X, Wb[:N], N, bias=bias), X.astype(np.float64) @ W[:N].T + bias)
     # SwiGLU over gate rows [0, N) and up rows [N, 2N)
+    gate, up = Xn @ W[:N].T, Xn @ W[N:].T
+    _close(eng.debug_gemm(2, X, Wb, N, gamma=g), gate / (1 + np.exp(-gate)) * up)
+
+
+@pytest.mark.parametrize("M", [16, 40])
+def test_epilogues_skinny_and_tiled(eng, M):
+    """M <= 16 runs the batched-decode kernel (fused RMSNorm), larger M the prefill kernel."""
+    N, K = 208, 1024
+    rng = np.random.default_rng(M)
+    X = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    Xn = X.astype(np.float64) / np.sqrt((X.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6) * g
+    Wb = _weights(2 * N, K, M + 5)
+    W = synth.bf16_bits_to_f32(Wb).astype(np.float64)
+    res = rng.standard_normal((M, N)).astype(np.float32)
+    _close(eng.debug_gemm(0, X, Wb[:N], N, gamma=g), Xn @ W[:N].T)
+    _close(eng.debug_gemm(1, X, Wb[:N], N, res=res), res + X.astype(np.float64) @ W[:N].T)
     gate, up = Xn @ W[:N].T, Xn @ W[N:].T
     _close(eng.debug_gemm(2, X, Wb, N, gamma=g), gate / (1 + np.exp(-gate)) * up)
 
