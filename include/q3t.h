@@ -39,7 +39,7 @@ typedef struct {
   const char *model_dir;   /* holds config.json + model.safetensors */
   int32_t device;          /* HIP device ordinal */
   int32_t max_cache_steps; /* Talker KV capacity per stream (default 512) */
-  int32_t max_streams;     /* stream slots (KV caches) to allocate (default 1) */
+  int32_t max_streams;     /* stream slots (KV caches) to allocate (default 1, at most 16) */
   int32_t use_graph;       /* 1 = replay each frame as one captured hipGraph (default) */
   int32_t kv_dtype;        /* KV cache element: 0 = fp32 (default, as the reference),
                               1 = bf16 (half the KV bytes, rounded once at the store) */
@@ -108,6 +108,34 @@ int q3t_stream_start(q3t_engine *engine, const float *prefill, int32_t prefill_s
  * [semantic, a1..a15]) into codes, which must hold max_chunk_frames * num_code_groups. */
 int q3t_stream_next_codes(q3t_stream *stream, int32_t max_chunk_frames, int32_t *codes,
                           q3t_chunk_info *info);
+
+/* One stream's inputs for q3t_streams_start: the arrays q3t_stream_start takes
+ * (TtsTextPrep::prepare_custom_voice_with_lookahead, text.rs:340-382). */
+typedef struct {
+  const float *prefill;   /* [prefill_steps, H] */
+  int32_t prefill_steps;
+  const float *trailing;  /* [trailing_steps, H] */
+  int32_t trailing_steps;
+  const float *tts_pad;   /* [H] */
+} q3t_stream_input;
+
+/* Multi-stream start (new; the reference serves one stream per engine): n independent
+ * start_stream_with_inputs calls (generation.rs:513-567) in one.  Same validation and
+ * capacity check per stream; takes n free slots; runs one Talker prefill over the prompt
+ * rows of all n streams (each stream attends only to its own rows and cache) and draws each
+ * stream's first semantic token.  opts and out have n entries.  Q3T_ERR_BUSY when fewer
+ * than n slots are free.  Each stream's codes equal what q3t_stream_start would produce. */
+int q3t_streams_start(q3t_engine *engine, int32_t n, const q3t_stream_input *inputs,
+                      const q3t_generate_options *opts, q3t_stream **out);
+
+/* Batched HipTtsStream::next_codes_chunk (generation.rs:876-963) over n streams of one
+ * engine: every frame advances all listed streams that have frames left with one pass over
+ * the weights (ragged positions, per-stream KV caches and options), until each has produced
+ * max_chunk_frames frames or ended.  Stream j's codes go to codes + j * max_chunk_frames *
+ * num_code_groups and its chunk to info[j] (frames = 0: nothing left, the reference's None).
+ * Streams not listed are untouched. */
+int q3t_streams_next_codes(q3t_engine *engine, q3t_stream *const *streams, int32_t n,
+                           int32_t max_chunk_frames, int32_t *codes, q3t_chunk_info *info);
 
 /* Drops the stream and frees its slot (HipTtsStream's Drop). */
 int q3t_stream_destroy(q3t_stream *stream);

@@ -91,6 +91,22 @@ struct AttnArgs {
   int32_t part_chunks;
   int32_t chunk;        // key rows per workgroup (attn_chunk_len(cap))
   int32_t partial_out;  // 1: write partials for the O projection to merge; 0: write `out`
+  // Stream rows (grid z): row r reads qkv + r * ld_qkv, state st + r, caches + r * kv_row
+  // elements, and writes out + r * ld_out / part + r * part_row.  row_on (null for one
+  // stream) masks rows that are not part of the launch.
+  int32_t ld_qkv, ld_out;
+  int64_t kv_row, part_row;
+  const int32_t *row_on;
+};
+
+// Merge of split-attention partials into attention outputs, one workgroup per stream row.
+struct AttnMergeArgs {
+  const float *part;    // [rows][kv_heads][part_chunks][G][2 + d]
+  float *out;           // [rows][ld_out]
+  int32_t q_heads, kv_heads, part_chunks, chunk, pos_mode, pos_const, skip, ld_out;
+  int64_t part_row;
+  const SlotState *st;  // [rows]
+  const int32_t *row_on;
 };
 
 // Y[M][N] = X[M][K] . W[N][K]^T with the GEMV epilogues (matrix-core path for many rows).
@@ -104,6 +120,7 @@ struct GemmArgs {
   const float *bias;       // EPI_BIAS: [N]
   int32_t M, N, K, ldx, ldy, ldr;
   float eps;               // skinny GEMM with a fused RMSNorm
+  const int32_t *row_on;   // skinny GEMM: row m is stored only where row_on[m] (null: all rows)
 };
 
 // Prompt prefill attention over rows at positions pos0 .. pos0 + P - 1.
@@ -131,6 +148,11 @@ struct SelectTalkerArgs {
   int32_t V, H, groups;
   float eps;
   int32_t after_frame;      // 0: token drawn after the prefill; 1: after the current frame
+  // Stream rows (grid x): row r uses logits + r * V, x + r * H, cp_prefix + r * 2H,
+  // codes + r * codes_row, trace + r * trace_row, st + r, prm + r; rows where row_on is 0
+  // are skipped (row_on null: one stream).
+  int64_t codes_row, trace_row;
+  const int32_t *row_on;
 };
 
 struct SelectCpArgs {
@@ -147,6 +169,10 @@ struct SelectCpArgs {
   SlotState *st;
   const SlotParams *prm;
   int32_t Vc, Ht, groups, group;
+  // Stream rows (grid x): logits + r * Vc; cur, emb_sum, talker_in + r * Ht; codes, trace,
+  // trailing + r * their row strides; st + r, prm + r.
+  int64_t codes_row, trace_row, trailing_row;
+  const int32_t *row_on;
 };
 
 }  // namespace q3t

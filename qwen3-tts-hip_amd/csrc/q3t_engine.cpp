@@ -287,10 +287,10 @@ void load_stack(const SafeTensors &st, const std::string &prefix, const Dims &d,
 
 struct Slot {
   bool in_use = false;
+  // Views into the engine's pools (row `index` of each).
   char *t_k = nullptr, *t_v = nullptr, *c_k = nullptr, *c_v = nullptr;  // KV caches (fp32 or bf16)
   float *x_t, *t_in, *qkv, *attn, *act, *logits_t, *logits_c, *x_c, *cp_prefix, *cp_in, *cur, *emb_sum;
-  float *trailing, *prefill;
-  float *px, *pqkv, *pattn, *pact, *pinv;  // prefill rows: [cap][H], [cap][qkv], [cap][q_out], [cap][I], [cap]
+  float *trailing;
   float *attn_part;      // attention partials [kv_heads][chunks][G][2 + head_dim]
   int attn_part_chunks = 0;
   int32_t *codes;
@@ -301,6 +301,39 @@ struct Slot {
   hipGraphExec_t graph = nullptr;
   bool graph_traced = false;
   SlotState *h_state = nullptr;  // pinned host mirror
+};
+
+// Per-stream device buffers for all slots, laid out as rows: slot i's buffer is
+// base + i * (its row stride), so a batched kernel addresses stream row r directly and a
+// single-stream launch is the one-row case.  The prefill workspace is shared: one prefill
+// (of one or several streams) runs at a time.
+struct Pools {
+  int n = 0;
+  size_t t_kv_row = 0, c_kv_row = 0;  // KV elements per slot (K or V, all layers)
+  int s_qkv = 0, s_attn = 0, s_act = 0;
+  int part_chunks = 0;
+  int64_t part_row = 0, trailing_row = 0, codes_row = 0, trace_t_row = 0, trace_c_row = 0;
+  char *t_k = nullptr, *t_v = nullptr, *c_k = nullptr, *c_v = nullptr;
+  float *x_t = nullptr, *t_in = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits_t = nullptr,
+        *logits_c = nullptr, *x_c = nullptr, *cp_prefix = nullptr, *cp_in = nullptr, *cur = nullptr,
+        *emb_sum = nullptr, *trailing = nullptr, *attn_part = nullptr, *trace_t = nullptr, *trace_c = nullptr;
+  int32_t *codes = nullptr;
+  SlotState *st = nullptr;
+  SlotParams *prm = nullptr;
+  int32_t *row_on = nullptr;                            // [n] rows a batched launch covers
+  int prefill_rows = 0;                                 // n * cap
+  float *px = nullptr, *pqkv = nullptr, *pattn = nullptr, *pact = nullptr, *pinv = nullptr;
+  SlotState *h_states = nullptr;                        // pinned [n]
+  int32_t *h_row_on = nullptr;                          // pinned [n]
+  hipStream_t stream = nullptr;                         // batched work
+  hipGraphExec_t graph = nullptr;                       // batched frame, keyed by (rows, traced)
+  int graph_rows = 0;
+  bool graph_traced = false;
+};
+
+// One stream's rows in a (possibly multi-stream) prompt prefill.
+struct PrefillSeg {
+  int slot, row0, P;
 };
 
 }  // namespace
@@ -324,6 +357,7 @@ struct Engine {
   uint16_t *proj_w = nullptr;    // [Hc][Ht]
   float *proj_b = nullptr;
   std::vector<Slot> slots;
+  Pools pools;
   int64_t device_bytes = 0;
 
   // nt: stream the weights with non-temporal loads (Talker weights are read once per frame).
@@ -372,39 +406,48 @@ struct Engine {
     }
   }
 
-  // Talker prompt prefill on the matrix cores: every layer runs over all P rows at once
-  // (decode.rs:845-880, 1077-1298); the last row's output lands in x_t.
-  void prefill_rows(Slot &sl, int P, hipStream_t s) {
+  // Talker prompt prefill on the matrix cores: every layer runs over the prompt rows of all
+  // segments at once (decode.rs:845-880, 1077-1298); attention runs per segment against
+  // that stream's own cache.  The prompt rows are in pools.px; each segment's last row's
+  // output lands in its slot's x_t.
+  void prefill_segments(const std::vector<PrefillSeg> &segs, int M, hipStream_t s) {
     const Dims &d = td;
+    Pools &p = pools;
     const int H = d.hidden, Q = d.qkv_rows(), O = d.q_out(), I = d.intermediate;
-    HIPC(hipMemcpyAsync(sl.px, sl.prefill, (size_t)P * H * 4, hipMemcpyDeviceToDevice, s));
-    const size_t cache_layer = (size_t)d.kv_heads * talker.cap * d.head_dim * (kv_bf16 ? 2 : 4);
+    if (M <= 0 || M > p.prefill_rows) fail(Q3T_ERR_CAPACITY, "prefill of %d rows exceeds the workspace", M);
+    const size_t esz = kv_bf16 ? 2 : 4;
+    const size_t cache_layer = (size_t)d.kv_heads * talker.cap * d.head_dim * esz;
     for (int l = 0; l < d.layers; ++l) {
       const LayerW &L = talker.layers[l];
-      hip_check(launch_row_rms(sl.px, H, P, H, d.eps, sl.pinv, s), "launch_row_rms");
+      hip_check(launch_row_rms(p.px, H, M, H, d.eps, p.pinv, s), "launch_row_rms");
       GemmArgs g{};
-      g.X = sl.px; g.ldx = H; g.row_scale = sl.pinv; g.gamma = L.g_in;
-      g.W = L.qkv; g.Y = sl.pqkv; g.ldy = Q; g.M = P; g.N = Q; g.K = H;
+      g.X = p.px; g.ldx = H; g.row_scale = p.pinv; g.gamma = L.g_in;
+      g.W = L.qkv; g.Y = p.pqkv; g.ldy = Q; g.M = M; g.N = Q; g.K = H;
       hip_check(launch_gemm(EPI_STORE, g, s), "launch_gemm(qkv)");
-      PrefillAttnArgs pa{sl.pqkv, L.gq, L.gk, talker.rope, sl.t_k + l * cache_layer, sl.t_v + l * cache_layer,
-                         sl.pattn, P, 0, Q, O, d.q_heads, d.kv_heads, talker.cap, d.eps,
-                         1.0f / std::sqrt((float)d.head_dim), kv_bf16};
-      hip_check(launch_prefill_attention(pa, s), "launch_prefill_attention");
+      for (const PrefillSeg &sg : segs) {
+        const Slot &sl = slots[sg.slot];
+        PrefillAttnArgs pa{p.pqkv + (size_t)sg.row0 * Q, L.gq, L.gk, talker.rope, sl.t_k + l * cache_layer,
+                           sl.t_v + l * cache_layer, p.pattn + (size_t)sg.row0 * O, sg.P, 0, Q, O, d.q_heads,
+                           d.kv_heads, talker.cap, d.eps, 1.0f / std::sqrt((float)d.head_dim), kv_bf16};
+        hip_check(launch_prefill_attention(pa, s), "launch_prefill_attention");
+      }
       g = GemmArgs{};
-      g.X = sl.pattn; g.ldx = O; g.W = L.o; g.res = sl.px; g.ldr = H; g.Y = sl.px; g.ldy = H;
-      g.M = P; g.N = H; g.K = O;
+      g.X = p.pattn; g.ldx = O; g.W = L.o; g.res = p.px; g.ldr = H; g.Y = p.px; g.ldy = H;
+      g.M = M; g.N = H; g.K = O;
       hip_check(launch_gemm(EPI_RESIDUAL, g, s), "launch_gemm(o)");
-      hip_check(launch_row_rms(sl.px, H, P, H, d.eps, sl.pinv, s), "launch_row_rms");
+      hip_check(launch_row_rms(p.px, H, M, H, d.eps, p.pinv, s), "launch_row_rms");
       g = GemmArgs{};
-      g.X = sl.px; g.ldx = H; g.row_scale = sl.pinv; g.gamma = L.g_post;
-      g.W = L.gu; g.Y = sl.pact; g.ldy = I; g.M = P; g.N = I; g.K = H;
+      g.X = p.px; g.ldx = H; g.row_scale = p.pinv; g.gamma = L.g_post;
+      g.W = L.gu; g.Y = p.pact; g.ldy = I; g.M = M; g.N = I; g.K = H;
       hip_check(launch_gemm(EPI_SWIGLU, g, s), "launch_gemm(gate_up)");
       g = GemmArgs{};
-      g.X = sl.pact; g.ldx = I; g.W = L.down; g.res = sl.px; g.ldr = H; g.Y = sl.px; g.ldy = H;
-      g.M = P; g.N = H; g.K = I;
+      g.X = p.pact; g.ldx = I; g.W = L.down; g.res = p.px; g.ldr = H; g.Y = p.px; g.ldy = H;
+      g.M = M; g.N = H; g.K = I;
       hip_check(launch_gemm(EPI_RESIDUAL, g, s), "launch_gemm(down)");
     }
-    HIPC(hipMemcpyAsync(sl.x_t, sl.px + (size_t)(P - 1) * H, (size_t)H * 4, hipMemcpyDeviceToDevice, s));
+    for (const PrefillSeg &sg : segs)
+      HIPC(hipMemcpyAsync(slots[sg.slot].x_t, p.px + (size_t)(sg.row0 + sg.P - 1) * H, (size_t)H * 4,
+                          hipMemcpyDeviceToDevice, s));
   }
 
   void select_talker(Slot &sl, int after_frame, hipStream_t s) {
@@ -452,6 +495,114 @@ struct Engine {
     select_talker(sl, 1, s);
     hip_check(launch_frame_end(sl.st, sl.prm, 1, s), "launch_frame_end");
   }
+
+  // ----- stream rows: the batched frame over slots 0..rows-1, masked by pools.row_on -----
+
+  // Skinny matrix-core GEMM over the stream rows (row m of X, res, Y at m * ld).
+  void rgemm(int epi, bool norm, const uint16_t *W, const float *X, int ldx, const float *gamma, float eps,
+             const float *res, int ldr, const float *bias, float *Y, int ldy, int N, int K, int rows, hipStream_t s) {
+    GemmArgs g{};
+    g.X = X; g.ldx = ldx; g.gamma = gamma; g.eps = eps; g.W = W; g.res = res; g.ldr = ldr; g.bias = bias;
+    g.Y = Y; g.ldy = ldy; g.M = rows; g.N = N; g.K = K; g.row_on = pools.row_on;
+    hip_check(launch_gemm_skinny(epi, norm, g, s), "launch_gemm_skinny");
+  }
+
+  // One decoder-stack step of every stream row (each at its own position and cache).
+  void rows_stack_step(const StackW &w, char *kc, char *vc, size_t kv_row, const float *in, int ldin, float *x,
+                       int rows, int pos_mode, int pos_const, int skip, hipStream_t s) {
+    const Dims &d = w.d;
+    Pools &p = pools;
+    const int H = d.hidden;
+    const size_t cache_layer = (size_t)d.kv_heads * w.cap * d.head_dim * (kv_bf16 ? 2 : 4);
+    const int partial = attn_chunks(w.cap) > 1 ? 1 : 0;
+    for (int l = 0; l < d.layers; ++l) {
+      const LayerW &L = w.layers[l];
+      const float *src = l == 0 ? in : x;
+      const int lds = l == 0 ? ldin : H;
+      rgemm(EPI_STORE, true, L.qkv, src, lds, L.g_in, d.eps, nullptr, 0, nullptr, p.qkv, p.s_qkv, d.qkv_rows(), H,
+            rows, s);
+      AttnArgs aa{p.qkv,    L.gq,    L.gk,     w.rope,  kc + l * cache_layer, vc + l * cache_layer,
+                  p.attn,   d.q_heads, d.kv_heads, w.cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
+                  pos_mode, pos_const, skip,    kv_bf16, p.st,   p.attn_part, p.part_chunks,
+                  attn_chunk_len(w.cap), partial};
+      aa.ld_qkv = p.s_qkv;
+      aa.ld_out = p.s_attn;
+      aa.kv_row = (int64_t)kv_row;
+      aa.part_row = p.part_row;
+      aa.row_on = p.row_on;
+      hip_check(launch_attn_decode(aa, d.head_dim, s, nullptr, rows), "launch_attn_decode(rows)");
+      if (partial) {
+        AttnMergeArgs m{p.attn_part, p.attn, d.q_heads, d.kv_heads, p.part_chunks, attn_chunk_len(w.cap),
+                        pos_mode,    pos_const, skip,   p.s_attn,   p.part_row,    p.st,
+                        p.row_on};
+        hip_check(launch_attn_merge(m, rows, s), "launch_attn_merge");
+      }
+      rgemm(EPI_RESIDUAL, false, L.o, p.attn, p.s_attn, nullptr, 0.f, src, lds, nullptr, x, H, H, d.q_out(), rows,
+            s);
+      rgemm(EPI_SWIGLU, true, L.gu, x, H, L.g_post, d.eps, nullptr, 0, nullptr, p.act, p.s_act, d.intermediate, H,
+            rows, s);
+      rgemm(EPI_RESIDUAL, false, L.down, p.act, p.s_act, nullptr, 0.f, x, H, nullptr, x, H, H, d.intermediate, rows,
+            s);
+    }
+  }
+
+  void select_talker_rows(int rows, int after_frame, hipStream_t s) {
+    Pools &p = pools;
+    SelectTalkerArgs a{p.logits_t, p.x_t, t_norm, codec_emb, p.cp_prefix, p.codes, trace ? p.trace_t : nullptr,
+                       p.st, p.prm, td.vocab, td.hidden, groups, td.eps, after_frame};
+    a.codes_row = p.codes_row;
+    a.trace_row = p.trace_t_row;
+    a.row_on = p.row_on;
+    hip_check(launch_select_talker(a, s, rows), "launch_select_talker(rows)");
+  }
+
+  // enqueue_frame for stream rows 0..rows-1 at once: the weights of every pass are read
+  // once for all rows (skinny matrix-core GEMMs); attention, selection and the loop state
+  // are per row.  Rows that have ended or are masked out keep their state.
+  void enqueue_rows_frame(int rows, hipStream_t s) {
+    Pools &p = pools;
+    const int Ht = talker_hidden, Hc = cd.hidden, Vc = cd.vocab, nac = groups - 1;
+    const float *in0 = p.cp_prefix, *in1 = p.cp_prefix + Ht;
+    int ldin = 2 * Ht;
+    if (has_proj) {
+      rgemm(EPI_BIAS, false, proj_w, p.cp_prefix, 2 * Ht, nullptr, 0.f, nullptr, 0, proj_b, p.cp_in, 3 * Hc, Hc, Ht,
+            rows, s);
+      rgemm(EPI_BIAS, false, proj_w, p.cp_prefix + Ht, 2 * Ht, nullptr, 0.f, nullptr, 0, proj_b, p.cp_in + Hc,
+            3 * Hc, Hc, Ht, rows, s);
+      in0 = p.cp_in;
+      in1 = p.cp_in + Hc;
+      ldin = 3 * Hc;
+    }
+    rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in0, ldin, p.x_c, rows, POS_CONST, 0, SKIP_DONE, s);
+    rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in1, ldin, p.x_c, rows, POS_CONST, 1, SKIP_DONE, s);
+    for (int g = 0; g < nac; ++g) {
+      if (g > 0) {
+        const float *in = p.cur;
+        int ld = Ht;
+        if (has_proj) {
+          rgemm(EPI_BIAS, false, proj_w, p.cur, Ht, nullptr, 0.f, nullptr, 0, proj_b, p.cp_in + 2 * Hc, 3 * Hc, Hc,
+                Ht, rows, s);
+          in = p.cp_in + 2 * Hc;
+          ld = 3 * Hc;
+        }
+        rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in, ld, p.x_c, rows, POS_CONST, g + 1, SKIP_DONE, s);
+      }
+      rgemm(EPI_STORE, true, lm_heads + (size_t)g * Vc * Hc, p.x_c, Hc, c_norm, cd.eps, nullptr, 0, nullptr,
+            p.logits_c, Vc, Vc, Hc, rows, s);
+      SelectCpArgs a{p.logits_c, cp_emb + (size_t)g * Vc * Ht, p.cur, p.emb_sum, p.codes,
+                     trace ? p.trace_c : nullptr, p.t_in, codec_emb, p.trailing, p.st, p.prm, Vc, Ht, groups, g};
+      a.codes_row = p.codes_row;
+      a.trace_row = p.trace_c_row;
+      a.trailing_row = p.trailing_row;
+      a.row_on = p.row_on;
+      hip_check(launch_select_cp(a, s, rows), "launch_select_cp(rows)");
+    }
+    rows_stack_step(talker, p.t_k, p.t_v, p.t_kv_row, p.t_in, Ht, p.x_t, rows, POS_TALKER_FRAME, 0, SKIP_TALKER, s);
+    rgemm(EPI_STORE, true, codec_head, p.x_t, Ht, t_norm, td.eps, nullptr, 0, nullptr, p.logits_t, td.vocab,
+          td.vocab, Ht, rows, s);
+    select_talker_rows(rows, 1, s);
+    hip_check(launch_frame_end(p.st, p.prm, 1, s, rows, p.row_on), "launch_frame_end(rows)");
+  }
 };
 
 struct Stream {
@@ -488,78 +639,124 @@ std::string read_file(const std::string &path) {
   return ss.str();
 }
 
-void alloc_slot(Engine &e, Slot &s) {
+void alloc_pools(Engine &e, int n) {
   int64_t &t = e.device_bytes;
+  Pools &p = e.pools;
   const Dims &td = e.td, &cd = e.cd;
-  const size_t tcache = (size_t)td.layers * td.kv_heads * e.cap * td.head_dim;
-  const size_t ccache = (size_t)cd.layers * cd.kv_heads * e.cp.cap * cd.head_dim;
   const size_t esz = e.kv_bf16 ? 2 : 4;
-  s.t_k = dev_alloc<char>(tcache * esz, t);
-  s.t_v = dev_alloc<char>(tcache * esz, t);
-  s.c_k = dev_alloc<char>(ccache * esz, t);
-  s.c_v = dev_alloc<char>(ccache * esz, t);
-  HIPC(hipMemset(s.t_k, 0, tcache * esz));
-  HIPC(hipMemset(s.t_v, 0, tcache * esz));
-  HIPC(hipMemset(s.c_k, 0, ccache * esz));
-  HIPC(hipMemset(s.c_v, 0, ccache * esz));
   const int Ht = e.talker_hidden, Hc = cd.hidden;
-  const int qkv = std::max(td.qkv_rows(), cd.qkv_rows());
-  s.x_t = dev_alloc<float>(Ht, t);
-  s.t_in = dev_alloc<float>(Ht, t);
-  s.qkv = dev_alloc<float>(qkv, t);
-  s.attn = dev_alloc<float>(std::max(td.q_out(), cd.q_out()), t);
-  s.act = dev_alloc<float>(std::max(td.intermediate, cd.intermediate), t);
-  s.logits_t = dev_alloc<float>(td.vocab, t);
-  s.logits_c = dev_alloc<float>(cd.vocab, t);
-  s.x_c = dev_alloc<float>(Hc, t);
-  s.cp_prefix = dev_alloc<float>(2 * (size_t)Ht, t);
-  s.cp_in = dev_alloc<float>(3 * (size_t)Hc, t);
-  s.cur = dev_alloc<float>(Ht, t);
-  s.emb_sum = dev_alloc<float>(Ht, t);
-  s.trailing = dev_alloc<float>((size_t)(e.cap + 1) * Ht, t);
-  s.prefill = dev_alloc<float>((size_t)e.cap * Ht, t);
-  s.codes = dev_alloc<int32_t>((size_t)e.cap * e.groups, t);
-  s.px = dev_alloc<float>((size_t)e.cap * Ht, t);
-  s.pqkv = dev_alloc<float>((size_t)e.cap * td.qkv_rows(), t);
-  s.pattn = dev_alloc<float>((size_t)e.cap * td.q_out(), t);
-  s.pact = dev_alloc<float>((size_t)e.cap * td.intermediate, t);
-  s.pinv = dev_alloc<float>((size_t)e.cap, t);
-  s.attn_part_chunks = std::max(attn_chunks(e.cap), attn_chunks(e.cp.cap));
+  p.n = n;
+  p.t_kv_row = (size_t)td.layers * td.kv_heads * e.cap * td.head_dim;
+  p.c_kv_row = (size_t)cd.layers * cd.kv_heads * e.cp.cap * cd.head_dim;
+  p.s_qkv = std::max(td.qkv_rows(), cd.qkv_rows());
+  p.s_attn = std::max(td.q_out(), cd.q_out());
+  p.s_act = std::max(td.intermediate, cd.intermediate);
+  p.part_chunks = std::max(attn_chunks(e.cap), attn_chunks(e.cp.cap));
   const int kvh = std::max(td.kv_heads, cd.kv_heads);
   const int gq = std::max(td.q_heads / td.kv_heads, cd.q_heads / cd.kv_heads);
-  s.attn_part = dev_alloc<float>((size_t)kvh * s.attn_part_chunks * gq * (td.head_dim + 2), t);
-  HIPC(hipMemset(s.attn_part, 0, (size_t)kvh * s.attn_part_chunks * gq * (td.head_dim + 2) * 4));
-  for (auto [p, n] : std::initializer_list<std::pair<float *, size_t>>{
-           {s.x_t, (size_t)Ht}, {s.t_in, (size_t)Ht}, {s.qkv, (size_t)qkv},
-           {s.attn, (size_t)std::max(td.q_out(), cd.q_out())},
-           {s.act, (size_t)std::max(td.intermediate, cd.intermediate)}, {s.x_c, (size_t)Hc},
-           {s.cp_prefix, 2 * (size_t)Ht}, {s.cp_in, 3 * (size_t)Hc}, {s.cur, (size_t)Ht}, {s.emb_sum, (size_t)Ht}})
-    HIPC(hipMemset(p, 0, n * 4));
-  s.st = dev_alloc<SlotState>(1, t);
-  s.prm = dev_alloc<SlotParams>(1, t);
-  HIPC(hipMemset(s.st, 0, sizeof(SlotState)));
-  HIPC(hipMemset(s.prm, 0, sizeof(SlotParams)));
-  HIPC(hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking));
-  HIPC(hipHostMalloc((void **)&s.h_state, sizeof(SlotState), hipHostMallocDefault));
+  p.part_row = (int64_t)kvh * p.part_chunks * gq * (td.head_dim + 2);
+  p.trailing_row = (int64_t)(e.cap + 1) * Ht;
+  p.codes_row = (int64_t)e.cap * e.groups;
+  auto zeroed = [&](size_t bytes) {
+    char *q = dev_alloc<char>(bytes, t);
+    HIPC(hipMemset(q, 0, bytes));
+    return q;
+  };
+  auto fz = [&](size_t per_row) { return (float *)zeroed(per_row * n * 4); };
+  p.t_k = zeroed(p.t_kv_row * esz * n);
+  p.t_v = zeroed(p.t_kv_row * esz * n);
+  p.c_k = zeroed(p.c_kv_row * esz * n);
+  p.c_v = zeroed(p.c_kv_row * esz * n);
+  p.x_t = fz(Ht);
+  p.t_in = fz(Ht);
+  p.qkv = fz(p.s_qkv);
+  p.attn = fz(p.s_attn);
+  p.act = fz(p.s_act);
+  p.logits_t = fz(td.vocab);
+  p.logits_c = fz(cd.vocab);
+  p.x_c = fz(Hc);
+  p.cp_prefix = fz(2 * (size_t)Ht);
+  p.cp_in = fz(3 * (size_t)Hc);
+  p.cur = fz(Ht);
+  p.emb_sum = fz(Ht);
+  p.trailing = fz(p.trailing_row);
+  p.attn_part = fz(p.part_row);
+  p.codes = (int32_t *)zeroed((size_t)p.codes_row * n * 4);
+  p.st = (SlotState *)zeroed(sizeof(SlotState) * n);
+  p.prm = (SlotParams *)zeroed(sizeof(SlotParams) * n);
+  p.row_on = (int32_t *)zeroed(sizeof(int32_t) * n);
+  p.prefill_rows = n * e.cap;
+  p.px = dev_alloc<float>((size_t)p.prefill_rows * Ht, t);
+  p.pqkv = dev_alloc<float>((size_t)p.prefill_rows * td.qkv_rows(), t);
+  p.pattn = dev_alloc<float>((size_t)p.prefill_rows * td.q_out(), t);
+  p.pact = dev_alloc<float>((size_t)p.prefill_rows * td.intermediate, t);
+  p.pinv = dev_alloc<float>((size_t)p.prefill_rows, t);
+  HIPC(hipHostMalloc((void **)&p.h_states, sizeof(SlotState) * n, hipHostMallocDefault));
+  HIPC(hipHostMalloc((void **)&p.h_row_on, sizeof(int32_t) * n, hipHostMallocDefault));
+  std::memset(p.h_row_on, 0, sizeof(int32_t) * n);
+  HIPC(hipStreamCreateWithFlags(&p.stream, hipStreamNonBlocking));
+  e.slots.resize(n);
+  for (int i = 0; i < n; ++i) {
+    Slot &sl = e.slots[i];
+    sl.t_k = p.t_k + p.t_kv_row * esz * i;
+    sl.t_v = p.t_v + p.t_kv_row * esz * i;
+    sl.c_k = p.c_k + p.c_kv_row * esz * i;
+    sl.c_v = p.c_v + p.c_kv_row * esz * i;
+    sl.x_t = p.x_t + (size_t)i * Ht;
+    sl.t_in = p.t_in + (size_t)i * Ht;
+    sl.qkv = p.qkv + (size_t)i * p.s_qkv;
+    sl.attn = p.attn + (size_t)i * p.s_attn;
+    sl.act = p.act + (size_t)i * p.s_act;
+    sl.logits_t = p.logits_t + (size_t)i * td.vocab;
+    sl.logits_c = p.logits_c + (size_t)i * cd.vocab;
+    sl.x_c = p.x_c + (size_t)i * Hc;
+    sl.cp_prefix = p.cp_prefix + (size_t)i * 2 * Ht;
+    sl.cp_in = p.cp_in + (size_t)i * 3 * Hc;
+    sl.cur = p.cur + (size_t)i * Ht;
+    sl.emb_sum = p.emb_sum + (size_t)i * Ht;
+    sl.trailing = p.trailing + (size_t)i * p.trailing_row;
+    sl.attn_part = p.attn_part + (size_t)i * p.part_row;
+    sl.attn_part_chunks = p.part_chunks;
+    sl.codes = p.codes + (size_t)i * p.codes_row;
+    sl.st = p.st + i;
+    sl.prm = p.prm + i;
+    sl.h_state = p.h_states + i;
+    HIPC(hipStreamCreateWithFlags(&sl.stream, hipStreamNonBlocking));
+  }
 }
 
-void free_slot(Slot &s) {
-  if (s.graph) (void)hipGraphExecDestroy(s.graph);
-  void *ptrs[] = {s.t_k,    s.t_v,   s.c_k,       s.c_v,   s.x_t,     s.t_in,     s.qkv,      s.attn,
-                  s.act,    s.logits_t, s.logits_c, s.x_c, s.cp_prefix, s.cp_in, s.cur,      s.emb_sum,
-                  s.trailing, s.prefill, s.codes,   s.st,    s.prm,     s.trace_t,  s.trace_c,
-                  s.attn_part, s.px,  s.pqkv,  s.pattn, s.pact,  s.pinv};
-  for (void *p : ptrs)
-    if (p) (void)hipFree(p);
-  if (s.stream) (void)hipStreamDestroy(s.stream);
-  if (s.h_state) (void)hipHostFree(s.h_state);
-  s = Slot();
+void free_pools(Engine &e) {
+  for (Slot &sl : e.slots) {
+    if (sl.graph) (void)hipGraphExecDestroy(sl.graph);
+    if (sl.stream) (void)hipStreamDestroy(sl.stream);
+  }
+  e.slots.clear();
+  Pools &p = e.pools;
+  if (p.graph) (void)hipGraphExecDestroy(p.graph);
+  if (p.stream) (void)hipStreamDestroy(p.stream);
+  void *ptrs[] = {p.t_k,      p.t_v,     p.c_k,   p.c_v,      p.x_t,      p.t_in,    p.qkv,  p.attn,
+                  p.act,      p.logits_t, p.logits_c, p.x_c,  p.cp_prefix, p.cp_in,  p.cur,  p.emb_sum,
+                  p.trailing, p.attn_part, p.trace_t, p.trace_c, p.codes,  p.st,      p.prm,  p.row_on,
+                  p.px,       p.pqkv,    p.pattn, p.pact,     p.pinv};
+  for (void *q : ptrs)
+    if (q) (void)hipFree(q);
+  if (p.h_states) (void)hipHostFree(p.h_states);
+  if (p.h_row_on) (void)hipHostFree(p.h_row_on);
+  p = Pools();
 }
 
-void ensure_trace(Engine &e, Slot &s) {
-  if (!e.trace || s.trace_t) return;
-  s.trace_t = dev_alloc<float>((size_t)(e.cap + 1) * e.td.vocab, e.device_bytes);
-  s.trace_c = dev_alloc<float>((size_t)e.cap * (e.groups - 1) * e.cd.vocab, e.device_bytes);
+// Logit trace buffers for every slot, allocated the first time a traced stream starts.
+void ensure_trace(Engine &e) {
+  Pools &p = e.pools;
+  if (!e.trace || p.trace_t) return;
+  p.trace_t_row = (int64_t)(e.cap + 1) * e.td.vocab;
+  p.trace_c_row = (int64_t)e.cap * (e.groups - 1) * e.cd.vocab;
+  p.trace_t = dev_alloc<float>((size_t)p.trace_t_row * p.n, e.device_bytes);
+  p.trace_c = dev_alloc<float>((size_t)p.trace_c_row * p.n, e.device_bytes);
+  for (int i = 0; i < p.n; ++i) {
+    e.slots[i].trace_t = p.trace_t + (size_t)i * p.trace_t_row;
+    e.slots[i].trace_c = p.trace_c + (size_t)i * p.trace_c_row;
+  }
 }
 
 void sync_state(Slot &s) {
@@ -593,6 +790,50 @@ void run_frames(Engine &e, Slot &s, int n) {
   } else {
     for (int i = 0; i < n; ++i) e.enqueue_frame(s, s.stream);
   }
+}
+
+// n batched frames over stream rows 0..rows-1 (pools.row_on already on the device).
+void run_rows_frames(Engine &e, int rows, int n) {
+  Pools &p = e.pools;
+  if (e.use_graph) {
+    if (!p.graph || p.graph_rows != rows || p.graph_traced != (bool)e.trace) {
+      if (p.graph) {
+        HIPC(hipGraphExecDestroy(p.graph));
+        p.graph = nullptr;
+      }
+      hipGraph_t g;
+      HIPC(hipStreamBeginCapture(p.stream, hipStreamCaptureModeThreadLocal));
+      try {
+        e.enqueue_rows_frame(rows, p.stream);
+      } catch (...) {
+        (void)hipStreamEndCapture(p.stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+      }
+      HIPC(hipStreamEndCapture(p.stream, &g));
+      const hipError_t err = hipGraphInstantiate(&p.graph, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      hip_check(err, "hipGraphInstantiate");
+      p.graph_rows = rows;
+      p.graph_traced = (bool)e.trace;
+    }
+    for (int i = 0; i < n; ++i) HIPC(hipGraphLaunch(p.graph, p.stream));
+  } else {
+    for (int i = 0; i < n; ++i) e.enqueue_rows_frame(rows, p.stream);
+  }
+}
+
+// Marks the rows of `slots_on` (others off) and returns the row count a launch must cover.
+int set_rows(Engine &e, const std::vector<int> &slots_on, hipStream_t s) {
+  Pools &p = e.pools;
+  int rows = 0;
+  std::memset(p.h_row_on, 0, sizeof(int32_t) * p.n);
+  for (int i : slots_on) {
+    p.h_row_on[i] = 1;
+    rows = std::max(rows, i + 1);
+  }
+  HIPC(hipMemcpyAsync(p.row_on, p.h_row_on, sizeof(int32_t) * p.n, hipMemcpyHostToDevice, s));
+  return rows;
 }
 
 }  // namespace
@@ -643,6 +884,7 @@ int q3t_engine_create(const q3t_engine_options *opts, q3t_engine **out) {
     if (opts->kv_dtype != 0 && opts->kv_dtype != 1) fail(Q3T_ERR_INVALID, "kv_dtype must be 0 (fp32) or 1 (bf16)");
     e->kv_bf16 = opts->kv_dtype;
     const int nslots = opts->max_streams > 0 ? opts->max_streams : 1;
+    if (nslots > kMaxRows) fail(Q3T_ERR_INVALID, "max_streams %d exceeds %d", nslots, kMaxRows);
     const std::string dir = opts->model_dir;
     const json::Value cfg = json::parse(read_file(dir + "/config.json"));
     const json::Value &tc = cfg.at("talker_config");
@@ -706,8 +948,12 @@ int q3t_engine_create(const q3t_engine_options *opts, q3t_engine **out) {
       e->proj_w = upload_bf16({"talker.code_predictor.small_to_mtp_projection.weight"}, {Hc, Ht});
       e->proj_b = upload_f32("talker.code_predictor.small_to_mtp_projection.bias", Hc);
     }
-    e->slots.resize(nslots);
-    for (auto &s : e->slots) alloc_slot(*e, s);
+    try {
+      alloc_pools(*e, nslots);
+    } catch (...) {
+      free_pools(*e);
+      throw;
+    }
     HIPC(hipDeviceSynchronize());
     *out = e.release();
   });
@@ -718,7 +964,7 @@ int q3t_engine_destroy(q3t_engine *e) {
     if (!e) return;
     (void)hipSetDevice(e->device);
     (void)hipDeviceSynchronize();
-    for (auto &s : e->slots) q3t::free_slot(s);
+    q3t::free_pools(*e);
     void *ptrs[] = {e->talker.mats, e->talker.gains, e->talker.rope, e->cp.mats,    e->cp.gains,
                     e->cp.rope,     e->codec_head,   e->codec_emb,   e->t_norm,     e->c_norm,
                     e->lm_heads,    e->cp_emb,       e->proj_w,      e->proj_b};
@@ -757,20 +1003,82 @@ int q3t_engine_set_trace(q3t_engine *e, int32_t enabled) {
   });
 }
 
+}  // extern "C"
+
+namespace q3t {
+namespace {
+
+void validate_input(const Engine &e, const q3t_stream_input &in, const q3t_generate_options *o) {
+  validate_options(o);
+  if (in.prefill_steps <= 0) fail(Q3T_ERR_INVALID, "prefill steps must be non-zero");
+  if (!in.prefill || !in.tts_pad || (in.trailing_steps > 0 && !in.trailing) || in.trailing_steps < 0)
+    fail(Q3T_ERR_INVALID, "null input array");
+  if ((int64_t)in.prefill_steps + o->max_frames > e.cap)
+    fail(Q3T_ERR_CAPACITY,
+         "requested %lld cache steps but engine was loaded for %d; call load_with_max_frames with a larger "
+         "max_frames",
+         (long long)in.prefill_steps + o->max_frames, e.cap);
+}
+
+// Uploads one stream's inputs (prompt rows into the prefill workspace at row0, trailing
+// rows then tts_pad, loop state, options) onto stream s.
+void stage_stream(Engine &e, int slot, int row0, const q3t_stream_input &in, const q3t_generate_options *o,
+                  hipStream_t s) {
+  Slot &sl = e.slots[slot];
+  const int Ht = e.talker_hidden;
+  const int rows = std::min<int>(in.trailing_steps, e.cap);
+  HIPC(hipMemcpyAsync(e.pools.px + (size_t)row0 * Ht, in.prefill, (size_t)in.prefill_steps * Ht * 4,
+                      hipMemcpyHostToDevice, s));
+  if (rows > 0)
+    HIPC(hipMemcpyAsync(sl.trailing, in.trailing, (size_t)rows * Ht * 4, hipMemcpyHostToDevice, s));
+  HIPC(hipMemcpyAsync(sl.trailing + (size_t)rows * Ht, in.tts_pad, (size_t)Ht * 4, hipMemcpyHostToDevice, s));
+  SlotState st0{};
+  st0.frame = 0;
+  st0.semantic = -1;
+  st0.done = 0;
+  st0.prefill_steps = in.prefill_steps;
+  st0.max_frames = o->max_frames;
+  st0.trailing_rows = rows;
+  SlotParams pr{};
+  pr.talker = SamplingParams{o->do_sample ? 1 : 0, o->top_k, o->top_p, o->temperature};
+  pr.cp = SamplingParams{o->subtalker_dosample ? 1 : 0, o->subtalker_top_k, o->subtalker_top_p,
+                         o->subtalker_temperature};
+  pr.repetition_penalty = o->repetition_penalty;
+  pr.use_history = (o->repetition_penalty != 1.0f || o->do_sample) ? 1 : 0;
+  pr.seed_lo = (uint32_t)(o->seed & 0xffffffffu);
+  pr.seed_hi = (uint32_t)(o->seed >> 32);
+  pr.trace = e.trace;
+  pr.codec_eos = e.codec_eos;
+  // Pageable sources: hipMemcpy returns once the host copy is taken.
+  HIPC(hipStreamSynchronize(s));
+  HIPC(hipMemcpy(sl.st, &st0, sizeof(SlotState), hipMemcpyHostToDevice));
+  HIPC(hipMemcpy(sl.prm, &pr, sizeof(SlotParams), hipMemcpyHostToDevice));
+}
+
+q3t_stream *new_stream(Engine &e, int slot, int max_frames) {
+  Slot &sl = e.slots[slot];
+  sl.in_use = true;
+  auto *stream = new q3t_stream();
+  stream->engine = &e;
+  stream->slot = slot;
+  stream->max_frames = max_frames;
+  stream->done = sl.h_state->done;
+  return stream;
+}
+
+}  // namespace
+}  // namespace q3t
+
+extern "C" {
+
 int q3t_stream_start(q3t_engine *e, const float *prefill, int32_t P, const float *trailing, int32_t T,
                      const float *tts_pad, const q3t_generate_options *o, q3t_stream **out) {
   return guarded([&] {
     using namespace q3t;
     if (!e || !out) fail(Q3T_ERR_INVALID, "null engine or output");
     *out = nullptr;
-    validate_options(o);
-    if (P <= 0) fail(Q3T_ERR_INVALID, "prefill steps must be non-zero");
-    if (!prefill || !tts_pad || (T > 0 && !trailing) || T < 0) fail(Q3T_ERR_INVALID, "null input array");
-    if ((int64_t)P + o->max_frames > e->cap)
-      fail(Q3T_ERR_CAPACITY,
-           "requested %lld cache steps but engine was loaded for %d; call load_with_max_frames with a larger "
-           "max_frames",
-           (long long)P + o->max_frames, e->cap);
+    const q3t_stream_input in{prefill, P, trailing, T, tts_pad};
+    validate_input(*e, in, o);
     int slot = -1;
     for (size_t i = 0; i < e->slots.size(); ++i)
       if (!e->slots[i].in_use) {
@@ -780,51 +1088,102 @@ int q3t_stream_start(q3t_engine *e, const float *prefill, int32_t P, const float
     if (slot < 0) fail(Q3T_ERR_BUSY, "all %zu stream slots are in use", e->slots.size());
     HIPC(hipSetDevice(e->device));
     Slot &s = e->slots[slot];
-    ensure_trace(*e, s);
-    const int Ht = e->talker_hidden;
-    const int rows = std::min<int>(T, e->cap);
-    // Inputs: prefill rows, trailing rows then tts_pad as the row after the last.
-    HIPC(hipMemcpyAsync(s.prefill, prefill, (size_t)P * Ht * 4, hipMemcpyHostToDevice, s.stream));
-    if (rows > 0)
-      HIPC(hipMemcpyAsync(s.trailing, trailing, (size_t)rows * Ht * 4, hipMemcpyHostToDevice, s.stream));
-    HIPC(hipMemcpyAsync(s.trailing + (size_t)rows * Ht, tts_pad, (size_t)Ht * 4, hipMemcpyHostToDevice, s.stream));
-    SlotState st0{};
-    st0.frame = 0;
-    st0.semantic = -1;
-    st0.done = 0;
-    st0.prefill_steps = P;
-    st0.max_frames = o->max_frames;
-    st0.trailing_rows = rows;
-    SlotParams pr{};
-    pr.talker = SamplingParams{o->do_sample ? 1 : 0, o->top_k, o->top_p, o->temperature};
-    pr.cp = SamplingParams{o->subtalker_dosample ? 1 : 0, o->subtalker_top_k, o->subtalker_top_p,
-                           o->subtalker_temperature};
-    pr.repetition_penalty = o->repetition_penalty;
-    pr.use_history = (o->repetition_penalty != 1.0f || o->do_sample) ? 1 : 0;
-    pr.seed_lo = (uint32_t)(o->seed & 0xffffffffu);
-    pr.seed_hi = (uint32_t)(o->seed >> 32);
-    pr.trace = e->trace;
-    pr.codec_eos = e->codec_eos;
-    *s.h_state = st0;
-    HIPC(hipMemcpyAsync(s.st, s.h_state, sizeof(SlotState), hipMemcpyHostToDevice, s.stream));
-    HIPC(hipStreamSynchronize(s.stream));  // h_state is reused below
-    HIPC(hipMemcpyAsync(s.prm, &pr, sizeof(SlotParams), hipMemcpyHostToDevice, s.stream));
-    HIPC(hipStreamSynchronize(s.stream));
+    ensure_trace(*e);
+    stage_stream(*e, slot, 0, in, o, s.stream);
     // Talker prefill: positions 0..P-1, then the head and the first semantic token
     // (talker.rs:207-233).
-    e->prefill_rows(s, P, s.stream);
+    e->prefill_segments({PrefillSeg{slot, 0, P}}, P, s.stream);
     e->gemv(EPI_STORE, true, e->codec_head, s.x_t, e->t_norm, e->td.eps, nullptr, nullptr, s.logits_t, e->td.vocab,
             e->td.hidden, SKIP_NEVER, s.st, s.stream);
     e->select_talker(s, 0, s.stream);
     hip_check(launch_frame_end(s.st, s.prm, 0, s.stream), "launch_frame_end");
     sync_state(s);
-    s.in_use = true;
-    auto *stream = new q3t_stream();
-    stream->engine = e;
-    stream->slot = slot;
-    stream->max_frames = o->max_frames;
-    stream->done = s.h_state->done;
-    *out = stream;
+    *out = new_stream(*e, slot, o->max_frames);
+  });
+}
+
+int q3t_streams_start(q3t_engine *e, int32_t n, const q3t_stream_input *inputs, const q3t_generate_options *opts,
+                      q3t_stream **out) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || !inputs || !opts || !out) fail(Q3T_ERR_INVALID, "null argument");
+    if (n <= 0) fail(Q3T_ERR_INVALID, "stream count must be positive");
+    for (int j = 0; j < n; ++j) out[j] = nullptr;
+    for (int j = 0; j < n; ++j) validate_input(*e, inputs[j], &opts[j]);
+    std::vector<int> slots;
+    for (size_t i = 0; i < e->slots.size() && (int)slots.size() < n; ++i)
+      if (!e->slots[i].in_use) slots.push_back((int)i);
+    if ((int)slots.size() < n)
+      fail(Q3T_ERR_BUSY, "%d streams requested but only %zu of %zu slots are free", n, slots.size(), e->slots.size());
+    HIPC(hipSetDevice(e->device));
+    ensure_trace(*e);
+    Pools &p = e->pools;
+    // All prompts side by side in the prefill workspace: one GEMM per weight for every stream.
+    std::vector<PrefillSeg> segs;
+    int M = 0;
+    for (int j = 0; j < n; ++j) {
+      segs.push_back(PrefillSeg{slots[j], M, inputs[j].prefill_steps});
+      M += inputs[j].prefill_steps;
+    }
+    if (M > p.prefill_rows) fail(Q3T_ERR_CAPACITY, "prompts total %d rows; the workspace holds %d", M, p.prefill_rows);
+    for (int j = 0; j < n; ++j) stage_stream(*e, slots[j], segs[j].row0, inputs[j], &opts[j], p.stream);
+    e->prefill_segments(segs, M, p.stream);
+    const int rows = set_rows(*e, slots, p.stream);
+    e->rgemm(EPI_STORE, true, e->codec_head, p.x_t, e->talker_hidden, e->t_norm, e->td.eps, nullptr, 0, nullptr,
+             p.logits_t, e->td.vocab, e->td.vocab, e->talker_hidden, rows, p.stream);
+    e->select_talker_rows(rows, 0, p.stream);
+    hip_check(launch_frame_end(p.st, p.prm, 0, p.stream, rows, p.row_on), "launch_frame_end(rows)");
+    HIPC(hipMemcpyAsync(p.h_states, p.st, sizeof(SlotState) * rows, hipMemcpyDeviceToHost, p.stream));
+    HIPC(hipStreamSynchronize(p.stream));
+    for (int j = 0; j < n; ++j) out[j] = new_stream(*e, slots[j], opts[j].max_frames);
+  });
+}
+
+int q3t_streams_next_codes(q3t_engine *e, q3t_stream *const *streams, int32_t n, int32_t max_chunk, int32_t *codes,
+                           q3t_chunk_info *info) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || !streams || !info || (n > 0 && !codes)) fail(Q3T_ERR_INVALID, "null argument");
+    if (n <= 0) fail(Q3T_ERR_INVALID, "stream count must be positive");
+    if (max_chunk <= 0) fail(Q3T_ERR_INVALID, "max_chunk_frames must be non-zero");
+    std::vector<int> seen(e->slots.size(), 0), on, want(n, 0);
+    int nrun = 0;
+    for (int j = 0; j < n; ++j) {
+      q3t_stream *sp = streams[j];
+      if (!sp || sp->engine != e) fail(Q3T_ERR_INVALID, "stream %d is null or belongs to another engine", j);
+      if (seen[sp->slot]++) fail(Q3T_ERR_INVALID, "stream %d is listed twice", j);
+      info[j].frames = 0;
+      info[j].total_frames = sp->host_frame;
+      info[j].ended_by_eos = sp->done == 1;
+      if (sp->done || sp->host_frame >= sp->max_frames) continue;
+      want[j] = std::min(max_chunk, sp->max_frames - sp->host_frame);
+      nrun = std::max(nrun, want[j]);
+      on.push_back(sp->slot);
+    }
+    if (nrun == 0) return;
+    HIPC(hipSetDevice(e->device));
+    Pools &p = e->pools;
+    const int rows = set_rows(*e, on, p.stream);
+    // Streams that need fewer frames than nrun reach max_frames on the device and stop there.
+    run_rows_frames(*e, rows, nrun);
+    HIPC(hipMemcpyAsync(p.h_states, p.st, sizeof(SlotState) * rows, hipMemcpyDeviceToHost, p.stream));
+    HIPC(hipStreamSynchronize(p.stream));
+    for (int j = 0; j < n; ++j) {
+      q3t_stream *sp = streams[j];
+      if (!want[j]) continue;
+      const SlotState &hs = p.h_states[sp->slot];
+      const int produced = hs.frame - sp->host_frame;
+      if (produced < 0 || produced > want[j]) fail(Q3T_ERR_HIP, "device loop state is inconsistent");
+      if (produced > 0)
+        HIPC(hipMemcpy(codes + (size_t)j * max_chunk * e->groups,
+                       e->slots[sp->slot].codes + (size_t)sp->host_frame * e->groups,
+                       (size_t)produced * e->groups * 4, hipMemcpyDeviceToHost));
+      sp->host_frame += produced;
+      sp->done = hs.done;
+      info[j].frames = produced;
+      info[j].total_frames = sp->host_frame;
+      info[j].ended_by_eos = sp->done == 1;
+    }
   });
 }
 
@@ -862,6 +1221,7 @@ int q3t_stream_destroy(q3t_stream *sp) {
     Engine &e = *sp->engine;
     (void)hipSetDevice(e.device);
     (void)hipStreamSynchronize(e.slots[sp->slot].stream);
+    (void)hipStreamSynchronize(e.pools.stream);
     e.slots[sp->slot].in_use = false;
     delete sp;
   });
@@ -901,6 +1261,7 @@ int q3t_engine_synchronize(q3t_engine *e) {
     if (!e) fail(Q3T_ERR_INVALID, "null engine");
     HIPC(hipSetDevice(e->device));
     for (auto &s : e->slots) HIPC(hipStreamSynchronize(s.stream));
+    HIPC(hipStreamSynchronize(e->pools.stream));
   });
 }
 

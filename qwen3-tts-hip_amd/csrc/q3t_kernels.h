@@ -17,17 +17,23 @@ hipError_t launch_gemv(int epi, bool norm, bool streaming, const GemvArgs &a, hi
                        const LaunchTiming *timing = nullptr);
 bool gemv_supports_k(int K);
 
+// Most stream rows one batched launch covers (skinny GEMM rows, select workgroups).
+constexpr int kMaxRows = 16;
+
 // Fused q/k head RMSNorm + RoPE + KV-cache write + GQA decode attention, split over key
-// positions in chunks (one workgroup per (KV head, chunk)); the last chunk merges.
+// positions in chunks (one workgroup per (KV head, chunk, stream row)).  With partial_out
+// the chunks' partials are merged by the consumer (the O-projection GEMV, or
+// launch_attn_merge for stream rows).
 hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t stream,
-                              const LaunchTiming *timing = nullptr);
+                              const LaunchTiming *timing = nullptr, int rows = 1);
+hipError_t launch_attn_merge(const AttnMergeArgs &a, int rows, hipStream_t stream);
 int attn_max_cache_steps(int q_heads, int kv_heads);
 // Key rows per attention workgroup for a cache of `cap` rows, and the resulting number of
 // chunks (partials the workspace must hold per head).
 int attn_chunk_len(int cap);
 int attn_chunks(int cap);
 
-// Matrix-core GEMM (bf16 weights, fp32 activations split into two bf16 terms, fp32 accumulate)
+// Matrix-core GEMM (bf16 weights, fp32 activations split into three bf16 terms, fp32 accumulate)
 // for many rows: prompt prefill and batched decode.  Requires K % 32 == 0.
 hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t stream);
 // The same product for M <= 16 rows (batched decode); norm = fused RMSNorm of the rows with
@@ -40,12 +46,14 @@ hipError_t launch_row_rms(const float *X, int ldx, int M, int K, float eps, floa
 // Prefill attention: q/k norm + RoPE + KV store for P rows, then causal attention.
 hipError_t launch_prefill_attention(const PrefillAttnArgs &a, hipStream_t stream);
 
-hipError_t launch_select_talker(const SelectTalkerArgs &a, hipStream_t stream);
-hipError_t launch_select_cp(const SelectCpArgs &a, hipStream_t stream);
+// Token selection, one workgroup per stream row (rows > 1 needs row_on and the row strides).
+hipError_t launch_select_talker(const SelectTalkerArgs &a, hipStream_t stream, int rows = 1);
+hipError_t launch_select_cp(const SelectCpArgs &a, hipStream_t stream, int rows = 1);
 // n independent draws from one logit row (draw i uses Philox counter (i, kind, 0, 0)).
 hipError_t launch_sample_draws(const float *logits, int V, const SamplingParams &sp, uint64_t seed, int kind, int n,
                                int32_t *out, hipStream_t stream);
-hipError_t launch_frame_end(SlotState *st, const SlotParams *prm, int advance, hipStream_t stream);
+hipError_t launch_frame_end(SlotState *st, const SlotParams *prm, int advance, hipStream_t stream, int rows = 1,
+                            const int32_t *row_on = nullptr);
 
 // Largest vocabulary the select kernels hold in LDS.
 constexpr int kMaxVocab = 4096;

@@ -235,10 +235,13 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   static_assert(D == 128, "lane layout assumes head_dim 128");
   static_assert(G >= 1 && G <= 2, "query heads per KV head");
   static_assert(CH % 16 == 0 && CH <= kAttnMaxChunk, "chunk length");
-  if (skip_work(a.st, a.skip)) return;
+  const int row = blockIdx.z;
+  if (a.row_on && !a.row_on[row]) return;
+  const SlotState *st = a.st + row;
+  if (skip_work(st, a.skip)) return;
   const int h = blockIdx.x;
   const int c = blockIdx.y;
-  const int pos = (a.pos_mode == POS_TALKER_FRAME) ? a.st->prefill_steps + a.st->frame : a.pos_const;
+  const int pos = (a.pos_mode == POS_TALKER_FRAME) ? st->prefill_steps + st->frame : a.pos_const;
   if (pos < 0 || pos >= a.cap) return;  // host validates; never index outside the cache
   const int L = pos + 1;
   const int nchunks = (L + CH - 1) / CH;
@@ -253,8 +256,9 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   const int grp = lane >> 4;
   const int q_out = a.q_heads * D;
   const int kv_out = a.kv_heads * D;
-  KVT *kcache = reinterpret_cast<KVT *>(a.kcache);
-  KVT *vcache = reinterpret_cast<KVT *>(a.vcache);
+  KVT *kcache = reinterpret_cast<KVT *>(a.kcache) + row * a.kv_row;
+  KVT *vcache = reinterpret_cast<KVT *>(a.vcache) + row * a.kv_row;
+  const float *qkv = a.qkv + (size_t)row * a.ld_qkv;
   const KVT *kbase = kcache + (size_t)h * a.cap * D;
   const KVT *vbase = vcache + (size_t)h * a.cap * D;
 
@@ -271,8 +275,8 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   const bool has_vec = wave < G + 2 && (wave < G || owns_pos);
   float x0 = 0.f, x1 = 0.f;
   if (has_vec) {
-    const float *src = vec < G ? a.qkv + (h * G + vec) * D
-                               : (vec == G ? a.qkv + q_out + h * D : a.qkv + q_out + kv_out + h * D);
+    const float *src = vec < G ? qkv + (h * G + vec) * D
+                               : (vec == G ? qkv + q_out + h * D : qkv + q_out + kv_out + h * D);
     x0 = src[lane];
     x1 = src[lane + 64];
   }
@@ -389,10 +393,10 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   const int g_o = o / D, d_o = o % D;
   const float v_o = ((red[0][g_o][d_o] + red[1][g_o][d_o]) + red[2][g_o][d_o]) + red[3][g_o][d_o];
   if (!a.partial_out) {
-    a.out[(h * G + g_o) * D + d_o] = v_o / stat[g_o][1];
+    a.out[(size_t)row * a.ld_out + (h * G + g_o) * D + d_o] = v_o / stat[g_o][1];
     return;
   }
-  float *my = a.part + (((size_t)h * a.part_chunks + c) * G + g_o) * (D + 2);
+  float *my = a.part + row * a.part_row + (((size_t)h * a.part_chunks + c) * G + g_o) * (D + 2);
   my[2 + d_o] = v_o;
   if (d_o == 0) {
     my[0] = stat[g_o][0];
@@ -424,6 +428,39 @@ __device__ void merge_attention(const GemvArgs &a, float *xs) {
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) xs[base + j] = num[j] / den;
+  }
+}
+
+// Stream-row form of merge_attention for the batched frame: workgroup r merges row r's
+// partials into out + r * ld_out (same chunk order and arithmetic).
+__global__ __launch_bounds__(256) void k_attn_merge(AttnMergeArgs a) {
+  constexpr int D = 128;
+  const int row = blockIdx.x;
+  if (a.row_on && !a.row_on[row]) return;
+  const SlotState *st = a.st + row;
+  if (skip_work(st, a.skip)) return;
+  const int pos = (a.pos_mode == POS_TALKER_FRAME) ? st->prefill_steps + st->frame : a.pos_const;
+  const int nchunks = min((pos + a.chunk) / a.chunk, a.part_chunks);
+  const int G = a.q_heads / a.kv_heads;
+  const float *part = a.part + row * a.part_row;
+  float *out = a.out + (size_t)row * a.ld_out;
+  for (int base = threadIdx.x * 8; base < a.q_heads * D; base += 256 * 8) {
+    const int hq = base / D, d0 = base % D;
+    const int h = hq / G, g = hq % G;
+    const float *p0 = part + (((size_t)h * a.part_chunks) * G + g) * (D + 2);
+    const size_t stride = (size_t)G * (D + 2);
+    float M = -FLT_MAX;
+    for (int c = 0; c < nchunks; ++c) M = fmaxf(M, p0[c * stride]);
+    float den = 0.f, num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < nchunks; ++c) {
+      const float *pc = p0 + c * stride;
+      const float w = expf(pc[0] - M);
+      den = fmaf(w, pc[1], den);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) num[j] = fmaf(w, pc[2 + d0 + j], num[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) out[base + j] = num[j] / den;
   }
 }
 
@@ -655,7 +692,7 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int m = 4 * kb + e;
-    if (m >= a.M || n >= a.N) continue;
+    if (m >= a.M || n >= a.N || (a.row_on && !a.row_on[m])) continue;
     float v = sum[0][e];
     if constexpr (EPI == EPI_SWIGLU) {
       v = v / (1.0f + expf(-v)) * sum[T - 1][e];
@@ -1010,7 +1047,16 @@ __device__ int block_sample(SelectShared &sh, int V, const SamplingParams &sp, f
 }
 
 __global__ __launch_bounds__(1024) void k_select_talker(SelectTalkerArgs a) {
+  const int row = blockIdx.x;
+  if (a.row_on && !a.row_on[row]) return;
+  a.st += row;
+  a.prm += row;
   if (a.after_frame && skip_work(a.st, SKIP_TALKER)) return;
+  a.logits += (size_t)row * a.V;
+  a.x += (size_t)row * a.H;
+  a.cp_prefix += (size_t)row * 2 * a.H;
+  a.codes += row * a.codes_row;
+  if (a.trace) a.trace += row * a.trace_row;
   __shared__ SelectShared sh;
   __shared__ unsigned char seen[kMaxVocab];
   __shared__ float red[16];
@@ -1057,7 +1103,18 @@ __global__ __launch_bounds__(1024) void k_select_talker(SelectTalkerArgs a) {
 }
 
 __global__ __launch_bounds__(1024) void k_select_cp(SelectCpArgs a) {
+  const int row = blockIdx.x;
+  if (a.row_on && !a.row_on[row]) return;
+  a.st += row;
+  a.prm += row;
   if (skip_work(a.st, SKIP_DONE)) return;
+  a.logits += (size_t)row * a.Vc;
+  a.cur += (size_t)row * a.Ht;
+  a.emb_sum += (size_t)row * a.Ht;
+  a.talker_in += (size_t)row * a.Ht;
+  a.codes += row * a.codes_row;
+  a.trailing += row * a.trailing_row;
+  if (a.trace) a.trace += row * a.trace_row;
   __shared__ SelectShared sh;
   const int tid = threadIdx.x;
   const SlotParams prm = *a.prm;
@@ -1101,8 +1158,13 @@ __global__ __launch_bounds__(1024) void k_sample_draws(const float *logits, int 
 }
 
 // Ends a frame (advance = 1) or checks the token drawn after the prefill (advance = 0).
-__global__ void k_frame_end(SlotState *st, const SlotParams *prm, int advance) {
-  if (threadIdx.x != 0 || st->done) return;
+// Thread r handles stream row r (rows <= 64).
+__global__ void k_frame_end(SlotState *st, const SlotParams *prm, int advance, int rows, const int32_t *row_on) {
+  const int r = threadIdx.x;
+  if (r >= rows || (row_on && !row_on[r])) return;
+  st += r;
+  prm += r;
+  if (st->done) return;
   const int f = st->frame + advance;
   st->frame = f;
   if (st->semantic == prm->codec_eos)
@@ -1223,12 +1285,14 @@ int attn_max_cache_steps(int q_heads, int kv_heads) {
   return kAttnMaxChunk * 64;  // at most 64 partial chunks per head
 }
 
-hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t s, const LaunchTiming *t) {
+hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t s, const LaunchTiming *t, int rows) {
   if (head_dim != 128 || a.kv_heads <= 0 || a.q_heads % a.kv_heads) return hipErrorInvalidValue;
+  if (rows < 1 || rows > kMaxRows || (rows > 1 && (!a.row_on || a.ld_qkv <= 0 || a.kv_row <= 0))) return hipErrorInvalidValue;
+  if (rows > 1 && (a.partial_out ? a.part_row <= 0 : a.ld_out <= 0)) return hipErrorInvalidValue;
   const int G = a.q_heads / a.kv_heads;
   if (a.cap > attn_max_cache_steps(a.q_heads, a.kv_heads) || a.chunk != attn_chunk_len(a.cap)) return hipErrorInvalidValue;
   if (a.partial_out ? a.part_chunks < attn_chunks(a.cap) : attn_chunks(a.cap) != 1) return hipErrorInvalidValue;
-  const dim3 grid(a.kv_heads, attn_chunks(a.cap)), block(256);
+  const dim3 grid(a.kv_heads, attn_chunks(a.cap), rows), block(256);
 #define Q3T_ATTN_CASE(GG, TT, CC) \
   if (G == GG && a.chunk == CC) {  \
     launch_timed(k_attn_split<128, GG, TT, CC>, grid, block, 0, s, t, a); \
@@ -1327,15 +1391,28 @@ hipError_t launch_prefill_attention(const PrefillAttnArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_select_talker(const SelectTalkerArgs &a, hipStream_t s) {
-  if (a.V > kMaxVocab || a.V < 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_select_talker, dim3(1), dim3(1024), 0, s, a);
+hipError_t launch_attn_merge(const AttnMergeArgs &a, int rows, hipStream_t s) {
+  if (rows < 1 || rows > kMaxRows || a.kv_heads <= 0 || a.q_heads % a.kv_heads || a.chunk <= 0 ||
+      a.part_chunks <= 0 || a.q_heads * 128 > a.ld_out || (rows > 1 && (!a.row_on || a.part_row <= 0)))
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_attn_merge, dim3(rows), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
-hipError_t launch_select_cp(const SelectCpArgs &a, hipStream_t s) {
+hipError_t launch_select_talker(const SelectTalkerArgs &a, hipStream_t s, int rows) {
+  if (a.V > kMaxVocab || a.V < 1024) return hipErrorInvalidValue;
+  if (rows < 1 || rows > kMaxRows || (rows > 1 && (!a.row_on || a.codes_row <= 0 || (a.trace && a.trace_row <= 0))))
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_select_talker, dim3(rows), dim3(1024), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_select_cp(const SelectCpArgs &a, hipStream_t s, int rows) {
   if (a.Vc > kMaxVocab) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_select_cp, dim3(1), dim3(1024), 0, s, a);
+  if (rows < 1 || rows > kMaxRows ||
+      (rows > 1 && (!a.row_on || a.codes_row <= 0 || a.trailing_row <= 0 || (a.trace && a.trace_row <= 0))))
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_select_cp, dim3(rows), dim3(1024), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1347,8 +1424,10 @@ hipError_t launch_sample_draws(const float *logits, int V, const SamplingParams 
   return hipGetLastError();
 }
 
-hipError_t launch_frame_end(SlotState *st, const SlotParams *prm, int advance, hipStream_t s) {
-  hipLaunchKernelGGL(k_frame_end, dim3(1), dim3(64), 0, s, st, prm, advance);
+hipError_t launch_frame_end(SlotState *st, const SlotParams *prm, int advance, hipStream_t s, int rows,
+                            const int32_t *row_on) {
+  if (rows < 1 || rows > kMaxRows || (rows > 1 && !row_on)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_frame_end, dim3(1), dim3(64), 0, s, st, prm, advance, rows, row_on);
   return hipGetLastError();
 }
 

@@ -28,7 +28,7 @@ from __future__ import annotations
 import ctypes
 import dataclasses
 import os
-from typing import Optional, Sequence, Union
+from typing import List, Optional, Sequence, Union
 
 import numpy as np
 
@@ -110,6 +110,12 @@ class _ChunkInfo(ctypes.Structure):
                 ("ended_by_eos", ctypes.c_int32)]
 
 
+class _StreamInput(ctypes.Structure):
+    _fields_ = [("prefill", ctypes.POINTER(ctypes.c_float)), ("prefill_steps", ctypes.c_int32),
+                ("trailing", ctypes.POINTER(ctypes.c_float)), ("trailing_steps", ctypes.c_int32),
+                ("tts_pad", ctypes.POINTER(ctypes.c_float))]
+
+
 _lib = None
 
 
@@ -134,6 +140,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                                             f32p, P(_GenerateOptions), P(ctypes.c_void_p)]),
         "q3t_stream_next_codes": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, i32p, P(_ChunkInfo)]),
         "q3t_stream_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+        "q3t_streams_start": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, P(_StreamInput), P(_GenerateOptions),
+                                             P(ctypes.c_void_p)]),
+        "q3t_streams_next_codes": (ctypes.c_int, [ctypes.c_void_p, P(ctypes.c_void_p), ctypes.c_int32,
+                                                  ctypes.c_int32, i32p, P(_ChunkInfo)]),
         "q3t_generate_codes": (ctypes.c_int, [ctypes.c_void_p, f32p, ctypes.c_int32, f32p, ctypes.c_int32,
                                               f32p, P(_GenerateOptions), i32p, i32p, i32p]),
         "q3t_stream_read_talker_logits": (ctypes.c_int, [ctypes.c_void_p, f32p, ctypes.c_int32, i32p]),
@@ -396,22 +406,72 @@ class HipTtsEngine:
         inp = self._prepare(inputs, options, stream_options.text_lookahead_tokens)
         return HipTtsStream(self, inp, options, stream_options)
 
+    # -- several streams at once (no counterpart in the reference: one stream per engine) --
+    def start_streams(self, inputs: List[Inputs], options: List[GenerateOptions],
+                      stream_options: StreamOptions = StreamOptions()) -> List["HipTtsStream"]:
+        """``q3t_streams_start``: n ``start_stream`` calls with one prefill over all prompts."""
+        if len(inputs) != len(options) or not inputs:
+            raise InvalidInputError(Q3T_ERR_INVALID, "need one GenerateOptions per input")
+        stream_options.validate()
+        n = len(inputs)
+        prepared = [self._prepare(i, o, stream_options.text_lookahead_tokens) for i, o in zip(inputs, options)]
+        keep = []
+        ins = (_StreamInput * n)()
+        opts = (_GenerateOptions * n)()
+        for j, (inp, o) in enumerate(zip(prepared, options)):
+            pre, trail, pad = _f32(inp.prefill), _f32(inp.trailing_text), _f32(inp.tts_pad_embed)
+            keep += [pre, trail, pad]
+            ins[j] = _StreamInput(_fptr(pre), pre.shape[0], _fptr(trail), trail.shape[0], _fptr(pad))
+            opts[j] = o._c()
+        handles = (ctypes.c_void_p * n)()
+        _check(_lib.q3t_streams_start(self._h, n, ins, opts, handles))
+        return [HipTtsStream(self, inp, o, stream_options, handle=ctypes.c_void_p(h))
+                for inp, o, h in zip(prepared, options, handles)]
+
+    def next_codes_chunks(self, streams: List["HipTtsStream"],
+                          max_chunk_frames: int) -> List[Optional[GeneratedCodesChunk]]:
+        """``q3t_streams_next_codes``: ``next_codes_chunk`` of every listed stream, run as one
+        batch (one pass over the weights per frame for all of them)."""
+        if max_chunk_frames <= 0:
+            raise InvalidInputError(Q3T_ERR_INVALID, "max_chunk_frames must be non-zero")
+        n = len(streams)
+        handles = (ctypes.c_void_p * n)(*[s._h.value if s._h else None for s in streams])
+        buf = np.zeros((n, max_chunk_frames, self.code_groups), dtype=np.int32)
+        infos = (_ChunkInfo * n)()
+        _check(_lib.q3t_streams_next_codes(self._h, handles, n, max_chunk_frames, _iptr(buf), infos))
+        return [s._accept(buf[j], infos[j]) for j, s in enumerate(streams)]
+
+    def generate_codes_batch(self, inputs: List[Inputs], options: List[GenerateOptions],
+                             chunk_frames: int = 6) -> List[GeneratedCodes]:
+        """Start every stream together and pull chunks for all of them until each has ended."""
+        streams = self.start_streams(inputs, options, StreamOptions(text_lookahead_tokens=1 << 30))
+        try:
+            live = list(streams)
+            while live:
+                chunks = self.next_codes_chunks(live, chunk_frames)
+                live = [s for s, c in zip(live, chunks) if c is not None]
+            return [s.finish_codes() for s in streams]
+        finally:
+            for s in streams:
+                s.close()
+
 
 class HipTtsStream:
     """``HipTtsStream`` (generation.rs:145-163, 876-997).  Must not outlive its engine."""
 
     def __init__(self, engine: HipTtsEngine, inputs: PreparedInputs, options: GenerateOptions,
-                 stream_options: StreamOptions):
+                 stream_options: StreamOptions, handle: Optional[ctypes.c_void_p] = None):
         self.engine = engine
         self.inputs = inputs
         self.options = options
         self.stream_options = stream_options
-        o = options._c()
-        pre, trail, pad = _f32(inputs.prefill), _f32(inputs.trailing_text), _f32(inputs.tts_pad_embed)
-        h = ctypes.c_void_p()
-        _check(_lib.q3t_stream_start(engine._h, _fptr(pre), pre.shape[0], _fptr(trail), trail.shape[0],
-                                     _fptr(pad), ctypes.byref(o), ctypes.byref(h)))
-        self._h = h
+        if handle is None:
+            o = options._c()
+            pre, trail, pad = _f32(inputs.prefill), _f32(inputs.trailing_text), _f32(inputs.tts_pad_embed)
+            handle = ctypes.c_void_p()
+            _check(_lib.q3t_stream_start(engine._h, _fptr(pre), pre.shape[0], _fptr(trail), trail.shape[0],
+                                         _fptr(pad), ctypes.byref(o), ctypes.byref(handle)))
+        self._h = handle
         self.prefill_steps = inputs.prefill_steps
         self._codes = []
         self.frame = 0
@@ -423,6 +483,9 @@ class HipTtsStream:
         buf = np.zeros((max_chunk_frames, self.engine.code_groups), dtype=np.int32)
         info = _ChunkInfo()
         _check(_lib.q3t_stream_next_codes(self._h, max_chunk_frames, _iptr(buf), ctypes.byref(info)))
+        return self._accept(buf, info)
+
+    def _accept(self, buf: np.ndarray, info: _ChunkInfo) -> Optional[GeneratedCodesChunk]:
         self.frame = info.total_frames
         self.ended_by_eos = bool(info.ended_by_eos)
         if info.frames == 0:

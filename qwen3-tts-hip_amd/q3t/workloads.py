@@ -72,3 +72,62 @@ WORKLOADS: Dict[str, Workload] = {w.name: w for w in [
              temperature=0.9, repetition_penalty=1.05, sample_seed=7),
     Workload("tinyproj_greedy", "tiny-proj", 24, 3, 16, 128, None),
 ]}
+
+
+@dataclasses.dataclass(frozen=True)
+class MultiWorkload:
+    """independent streams generated together on one engine.
+
+    Stream j's prompt length, frame budget and content ids come from one generator seeded
+    with `seed`, in this order: all lengths, all frame budgets, then each prompt.  Every
+    prompt goes into the prefill whole (non-streaming, P = 9 + length), so the prefill is one
+    matrix-core GEMM over all streams' rows.  The KV capacity is max(P + frames) rounded up
+    to 64.  With `sampled_every` = k > 0, every k-th stream (j % k == k - 1) samples with
+    the config-3 options and seed j; the rest are greedy."""
+    name: str
+    spec: str
+    streams: int
+    prompt_range: tuple   # content tokens, inclusive
+    frames_range: tuple   # inclusive
+    seed: int
+    chunk_frames: int = 6
+    sampled_every: int = 0
+    weight_seed: int = 0
+
+    def plan(self):
+        rng = np.random.default_rng(self.seed)
+        lengths = rng.integers(self.prompt_range[0], self.prompt_range[1] + 1, self.streams)
+        frames = rng.integers(self.frames_range[0], self.frames_range[1] + 1, self.streams)
+        prompts = [rng.integers(0, 151643, int(n)) for n in lengths]
+        return [int(n) for n in lengths], [int(f) for f in frames], prompts
+
+    @property
+    def max_cache_steps(self) -> int:
+        lengths, frames, _ = self.plan()
+        need = max(9 + n + f for n, f in zip(lengths, frames))
+        return (need + 63) // 64 * 64
+
+    def options_kwargs(self):
+        _, frames, _ = self.plan()
+        out = []
+        for j, f in enumerate(frames):
+            if self.sampled_every and j % self.sampled_every == self.sampled_every - 1:
+                out.append(dict(max_frames=f, do_sample=True, top_k=50, top_p=1.0, temperature=0.9,
+                                repetition_penalty=1.05, subtalker_dosample=True, subtalker_top_k=50,
+                                subtalker_top_p=1.0, subtalker_temperature=0.9, seed=j))
+            else:
+                out.append(dict(max_frames=f, do_sample=False, repetition_penalty=1.0, subtalker_dosample=False,
+                                seed=0))
+        return out
+
+    def inputs(self, model: "synth.SyntheticModel"):
+        prep = textprep.TextPrep(model)
+        return [prep.prepare(p) for p in self.plan()[2]]
+
+
+MULTI_WORKLOADS: Dict[str, MultiWorkload] = {w.name: w for w in [
+    # config 5: 16 streams, prompts U[16, 512], frames U[64, 240], seed 2
+    MultiWorkload("cfg5_0.6b_multistream", "0.6b", 16, (16, 512), (64, 240), 2),
+    # small shapes: ragged greedy + sampled streams for quick parity runs
+    MultiWorkload("tiny_multistream", "tiny", 6, (4, 40), (8, 24), 5, chunk_frames=5, sampled_every=3),
+]}

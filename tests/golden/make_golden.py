@@ -6,6 +6,9 @@ Each fixture holds one oracle rollout of a workload from q3t/workloads.py: the c
 the raw Talker logits (float16; the parity tolerance is 2e-2), the top-2 margins of every
 argmax (for the near-tie policy) and the first frames' CodePredictor logits, plus the
 weight checksum so a test can tell that it rebuilt the same synthetic model.
+
+A multi-stream workload (MULTI_WORKLOADS) holds one independent single-stream rollout per
+stream (streams do not interact), with the first Talker logit rows of each.
 """
 from __future__ import annotations
 
@@ -23,11 +26,12 @@ sys.path.insert(0, os.path.join(ROOT, "qwen3-tts-hip_amd"))
 
 from oracle.model import GenerateOptions, Oracle  # noqa: E402
 from q3t import synth  # noqa: E402
-from q3t.workloads import WORKLOADS  # noqa: E402
+from q3t.workloads import MULTI_WORKLOADS, WORKLOADS  # noqa: E402
 
 # Talker-logit rows kept per fixture (the codes and margins are always complete).
 MAX_LOGIT_ROWS = 256
 CP_LOGIT_FRAMES = 2
+MULTI_LOGIT_ROWS = 4
 
 
 def make(name: str) -> str:
@@ -54,7 +58,33 @@ def make(name: str) -> str:
     return path
 
 
+def make_multi(name: str) -> str:
+    w = MULTI_WORKLOADS[name]
+    t0 = time.time()
+    model = synth.SyntheticModel.build(w.spec, w.weight_seed)
+    inputs = w.inputs(model)
+    oracle = Oracle(model.tensors, model.config(), max_cache_steps=w.max_cache_steps, dtype=np.float64)
+    arrays, frames, eos = {}, [], []
+    for j, (inp, kw) in enumerate(zip(inputs, w.options_kwargs())):
+        tr = oracle.rollout(inp.prefill, inp.trailing_text, inp.tts_pad_embed, GenerateOptions(**kw))
+        arrays[f"codes_{j}"] = tr.codes
+        arrays[f"talker_margins_{j}"] = tr.talker_margins
+        arrays[f"cp_margins_{j}"] = tr.cp_margins
+        arrays[f"talker_logits_{j}"] = tr.talker_logits[:MULTI_LOGIT_ROWS].astype(np.float16)
+        frames.append(tr.frames)
+        eos.append(bool(tr.ended_by_eos))
+        print(f"  stream {j}: P={inp.prefill_steps} frames={tr.frames} ({time.time() - t0:.0f} s)", flush=True)
+    meta = dict(workload=name, spec=w.spec, weight_seed=w.weight_seed, checksum=model.checksum(),
+                streams=w.streams, prefill_steps=[int(i.prefill_steps) for i in inputs], frames=frames,
+                ended_by_eos=eos, options=w.options_kwargs(), max_cache_steps=w.max_cache_steps,
+                oracle_dtype="float64", seconds=round(time.time() - t0, 1))
+    path = os.path.join(HERE, f"{name}.npz")
+    np.savez_compressed(path, meta=np.array(json.dumps(meta)), **arrays)
+    print(f"{name}: {sum(frames)} frames over {w.streams} streams, {meta['seconds']} s -> {path}", flush=True)
+    return path
+
+
 if __name__ == "__main__":
-    names = sys.argv[1:] or [n for n in WORKLOADS if not n.startswith("cfg1")]
+    names = sys.argv[1:] or ([n for n in WORKLOADS if not n.startswith("cfg1")] + list(MULTI_WORKLOADS))
     for n in names:
-        make(n)
+        make_multi(n) if n in MULTI_WORKLOADS else make(n)

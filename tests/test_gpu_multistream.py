@@ -1,0 +1,172 @@
+"""GPU parity of the multi-stream path: q3t_streams_start runs one
+prefill over every stream's prompt rows, q3t_streams_next_codes advances all listed
+streams with one pass over the weights per frame.  Streams are independent, so each must
+reproduce its own single-stream oracle rollout (tests/golden/<workload>.npz holds one per
+stream) and the single-stream engine path.
+"""
+import time
+
+import numpy as np
+import pytest
+
+from q3t import engine as E
+from q3t.workloads import MULTI_WORKLOADS
+
+from parity import LOGIT_TOL, check_codes, fixture_exists, load_fixture
+
+pytestmark = pytest.mark.gpu
+
+
+def stream_fixture(fx, j):
+    m = fx["meta"]
+    return {"codes": fx[f"codes_{j}"], "talker_margins": fx[f"talker_margins_{j}"],
+            "cp_margins": fx[f"cp_margins_{j}"], "talker_logits": fx[f"talker_logits_{j}"],
+            "meta": {"ended_by_eos": m["ended_by_eos"][j]}}
+
+
+def run_batch(models, name, use_graph=True, trace=False, chunk=None, kv_bf16=False):
+    w = MULTI_WORKLOADS[name]
+    model, d = models.get(w.spec, w.weight_seed)
+    inputs = w.inputs(model)
+    opts = [E.GenerateOptions(**kw) for kw in w.options_kwargs()]
+    print(f"[gpu] batch {name} streams={w.streams} graph={use_graph} chunk={chunk}", flush=True)
+    eng = E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=w.max_cache_steps, max_streams=w.streams,
+                                            use_graph=use_graph, kv_bf16=kv_bf16))
+    try:
+        eng.set_trace(trace)
+        t0 = time.perf_counter()
+        streams = eng.start_streams(inputs, opts, E.StreamOptions(text_lookahead_tokens=1 << 30))
+        t1 = time.perf_counter()
+        live, sizes, calls = list(streams), [[] for _ in streams], 0
+        while live:
+            chunks = eng.next_codes_chunks(live, chunk or w.chunk_frames)
+            calls += 1
+            for s, c in zip(live, chunks):
+                if c is not None:
+                    sizes[streams.index(s)].append((c.frames, c.total_frames))
+            live = [s for s, c in zip(live, chunks) if c is not None]
+        eng.synchronize()
+        t2 = time.perf_counter()
+        logits = [s.talker_logits() for s in streams] if trace else None
+        out = [s.finish_codes() for s in streams]
+    finally:
+        eng.close()
+    frames = sum(o.frames for o in out)
+    print(f"{name}: prefill {1e3 * (t1 - t0):.1f} ms, {frames} frames in {t2 - t1:.3f} s "
+          f"({frames / (t2 - t1):.1f} frames/s aggregate, {calls} calls)", flush=True)
+    return dict(codes=[o.codes for o in out], eos=[o.ended_by_eos for o in out], logits=logits, sizes=sizes,
+                frames_per_s=frames / (t2 - t1))
+
+
+def run_single(models, name, j, use_graph=True):
+    w = MULTI_WORKLOADS[name]
+    model, d = models.get(w.spec, w.weight_seed)
+    inp = w.inputs(model)[j]
+    opts = E.GenerateOptions(**w.options_kwargs()[j])
+    with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=w.max_cache_steps, use_graph=use_graph)) as eng:
+        return eng.generate_codes(inp, opts)
+
+
+def test_tiny_multistream_matches_oracle(models):
+    name = "tiny_multistream"
+    fx = load_fixture(name)
+    w = MULTI_WORKLOADS[name]
+    model, _ = models.get(w.spec, w.weight_seed)
+    assert model.checksum() == fx["meta"]["checksum"]
+    r = run_batch(models, name, trace=True)
+    for j in range(w.streams):
+        sf = stream_fixture(fx, j)
+        greedy = not w.options_kwargs()[j]["do_sample"]
+        same = check_codes(r["codes"][j], r["eos"][j], sf, allow_ties=greedy)
+        rows = min(len(sf["talker_logits"]), same + 1)
+        err = float(np.abs(r["logits"][j][:rows] - sf["talker_logits"][:rows].astype(np.float32)).max())
+        print(f"stream {j}: {same} frames identical, talker logit err {err:.2e}")
+        assert err <= LOGIT_TOL
+
+
+def test_multistream_equals_single_stream_path(models):
+    name = "tiny_multistream"
+    r = run_batch(models, name)
+    for j in range(MULTI_WORKLOADS[name].streams):
+        g = run_single(models, name, j)
+        np.testing.assert_array_equal(r["codes"][j], g.codes, err_msg=f"stream {j}")
+
+
+def test_multistream_graph_replay_equals_eager(models):
+    a = run_batch(models, "tiny_multistream", use_graph=True)
+    b = run_batch(models, "tiny_multistream", use_graph=False)
+    for j, (x, y) in enumerate(zip(a["codes"], b["codes"])):
+        np.testing.assert_array_equal(x, y, err_msg=f"stream {j}")
+
+
+def test_multistream_chunks_are_per_stream(models):
+    w = MULTI_WORKLOADS["tiny_multistream"]
+    r = run_batch(models, "tiny_multistream", chunk=4)
+    _, frames, _ = w.plan()
+    for j, sz in enumerate(r["sizes"]):
+        n = [f for f, _ in sz]
+        assert all(k == 4 for k in n[:-1]) and 0 < n[-1] <= 4, (j, n)
+        assert [t for _, t in sz] == list(np.cumsum(n))
+        assert sum(n) == len(r["codes"][j]) <= frames[j]
+
+
+def test_unlisted_stream_is_untouched(models):
+    """Stepping a subset must leave the other live streams exactly where they were."""
+    name = "tiny_multistream"
+    w = MULTI_WORKLOADS[name]
+    model, d = models.get(w.spec, w.weight_seed)
+    inputs = w.inputs(model)[:3]
+    opts = [E.GenerateOptions(**kw) for kw in w.options_kwargs()[:3]]
+    ref = [run_single(models, name, j).codes for j in range(3)]
+    with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=w.max_cache_steps, max_streams=4)) as eng:
+        s = eng.start_streams(inputs, opts, E.StreamOptions(text_lookahead_tokens=1 << 30))
+        for _ in range(3):
+            eng.next_codes_chunks([s[0], s[2]], 3)     # stream 1 waits
+        while s[1].next_codes_chunk(5) is not None:    # then runs alone on the single-stream path
+            pass
+        while any(c is not None for c in eng.next_codes_chunks([s[0], s[2]], 7)):
+            pass
+        got = [x.finish_codes().codes for x in s]
+    for j in range(3):
+        np.testing.assert_array_equal(got[j], ref[j], err_msg=f"stream {j}")
+
+
+def test_streams_start_reports_busy_and_capacity(models):
+    w = MULTI_WORKLOADS["tiny_multistream"]
+    model, d = models.get(w.spec, w.weight_seed)
+    inputs = w.inputs(model)
+    opts = [E.GenerateOptions(**kw) for kw in w.options_kwargs()]
+    lk = E.StreamOptions(text_lookahead_tokens=1 << 30)
+    with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=w.max_cache_steps, max_streams=2)) as eng:
+        with pytest.raises(E.BusyError):
+            eng.start_streams(inputs[:3], opts[:3], lk)
+        one = eng.start_stream(inputs[0], opts[0], lk)
+        with pytest.raises(E.BusyError):
+            eng.start_streams(inputs[1:3], opts[1:3], lk)
+        two = eng.start_streams(inputs[1:2], opts[1:2], lk)
+        one.close()
+        two[0].close()
+        big = E.GenerateOptions(**{**w.options_kwargs()[0], "max_frames": w.max_cache_steps})
+        with pytest.raises(E.CapacityError):
+            eng.start_streams(inputs[:1], [big], lk)
+
+
+@pytest.mark.skipif(not fixture_exists("cfg5_0.6b_multistream"), reason="config-5 fixture not generated")
+def test_cfg5_sixteen_streams_match_oracle(models):
+    name = "cfg5_0.6b_multistream"
+    fx = load_fixture(name)
+    w = MULTI_WORKLOADS[name]
+    model, _ = models.get(w.spec, w.weight_seed)
+    assert model.checksum() == fx["meta"]["checksum"]
+    r = run_batch(models, name, trace=True)
+    identical = 0
+    for j in range(w.streams):
+        sf = stream_fixture(fx, j)
+        same = check_codes(r["codes"][j], r["eos"][j], sf)
+        identical += same == len(sf["codes"])
+        rows = min(len(sf["talker_logits"]), same + 1)
+        err = float(np.abs(r["logits"][j][:rows] - sf["talker_logits"][:rows].astype(np.float32)).max())
+        print(f"stream {j}: P={fx['meta']['prefill_steps'][j]} {same}/{len(sf['codes'])} frames identical, "
+              f"talker logit err {err:.2e}")
+        assert err <= LOGIT_TOL
+    print(f"{identical}/{w.streams} streams bit-identical over every frame")
