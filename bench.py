@@ -12,6 +12,7 @@ Prints one JSON line.  Besides the contract fields it carries:
   rtf, frame_ms                  per-frame latency view of the same run
   frame_algorithmic_GBps         bytes one frame must move (weights + KV) / frame time
   roofline                       the dominant kernel, timed live with HIP events
+  multistream                    BASELINE config 5 (16 streams together) on the same model
   cpu_baseline                   the float32 CPU oracle on BASELINE config 1 (bounded sample)
 """
 from __future__ import annotations
@@ -103,6 +104,56 @@ def cpu_baseline(seconds_budget: float) -> dict:
                       f"{os.cpu_count()}"}
 
 
+def multistream(eng_cls, model_dir: str, name: str, steps: int, warmup: int, use_graph: bool) -> dict:
+    """BASELINE config 5 on the same model: every stream started together (one prefill over
+    all prompts), then chunks pulled for all live streams at once until each has ended.
+    A step is one such generation; value = frames of all streams / seconds."""
+    from q3t import engine as E
+    from q3t import synth
+    from q3t.workloads import MULTI_WORKLOADS
+
+    w = MULTI_WORKLOADS[name]
+    model = synth.SyntheticModel.build(w.spec, w.weight_seed)
+    inputs = w.inputs(model)
+    del model
+    opts = [E.GenerateOptions(**kw) for kw in w.options_kwargs()]
+    eng = eng_cls(model_dir, E.EngineOptions(max_cache_steps=w.max_cache_steps, max_streams=w.streams,
+                                             use_graph=use_graph))
+    lk = E.StreamOptions(text_lookahead_tokens=1 << 30)
+
+    def one():
+        t0 = time.perf_counter()
+        streams = eng.start_streams(inputs, opts, lk)
+        t1 = time.perf_counter()
+        live, n = list(streams), 0
+        while live:
+            chunks = eng.next_codes_chunks(live, w.chunk_frames)
+            n += sum(c.frames for c in chunks if c is not None)
+            live = [s for s, c in zip(live, chunks) if c is not None]
+        for s in streams:
+            s.close()
+        return n, t1 - t0
+
+    for _ in range(warmup):
+        one()
+    eng.synchronize()
+    t0 = time.perf_counter()
+    frames, prefill_s = 0, 0.0
+    for _ in range(steps):
+        n, p = one()
+        frames += n
+        prefill_s += p
+    eng.synchronize()
+    el = time.perf_counter() - t0
+    eng.close()
+    lengths, budgets, _ = w.plan()
+    return {"workload": name, "streams": w.streams, "value": round(frames / el, 2), "unit": "frames/s (all streams)",
+            "steps": steps, "warmup": warmup, "ms_per_step": round(1000 * el / steps, 3),
+            "frames_per_step": frames // steps, "prefill_rows": sum(9 + n for n in lengths),
+            "prefill_ms": round(1000 * prefill_s / steps, 3), "kv_capacity": w.max_cache_steps,
+            "rtf_per_stream": round(el / steps * w.streams / (frames / steps) / FRAME_SECONDS, 5)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -114,6 +165,9 @@ def main() -> int:
     ap.add_argument("--eager", action="store_true", help="launch every kernel from the host (no graph)")
     ap.add_argument("--kv-bf16", action="store_true")
     ap.add_argument("--frames", type=int, default=0, help="override the workload's frame count (profiling runs)")
+    ap.add_argument("--multistream", default="cfg5_0.6b_multistream",
+                    help="multi-stream workload reported beside the headline line ('' to skip)")
+    ap.add_argument("--multistream-only", action="store_true", help="run only the multi-stream workload")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -136,6 +190,12 @@ def main() -> int:
     model.write(tmp)
     spec = model.spec
     del model
+    if args.multistream_only:
+        print(json.dumps(multistream(E.HipTtsEngine, tmp, args.multistream, args.steps, args.warmup,
+                                     not args.eager)))
+        import shutil
+        shutil.rmtree(tmp, ignore_errors=True)
+        return 0
     eng = E.HipTtsEngine(tmp, E.EngineOptions(max_cache_steps=w.max_cache_steps, use_graph=not args.eager,
                                               kv_bf16=args.kv_bf16))
     opts = E.GenerateOptions(**w.options_kwargs())
@@ -169,6 +229,9 @@ def main() -> int:
     roofline = eng.dominant_kernel_roofline(HBM_PEAK_GBPS)
     roofline["traffic"] = measured_traffic(w.name, roofline["kernel"])
     eng.close()
+    multi = None
+    if args.multistream and w.spec == "0.6b" and w.weight_seed == 0:
+        multi = multistream(E.HipTtsEngine, tmp, args.multistream, max(1, min(args.steps, 2)), 1, not args.eager)
     import shutil
     shutil.rmtree(tmp, ignore_errors=True)
 
@@ -195,6 +258,8 @@ def main() -> int:
         "frame_algorithmic_bytes": int(fb),
         "roofline": roofline,
     }
+    if multi is not None:
+        out["multistream"] = multi
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out))

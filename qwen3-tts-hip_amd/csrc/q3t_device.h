@@ -97,6 +97,7 @@ struct AttnArgs {
   int32_t ld_qkv, ld_out;
   int64_t kv_row, part_row;
   const int32_t *row_on;
+  int32_t out_t16;      // direct output in T16 (rows <= 16) instead of out + r * ld_out
 };
 
 // Merge of split-attention partials into attention outputs, one workgroup per stream row.
@@ -107,7 +108,17 @@ struct AttnMergeArgs {
   int64_t part_row;
   const SlotState *st;  // [rows]
   const int32_t *row_on;
+  int32_t out_t16;      // output in T16 instead of out + r * ld_out
 };
+
+// Tiled 16-row activation layout ("T16") used between the skinny GEMMs of the batched frame:
+// element (m, k) of a [16][K] block sits at t16_index(m, k).  Each 32-wide k step is one
+// contiguous 2 KiB block in the order the matrix cores take their A operand (lane
+// m + 16 * ((k % 32) / 8) holds k % 8 = 0..7), so a wave loads it with unit-stride 32-byte
+// reads instead of touching 16 rows per instruction.
+__host__ __device__ inline size_t t16_index(int m, int k) {
+  return ((size_t)(k >> 5) * 64 + ((k >> 3) & 3) * 16 + m) * 8 + (k & 7);
+}
 
 // Y[M][N] = X[M][K] . W[N][K]^T with the GEMV epilogues (matrix-core path for many rows).
 struct GemmArgs {
@@ -121,6 +132,9 @@ struct GemmArgs {
   int32_t M, N, K, ldx, ldy, ldr;
   float eps;               // skinny GEMM with a fused RMSNorm
   const int32_t *row_on;   // skinny GEMM: row m is stored only where row_on[m] (null: all rows)
+  // skinny GEMM layouts: X / Y / res in T16 (ld ignored) instead of row-major, and W packed
+  // as [N/16][K/32][64 lanes][8] (each k step of a 16-column tile is 1 KiB contiguous).
+  int32_t x_t16, y_t16, r_t16, w_packed;
 };
 
 // Prompt prefill attention over rows at positions pos0 .. pos0 + P - 1.
@@ -153,6 +167,7 @@ struct SelectTalkerArgs {
   // are skipped (row_on null: one stream).
   int64_t codes_row, trace_row;
   const int32_t *row_on;
+  int32_t x_t16;            // x is a T16 block (row r = stream row r) instead of x + r * H
 };
 
 struct SelectCpArgs {

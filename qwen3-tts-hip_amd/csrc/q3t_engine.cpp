@@ -216,12 +216,15 @@ T *dev_alloc(size_t n, int64_t &tally) {
 struct LayerW {
   const uint16_t *qkv, *o, *gu, *down;
   const float *g_in, *g_post, *gq, *gk;
+  // The same matrices in the skinny GEMM's packed layout (multi-stream engines only).
+  const uint16_t *qkv_p = nullptr, *o_p = nullptr, *gu_p = nullptr, *down_p = nullptr;
 };
 
 struct StackW {
   Dims d;
   std::vector<LayerW> layers;
   uint16_t *mats = nullptr;
+  uint16_t *mats_p = nullptr;  // packed copy, same offsets
   float *gains = nullptr;
   float2 *rope = nullptr;  // [cap][head_dim / 2]
   int cap = 0;
@@ -356,8 +359,14 @@ struct Engine {
   uint16_t *cp_emb = nullptr;    // [groups-1][Vc][Ht]
   uint16_t *proj_w = nullptr;    // [Hc][Ht]
   float *proj_b = nullptr;
+  // Packed copies for the batched frame's skinny GEMMs (multi-stream engines only).
+  uint16_t *codec_head_p = nullptr, *lm_heads_p = nullptr, *proj_w_p = nullptr;
+  // Batched-frame activations in T16 (16 stream rows): residual streams, attention output,
+  // MLP activation, projected CodePredictor inputs.
+  float *bx_t = nullptr, *bx_c = nullptr, *battn = nullptr, *bact = nullptr, *bcp_in = nullptr;
   std::vector<Slot> slots;
   Pools pools;
+  bool rows_ok = false;  // the batched frame's fused-norm GEMMs support both hidden sizes
   int64_t device_bytes = 0;
 
   // nt: stream the weights with non-temporal loads (Talker weights are read once per frame).
@@ -498,31 +507,44 @@ struct Engine {
 
   // ----- stream rows: the batched frame over slots 0..rows-1, masked by pools.row_on -----
 
-  // Skinny matrix-core GEMM over the stream rows (row m of X, res, Y at m * ld).
-  void rgemm(int epi, bool norm, const uint16_t *W, const float *X, int ldx, const float *gamma, float eps,
-             const float *res, int ldr, const float *bias, float *Y, int ldy, int N, int K, int rows, hipStream_t s) {
+  // An activation operand of the batched frame: row-major with leading dimension ld, or a
+  // T16 block (ld < 0).
+  struct Act {
+    const float *p;
+    int ld;
+  };
+  static Act t16(const float *p) { return Act{p, -1}; }
+
+  // Skinny matrix-core GEMM over the stream rows, packed weights Wp.
+  void rgemm(int epi, bool norm, const uint16_t *Wp, Act X, const float *gamma, float eps, Act res,
+             const float *bias, Act Y, int N, int K, int rows, hipStream_t s) {
     GemmArgs g{};
-    g.X = X; g.ldx = ldx; g.gamma = gamma; g.eps = eps; g.W = W; g.res = res; g.ldr = ldr; g.bias = bias;
-    g.Y = Y; g.ldy = ldy; g.M = rows; g.N = N; g.K = K; g.row_on = pools.row_on;
+    g.X = X.p; g.ldx = X.ld < 0 ? K : X.ld; g.x_t16 = X.ld < 0;
+    g.gamma = gamma; g.eps = eps; g.W = Wp; g.w_packed = 1;
+    g.res = res.p; g.ldr = res.ld < 0 ? N : res.ld; g.r_t16 = res.ld < 0;
+    g.bias = bias;
+    g.Y = const_cast<float *>(Y.p); g.ldy = Y.ld < 0 ? N : Y.ld; g.y_t16 = Y.ld < 0;
+    g.M = rows; g.N = N; g.K = K; g.row_on = pools.row_on;
     hip_check(launch_gemm_skinny(epi, norm, g, s), "launch_gemm_skinny");
   }
 
-  // One decoder-stack step of every stream row (each at its own position and cache).
-  void rows_stack_step(const StackW &w, char *kc, char *vc, size_t kv_row, const float *in, int ldin, float *x,
-                       int rows, int pos_mode, int pos_const, int skip, hipStream_t s) {
+  // One decoder-stack step of every stream row (each at its own position and cache).  The
+  // residual stream x is a T16 block; `in` feeds layer 0.
+  void rows_stack_step(const StackW &w, char *kc, char *vc, size_t kv_row, Act in, float *x, int rows, int pos_mode,
+                       int pos_const, int skip, hipStream_t s) {
     const Dims &d = w.d;
     Pools &p = pools;
     const int H = d.hidden;
     const size_t cache_layer = (size_t)d.kv_heads * w.cap * d.head_dim * (kv_bf16 ? 2 : 4);
     const int partial = attn_chunks(w.cap) > 1 ? 1 : 0;
+    const Act none{nullptr, 0};
     for (int l = 0; l < d.layers; ++l) {
       const LayerW &L = w.layers[l];
-      const float *src = l == 0 ? in : x;
-      const int lds = l == 0 ? ldin : H;
-      rgemm(EPI_STORE, true, L.qkv, src, lds, L.g_in, d.eps, nullptr, 0, nullptr, p.qkv, p.s_qkv, d.qkv_rows(), H,
+      const Act src = l == 0 ? in : t16(x);
+      rgemm(EPI_STORE, true, L.qkv_p, src, L.g_in, d.eps, none, nullptr, Act{p.qkv, p.s_qkv}, d.qkv_rows(), H,
             rows, s);
       AttnArgs aa{p.qkv,    L.gq,    L.gk,     w.rope,  kc + l * cache_layer, vc + l * cache_layer,
-                  p.attn,   d.q_heads, d.kv_heads, w.cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
+                  battn,    d.q_heads, d.kv_heads, w.cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
                   pos_mode, pos_const, skip,    kv_bf16, p.st,   p.attn_part, p.part_chunks,
                   attn_chunk_len(w.cap), partial};
       aa.ld_qkv = p.s_qkv;
@@ -530,29 +552,29 @@ struct Engine {
       aa.kv_row = (int64_t)kv_row;
       aa.part_row = p.part_row;
       aa.row_on = p.row_on;
+      aa.out_t16 = 1;
       hip_check(launch_attn_decode(aa, d.head_dim, s, nullptr, rows), "launch_attn_decode(rows)");
       if (partial) {
-        AttnMergeArgs m{p.attn_part, p.attn, d.q_heads, d.kv_heads, p.part_chunks, attn_chunk_len(w.cap),
-                        pos_mode,    pos_const, skip,   p.s_attn,   p.part_row,    p.st,
-                        p.row_on};
+        AttnMergeArgs m{p.attn_part, battn, d.q_heads, d.kv_heads, p.part_chunks, attn_chunk_len(w.cap),
+                        pos_mode,    pos_const, skip, p.s_attn,  p.part_row,    p.st,
+                        p.row_on,    1};
         hip_check(launch_attn_merge(m, rows, s), "launch_attn_merge");
       }
-      rgemm(EPI_RESIDUAL, false, L.o, p.attn, p.s_attn, nullptr, 0.f, src, lds, nullptr, x, H, H, d.q_out(), rows,
-            s);
-      rgemm(EPI_SWIGLU, true, L.gu, x, H, L.g_post, d.eps, nullptr, 0, nullptr, p.act, p.s_act, d.intermediate, H,
+      rgemm(EPI_RESIDUAL, false, L.o_p, t16(battn), nullptr, 0.f, src, nullptr, t16(x), H, d.q_out(), rows, s);
+      rgemm(EPI_SWIGLU, true, L.gu_p, t16(x), L.g_post, d.eps, none, nullptr, t16(bact), d.intermediate, H, rows, s);
+      rgemm(EPI_RESIDUAL, false, L.down_p, t16(bact), nullptr, 0.f, t16(x), nullptr, t16(x), H, d.intermediate,
             rows, s);
-      rgemm(EPI_RESIDUAL, false, L.down, p.act, p.s_act, nullptr, 0.f, x, H, nullptr, x, H, H, d.intermediate, rows,
-            s);
     }
   }
 
-  void select_talker_rows(int rows, int after_frame, hipStream_t s) {
+  void select_talker_rows(int rows, int after_frame, Act x, hipStream_t s) {
     Pools &p = pools;
-    SelectTalkerArgs a{p.logits_t, p.x_t, t_norm, codec_emb, p.cp_prefix, p.codes, trace ? p.trace_t : nullptr,
+    SelectTalkerArgs a{p.logits_t, x.p, t_norm, codec_emb, p.cp_prefix, p.codes, trace ? p.trace_t : nullptr,
                        p.st, p.prm, td.vocab, td.hidden, groups, td.eps, after_frame};
     a.codes_row = p.codes_row;
     a.trace_row = p.trace_t_row;
     a.row_on = p.row_on;
+    a.x_t16 = x.ld < 0;
     hip_check(launch_select_talker(a, s, rows), "launch_select_talker(rows)");
   }
 
@@ -562,33 +584,28 @@ struct Engine {
   void enqueue_rows_frame(int rows, hipStream_t s) {
     Pools &p = pools;
     const int Ht = talker_hidden, Hc = cd.hidden, Vc = cd.vocab, nac = groups - 1;
-    const float *in0 = p.cp_prefix, *in1 = p.cp_prefix + Ht;
-    int ldin = 2 * Ht;
+    const Act none{nullptr, 0};
+    const size_t hc16 = (size_t)16 * Hc;
+    Act in0{p.cp_prefix, 2 * Ht}, in1{p.cp_prefix + Ht, 2 * Ht};
     if (has_proj) {
-      rgemm(EPI_BIAS, false, proj_w, p.cp_prefix, 2 * Ht, nullptr, 0.f, nullptr, 0, proj_b, p.cp_in, 3 * Hc, Hc, Ht,
-            rows, s);
-      rgemm(EPI_BIAS, false, proj_w, p.cp_prefix + Ht, 2 * Ht, nullptr, 0.f, nullptr, 0, proj_b, p.cp_in + Hc,
-            3 * Hc, Hc, Ht, rows, s);
-      in0 = p.cp_in;
-      in1 = p.cp_in + Hc;
-      ldin = 3 * Hc;
+      rgemm(EPI_BIAS, false, proj_w_p, in0, nullptr, 0.f, none, proj_b, t16(bcp_in), Hc, Ht, rows, s);
+      rgemm(EPI_BIAS, false, proj_w_p, in1, nullptr, 0.f, none, proj_b, t16(bcp_in + hc16), Hc, Ht, rows, s);
+      in0 = t16(bcp_in);
+      in1 = t16(bcp_in + hc16);
     }
-    rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in0, ldin, p.x_c, rows, POS_CONST, 0, SKIP_DONE, s);
-    rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in1, ldin, p.x_c, rows, POS_CONST, 1, SKIP_DONE, s);
+    rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in0, bx_c, rows, POS_CONST, 0, SKIP_DONE, s);
+    rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in1, bx_c, rows, POS_CONST, 1, SKIP_DONE, s);
     for (int g = 0; g < nac; ++g) {
       if (g > 0) {
-        const float *in = p.cur;
-        int ld = Ht;
+        Act in{p.cur, Ht};
         if (has_proj) {
-          rgemm(EPI_BIAS, false, proj_w, p.cur, Ht, nullptr, 0.f, nullptr, 0, proj_b, p.cp_in + 2 * Hc, 3 * Hc, Hc,
-                Ht, rows, s);
-          in = p.cp_in + 2 * Hc;
-          ld = 3 * Hc;
+          rgemm(EPI_BIAS, false, proj_w_p, in, nullptr, 0.f, none, proj_b, t16(bcp_in + 2 * hc16), Hc, Ht, rows, s);
+          in = t16(bcp_in + 2 * hc16);
         }
-        rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in, ld, p.x_c, rows, POS_CONST, g + 1, SKIP_DONE, s);
+        rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in, bx_c, rows, POS_CONST, g + 1, SKIP_DONE, s);
       }
-      rgemm(EPI_STORE, true, lm_heads + (size_t)g * Vc * Hc, p.x_c, Hc, c_norm, cd.eps, nullptr, 0, nullptr,
-            p.logits_c, Vc, Vc, Hc, rows, s);
+      rgemm(EPI_STORE, true, lm_heads_p + (size_t)g * Vc * Hc, t16(bx_c), c_norm, cd.eps, none, nullptr,
+            Act{p.logits_c, Vc}, Vc, Hc, rows, s);
       SelectCpArgs a{p.logits_c, cp_emb + (size_t)g * Vc * Ht, p.cur, p.emb_sum, p.codes,
                      trace ? p.trace_c : nullptr, p.t_in, codec_emb, p.trailing, p.st, p.prm, Vc, Ht, groups, g};
       a.codes_row = p.codes_row;
@@ -597,10 +614,11 @@ struct Engine {
       a.row_on = p.row_on;
       hip_check(launch_select_cp(a, s, rows), "launch_select_cp(rows)");
     }
-    rows_stack_step(talker, p.t_k, p.t_v, p.t_kv_row, p.t_in, Ht, p.x_t, rows, POS_TALKER_FRAME, 0, SKIP_TALKER, s);
-    rgemm(EPI_STORE, true, codec_head, p.x_t, Ht, t_norm, td.eps, nullptr, 0, nullptr, p.logits_t, td.vocab,
+    rows_stack_step(talker, p.t_k, p.t_v, p.t_kv_row, Act{p.t_in, Ht}, bx_t, rows, POS_TALKER_FRAME, 0,
+                    SKIP_TALKER, s);
+    rgemm(EPI_STORE, true, codec_head_p, t16(bx_t), t_norm, td.eps, none, nullptr, Act{p.logits_t, td.vocab},
           td.vocab, Ht, rows, s);
-    select_talker_rows(rows, 1, s);
+    select_talker_rows(rows, 1, t16(bx_t), s);
     hip_check(launch_frame_end(p.st, p.prm, 1, s, rows, p.row_on), "launch_frame_end(rows)");
   }
 };
@@ -743,6 +761,56 @@ void free_pools(Engine &e) {
   if (p.h_states) (void)hipHostFree(p.h_states);
   if (p.h_row_on) (void)hipHostFree(p.h_row_on);
   p = Pools();
+}
+
+// Packed weight copies and T16 activations for the batched frame (engines with more than
+// one stream slot).  Packing runs on the device from the row-major copies.
+void alloc_rows(Engine &e) {
+  int64_t &t = e.device_bytes;
+  const Dims &td = e.td, &cd = e.cd;
+  auto pack_stack = [&](StackW &w) {
+    const Dims &d = w.d;
+    const size_t per_layer = (size_t)d.qkv_rows() * d.hidden + (size_t)d.hidden * d.q_out() +
+                             (size_t)2 * d.intermediate * d.hidden + (size_t)d.hidden * d.intermediate;
+    w.mats_p = dev_alloc<uint16_t>(per_layer * d.layers, t);
+    for (LayerW &L : w.layers) {
+      auto at = [&](const uint16_t *m) { return w.mats_p + (m - w.mats); };
+      L.qkv_p = at(L.qkv);
+      L.o_p = at(L.o);
+      L.gu_p = at(L.gu);
+      L.down_p = at(L.down);
+      hip_check(launch_pack_weights(L.qkv, const_cast<uint16_t *>(L.qkv_p), d.qkv_rows(), d.hidden, nullptr), "pack");
+      hip_check(launch_pack_weights(L.o, const_cast<uint16_t *>(L.o_p), d.hidden, d.q_out(), nullptr), "pack");
+      hip_check(launch_pack_weights(L.gu, const_cast<uint16_t *>(L.gu_p), 2 * d.intermediate, d.hidden, nullptr),
+                "pack");
+      hip_check(launch_pack_weights(L.down, const_cast<uint16_t *>(L.down_p), d.hidden, d.intermediate, nullptr),
+                "pack");
+    }
+  };
+  pack_stack(e.talker);
+  pack_stack(e.cp);
+  const int Ht = e.talker_hidden, Hc = cd.hidden, Vt = td.vocab, Vc = cd.vocab, nac = e.groups - 1;
+  e.codec_head_p = dev_alloc<uint16_t>((size_t)Vt * Ht, t);
+  hip_check(launch_pack_weights(e.codec_head, e.codec_head_p, Vt, Ht, nullptr), "pack");
+  e.lm_heads_p = dev_alloc<uint16_t>((size_t)nac * Vc * Hc, t);
+  for (int g = 0; g < nac; ++g)
+    hip_check(launch_pack_weights(e.lm_heads + (size_t)g * Vc * Hc, e.lm_heads_p + (size_t)g * Vc * Hc, Vc, Hc,
+                                  nullptr),
+              "pack");
+  if (e.has_proj) {
+    e.proj_w_p = dev_alloc<uint16_t>((size_t)Hc * Ht, t);
+    hip_check(launch_pack_weights(e.proj_w, e.proj_w_p, Hc, Ht, nullptr), "pack");
+  }
+  auto zeroed = [&](size_t n) {
+    float *q = dev_alloc<float>(n, t);
+    HIPC(hipMemset(q, 0, n * 4));
+    return q;
+  };
+  e.bx_t = zeroed((size_t)16 * Ht);
+  e.bx_c = zeroed((size_t)16 * Hc);
+  e.battn = zeroed((size_t)16 * std::max(td.q_out(), cd.q_out()));
+  e.bact = zeroed((size_t)16 * std::max(td.intermediate, cd.intermediate));
+  e.bcp_in = zeroed((size_t)3 * 16 * Hc);
 }
 
 // Logit trace buffers for every slot, allocated the first time a traced stream starts.
@@ -912,6 +980,7 @@ int q3t_engine_create(const q3t_engine_options *opts, q3t_engine **out) {
       fail(Q3T_ERR_INVALID, "max_cache_steps %d exceeds the attention kernel limit %d", e->cap,
            attn_max_cache_steps(td.q_heads, td.kv_heads));
     if (e->codec_eos < 0 || e->codec_eos >= td.vocab) fail(Q3T_ERR_INVALID, "codec_eos out of range");
+    e->rows_ok = gemm_skinny_supports(kMaxRows, td.hidden, true) && gemm_skinny_supports(kMaxRows, cd.hidden, true);
 
     SafeTensors st(dir + "/model.safetensors");
     HIPC(hipSetDevice(e->device));
@@ -950,6 +1019,7 @@ int q3t_engine_create(const q3t_engine_options *opts, q3t_engine **out) {
     }
     try {
       alloc_pools(*e, nslots);
+      if (nslots > 1 && e->rows_ok) alloc_rows(*e);
     } catch (...) {
       free_pools(*e);
       throw;
@@ -965,9 +1035,11 @@ int q3t_engine_destroy(q3t_engine *e) {
     (void)hipSetDevice(e->device);
     (void)hipDeviceSynchronize();
     q3t::free_pools(*e);
-    void *ptrs[] = {e->talker.mats, e->talker.gains, e->talker.rope, e->cp.mats,    e->cp.gains,
-                    e->cp.rope,     e->codec_head,   e->codec_emb,   e->t_norm,     e->c_norm,
-                    e->lm_heads,    e->cp_emb,       e->proj_w,      e->proj_b};
+    void *ptrs[] = {e->talker.mats, e->talker.gains, e->talker.rope, e->cp.mats,     e->cp.gains,
+                    e->cp.rope,     e->codec_head,   e->codec_emb,   e->t_norm,      e->c_norm,
+                    e->lm_heads,    e->cp_emb,       e->proj_w,      e->proj_b,      e->talker.mats_p,
+                    e->cp.mats_p,   e->codec_head_p, e->lm_heads_p,  e->proj_w_p,    e->bx_t,
+                    e->bx_c,        e->battn,        e->bact,        e->bcp_in};
     for (void *p : ptrs)
       if (p) (void)hipFree(p);
     delete e;
@@ -1108,6 +1180,8 @@ int q3t_streams_start(q3t_engine *e, int32_t n, const q3t_stream_input *inputs, 
     using namespace q3t;
     if (!e || !inputs || !opts || !out) fail(Q3T_ERR_INVALID, "null argument");
     if (n <= 0) fail(Q3T_ERR_INVALID, "stream count must be positive");
+    if (!e->rows_ok) fail(Q3T_ERR_INVALID, "multi-stream batching needs hidden sizes of at most 2048");
+    if (!e->bx_t) fail(Q3T_ERR_INVALID, "multi-stream calls need an engine created with max_streams > 1");
     for (int j = 0; j < n; ++j) out[j] = nullptr;
     for (int j = 0; j < n; ++j) validate_input(*e, inputs[j], &opts[j]);
     std::vector<int> slots;
@@ -1129,9 +1203,10 @@ int q3t_streams_start(q3t_engine *e, int32_t n, const q3t_stream_input *inputs, 
     for (int j = 0; j < n; ++j) stage_stream(*e, slots[j], segs[j].row0, inputs[j], &opts[j], p.stream);
     e->prefill_segments(segs, M, p.stream);
     const int rows = set_rows(*e, slots, p.stream);
-    e->rgemm(EPI_STORE, true, e->codec_head, p.x_t, e->talker_hidden, e->t_norm, e->td.eps, nullptr, 0, nullptr,
-             p.logits_t, e->td.vocab, e->td.vocab, e->talker_hidden, rows, p.stream);
-    e->select_talker_rows(rows, 0, p.stream);
+    e->rgemm(EPI_STORE, true, e->codec_head_p, Engine::Act{p.x_t, e->talker_hidden}, e->t_norm, e->td.eps,
+             Engine::Act{nullptr, 0}, nullptr, Engine::Act{p.logits_t, e->td.vocab}, e->td.vocab, e->talker_hidden,
+             rows, p.stream);
+    e->select_talker_rows(rows, 0, Engine::Act{p.x_t, e->talker_hidden}, p.stream);
     hip_check(launch_frame_end(p.st, p.prm, 0, p.stream, rows, p.row_on), "launch_frame_end(rows)");
     HIPC(hipMemcpyAsync(p.h_states, p.st, sizeof(SlotState) * rows, hipMemcpyDeviceToHost, p.stream));
     HIPC(hipStreamSynchronize(p.stream));
@@ -1146,6 +1221,8 @@ int q3t_streams_next_codes(q3t_engine *e, q3t_stream *const *streams, int32_t n,
     if (!e || !streams || !info || (n > 0 && !codes)) fail(Q3T_ERR_INVALID, "null argument");
     if (n <= 0) fail(Q3T_ERR_INVALID, "stream count must be positive");
     if (max_chunk <= 0) fail(Q3T_ERR_INVALID, "max_chunk_frames must be non-zero");
+    if (!e->rows_ok) fail(Q3T_ERR_INVALID, "multi-stream batching needs hidden sizes of at most 2048");
+    if (!e->bx_t) fail(Q3T_ERR_INVALID, "multi-stream calls need an engine created with max_streams > 1");
     std::vector<int> seen(e->slots.size(), 0), on, want(n, 0);
     int nrun = 0;
     for (int j = 0; j < n; ++j) {
@@ -1414,7 +1491,7 @@ int q3t_debug_gemm(q3t_engine *e, int32_t epi, const float *X, int32_t M, int32_
       g.ldr = N;
       if (res) g.res = (const float *)up(res, (size_t)M * N * 4);
       if (bias) g.bias = (const float *)up(bias, (size_t)N * 4);
-      if (gemm_skinny_supports(M, K)) {  // the batched-decode kernel (fused RMSNorm)
+      if (gemm_skinny_supports(M, K, gamma != nullptr)) {  // the batched-decode kernel (fused RMSNorm)
         if (gamma) g.gamma = (const float *)up(gamma, (size_t)K * 4);
         g.eps = eps;
         hip_check(launch_gemm_skinny(epi, gamma != nullptr, g, nullptr), "launch_gemm_skinny");

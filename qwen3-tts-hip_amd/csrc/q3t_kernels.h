@@ -37,9 +37,13 @@ int attn_chunks(int cap);
 // for many rows: prompt prefill and batched decode.  Requires K % 32 == 0.
 hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t stream);
 // The same product for M <= 16 rows (batched decode); norm = fused RMSNorm of the rows with
-// gain gamma (row_scale must be null).  Requires K = 512 * c, c in {1, 2, 3, 4, 6, 8, 12}.
-bool gemm_skinny_supports(int M, int K);
+// gain gamma (row_scale must be null).  Requires K = 512 * c, c in {1, 2, 3, 4, 6, 8, 12}
+// (K <= 2048 with norm).
+bool gemm_skinny_supports(int M, int K, bool norm);
 hipError_t launch_gemm_skinny(int epi, bool norm, const GemmArgs &a, hipStream_t stream);
+// dst = src [rows][K] bf16 in the skinny GEMM's packed layout (GemmArgs::w_packed).
+// Requires rows % 16 == 0 and K % 32 == 0.
+hipError_t launch_pack_weights(const uint16_t *src, uint16_t *dst, int rows, int K, hipStream_t stream);
 // inv_rms[m] = 1 / sqrt(mean(X[m]^2) + eps).
 hipError_t launch_row_rms(const float *X, int ldx, int M, int K, float eps, float *inv_rms, hipStream_t stream);
 

@@ -27,15 +27,40 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return (uint16_t)(u >> 16);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+// Cross-lane reductions on DPP (data-parallel primitives: VALU lane permutes, no LDS round
+// trip).  Each step adds a permuted copy: quad_perm [1,0,3,2] and [2,3,0,1] (quads),
+// row_half_mirror and row_mirror (rows of 16), then row_bcast:15 / row_bcast:31 fold the
+// four rows into lane 63.  The order is fixed, so results are deterministic.
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ float dpp_f(float v, float fill) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, fill), __builtin_bit_cast(int, v),
+                                                               CTRL, ROWS, 0xf, false));
+}
+
+// Sum over each row of 16 lanes, in every lane of the row.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<0xB1>(v, 0.f);
+  v += dpp_f<0x4E>(v, 0.f);
+  v += dpp_f<0x141>(v, 0.f);
+  v += dpp_f<0x140>(v, 0.f);
   return v;
 }
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  v += dpp_f<0x142, 0xa>(v, 0.f);
+  v += dpp_f<0x143, 0xc>(v, 0.f);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
-  return v;
+  v = fmaxf(v, dpp_f<0xB1>(v, v));
+  v = fmaxf(v, dpp_f<0x4E>(v, v));
+  v = fmaxf(v, dpp_f<0x141>(v, v));
+  v = fmaxf(v, dpp_f<0x140>(v, v));
+  v = fmaxf(v, dpp_f<0x142, 0xa>(v, v));
+  v = fmaxf(v, dpp_f<0x143, 0xc>(v, v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 __device__ __forceinline__ bool skip_work(const SlotState *st, int mode) {
@@ -110,6 +135,11 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
       gv[c][4] = g1.x; gv[c][5] = g1.y; gv[c][6] = g1.z; gv[c][7] = g1.w;
     }
   }
+  // The epilogue operand of this lane's output row (lane r stores row unit0 + r), loaded
+  // before the weights so that the store waits on nothing.
+  float eadd = 0.f;
+  if constexpr (EPI == EPI_RESIDUAL) eadd = a.res[min(unit0 + min(lane, RW - 1), a.N - 1)];
+  if constexpr (EPI == EPI_BIAS) eadd = a.bias[min(unit0 + min(lane, RW - 1), a.N - 1)];
   // Rows past the end (a partial last workgroup) load the last row instead of branching;
   // their results are never stored.
   uint4 w[NR][KC];
@@ -161,9 +191,9 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
       if constexpr (EPI == EPI_STORE) {
         a.out[unit] = acc[r];
       } else if constexpr (EPI == EPI_RESIDUAL) {
-        a.out[unit] = a.res[unit] + acc[r];
+        a.out[unit] = eadd + acc[r];
       } else if constexpr (EPI == EPI_BIAS) {
-        a.out[unit] = acc[r] + a.bias[unit];
+        a.out[unit] = acc[r] + eadd;
       } else {
         const float g = acc[2 * r], u = acc[2 * r + 1];
         a.out[unit] = g / (1.0f + expf(-g)) * u;
@@ -335,10 +365,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
       float sacc = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) sacc = fmaf(qs[g * D + sub * 8 + j], kv[j], sacc);
-      sacc += __shfl_xor(sacc, 8, 16);
-      sacc += __shfl_xor(sacc, 4, 16);
-      sacc += __shfl_xor(sacc, 2, 16);
-      sacc += __shfl_xor(sacc, 1, 16);
+      sacc = row16_sum(sacc);
       if (sub == 0 && t < t1) sc[g][t - t0] = sacc * a.scale;
     }
   }
@@ -393,7 +420,8 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   const int g_o = o / D, d_o = o % D;
   const float v_o = ((red[0][g_o][d_o] + red[1][g_o][d_o]) + red[2][g_o][d_o]) + red[3][g_o][d_o];
   if (!a.partial_out) {
-    a.out[(size_t)row * a.ld_out + (h * G + g_o) * D + d_o] = v_o / stat[g_o][1];
+    const int k = (h * G + g_o) * D + d_o;
+    a.out[a.out_t16 ? t16_index(row, k) : (size_t)row * a.ld_out + k] = v_o / stat[g_o][1];
     return;
   }
   float *my = a.part + row * a.part_row + (((size_t)h * a.part_chunks + c) * G + g_o) * (D + 2);
@@ -443,7 +471,6 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnMergeArgs a) {
   const int nchunks = min((pos + a.chunk) / a.chunk, a.part_chunks);
   const int G = a.q_heads / a.kv_heads;
   const float *part = a.part + row * a.part_row;
-  float *out = a.out + (size_t)row * a.ld_out;
   for (int base = threadIdx.x * 8; base < a.q_heads * D; base += 256 * 8) {
     const int hq = base / D, d0 = base % D;
     const int h = hq / G, g = hq % G;
@@ -460,7 +487,8 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnMergeArgs a) {
       for (int j = 0; j < 8; ++j) num[j] = fmaf(w, pc[2 + d0 + j], num[j]);
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) out[base + j] = num[j] / den;
+    for (int j = 0; j < 8; ++j)
+      a.out[a.out_t16 ? t16_index(row, base + j) : (size_t)row * a.ld_out + base + j] = num[j] / den;
   }
 }
 
@@ -478,18 +506,25 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnMergeArgs a) {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
 // x = hi + mid + lo, each a bf16: 24 significant bits, so every product with a bf16 weight
 // is exact and the GEMM matches an fp32 GEMV up to the order of the fp32 additions.
+// hi = bf16(x) (round to nearest even, v_cvt_pk_bf16_f32 on two lanes at a time); x - hi is
+// exact in fp32 and holds the remaining 16 bits, split the same way into mid and lo.
 __device__ __forceinline__ void split_bf16x8(const float *x, bf16x8_t &hi, bf16x8_t &mid, bf16x8_t &lo) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const uint16_t h = f32_to_bf16(x[e]);
-    const float r1 = x[e] - bf16_to_f32(h);
-    const uint16_t m = f32_to_bf16(r1);
-    const uint16_t l = f32_to_bf16(r1 - bf16_to_f32(m));
-    hi[e] = __builtin_bit_cast(__bf16, h);
-    mid[e] = __builtin_bit_cast(__bf16, m);
-    lo[e] = __builtin_bit_cast(__bf16, l);
+  for (int e = 0; e < 8; e += 2) {
+    const f32x2_t v = {x[e], x[e + 1]};
+    const bf16x2_t h = __builtin_convertvector(v, bf16x2_t);
+    const f32x2_t r1 = v - __builtin_convertvector(h, f32x2_t);
+    const bf16x2_t m = __builtin_convertvector(r1, bf16x2_t);
+    const f32x2_t r2 = r1 - __builtin_convertvector(m, f32x2_t);
+    const bf16x2_t l = __builtin_convertvector(r2, bf16x2_t);
+    hi[e] = h[0]; hi[e + 1] = h[1];
+    mid[e] = m[0]; mid[e + 1] = m[1];
+    lo[e] = l[0]; lo[e + 1] = l[1];
   }
 }
 
@@ -604,6 +639,8 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
 // NORM the rows' RMSNorm is computed from the same loads (sum of squares reduced across the
 // workgroup) and applied before the split.
 // ---------------------------------------------------------------------------------------
+__device__ const int32_t kAllRowsOn[16] = {1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1};
+
 template <int EPI, bool NORM, int KS>  // KS = 32-wide k steps per wave = K / (16 * 32)
 __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
   constexpr int T = (EPI == EPI_SWIGLU) ? 2 : 1;
@@ -618,91 +655,116 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
   __shared__ float ssq[16][16];
   __shared__ float inv_rms[16];
 
-  float xa[KS][8];
-  uint4 wb[KS][T];
-#pragma unroll
-  for (int st = 0; st < KS; ++st) {
-    const int k = kbase + st * 32 + 8 * kb;
-    const float4 *px = reinterpret_cast<const float4 *>(a.X + (size_t)arow * a.ldx + k);
-    const float4 p0 = px[0], p1 = px[1];
-    xa[st][0] = p0.x; xa[st][1] = p0.y; xa[st][2] = p0.z; xa[st][3] = p0.w;
-    xa[st][4] = p1.x; xa[st][5] = p1.y; xa[st][6] = p1.z; xa[st][7] = p1.w;
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-      const int col = min(n0 + li, a.N - 1) + t * a.N;
-      wb[st][t] = *reinterpret_cast<const uint4 *>(a.W + (size_t)col * a.K + k);
-    }
-  }
-  __builtin_amdgcn_sched_barrier(0);
+  // Output (om, on) of this thread's epilogue (threads 0..255, one output each).  Its
+  // residual / bias / row mask are loaded first so that the epilogue waits on nothing.
+  const int ot = threadIdx.x;
+  const int ol = ot >> 2, oe = ot & 3;
+  const int om = 4 * (ol >> 4) + oe, on = n0 + (ol & 15);
+  const int cm = min(om, a.M - 1), cn = min(on, a.N - 1);
+  const int oflag = (a.row_on ? a.row_on : kAllRowsOn)[cm];  // no branch: the wait stays at the use
+  float oadd = 0.f;
+  if constexpr (EPI == EPI_RESIDUAL) oadd = a.res[a.r_t16 ? t16_index(cm, cn) : (size_t)cm * a.ldr + cn];
+  if constexpr (EPI == EPI_BIAS) oadd = a.bias[cn];
 
-  if constexpr (NORM) {
-    float ss = 0.f;
-#pragma unroll
-    for (int st = 0; st < KS; ++st)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss = fmaf(xa[st][e], xa[st][e], ss);
-    ss += __shfl_xor(ss, 16, 64);  // the four lanes of a row (kb = 0..3)
-    ss += __shfl_xor(ss, 32, 64);
-    if (kb == 0) ssq[wave][li] = ss;
-    __syncthreads();
-    if (threadIdx.x < 16) {
-      float tot = 0.f;
-      for (int w = 0; w < 16; ++w) tot += ssq[w][threadIdx.x];
-      inv_rms[threadIdx.x] = 1.0f / sqrtf(tot / (float)a.K + a.eps);
-    }
-    __syncthreads();
-    const float r = inv_rms[li];
-#pragma unroll
-    for (int st = 0; st < KS; ++st) {
-      const int k = kbase + st * 32 + 8 * kb;
-      const float4 *pg = reinterpret_cast<const float4 *>(a.gamma + k);
-      const float4 g0 = pg[0], g1 = pg[1];
-      const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xa[st][e] = (xa[st][e] * r) * g[e];
-    }
-  }
-
+  // k steps in passes of KP (all loads of a pass in flight together): registers for
+  // KP <= 6 steps, so K = 512 * {8, 12} runs as two passes instead of spilling.
+  constexpr int KP = KS <= 6 ? KS : (KS % 6 == 0 ? 6 : 4);
+  static_assert(KS % KP == 0, "pass length");
+  static_assert(!NORM || KS <= 4, "the fused RMSNorm keeps the whole row slice in registers");
   f32x4_t acc[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int st = 0; st < KS; ++st) {
-    bf16x8_t hi, mid, lo;
-    split_bf16x8(xa[st], hi, mid, lo);
+  for (int p0 = 0; p0 < KS; p0 += KP) {
+    float xa[KP][8];
+    float ga[NORM ? KP : 1][8];
+    uint4 wb[KP][T];
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-      const bf16x8_t b = __builtin_bit_cast(bf16x8_t, wb[st][t]);
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b, acc[t], 0, 0, 0);
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, b, acc[t], 0, 0, 0);
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b, acc[t], 0, 0, 0);
+    for (int st = 0; st < KP; ++st) {
+      const int k0 = kbase + (p0 + st) * 32;
+      const int k = k0 + 8 * kb;
+      const float4 *px = reinterpret_cast<const float4 *>(
+          a.x_t16 ? a.X + ((size_t)(k0 >> 5) * 64 + lane) * 8 : a.X + (size_t)arow * a.ldx + k);
+      const float4 x0 = px[0], x1 = px[1];
+      xa[st][0] = x0.x; xa[st][1] = x0.y; xa[st][2] = x0.z; xa[st][3] = x0.w;
+      xa[st][4] = x1.x; xa[st][5] = x1.y; xa[st][6] = x1.z; xa[st][7] = x1.w;
+      if constexpr (NORM) {
+        const float4 *pg = reinterpret_cast<const float4 *>(a.gamma + k);
+        const float4 g0 = pg[0], g1 = pg[1];
+        ga[st][0] = g0.x; ga[st][1] = g0.y; ga[st][2] = g0.z; ga[st][3] = g0.w;
+        ga[st][4] = g1.x; ga[st][5] = g1.y; ga[st][6] = g1.z; ga[st][7] = g1.w;
+      }
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        if (a.w_packed) {  // tile blockIdx.x (+ N / 16 for the up rows), k step k0 / 32
+          const size_t tile = blockIdx.x + (size_t)t * (a.N >> 4);
+          wb[st][t] = *reinterpret_cast<const uint4 *>(a.W + ((tile * (a.K >> 5) + (k0 >> 5)) * 64 + lane) * 8);
+        } else {
+          const int col = min(n0 + li, a.N - 1) + t * a.N;
+          wb[st][t] = *reinterpret_cast<const uint4 *>(a.W + (size_t)col * a.K + k);
+        }
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    if constexpr (NORM) {  // single pass: this wave holds its whole k range of every row
+      float ss = 0.f;
+#pragma unroll
+      for (int st = 0; st < KP; ++st)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(xa[st][e], xa[st][e], ss);
+      ss += __shfl_xor(ss, 16, 64);  // the four lanes of a row (kb = 0..3)
+      ss += __shfl_xor(ss, 32, 64);
+      if (kb == 0) ssq[wave][li] = ss;
+      __syncthreads();
+      if (threadIdx.x < 16) {
+        float tot = 0.f;
+        for (int w = 0; w < 16; ++w) tot += ssq[w][threadIdx.x];
+        inv_rms[threadIdx.x] = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+      }
+      __syncthreads();
+      const float r = inv_rms[li];
+#pragma unroll
+      for (int st = 0; st < KP; ++st)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xa[st][e] = (xa[st][e] * r) * ga[st][e];
+    }
+
+#pragma unroll
+    for (int st = 0; st < KP; ++st) {
+      bf16x8_t hi, mid, lo;
+      split_bf16x8(xa[st], hi, mid, lo);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const bf16x8_t b = __builtin_bit_cast(bf16x8_t, wb[st][t]);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, b, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b, acc[t], 0, 0, 0);
+      }
     }
   }
 #pragma unroll
   for (int t = 0; t < T; ++t) part[wave][t][lane] = acc[t];
   __syncthreads();
-  if (wave != 0) return;
-  f32x4_t sum[T];
+  if (ot >= 256) return;
+  // Sum of the 16 waves' k ranges in wave order (C[i][j] sits in lane j + 16 (i / 4),
+  // element i % 4: this thread's (om, on) is lane ol, element oe).
+  float v[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) {
-    sum[t] = part[0][t][lane];
-    for (int w = 1; w < 16; ++w) sum[t] += part[w][t][lane];
-  }
-  const int n = n0 + li;
+    float sacc = part[0][t][ol][oe];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int m = 4 * kb + e;
-    if (m >= a.M || n >= a.N || (a.row_on && !a.row_on[m])) continue;
-    float v = sum[0][e];
-    if constexpr (EPI == EPI_SWIGLU) {
-      v = v / (1.0f + expf(-v)) * sum[T - 1][e];
-    } else if constexpr (EPI == EPI_RESIDUAL) {
-      v = a.res[(size_t)m * a.ldr + n] + v;
-    } else if constexpr (EPI == EPI_BIAS) {
-      v = v + a.bias[n];
-    }
-    a.Y[(size_t)m * a.ldy + n] = v;
+    for (int w = 1; w < 16; ++w) sacc += part[w][t][ol][oe];
+    v[t] = sacc;
   }
+  if (om >= a.M || on >= a.N || !oflag) return;
+  float y = v[0];
+  if constexpr (EPI == EPI_SWIGLU) {
+    y = y / (1.0f + expf(-y)) * v[T - 1];
+  } else if constexpr (EPI == EPI_RESIDUAL || EPI == EPI_BIAS) {
+    y = (EPI == EPI_RESIDUAL) ? oadd + y : y + oadd;
+  }
+  a.Y[a.y_t16 ? t16_index(om, on) : (size_t)om * a.ldy + on] = y;
 }
 
 // inv_rms[m] = 1 / sqrt(mean(X[m]^2) + eps), one wave per row.
@@ -796,10 +858,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs a) {
         float sacc = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) sacc = fmaf(qs[g * D + sub * 8 + j], kv[j], sacc);
-        sacc += __shfl_xor(sacc, 8, 16);
-        sacc += __shfl_xor(sacc, 4, 16);
-        sacc += __shfl_xor(sacc, 2, 16);
-        sacc += __shfl_xor(sacc, 1, 16);
+        sacc = row16_sum(sacc);
         if (sub == 0 && t < t1) sc[g][t - t0] = sacc * a.scale;
       }
     }
@@ -1053,7 +1112,7 @@ __global__ __launch_bounds__(1024) void k_select_talker(SelectTalkerArgs a) {
   a.prm += row;
   if (a.after_frame && skip_work(a.st, SKIP_TALKER)) return;
   a.logits += (size_t)row * a.V;
-  a.x += (size_t)row * a.H;
+  if (!a.x_t16) a.x += (size_t)row * a.H;
   a.cp_prefix += (size_t)row * 2 * a.H;
   a.codes += row * a.codes_row;
   if (a.trace) a.trace += row * a.trace_row;
@@ -1088,8 +1147,9 @@ __global__ __launch_bounds__(1024) void k_select_talker(SelectTalkerArgs a) {
   if (tid == 0) a.st->semantic = tok;
 
   // CodePredictor prefix: [RMSNorm(x) * gamma ; codec_emb[tok]]
+  auto xv = [&](int i) { return a.x_t16 ? a.x[t16_index(row, i)] : a.x[i]; };
   float ss = 0.f;
-  for (int i = tid; i < a.H; i += 1024) ss = fmaf(a.x[i], a.x[i], ss);
+  for (int i = tid; i < a.H; i += 1024) ss = fmaf(xv(i), xv(i), ss);
   ss = wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
@@ -1097,7 +1157,7 @@ __global__ __launch_bounds__(1024) void k_select_talker(SelectTalkerArgs a) {
   for (int w = 0; w < 16; ++w) tot += red[w];
   const float inv = 1.0f / sqrtf(tot / (float)a.H + a.eps);
   for (int i = tid; i < a.H; i += 1024) {
-    a.cp_prefix[i] = (a.x[i] * inv) * a.gamma[i];
+    a.cp_prefix[i] = (xv(i) * inv) * a.gamma[i];
     a.cp_prefix[a.H + i] = bf16_to_f32(a.codec_emb[(size_t)tok * a.H + i]);
   }
 }
@@ -1171,6 +1231,21 @@ __global__ void k_frame_end(SlotState *st, const SlotParams *prm, int advance, i
     st->done = 1;
   else if (f >= st->max_frames)
     st->done = 2;
+}
+
+// dst = src [rows][K] repacked for the skinny GEMM: [rows / 16][K / 32][64 lanes][8], lane
+// j + 16 kb of (tile, step) holding src[16 tile + j][32 step + 8 kb .. + 8].
+__global__ void k_pack_w(const uint16_t *src, uint16_t *dst, int rows, int K) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int ksteps = K >> 5;
+  if (i >= (size_t)(rows >> 4) * ksteps * 64) return;
+  const int lane = (int)(i & 63);
+  const size_t rest = i >> 6;
+  const int step = (int)(rest % ksteps);
+  const size_t tile = rest / ksteps;
+  const int j = lane & 15, kb = lane >> 4;
+  *reinterpret_cast<uint4 *>(dst + i * 8) =
+      *reinterpret_cast<const uint4 *>(src + (tile * 16 + j) * (size_t)K + step * 32 + kb * 8);
 }
 
 }  // namespace
@@ -1334,19 +1409,32 @@ static hipError_t skinny_ks(const GemmArgs &a, hipStream_t s) {
     case 2: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 2>), grid, block, 0, s, a); break;
     case 3: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 3>), grid, block, 0, s, a); break;
     case 4: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 4>), grid, block, 0, s, a); break;
-    case 6: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 6>), grid, block, 0, s, a); break;
-    case 8: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 8>), grid, block, 0, s, a); break;
-    case 12: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 12>), grid, block, 0, s, a); break;
+    case 6:
+      if constexpr (NORM) return hipErrorInvalidValue;
+      else hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 6>), grid, block, 0, s, a);
+      break;
+    case 8:
+      if constexpr (NORM) return hipErrorInvalidValue;
+      else hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 8>), grid, block, 0, s, a);
+      break;
+    case 12:
+      if constexpr (NORM) return hipErrorInvalidValue;
+      else hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 12>), grid, block, 0, s, a);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
-bool gemm_skinny_supports(int M, int K) { return M >= 1 && M <= 16 && gemv_supports_k(K); }
+bool gemm_skinny_supports(int M, int K, bool norm) {
+  return M >= 1 && M <= 16 && gemv_supports_k(K) && (!norm || K <= 2048);
+}
 
 hipError_t launch_gemm_skinny(int epi, bool norm, const GemmArgs &a, hipStream_t s) {
-  if (!gemm_skinny_supports(a.M, a.K) || a.N <= 0 || a.ldx % 4 || (norm && (!a.gamma || a.row_scale)))
+  if (!gemm_skinny_supports(a.M, a.K, norm) || a.N <= 0 || a.ldx % 4 || (norm && (!a.gamma || a.row_scale)))
     return hipErrorInvalidValue;
+  // T16 output / residual needs N % 32 (whole k steps); packed weights need whole 16-column tiles.
+  if (((a.y_t16 || a.r_t16) && a.N % 32) || (a.w_packed && a.N % 16)) return hipErrorInvalidValue;
   switch (epi) {
     case EPI_STORE: return norm ? skinny_ks<EPI_STORE, true>(a, s) : skinny_ks<EPI_STORE, false>(a, s);
     case EPI_RESIDUAL: return norm ? hipErrorInvalidValue : skinny_ks<EPI_RESIDUAL, false>(a, s);
@@ -1354,6 +1442,13 @@ hipError_t launch_gemm_skinny(int epi, bool norm, const GemmArgs &a, hipStream_t
     case EPI_BIAS: return norm ? hipErrorInvalidValue : skinny_ks<EPI_BIAS, false>(a, s);
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_pack_weights(const uint16_t *src, uint16_t *dst, int rows, int K, hipStream_t s) {
+  if (rows <= 0 || rows % 16 || K <= 0 || K % 32 || !src || !dst) return hipErrorInvalidValue;
+  const size_t n = (size_t)(rows / 16) * (K / 32) * 64;
+  hipLaunchKernelGGL(k_pack_w, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, dst, rows, K);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {

@@ -1,4 +1,4 @@
-"""The matrix-core GEMM (bf16 weights, fp32 activations as two bf16 terms, fp32 accumulate)
+"""The matrix-core GEMM (bf16 weights, fp32 activations as three bf16 terms, fp32 accumulate)
 against a float64 numpy product, through the C ABI test hook q3t_debug_gemm."""
 import numpy as np
 import pytest

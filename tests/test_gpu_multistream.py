@@ -84,8 +84,8 @@ def test_tiny_multistream_matches_oracle(models):
         assert err <= LOGIT_TOL
 
 
-def test_multistream_equals_single_stream_path(models):
-    name = "tiny_multistream"
+@pytest.mark.parametrize("name", ["tiny_multistream", "tinyproj_multistream"])
+def test_multistream_equals_single_stream_path(models, name):
     r = run_batch(models, name)
     for j in range(MULTI_WORKLOADS[name].streams):
         g = run_single(models, name, j)
