@@ -169,7 +169,9 @@ int q3t_engine_synchronize(q3t_engine *engine);
  * dependent launches included) and the algorithmic bytes one launch moves.
  *   kernel 0: QKV GEMV (+ input RMSNorm)    1: O GEMV (+ residual)
  *          2: gate/up GEMV (+ RMSNorm, SwiGLU)    3: down GEMV (+ residual)
- *          4: Talker attention over a full cache
+ *          4: Talker attention over a full cache  5: CodePredictor attention (positions 0..15)
+ *          6: greedy CodePredictor selection     7: Talker attention at half the cache
+ *          8: CodePredictor LM-head GEMV
  * Slot 0 must not hold a stream. */
 int q3t_bench_kernel(q3t_engine *engine, int32_t kernel, int32_t iters, double *avg_us,
                      double *bytes_per_launch);

@@ -1347,7 +1347,7 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
     using namespace q3t;
     if (!e || !avg_us || !bytes) fail(Q3T_ERR_INVALID, "null argument");
     if (iters <= 0 || iters > 8192) fail(Q3T_ERR_INVALID, "iters must be in 1..8192");
-    if (kernel < 0 || kernel > 4) fail(Q3T_ERR_INVALID, "unknown kernel class %d", kernel);
+    if (kernel < 0 || kernel > 8) fail(Q3T_ERR_INVALID, "unknown kernel class %d", kernel);
     Slot &s = e->slots[0];
     if (s.in_use) fail(Q3T_ERR_BUSY, "stream slot 0 is in use");
     HIPC(hipSetDevice(e->device));
@@ -1363,8 +1363,22 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
       for (int l = 0; l < td.layers; ++l) seq.push_back({&e->talker, l});
       for (int g = 0; g < e->groups - 1; ++g)
         for (int l = 0; l < cd.layers; ++l) seq.push_back({&e->cp, l});
+    } else if (kernel == 5) {  // CodePredictor attention: positions 0..groups-1, each over 5 layers
+      for (int p = 0; p < e->groups; ++p)
+        for (int l = 0; l < cd.layers; ++l) seq.push_back({&e->cp, l});
+    } else if (kernel == 6 || kernel == 8) {  // one per CodePredictor group
+      for (int g = 0; g < e->groups - 1; ++g) seq.push_back({&e->cp, 0});
     } else {
       for (int l = 0; l < td.layers; ++l) seq.push_back({&e->talker, l});
+    }
+    if (kernel == 6) {  // greedy selection, fixed state (frame 0, not done)
+      SlotState st0{};
+      st0.semantic = 0;
+      st0.max_frames = 1;
+      HIPC(hipMemcpy(s.st, &st0, sizeof st0, hipMemcpyHostToDevice));
+      SlotParams pr{};
+      pr.codec_eos = e->codec_eos;
+      HIPC(hipMemcpy(s.prm, &pr, sizeof pr, hipMemcpyHostToDevice));
     }
     double total_bytes = 0.0;
     auto enqueue = [&](int i, bool count) {
@@ -1415,6 +1429,45 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
                       attn_chunk_len(l.w->cap), attn_chunks(l.w->cap) > 1 ? 1 : 0};
           hip_check(launch_attn_decode(aa, d.head_dim, s.stream), "launch_attn_decode");
           b = 2.0 * esz * d.kv_heads * d.head_dim * l.w->cap + 4.0 * (d.qkv_rows() + d.q_out());
+          break;
+        }
+        case 5: {  // CodePredictor attention at position (i / layers) % groups (one chunk, direct output)
+          const size_t esz = e->kv_bf16 ? 2 : 4;
+          const size_t layer_bytes = (size_t)d.kv_heads * l.w->cap * d.head_dim * esz;
+          const int pos = (i / d.layers) % e->groups;
+          AttnArgs aa{s.qkv, W.gq, W.gk, l.w->rope, s.c_k + layer_bytes * l.layer, s.c_v + layer_bytes * l.layer,
+                      s.attn, d.q_heads, d.kv_heads, l.w->cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
+                      POS_CONST, pos, SKIP_NEVER, e->kv_bf16, s.st, s.attn_part, s.attn_part_chunks,
+                      attn_chunk_len(l.w->cap), 0};
+          hip_check(launch_attn_decode(aa, d.head_dim, s.stream), "launch_attn_decode");
+          b = 2.0 * esz * d.kv_heads * d.head_dim * (pos + 1) + 4.0 * (d.qkv_rows() + d.q_out());
+          break;
+        }
+        case 6: {  // greedy CodePredictor token selection + embedding gathers
+          const int g = i % (e->groups - 1);
+          SelectCpArgs a{s.logits_c, e->cp_emb + (size_t)g * cd.vocab * e->talker_hidden, s.cur, s.emb_sum, s.codes,
+                         nullptr, s.t_in, e->codec_emb, s.trailing, s.st, s.prm, cd.vocab, e->talker_hidden,
+                         e->groups, g};
+          hip_check(launch_select_cp(a, s.stream), "launch_select_cp");
+          b = 4.0 * cd.vocab + 2.0 * e->talker_hidden;
+          break;
+        }
+        case 7: {  // Talker attention at half the cache (split chunks; the O-projection merge not included)
+          const size_t esz = e->kv_bf16 ? 2 : 4;
+          const size_t layer_bytes = (size_t)d.kv_heads * l.w->cap * d.head_dim * esz;
+          AttnArgs aa{s.qkv, W.gq, W.gk, l.w->rope, s.t_k + layer_bytes * l.layer, s.t_v + layer_bytes * l.layer,
+                      s.attn, d.q_heads, d.kv_heads, l.w->cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
+                      POS_CONST, l.w->cap / 2, SKIP_NEVER, e->kv_bf16, s.st, s.attn_part, s.attn_part_chunks,
+                      attn_chunk_len(l.w->cap), attn_chunks(l.w->cap) > 1 ? 1 : 0};
+          hip_check(launch_attn_decode(aa, d.head_dim, s.stream), "launch_attn_decode");
+          b = 2.0 * esz * d.kv_heads * d.head_dim * (l.w->cap / 2 + 1) + 4.0 * (d.qkv_rows() + d.q_out());
+          break;
+        }
+        case 8: {  // CodePredictor LM head (final norm prologue)
+          const int g = i % (e->groups - 1);
+          e->gemv(EPI_STORE, true, e->lm_heads + (size_t)g * cd.vocab * cd.hidden, s.x_c, e->c_norm, cd.eps,
+                  nullptr, nullptr, s.logits_c, cd.vocab, cd.hidden, SKIP_NEVER, s.st, s.stream);
+          b = 2.0 * cd.vocab * cd.hidden + 4.0 * (2 * cd.hidden + cd.vocab);
           break;
         }
       }
