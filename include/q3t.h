@@ -158,6 +158,25 @@ int q3t_stream_read_talker_logits(q3t_stream *stream, float *out, int32_t capaci
 int q3t_stream_read_cp_logits(q3t_stream *stream, float *out, int32_t capacity_frames,
                               int32_t *frames);
 
+/* Parity hooks on the reference's own seams (all run greedy on stream slot 0, which must not
+ * hold a stream; ERR_BUSY otherwise):
+ *   q3t_debug_talker_prefill  HipTalker::prefill_from_host (talker.rs:140-205): the Talker
+ *     prefill of `steps` rows [steps, H]; hidden = final RMSNorm of the last row [H], logits =
+ *     raw codec-head logits [talker_vocab], token = argmax of the suppressed logits.  Slot 0's
+ *     KV cache keeps the prefill for q3t_debug_talker_step.
+ *   q3t_debug_talker_step     HipTalker::decode_step_from_host (talker.rs:235-295): one
+ *     Talker step of input [H] at position `offset` over slot 0's cache rows 0..offset-1;
+ *     same outputs.
+ *   q3t_debug_code_predictor  HipCodePredictor::generate_from_host (code_predictor.rs:277-302):
+ *     the greedy CodePredictor over the prefix [talker_hidden; semantic_embed] (each
+ *     talker-hidden wide); tokens [num_code_groups - 1], embedding_sum [talker_hidden]. */
+int q3t_debug_talker_prefill(q3t_engine *engine, const float *prefill, int32_t steps, float *hidden,
+                             float *logits, int32_t *token);
+int q3t_debug_talker_step(q3t_engine *engine, const float *input, int32_t offset, float *hidden,
+                          float *logits, int32_t *token);
+int q3t_debug_code_predictor(q3t_engine *engine, const float *talker_hidden,
+                             const float *semantic_embed, int32_t *tokens, float *embedding_sum);
+
 /* Waits until every stream slot of the engine is idle. */
 int q3t_engine_synchronize(q3t_engine *engine);
 

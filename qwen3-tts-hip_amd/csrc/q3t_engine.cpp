@@ -469,6 +469,17 @@ struct Engine {
   // Everything one frame does after its semantic token is known (generation.rs:697-741):
   // CodePredictor groups 0..14, the next Talker step, token selection, frame bookkeeping.
   void enqueue_frame(Slot &sl, hipStream_t s) {
+    enqueue_code_predictor(sl, s);
+    stack_step(talker, sl.t_k, sl.t_v, sl.t_in, sl.x_t, sl, POS_TALKER_FRAME, 0, SKIP_TALKER, s);
+    gemv(EPI_STORE, true, codec_head, sl.x_t, t_norm, td.eps, nullptr, nullptr, sl.logits_t, td.vocab, td.hidden,
+         SKIP_TALKER, sl.st, s, true);
+    select_talker(sl, 1, s);
+    hip_check(launch_frame_end(sl.st, sl.prm, 1, s), "launch_frame_end");
+  }
+
+  // The frame's CodePredictor (code_predictor.rs:366-471): prefix rows cp_prefix, then the 15
+  // acoustic groups; codes[frame], emb_sum and the next Talker input t_in are its outputs.
+  void enqueue_code_predictor(Slot &sl, hipStream_t s) {
     const int Ht = talker_hidden, Hc = cd.hidden, Vc = cd.vocab, nac = groups - 1;
     const float *in0 = sl.cp_prefix, *in1 = sl.cp_prefix + Ht;
     if (has_proj) {
@@ -498,11 +509,6 @@ struct Engine {
                      g};
       hip_check(launch_select_cp(a, s), "launch_select_cp");
     }
-    stack_step(talker, sl.t_k, sl.t_v, sl.t_in, sl.x_t, sl, POS_TALKER_FRAME, 0, SKIP_TALKER, s);
-    gemv(EPI_STORE, true, codec_head, sl.x_t, t_norm, td.eps, nullptr, nullptr, sl.logits_t, td.vocab, td.hidden,
-         SKIP_TALKER, sl.st, s, true);
-    select_talker(sl, 1, s);
-    hip_check(launch_frame_end(sl.st, sl.prm, 1, s), "launch_frame_end");
   }
 
   // ----- stream rows: the batched frame over slots 0..rows-1, masked by pools.row_on -----
@@ -1339,6 +1345,94 @@ int q3t_engine_synchronize(q3t_engine *e) {
     HIPC(hipSetDevice(e->device));
     for (auto &s : e->slots) HIPC(hipStreamSynchronize(s.stream));
     HIPC(hipStreamSynchronize(e->pools.stream));
+  });
+}
+
+}  // extern "C"
+
+namespace q3t {
+namespace {
+
+// Stream slot 0 prepared for a parity hook: free, greedy on both heads, no history, frame 0.
+Slot &hook_slot(Engine &e, int prefill_steps, int max_frames) {
+  Slot &s = e.slots[0];
+  if (s.in_use) fail(Q3T_ERR_BUSY, "stream slot 0 is in use");
+  HIPC(hipSetDevice(e.device));
+  HIPC(hipStreamSynchronize(s.stream));
+  SlotState st0{};
+  st0.semantic = 0;
+  st0.prefill_steps = prefill_steps;
+  st0.max_frames = max_frames;
+  SlotParams pr{};
+  pr.repetition_penalty = 1.0f;
+  pr.codec_eos = e.codec_eos;
+  HIPC(hipMemcpy(s.st, &st0, sizeof st0, hipMemcpyHostToDevice));
+  HIPC(hipMemcpy(s.prm, &pr, sizeof pr, hipMemcpyHostToDevice));
+  return s;
+}
+
+// Talker head on slot 0 after a prefill or step: normed hidden (the CodePredictor prefix's
+// first row), raw logits and the greedy token over the suppressed logits.
+void talker_head_out(Engine &e, Slot &s, float *hidden, float *logits, int32_t *token) {
+  e.gemv(EPI_STORE, true, e.codec_head, s.x_t, e.t_norm, e.td.eps, nullptr, nullptr, s.logits_t, e.td.vocab,
+         e.td.hidden, SKIP_NEVER, s.st, s.stream);
+  e.select_talker(s, 0, s.stream);
+  HIPC(hipStreamSynchronize(s.stream));
+  HIPC(hipMemcpy(hidden, s.cp_prefix, (size_t)e.td.hidden * 4, hipMemcpyDeviceToHost));
+  HIPC(hipMemcpy(logits, s.logits_t, (size_t)e.td.vocab * 4, hipMemcpyDeviceToHost));
+  SlotState st{};
+  HIPC(hipMemcpy(&st, s.st, sizeof st, hipMemcpyDeviceToHost));
+  *token = st.semantic;
+}
+
+}  // namespace
+}  // namespace q3t
+
+extern "C" {
+
+int q3t_debug_talker_prefill(q3t_engine *e, const float *prefill, int32_t steps, float *hidden, float *logits,
+                             int32_t *token) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || !prefill || !hidden || !logits || !token) fail(Q3T_ERR_INVALID, "null argument");
+    if (steps <= 0) fail(Q3T_ERR_INVALID, "prefill steps must be non-zero");
+    if (steps >= e->cap) fail(Q3T_ERR_CAPACITY, "prefill of %d steps needs a larger max_cache_steps (%d)", steps, e->cap);
+    Slot &s = hook_slot(*e, steps, 1);
+    HIPC(hipMemcpy(e->pools.px, prefill, (size_t)steps * e->td.hidden * 4, hipMemcpyHostToDevice));
+    e->prefill_segments({PrefillSeg{0, 0, steps}}, steps, s.stream);
+    talker_head_out(*e, s, hidden, logits, token);
+  });
+}
+
+int q3t_debug_talker_step(q3t_engine *e, const float *input, int32_t offset, float *hidden, float *logits,
+                          int32_t *token) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || !input || !hidden || !logits || !token) fail(Q3T_ERR_INVALID, "null argument");
+    if (offset < 0 || offset >= e->cap) fail(Q3T_ERR_CAPACITY, "offset %d outside the %d-step cache", offset, e->cap);
+    // position = prefill_steps + frame = offset; max_frames 2 keeps the step from being skipped
+    Slot &s = hook_slot(*e, offset, 2);
+    HIPC(hipMemcpy(s.t_in, input, (size_t)e->td.hidden * 4, hipMemcpyHostToDevice));
+    e->stack_step(e->talker, s.t_k, s.t_v, s.t_in, s.x_t, s, POS_TALKER_FRAME, 0, SKIP_TALKER, s.stream);
+    talker_head_out(*e, s, hidden, logits, token);
+  });
+}
+
+int q3t_debug_code_predictor(q3t_engine *e, const float *talker_hidden, const float *semantic_embed, int32_t *tokens,
+                             float *embedding_sum) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || !talker_hidden || !semantic_embed || !tokens || !embedding_sum) fail(Q3T_ERR_INVALID, "null argument");
+    Slot &s = hook_slot(*e, 0, 1);
+    const size_t row = (size_t)e->talker_hidden * 4;
+    HIPC(hipMemcpy(s.cp_prefix, talker_hidden, row, hipMemcpyHostToDevice));
+    HIPC(hipMemcpy(s.cp_prefix + e->talker_hidden, semantic_embed, row, hipMemcpyHostToDevice));
+    e->enqueue_code_predictor(s, s.stream);
+    HIPC(hipStreamSynchronize(s.stream));
+    std::vector<int32_t> codes(e->groups);
+    HIPC(hipMemcpy(codes.data(), s.codes, (size_t)e->groups * 4, hipMemcpyDeviceToHost));
+    for (int g = 1; g < e->groups; ++g) tokens[g - 1] = codes[g];
+    HIPC(hipMemcpy(embedding_sum, s.emb_sum, row, hipMemcpyDeviceToHost));
   });
 }
 

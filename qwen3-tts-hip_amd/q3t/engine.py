@@ -157,6 +157,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "q3t_debug_gemm": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, f32p, ctypes.c_int32, ctypes.c_int32,
                                           P(ctypes.c_uint16), ctypes.c_int32, f32p, ctypes.c_float, f32p, f32p,
                                           f32p]),
+        "q3t_debug_talker_prefill": (ctypes.c_int, [ctypes.c_void_p, f32p, ctypes.c_int32, f32p, f32p, i32p]),
+        "q3t_debug_talker_step": (ctypes.c_int, [ctypes.c_void_p, f32p, ctypes.c_int32, f32p, f32p, i32p]),
+        "q3t_debug_code_predictor": (ctypes.c_int, [ctypes.c_void_p, f32p, f32p, i32p, f32p]),
         "q3t_last_error": (ctypes.c_char_p, []),
     }
     for name, (res, args) in sigs.items():
@@ -369,6 +372,36 @@ class HipTtsEngine:
                                    _fptr(r) if r is not None else None, _fptr(b) if b is not None else None,
                                    _fptr(Y)))
         return Y
+
+    # -- parity hooks (the reference's prefill_from_host / decode_step_from_host /
+    #    generate_from_host seams) --------------------------------------------------------
+    def debug_talker_prefill(self, prefill: np.ndarray):
+        """(normed hidden [H], raw logits [V], greedy token) after a Talker prefill on slot 0."""
+        x = _f32(prefill)
+        hidden = np.zeros(self.info["talker_hidden"], np.float32)
+        logits = np.zeros(self.info["talker_vocab"], np.float32)
+        tok = ctypes.c_int32()
+        _check(_lib.q3t_debug_talker_prefill(self._h, _fptr(x), x.shape[0], _fptr(hidden), _fptr(logits),
+                                             ctypes.byref(tok)))
+        return hidden, logits, tok.value
+
+    def debug_talker_step(self, step_input: np.ndarray, offset: int):
+        """One Talker step at `offset` over slot 0's cache: (normed hidden, raw logits, greedy token)."""
+        x = _f32(step_input)
+        hidden = np.zeros(self.info["talker_hidden"], np.float32)
+        logits = np.zeros(self.info["talker_vocab"], np.float32)
+        tok = ctypes.c_int32()
+        _check(_lib.q3t_debug_talker_step(self._h, _fptr(x), int(offset), _fptr(hidden), _fptr(logits),
+                                          ctypes.byref(tok)))
+        return hidden, logits, tok.value
+
+    def debug_code_predictor(self, talker_hidden: np.ndarray, semantic_embed: np.ndarray):
+        """Greedy CodePredictor over [talker_hidden; semantic_embed]: (tokens [groups-1], embedding_sum)."""
+        th, se = _f32(talker_hidden), _f32(semantic_embed)
+        tokens = np.zeros(self.code_groups - 1, np.int32)
+        emb = np.zeros(self.info["talker_hidden"], np.float32)
+        _check(_lib.q3t_debug_code_predictor(self._h, _fptr(th), _fptr(se), _iptr(tokens), _fptr(emb)))
+        return tokens, emb
 
     def sampler_draw(self, logits: np.ndarray, n: int, do_sample: bool = True, top_k: int = 50,
                      top_p: float = 1.0, temperature: float = 0.9, seed: int = 0, kind: int = 0) -> np.ndarray:

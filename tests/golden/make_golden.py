@@ -58,6 +58,54 @@ def make(name: str) -> str:
     return path
 
 
+def deterministic_hidden(length: int, modulus: float, center: float) -> np.ndarray:
+    """The reference's fixture input (python-reference/qwen3_tts_reference.py:620-626)."""
+    return np.array([((i % int(modulus)) - center) / modulus for i in range(length)], dtype=np.float32)
+
+
+# Parity-hook fixtures: one per model spec, from the workload whose prefill they reuse.
+HOOK_WORKLOADS = {"tiny": "tiny_greedy", "tiny-proj": "tinyproj_greedy", "0.6b": "cfg2_0.6b_greedy",
+                  "1.7b": "cfg4_1.7b_greedy"}
+
+
+def make_hooks(spec: str) -> str:
+    """The reference's Talker-prefill and CodePredictor parity fixtures
+    (qwen3_tts_reference.py:487-523, 629-676; talker-prefill-parity.rs, code-predictor-parity.rs),
+    same array names, from the float64 oracle on the synthetic model of `spec`."""
+    from oracle.sampling import GREEDY
+    w = WORKLOADS[HOOK_WORKLOADS[spec]]
+    t0 = time.time()
+    model = synth.SyntheticModel.build(w.spec, w.weight_seed)
+    inputs = w.inputs(model)
+    o = Oracle(model.tensors, model.config(), max_cache_steps=w.max_cache_steps, dtype=np.float64)
+    P = inputs.prefill_steps
+    logits = o.prefill(inputs.prefill)
+    last_hidden = o.hidden.copy()
+    first_semantic, margin0 = o.talker_select(logits, None, 1.0, GREEDY, None)
+    prefix = o.prepare_code_predictor_prefix(first_semantic)
+    first_acoustic, emb_sum, _, cp_m = o.code_predictor(prefix)
+    step_input = o.build_step_input(first_semantic, emb_sum, inputs.trailing_text[0])
+    next_logits = o.decode(step_input, P)
+    next_semantic, margin1 = o.talker_select(next_logits, None, 1.0, GREEDY, None)
+    th = deterministic_hidden(o.t_dims.hidden, 17.0, 15.0)
+    se = deterministic_hidden(o.t_dims.hidden, 23.0, 11.0)
+    ac_tokens, ac_sum, _, ac_m = o.code_predictor(np.stack([th, se]).astype(np.float64))
+    path = os.path.join(HERE, f"hooks_{spec}.npz")
+    meta = dict(spec=spec, weight_seed=w.weight_seed, checksum=model.checksum(), workload=w.name,
+                prefill_steps=P, oracle_dtype="float64", seconds=round(time.time() - t0, 1))
+    np.savez_compressed(
+        path, meta=np.array(json.dumps(meta)), prefill=inputs.prefill.astype(np.float32),
+        last_hidden=last_hidden.astype(np.float32), logits=logits.astype(np.float32),
+        first_semantic=np.array([first_semantic]), first_acoustic=np.asarray(first_acoustic),
+        first_step_input=step_input.astype(np.float32), forward_next_logits=next_logits.astype(np.float32),
+        next_semantic=np.array([next_semantic]), talker_margins=np.array([margin0, margin1]),
+        first_cp_margins=np.asarray(cp_m), talker_hidden=th, semantic_embed=se,
+        acoustic_tokens=np.asarray(ac_tokens), embedding_sum=ac_sum.astype(np.float32),
+        acoustic_margins=np.asarray(ac_m))
+    print(f"hooks {spec}: {meta['seconds']} s -> {path}", flush=True)
+    return path
+
+
 def make_multi(name: str) -> str:
     w = MULTI_WORKLOADS[name]
     t0 = time.time()
@@ -85,6 +133,12 @@ def make_multi(name: str) -> str:
 
 
 if __name__ == "__main__":
-    names = sys.argv[1:] or ([n for n in WORKLOADS if not n.startswith("cfg1")] + list(MULTI_WORKLOADS))
+    names = sys.argv[1:] or ([n for n in WORKLOADS if not n.startswith("cfg1")] + list(MULTI_WORKLOADS) +
+                             [f"hooks_{s}" for s in HOOK_WORKLOADS])
     for n in names:
-        make_multi(n) if n in MULTI_WORKLOADS else make(n)
+        if n.startswith("hooks_"):
+            make_hooks(n[len("hooks_"):])
+        elif n in MULTI_WORKLOADS:
+            make_multi(n)
+        else:
+            make(n)

@@ -125,3 +125,29 @@ def test_option_validation():
         GenerateOptions(top_p=0.0).validate()
     with pytest.raises(ValueError):
         GenerateOptions(subtalker_temperature=0.0).validate()
+
+
+def test_hook_fixture_inputs_follow_the_reference_formula():
+    """deterministic_hidden (qwen3_tts_reference.py:620-626): ((i % m) - c) / m, and the hook
+    fixtures carry the reference's array names."""
+    import os
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(__file__), "golden"))
+    from make_golden import deterministic_hidden
+
+    from parity import fixture_exists, load_fixture
+    v = deterministic_hidden(40, 17.0, 15.0)
+    assert v[0] == np.float32(-15 / 17) and v[15] == 0.0 and v[16] == np.float32(1 / 17) and v[17] == v[0]
+    w = deterministic_hidden(30, 23.0, 11.0)
+    assert w[11] == 0.0 and w[22] == np.float32(11 / 23) and w[23] == np.float32(-11 / 23)
+    for spec in ("tiny", "0.6b"):
+        if not fixture_exists(f"hooks_{spec}"):
+            continue
+        fx = load_fixture(f"hooks_{spec}")
+        for name in ("prefill", "last_hidden", "logits", "first_semantic", "first_step_input",
+                     "forward_next_logits", "next_semantic", "talker_hidden", "semantic_embed",
+                     "acoustic_tokens", "embedding_sum"):
+            assert name in fx, name
+        H = fx["talker_hidden"].shape[0]
+        np.testing.assert_array_equal(fx["talker_hidden"], deterministic_hidden(H, 17.0, 15.0))
+        np.testing.assert_array_equal(fx["semantic_embed"], deterministic_hidden(H, 23.0, 11.0))
