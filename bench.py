@@ -104,7 +104,8 @@ def cpu_baseline(seconds_budget: float) -> dict:
                       f"{os.cpu_count()}"}
 
 
-def multistream(eng_cls, model_dir: str, name: str, steps: int, warmup: int, use_graph: bool) -> dict:
+def multistream(eng_cls, model_dir: str, name: str, steps: int, warmup: int, use_graph: bool,
+                frames_cap: int = 0) -> dict:
     """BASELINE config 5 on the same model: every stream started together (one prefill over
     all prompts), then chunks pulled for all live streams at once until each has ended.
     A step is one such generation; value = frames of all streams / seconds."""
@@ -117,6 +118,9 @@ def multistream(eng_cls, model_dir: str, name: str, steps: int, warmup: int, use
     inputs = w.inputs(model)
     del model
     opts = [E.GenerateOptions(**kw) for kw in w.options_kwargs()]
+    if frames_cap > 0:  # profiling runs: the same prefill, fewer frames
+        opts = [E.GenerateOptions(**{**kw, "max_frames": min(kw["max_frames"], frames_cap)})
+                for kw in w.options_kwargs()]
     eng = eng_cls(model_dir, E.EngineOptions(max_cache_steps=w.max_cache_steps, max_streams=w.streams,
                                              use_graph=use_graph))
     lk = E.StreamOptions(text_lookahead_tokens=1 << 30)
@@ -192,7 +196,7 @@ def main() -> int:
     del model
     if args.multistream_only:
         print(json.dumps(multistream(E.HipTtsEngine, tmp, args.multistream, args.steps, args.warmup,
-                                     not args.eager)))
+                                     not args.eager, args.frames)))
         import shutil
         shutil.rmtree(tmp, ignore_errors=True)
         return 0
