@@ -596,16 +596,23 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
       }
       split_bf16x8(xa[i], ahi[i], amid[i], alo[i]);
     }
+    // term-major (lo, mid, hi over all tiles): independent accumulations between two that depend
+    // on each other
 #pragma unroll
-    for (int j = 0; j < NB; ++j) {
-      const bf16x8_t b = __builtin_bit_cast(bf16x8_t, wb[j]);
+    for (int j = 0; j < NB; ++j)
 #pragma unroll
-      for (int i = 0; i < MB; ++i) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo[i], b, acc[i][j], 0, 0, 0);
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(amid[i], b, acc[i][j], 0, 0, 0);
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi[i], b, acc[i][j], 0, 0, 0);
-      }
-    }
+      for (int i = 0; i < MB; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(alo[i], __builtin_bit_cast(bf16x8_t, wb[j]), acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(amid[i], __builtin_bit_cast(bf16x8_t, wb[j]), acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int i = 0; i < MB; ++i)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ahi[i], __builtin_bit_cast(bf16x8_t, wb[j]), acc[i][j], 0, 0, 0);
   }
 
   // epilogue: lane holds C[4 * kb + e][li] of every tile
@@ -639,6 +646,154 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
 // NORM the rows' RMSNorm is computed from the same loads (sum of squares reduced across the
 // workgroup) and applied before the split.
 // ---------------------------------------------------------------------------------------
+// ---------------------------------------------------------------------------------------
+// Prefill GEMM, LDS-tiled: Y[M][N] = f(X)[M][K] . W[N][K]^T for many rows.
+// Block tile 128 rows x 128 weight rows, k step 32; four waves, each 64 x 64 (4 x 4 tiles of
+// v_mfma_f32_16x16x32_bf16), two blocks per CU.  Global loads (a wave reads 8 rows x 128 B of
+// X or 16 rows x 64 B of W per instruction) go to registers while the matrix cores work on
+// the previous tile, then into the other LDS buffer (double buffering).  X is scaled by the row's
+// 1/rms and the gain on the way into LDS; its fp32 values become hi/mid/lo bf16 terms after
+// the LDS read, as in k_gemm_mfma.  SwiGLU blocks hold 64 gate rows and the matching 64 up
+// rows (64 outputs).  Requires K % 32 == 0 and N % 128 == 0 (N % 64 for SwiGLU).
+// ---------------------------------------------------------------------------------------
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
+  constexpr int BM = 128, BW = 128, BK = 32;
+  constexpr int PA = BK + 4;  // fp32 row stride (pads the LDS banks)
+  constexpr int PB = BK + 8;  // bf16 row stride
+  constexpr bool SW = EPI == EPI_SWIGLU;
+  __shared__ float As[2][BM][PA];
+  __shared__ uint16_t Bs[2][BW][PB];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int li = lane & 15, kb = lane >> 4;
+  const int m0 = blockIdx.y * BM;
+  const int nb = blockIdx.x;
+  const int KT = a.K / BK;
+
+  // weight row of block row r
+  auto wrow = [&](int r) -> int {
+    if constexpr (SW) return r < 64 ? nb * 64 + r : a.N + nb * 64 + (r - 64);
+    else return nb * 128 + r;
+  };
+  // per thread and k step: 4 float4 of X (8 lanes x 16 B per 128-byte row), 2 uint4 of W
+  // (4 lanes x 16 B per 64-byte row)
+  constexpr int NA = BM * BK / 4 / 256, NB = BW * BK / 8 / 256, CA = BK / 4, CB = BK / 8;
+  float4 ra[NA];
+  float4 rg[NA];
+  uint4 rb[NB];
+  float rs[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const int row = (tid + 256 * i) / CA;
+    rs[i] = a.row_scale ? a.row_scale[min(m0 + row, a.M - 1)] : 1.0f;
+  }
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int idx = tid + 256 * i, row = idx / CA, c4 = idx % CA;
+      const int m = min(m0 + row, a.M - 1);
+      ra[i] = *reinterpret_cast<const float4 *>(a.X + (size_t)m * a.ldx + k0 + 4 * c4);
+      if (a.gamma) rg[i] = *reinterpret_cast<const float4 *>(a.gamma + k0 + 4 * c4);
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int idx = tid + 256 * i, row = idx / CB, c = idx % CB;
+      rb[i] = *reinterpret_cast<const uint4 *>(a.W + (size_t)wrow(row) * a.K + k0 + 8 * c);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) {
+      const int idx = tid + 256 * i, row = idx / CA, c4 = idx % CA;
+      float4 v = ra[i];
+      if (a.row_scale) {
+        v.x *= rs[i]; v.y *= rs[i]; v.z *= rs[i]; v.w *= rs[i];
+      }
+      if (a.gamma) {
+        v.x *= rg[i].x; v.y *= rg[i].y; v.z *= rg[i].z; v.w *= rg[i].w;
+      }
+      *reinterpret_cast<float4 *>(&As[buf][row][4 * c4]) = v;
+    }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int idx = tid + 256 * i, row = idx / CB, c = idx % CB;
+      *reinterpret_cast<uint4 *>(&Bs[buf][row][8 * c]) = rb[i];
+    }
+  };
+  // block weight row of the wave's B tile u
+  auto brow = [&](int u) -> int {
+    if constexpr (SW) return (u < 2 ? wn * 32 + u * 16 : 64 + wn * 32 + (u - 2) * 16);
+    else return wn * 64 + u * 16;
+  };
+
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[t][u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < KT) gload((kt + 1) * BK);
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      bf16x8_t bq[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        bq[u] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(&Bs[buf][brow(u) + li][ks * 32 + 8 * kb]));
+      bf16x8_t aq[3][4];  // [lo, mid, hi][tile]
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float *px = &As[buf][wm * 64 + t * 16 + li][ks * 32 + 8 * kb];
+        const float4 x0 = reinterpret_cast<const float4 *>(px)[0], x1 = reinterpret_cast<const float4 *>(px)[1];
+        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        split_bf16x8(xv, aq[2][t], aq[1][t], aq[0][t]);
+      }
+      // term-major: 16 independent accumulations between two that depend on each other;
+      // each accumulator still adds lo, mid, hi in that order.
+#pragma unroll
+      for (int q = 0; q < 3; ++q)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aq[q][t], bq[u], acc[t][u], 0, 0, 0);
+    }
+    if (kt + 1 < KT) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // C[i][j] of a tile sits in lane j + 16 (i / 4), element i % 4.
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int m = m0 + wm * 64 + t * 16 + 4 * kb + e;
+      if (m >= a.M) continue;
+      if constexpr (SW) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int n = nb * 64 + wn * 32 + u * 16 + li;
+          const float g = acc[t][u][e], up = acc[t][u + 2][e];
+          a.Y[(size_t)m * a.ldy + n] = g / (1.0f + expf(-g)) * up;
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int n = nb * 128 + wn * 64 + u * 16 + li;
+          float v = acc[t][u][e];
+          if constexpr (EPI == EPI_RESIDUAL) v = a.res[(size_t)m * a.ldr + n] + v;
+          if constexpr (EPI == EPI_BIAS) v = v + a.bias[n];
+          a.Y[(size_t)m * a.ldy + n] = v;
+        }
+      }
+    }
+}
+
 __device__ const int32_t kAllRowsOn[16] = {1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1};
 
 template <int EPI, bool NORM, int KS>  // KS = 32-wide k steps per wave = K / (16 * 32)
@@ -1391,7 +1546,10 @@ static hipError_t gemm_epi(const GemmArgs &a, hipStream_t s) {
   constexpr int NB = 4;
   constexpr int NT = (EPI == EPI_SWIGLU) ? NB / 2 : NB;
   const int cols_per_wg = 4 * 16 * NT;
-  if (a.M <= 16) {
+  if (a.M >= 128 && a.K % 32 == 0 && a.N % (EPI == EPI_SWIGLU ? 64 : 128) == 0 && a.ldx % 4 == 0) {
+    const int nout = EPI == EPI_SWIGLU ? 64 : 128;
+    hipLaunchKernelGGL((k_gemm_lds<EPI>), dim3(a.N / nout, (a.M + 127) / 128), dim3(256), 0, s, a);
+  } else if (a.M <= 16) {
     hipLaunchKernelGGL((k_gemm_mfma<EPI, 1, NB>), dim3((a.N + cols_per_wg - 1) / cols_per_wg, (a.M + 15) / 16),
                        dim3(256), 0, s, a);
   } else {

@@ -86,3 +86,24 @@ def test_epilogues_skinny_and_tiled(eng, M):
 def test_rejects_bad_shapes(eng):
     with pytest.raises(E.InvalidInputError):
         eng.debug_gemm(0, np.zeros((4, 48), np.float32), np.zeros((8, 48), np.uint16), 8)
+
+
+@pytest.mark.parametrize("M,K", [(128, 1024), (300, 2048), (521, 1024)])
+def test_prefill_tiles_all_epilogues(eng, M, K):
+    """M >= 128 with K % 64 == 0 runs the LDS-tiled prefill kernel: RMSNorm rows (1/rms and
+    gain applied on the way into LDS), store / residual / SwiGLU / bias epilogues."""
+    print(f"[gpu] gemm tiles M={M} K={K}", flush=True)
+    N = 256
+    rng = np.random.default_rng(M + K)
+    X = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    Xn = X.astype(np.float64) / np.sqrt((X.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6) * g
+    Wb = _weights(2 * N, K, M * 3 + 1)
+    W = synth.bf16_bits_to_f32(Wb).astype(np.float64)
+    res = rng.standard_normal((M, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    _close(eng.debug_gemm(0, X, Wb[:N], N, gamma=g), Xn @ W[:N].T)
+    _close(eng.debug_gemm(1, X, Wb[:N], N, res=res), res + X.astype(np.float64) @ W[:N].T)
+    _close(eng.debug_gemm(3, X, Wb[:N], N, bias=bias), X.astype(np.float64) @ W[:N].T + bias)
+    gate, up = Xn @ W[:N].T, Xn @ W[N:].T
+    _close(eng.debug_gemm(2, X, Wb, N, gamma=g), gate / (1 + np.exp(-gate)) * up)
