@@ -315,6 +315,9 @@ struct Pools {
   size_t t_kv_row = 0, c_kv_row = 0;  // KV elements per slot (K or V, all layers)
   int s_qkv = 0, s_attn = 0, s_act = 0;
   int part_chunks = 0;
+  // The batched frame splits the Talker's attention into shorter chunks (more workgroups,
+  // fewer bytes each) than one stream can: its partials are merged by k_attn_merge.
+  int rows_chunk = 0, rows_part_chunks = 0;
   int64_t part_row = 0, trailing_row = 0, codes_row = 0, trace_t_row = 0, trace_c_row = 0;
   char *t_k = nullptr, *t_v = nullptr, *c_k = nullptr, *c_v = nullptr;
   float *x_t = nullptr, *t_in = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits_t = nullptr,
@@ -333,6 +336,8 @@ struct Pools {
   int graph_rows = 0;
   bool graph_traced = false;
 };
+
+constexpr int kRowsAttnChunk = 32;
 
 // One stream's rows in a (possibly multi-stream) prompt prefill.
 struct PrefillSeg {
@@ -542,7 +547,9 @@ struct Engine {
     Pools &p = pools;
     const int H = d.hidden;
     const size_t cache_layer = (size_t)d.kv_heads * w.cap * d.head_dim * (kv_bf16 ? 2 : 4);
-    const int partial = attn_chunks(w.cap) > 1 ? 1 : 0;
+    const int chunk = p.rows_chunk;
+    const int nch = (w.cap + chunk - 1) / chunk;
+    const int partial = nch > 1 ? 1 : 0;
     const Act none{nullptr, 0};
     for (int l = 0; l < d.layers; ++l) {
       const LayerW &L = w.layers[l];
@@ -551,8 +558,8 @@ struct Engine {
             rows, s);
       AttnArgs aa{p.qkv,    L.gq,    L.gk,     w.rope,  kc + l * cache_layer, vc + l * cache_layer,
                   battn,    d.q_heads, d.kv_heads, w.cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
-                  pos_mode, pos_const, skip,    kv_bf16, p.st,   p.attn_part, p.part_chunks,
-                  attn_chunk_len(w.cap), partial};
+                  pos_mode, pos_const, skip,    kv_bf16, p.st,   p.attn_part, nch,
+                  chunk,    partial};
       aa.ld_qkv = p.s_qkv;
       aa.ld_out = p.s_attn;
       aa.kv_row = (int64_t)kv_row;
@@ -561,8 +568,8 @@ struct Engine {
       aa.out_t16 = 1;
       hip_check(launch_attn_decode(aa, d.head_dim, s, nullptr, rows), "launch_attn_decode(rows)");
       if (partial) {
-        AttnMergeArgs m{p.attn_part, battn, d.q_heads, d.kv_heads, p.part_chunks, attn_chunk_len(w.cap),
-                        pos_mode,    pos_const, skip, p.s_attn,  p.part_row,    p.st,
+        AttnMergeArgs m{p.attn_part, battn,     d.q_heads, d.kv_heads, nch,        chunk,
+                        pos_mode,    pos_const, skip,      p.s_attn,   p.part_row, p.st,
                         p.row_on,    1};
         hip_check(launch_attn_merge(m, rows, s), "launch_attn_merge");
       }
@@ -676,9 +683,11 @@ void alloc_pools(Engine &e, int n) {
   p.s_attn = std::max(td.q_out(), cd.q_out());
   p.s_act = std::max(td.intermediate, cd.intermediate);
   p.part_chunks = std::max(attn_chunks(e.cap), attn_chunks(e.cp.cap));
+  p.rows_chunk = kRowsAttnChunk;
+  p.rows_part_chunks = (e.cap + p.rows_chunk - 1) / p.rows_chunk;
   const int kvh = std::max(td.kv_heads, cd.kv_heads);
   const int gq = std::max(td.q_heads / td.kv_heads, cd.q_heads / cd.kv_heads);
-  p.part_row = (int64_t)kvh * p.part_chunks * gq * (td.head_dim + 2);
+  p.part_row = (int64_t)kvh * std::max(p.part_chunks, p.rows_part_chunks) * gq * (td.head_dim + 2);
   p.trailing_row = (int64_t)(e.cap + 1) * Ht;
   p.codes_row = (int64_t)e.cap * e.groups;
   auto zeroed = [&](size_t bytes) {

@@ -444,52 +444,83 @@ __device__ void merge_attention(const GemvArgs &a, float *xs) {
     const int h = hq / G, g = hq % G;
     const float *p0 = a.attn_part + (((size_t)h * a.attn_part_chunks) * G + g) * (D + 2);
     const size_t stride = (size_t)G * (D + 2);
-    float M = -FLT_MAX;
-    for (int c = 0; c < nchunks; ++c) M = fmaxf(M, p0[c * stride]);
-    float den = 0.f, num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int c = 0; c < nchunks; ++c) {
-      const float *pc = p0 + c * stride;
-      const float w = expf(pc[0] - M);
-      den = fmaf(w, pc[1], den);
+    // at most kAttnMaxChunks chunks: every partial is loaded at once (indices clamped), then
+    // the max and the weighted sums in chunk order
+    float mv[kAttnMaxChunks], lv[kAttnMaxChunks], av[kAttnMaxChunks][8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) num[j] = fmaf(w, pc[2 + d0 + j], num[j]);
+    for (int c = 0; c < kAttnMaxChunks; ++c) {
+      const float *pc = p0 + min(c, nchunks - 1) * stride;
+      mv[c] = pc[0];
+      lv[c] = pc[1];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) av[c][j] = pc[2 + d0 + j];  // records are 130 floats: not 16-B aligned
     }
+    float M = -FLT_MAX;
+#pragma unroll
+    for (int c = 0; c < kAttnMaxChunks; ++c)
+      if (c < nchunks) M = fmaxf(M, mv[c]);
+    float den = 0.f, num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < kAttnMaxChunks; ++c)
+      if (c < nchunks) {
+        const float w = expf(mv[c] - M);
+        den = fmaf(w, lv[c], den);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) num[j] = fmaf(w, av[c][j], num[j]);
+      }
 #pragma unroll
     for (int j = 0; j < 8; ++j) xs[base + j] = num[j] / den;
   }
 }
 
-// Stream-row form of merge_attention for the batched frame: workgroup r merges row r's
-// partials into out + r * ld_out (same chunk order and arithmetic).
+// Stream-row form of merge_attention for the batched frame: workgroup (h, r) merges KV head
+// h's G query heads of row r (thread = one output element), in chunk order as in
+// merge_attention.
 __global__ __launch_bounds__(256) void k_attn_merge(AttnMergeArgs a) {
   constexpr int D = 128;
-  const int row = blockIdx.x;
+  const int h = blockIdx.x;
+  const int row = blockIdx.y;
   if (a.row_on && !a.row_on[row]) return;
   const SlotState *st = a.st + row;
   if (skip_work(st, a.skip)) return;
+  const int G = a.q_heads / a.kv_heads;
+  if ((int)threadIdx.x >= G * D) return;
+  const int g = threadIdx.x / D, d = threadIdx.x % D;
   const int pos = (a.pos_mode == POS_TALKER_FRAME) ? st->prefill_steps + st->frame : a.pos_const;
   const int nchunks = min((pos + a.chunk) / a.chunk, a.part_chunks);
-  const int G = a.q_heads / a.kv_heads;
-  const float *part = a.part + row * a.part_row;
-  for (int base = threadIdx.x * 8; base < a.q_heads * D; base += 256 * 8) {
-    const int hq = base / D, d0 = base % D;
-    const int h = hq / G, g = hq % G;
-    const float *p0 = part + (((size_t)h * a.part_chunks) * G + g) * (D + 2);
-    const size_t stride = (size_t)G * (D + 2);
-    float M = -FLT_MAX;
-    for (int c = 0; c < nchunks; ++c) M = fmaxf(M, p0[c * stride]);
-    float den = 0.f, num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int c = 0; c < nchunks; ++c) {
-      const float *pc = p0 + c * stride;
-      const float w = expf(pc[0] - M);
-      den = fmaf(w, pc[1], den);
+  const float *p0 = a.part + row * a.part_row + (((size_t)h * a.part_chunks) * G + g) * (D + 2);
+  const size_t stride = (size_t)G * (D + 2);
+  // Loads in blocks of 8 chunks (indices clamped), so a block costs one memory round trip;
+  // max, then the weighted sums in chunk order.
+  float M = -FLT_MAX;
+  for (int c0 = 0; c0 < nchunks; c0 += 8) {
+    float mv[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) num[j] = fmaf(w, pc[2 + d0 + j], num[j]);
+    for (int j = 0; j < 8; ++j) mv[j] = p0[min(c0 + j, nchunks - 1) * stride];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (c0 + j < nchunks) M = fmaxf(M, mv[j]);
+  }
+  float den = 0.f, num = 0.f;
+  for (int c0 = 0; c0 < nchunks; c0 += 8) {
+    float mv[8], lv[8], av[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float *pc = p0 + min(c0 + j, nchunks - 1) * stride;
+      mv[j] = pc[0];
+      lv[j] = pc[1];
+      av[j] = pc[2 + d];
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      a.out[a.out_t16 ? t16_index(row, base + j) : (size_t)row * a.ld_out + base + j] = num[j] / den;
+      if (c0 + j < nchunks) {
+        const float w = expf(mv[j] - M);
+        den = fmaf(w, lv[j], den);
+        num = fmaf(w, av[j], num);
+      }
   }
+  const int k = (h * G + g) * D + d;
+  a.out[a.out_t16 ? t16_index(row, k) : (size_t)row * a.ld_out + k] = num / den;
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1520,9 +1551,14 @@ hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t s, co
   if (rows < 1 || rows > kMaxRows || (rows > 1 && (!a.row_on || a.ld_qkv <= 0 || a.kv_row <= 0))) return hipErrorInvalidValue;
   if (rows > 1 && (a.partial_out ? a.part_row <= 0 : a.ld_out <= 0)) return hipErrorInvalidValue;
   const int G = a.q_heads / a.kv_heads;
-  if (a.cap > attn_max_cache_steps(a.q_heads, a.kv_heads) || a.chunk != attn_chunk_len(a.cap)) return hipErrorInvalidValue;
-  if (a.partial_out ? a.part_chunks < attn_chunks(a.cap) : attn_chunks(a.cap) != 1) return hipErrorInvalidValue;
-  const dim3 grid(a.kv_heads, attn_chunks(a.cap), rows), block(256);
+  // chunk: attn_chunk_len(cap) for one stream (the O GEMV merges at most kAttnMaxChunks
+  // partials); any of 32 / 64 / 128 for stream rows (merged by k_attn_merge).
+  if (a.cap > attn_max_cache_steps(a.q_heads, a.kv_heads)) return hipErrorInvalidValue;
+  if (rows == 1 ? a.chunk != attn_chunk_len(a.cap) : (a.chunk != 32 && a.chunk != 64 && a.chunk != 128))
+    return hipErrorInvalidValue;
+  const int nch = (a.cap + a.chunk - 1) / a.chunk;
+  if (a.partial_out ? a.part_chunks < nch : nch != 1) return hipErrorInvalidValue;
+  const dim3 grid(a.kv_heads, nch, rows), block(256);
 #define Q3T_ATTN_CASE(GG, TT, CC) \
   if (G == GG && a.chunk == CC) {  \
     launch_timed(k_attn_split<128, GG, TT, CC>, grid, block, 0, s, t, a); \
@@ -1648,7 +1684,8 @@ hipError_t launch_attn_merge(const AttnMergeArgs &a, int rows, hipStream_t s) {
   if (rows < 1 || rows > kMaxRows || a.kv_heads <= 0 || a.q_heads % a.kv_heads || a.chunk <= 0 ||
       a.part_chunks <= 0 || a.q_heads * 128 > a.ld_out || (rows > 1 && (!a.row_on || a.part_row <= 0)))
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_merge, dim3(rows), dim3(256), 0, s, a);
+  if ((a.q_heads / a.kv_heads) * 128 > 256) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_attn_merge, dim3(a.kv_heads, rows), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
