@@ -8,7 +8,7 @@ namespace q3t {
 
 // Per-stream loop state, resident in device memory so that one captured frame graph can
 // be replayed frame after frame without host round trips.  Written only by the kernels
-// that end a frame (select + frame_end) and by the host at stream start.
+// that end a frame (the Talker's token selection) and by the host at stream start.
 struct SlotState {
   int32_t frame;          // frames completed so far
   int32_t semantic;       // semantic token that starts the next frame
@@ -71,6 +71,8 @@ struct GemvArgs {
   // Input = merge of attention partials (O projection after split attention), when set.
   const float *attn_part;
   int32_t attn_part_chunks, attn_chunk, attn_pos_mode, attn_pos_const, attn_q_heads, attn_kv_heads;
+  // rows = 2: a second input row x + ldx_r (res + ldr_r, out + ldo_r) against the same weights
+  int32_t rows, ldx_r, ldr_r, ldo_r;
 };
 
 struct AttnArgs {
@@ -168,6 +170,7 @@ struct SelectTalkerArgs {
   int64_t codes_row, trace_row;
   const int32_t *row_on;
   int32_t x_t16;            // x is a T16 block (row r = stream row r) instead of x + r * H
+  int32_t end_frame;        // also end the frame: advance the counter by after_frame, EOS / max_frames
 };
 
 struct SelectCpArgs {

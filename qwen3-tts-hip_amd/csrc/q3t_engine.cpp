@@ -464,10 +464,12 @@ struct Engine {
                           hipMemcpyDeviceToDevice, s));
   }
 
-  void select_talker(Slot &sl, int after_frame, hipStream_t s) {
+  // Talker token selection; end_frame = also the frame bookkeeping (counter, EOS, max_frames).
+  void select_talker(Slot &sl, int after_frame, hipStream_t s, bool end_frame = true) {
     SelectTalkerArgs a{sl.logits_t, sl.x_t, t_norm, codec_emb, sl.cp_prefix, sl.codes,
                        trace ? sl.trace_t : nullptr, sl.st, sl.prm, td.vocab, td.hidden, groups, td.eps,
                        after_frame};
+    a.end_frame = end_frame ? 1 : 0;
     hip_check(launch_select_talker(a, s), "launch_select_talker");
   }
 
@@ -478,25 +480,59 @@ struct Engine {
     stack_step(talker, sl.t_k, sl.t_v, sl.t_in, sl.x_t, sl, POS_TALKER_FRAME, 0, SKIP_TALKER, s);
     gemv(EPI_STORE, true, codec_head, sl.x_t, t_norm, td.eps, nullptr, nullptr, sl.logits_t, td.vocab, td.hidden,
          SKIP_TALKER, sl.st, s, true);
-    select_talker(sl, 1, s);
-    hip_check(launch_frame_end(sl.st, sl.prm, 1, s), "launch_frame_end");
+    select_talker(sl, 1, s);  // + frame bookkeeping
   }
 
   // The frame's CodePredictor (code_predictor.rs:366-471): prefix rows cp_prefix, then the 15
   // acoustic groups; codes[frame], emb_sum and the next Talker input t_in are its outputs.
+  // A GEMV over two input rows (x, x + ldx_r) -> (out, out + ldo_r), one pass over W.
+  void gemv2(int epi, bool norm, const uint16_t *W, const float *x, int ldx_r, const float *gamma, float eps,
+             const float *res, int ldr_r, const float *bias, float *out, int ldo_r, int N, int K, const Slot &sl,
+             hipStream_t s) {
+    GemvArgs a{W, x, gamma, res, bias, out, N, K, eps, SKIP_DONE, sl.st};
+    a.rows = 2;
+    a.ldx_r = ldx_r;
+    a.ldr_r = ldr_r;
+    a.ldo_r = ldo_r;
+    hip_check(launch_gemv(epi, norm, false, a, s), "launch_gemv(2 rows)");
+  }
+
+  // CodePredictor positions 0 and 1 (its 2-row prefix, code_predictor.rs:366-400) in one pass
+  // per layer: two-row GEMVs and the prefill attention kernels at P = 2 (rows in the prefill
+  // workspace, idle during frames).  Returns the position-1 output row.
+  const float *cp_prefix_pass(const float *in, int ldin, Slot &sl, hipStream_t s) {
+    const StackW &w = cp;
+    const Dims &d = w.d;
+    Pools &p = pools;
+    const int H = d.hidden, Q = d.qkv_rows(), O = d.q_out(), I = d.intermediate;
+    float *x2 = p.px;  // [2][H]
+    const size_t cache_layer = (size_t)d.kv_heads * w.cap * d.head_dim * (kv_bf16 ? 2 : 4);
+    for (int l = 0; l < d.layers; ++l) {
+      const LayerW &L = w.layers[l];
+      const float *src = l == 0 ? in : x2;
+      const int lds = l == 0 ? ldin : H;
+      gemv2(EPI_STORE, true, L.qkv, src, lds, L.g_in, d.eps, nullptr, 0, nullptr, p.pqkv, Q, Q, H, sl, s);
+      PrefillAttnArgs pa{p.pqkv, L.gq, L.gk, w.rope, sl.c_k + l * cache_layer, sl.c_v + l * cache_layer, p.pattn,
+                         2, 0, Q, O, d.q_heads, d.kv_heads, w.cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
+                         kv_bf16};
+      hip_check(launch_prefill_attention(pa, s), "launch_prefill_attention(cp)");
+      gemv2(EPI_RESIDUAL, false, L.o, p.pattn, O, nullptr, 0.f, src, lds, nullptr, x2, H, H, O, sl, s);
+      gemv2(EPI_SWIGLU, true, L.gu, x2, H, L.g_post, d.eps, nullptr, 0, nullptr, p.pact, I, I, H, sl, s);
+      gemv2(EPI_RESIDUAL, false, L.down, p.pact, I, nullptr, 0.f, x2, H, nullptr, x2, H, H, I, sl, s);
+    }
+    return x2 + H;
+  }
+
   void enqueue_code_predictor(Slot &sl, hipStream_t s) {
     const int Ht = talker_hidden, Hc = cd.hidden, Vc = cd.vocab, nac = groups - 1;
-    const float *in0 = sl.cp_prefix, *in1 = sl.cp_prefix + Ht;
+    const float *in = sl.cp_prefix;
+    int ldin = Ht;
     if (has_proj) {
-      gemv(EPI_BIAS, false, proj_w, sl.cp_prefix, nullptr, 0.f, nullptr, proj_b, sl.cp_in, Hc, Ht, SKIP_DONE,
-           sl.st, s);
-      gemv(EPI_BIAS, false, proj_w, sl.cp_prefix + Ht, nullptr, 0.f, nullptr, proj_b, sl.cp_in + Hc, Hc, Ht,
-           SKIP_DONE, sl.st, s);
-      in0 = sl.cp_in;
-      in1 = sl.cp_in + Hc;
+      gemv2(EPI_BIAS, false, proj_w, sl.cp_prefix, Ht, nullptr, 0.f, nullptr, 0, proj_b, sl.cp_in, Hc, Hc, Ht, sl, s);
+      in = sl.cp_in;
+      ldin = Hc;
     }
-    stack_step(cp, sl.c_k, sl.c_v, in0, sl.x_c, sl, POS_CONST, 0, SKIP_DONE, s);
-    stack_step(cp, sl.c_k, sl.c_v, in1, sl.x_c, sl, POS_CONST, 1, SKIP_DONE, s);
+    const float *x_pos1 = cp_prefix_pass(in, ldin, sl, s);
     for (int g = 0; g < nac; ++g) {
       if (g > 0) {
         const float *in = sl.cur;
@@ -507,8 +543,8 @@ struct Engine {
         }
         stack_step(cp, sl.c_k, sl.c_v, in, sl.x_c, sl, POS_CONST, g + 1, SKIP_DONE, s);
       }
-      gemv(EPI_STORE, true, lm_heads + (size_t)g * Vc * Hc, sl.x_c, c_norm, cd.eps, nullptr, nullptr, sl.logits_c,
-           Vc, Hc, SKIP_DONE, sl.st, s);
+      gemv(EPI_STORE, true, lm_heads + (size_t)g * Vc * Hc, g == 0 ? x_pos1 : sl.x_c, c_norm, cd.eps, nullptr,
+           nullptr, sl.logits_c, Vc, Hc, SKIP_DONE, sl.st, s);
       SelectCpArgs a{sl.logits_c, cp_emb + (size_t)g * Vc * Ht, sl.cur, sl.emb_sum, sl.codes,
                      trace ? sl.trace_c : nullptr, sl.t_in, codec_emb, sl.trailing, sl.st, sl.prm, Vc, Ht, groups,
                      g};
@@ -588,6 +624,7 @@ struct Engine {
     a.trace_row = p.trace_t_row;
     a.row_on = p.row_on;
     a.x_t16 = x.ld < 0;
+    a.end_frame = 1;
     hip_check(launch_select_talker(a, s, rows), "launch_select_talker(rows)");
   }
 
@@ -631,8 +668,7 @@ struct Engine {
                     SKIP_TALKER, s);
     rgemm(EPI_STORE, true, codec_head_p, t16(bx_t), t_norm, td.eps, none, nullptr, Act{p.logits_t, td.vocab},
           td.vocab, Ht, rows, s);
-    select_talker_rows(rows, 1, t16(bx_t), s);
-    hip_check(launch_frame_end(p.st, p.prm, 1, s, rows, p.row_on), "launch_frame_end(rows)");
+    select_talker_rows(rows, 1, t16(bx_t), s);  // + frame bookkeeping
   }
 };
 
@@ -1182,8 +1218,7 @@ int q3t_stream_start(q3t_engine *e, const float *prefill, int32_t P, const float
     e->prefill_segments({PrefillSeg{slot, 0, P}}, P, s.stream);
     e->gemv(EPI_STORE, true, e->codec_head, s.x_t, e->t_norm, e->td.eps, nullptr, nullptr, s.logits_t, e->td.vocab,
             e->td.hidden, SKIP_NEVER, s.st, s.stream);
-    e->select_talker(s, 0, s.stream);
-    hip_check(launch_frame_end(s.st, s.prm, 0, s.stream), "launch_frame_end");
+    e->select_talker(s, 0, s.stream);  // + the EOS / max_frames check of the first token
     sync_state(s);
     *out = new_stream(*e, slot, o->max_frames);
   });
@@ -1222,7 +1257,6 @@ int q3t_streams_start(q3t_engine *e, int32_t n, const q3t_stream_input *inputs, 
              Engine::Act{nullptr, 0}, nullptr, Engine::Act{p.logits_t, e->td.vocab}, e->td.vocab, e->talker_hidden,
              rows, p.stream);
     e->select_talker_rows(rows, 0, Engine::Act{p.x_t, e->talker_hidden}, p.stream);
-    hip_check(launch_frame_end(p.st, p.prm, 0, p.stream, rows, p.row_on), "launch_frame_end(rows)");
     HIPC(hipMemcpyAsync(p.h_states, p.st, sizeof(SlotState) * rows, hipMemcpyDeviceToHost, p.stream));
     HIPC(hipStreamSynchronize(p.stream));
     for (int j = 0; j < n; ++j) out[j] = new_stream(*e, slots[j], opts[j].max_frames);
@@ -1385,7 +1419,7 @@ Slot &hook_slot(Engine &e, int prefill_steps, int max_frames) {
 void talker_head_out(Engine &e, Slot &s, float *hidden, float *logits, int32_t *token) {
   e.gemv(EPI_STORE, true, e.codec_head, s.x_t, e.t_norm, e.td.eps, nullptr, nullptr, s.logits_t, e.td.vocab,
          e.td.hidden, SKIP_NEVER, s.st, s.stream);
-  e.select_talker(s, 0, s.stream);
+  e.select_talker(s, 0, s.stream, false);
   HIPC(hipStreamSynchronize(s.stream));
   HIPC(hipMemcpy(hidden, s.cp_prefix, (size_t)e.td.hidden * 4, hipMemcpyDeviceToHost));
   HIPC(hipMemcpy(logits, s.logits_t, (size_t)e.td.vocab * 4, hipMemcpyDeviceToHost));

@@ -12,7 +12,8 @@ struct LaunchTiming {
 
 // y = W x (optionally x := RMSNorm(x) * gamma first) with the epilogue `epi`.  `streaming`
 // selects non-temporal weight loads.  Requires K = 512 * c for c in {1, 2, 3, 4, 6, 8, 12};
-// returns hipErrorInvalidValue otherwise.
+// returns hipErrorInvalidValue otherwise.  a.rows = 2 (ordinary loads, K <= 3072) runs two
+// input rows against one pass over the weights.
 hipError_t launch_gemv(int epi, bool norm, bool streaming, const GemvArgs &a, hipStream_t stream,
                        const LaunchTiming *timing = nullptr);
 bool gemv_supports_k(int K);
@@ -56,8 +57,6 @@ hipError_t launch_select_cp(const SelectCpArgs &a, hipStream_t stream, int rows 
 // n independent draws from one logit row (draw i uses Philox counter (i, kind, 0, 0)).
 hipError_t launch_sample_draws(const float *logits, int V, const SamplingParams &sp, uint64_t seed, int kind, int n,
                                int32_t *out, hipStream_t stream);
-hipError_t launch_frame_end(SlotState *st, const SlotParams *prm, int advance, hipStream_t stream, int rows = 1,
-                            const int32_t *row_on = nullptr);
 
 // Largest vocabulary the select kernels hold in LDS.
 constexpr int kMaxVocab = 4096;

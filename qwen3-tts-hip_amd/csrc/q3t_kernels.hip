@@ -106,8 +106,11 @@ __device__ __forceinline__ uint4 load_w(const u32x4 *p) {
 __device__ void merge_attention(const GemvArgs &a, float *xs);
 
 // ATTN = the input vector is the merge of attention partials (see merge_attention).
-template <int EPI, bool NORM, int KC, int RW, bool NT, bool ATTN = false>
+// MR = input rows (1, or 2: row 1 at x + ldx_r, res + ldr_r, out + ldo_r) against the same
+// weight loads.
+template <int EPI, bool NORM, int KC, int RW, bool NT, bool ATTN = false, int MR = 1>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
+  static_assert(!ATTN || MR == 1, "the attention merge feeds one row");
   if (skip_work(a.st, a.skip)) return;
   constexpr int K = KC * 512;
   constexpr int NR = (EPI == EPI_SWIGLU) ? 2 * RW : RW;
@@ -119,15 +122,18 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   // Load order: activations (and the norm gain), then every weight row of this wave, then
   // nothing else until the arithmetic.  The norm then only waits for the small activation
   // loads while the whole launch's weights are in flight (one DRAM round trip per launch).
-  float xv[KC][8];
+  float xv[MR][KC][8];
   float gv[NORM ? KC : 1][8];
 #pragma unroll
   for (int c = 0; c < KC; ++c) {
     if constexpr (ATTN) break;
-    const float4 *px = reinterpret_cast<const float4 *>(a.x + c * 512 + lane * 8);
-    const float4 p0 = px[0], p1 = px[1];
-    xv[c][0] = p0.x; xv[c][1] = p0.y; xv[c][2] = p0.z; xv[c][3] = p0.w;
-    xv[c][4] = p1.x; xv[c][5] = p1.y; xv[c][6] = p1.z; xv[c][7] = p1.w;
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const float4 *px = reinterpret_cast<const float4 *>(a.x + m * a.ldx_r + c * 512 + lane * 8);
+      const float4 p0 = px[0], p1 = px[1];
+      xv[m][c][0] = p0.x; xv[m][c][1] = p0.y; xv[m][c][2] = p0.z; xv[m][c][3] = p0.w;
+      xv[m][c][4] = p1.x; xv[m][c][5] = p1.y; xv[m][c][6] = p1.z; xv[m][c][7] = p1.w;
+    }
     if constexpr (NORM) {
       const float4 *pg = reinterpret_cast<const float4 *>(a.gamma + c * 512 + lane * 8);
       const float4 g0 = pg[0], g1 = pg[1];
@@ -137,9 +143,13 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   }
   // The epilogue operand of this lane's output row (lane r stores row unit0 + r), loaded
   // before the weights so that the store waits on nothing.
-  float eadd = 0.f;
-  if constexpr (EPI == EPI_RESIDUAL) eadd = a.res[min(unit0 + min(lane, RW - 1), a.N - 1)];
-  if constexpr (EPI == EPI_BIAS) eadd = a.bias[min(unit0 + min(lane, RW - 1), a.N - 1)];
+  float eadd[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    eadd[m] = 0.f;
+    if constexpr (EPI == EPI_RESIDUAL) eadd[m] = a.res[m * a.ldr_r + min(unit0 + min(lane, RW - 1), a.N - 1)];
+    if constexpr (EPI == EPI_BIAS) eadd[m] = a.bias[min(unit0 + min(lane, RW - 1), a.N - 1)];
+  }
   // Rows past the end (a partial last workgroup) load the last row instead of branching;
   // their results are never stored.
   uint4 w[NR][KC];
@@ -158,48 +168,56 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 #pragma unroll
     for (int c = 0; c < KC; ++c)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) xv[c][j] = xs[c * 512 + lane * 8 + j];
+      for (int j = 0; j < 8; ++j) xv[0][c][j] = xs[c * 512 + lane * 8 + j];
   }
 
   if constexpr (NORM) {
-    float ss = 0.f;
 #pragma unroll
-    for (int c = 0; c < KC; ++c)
+    for (int m = 0; m < MR; ++m) {
+      float ss = 0.f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) ss = fmaf(xv[c][j], xv[c][j], ss);
-    ss = wave_sum(ss);
-    const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
+      for (int c = 0; c < KC; ++c)
 #pragma unroll
-    for (int c = 0; c < KC; ++c)
+        for (int j = 0; j < 8; ++j) ss = fmaf(xv[m][c][j], xv[m][c][j], ss);
+      ss = wave_sum(ss);
+      const float inv = 1.0f / sqrtf(ss / (float)K + a.eps);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) xv[c][j] = (xv[c][j] * inv) * gv[c][j];
-  }
-
-  float acc[NR];
+      for (int c = 0; c < KC; ++c)
 #pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    float s = 0.f;
-#pragma unroll
-    for (int c = 0; c < KC; ++c) s += dot8(w[r][c], xv[c]);
-    acc[r] = wave_sum(s);
-  }
-
-#pragma unroll
-  for (int r = 0; r < RW; ++r) {
-    const int unit = unit0 + r;
-    if (lane == r && unit < a.N) {
-      if constexpr (EPI == EPI_STORE) {
-        a.out[unit] = acc[r];
-      } else if constexpr (EPI == EPI_RESIDUAL) {
-        a.out[unit] = eadd + acc[r];
-      } else if constexpr (EPI == EPI_BIAS) {
-        a.out[unit] = acc[r] + eadd;
-      } else {
-        const float g = acc[2 * r], u = acc[2 * r + 1];
-        a.out[unit] = g / (1.0f + expf(-g)) * u;
-      }
+        for (int j = 0; j < 8; ++j) xv[m][c][j] = (xv[m][c][j] * inv) * gv[c][j];
     }
   }
+
+  float acc[MR][NR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      float s = 0.f;
+#pragma unroll
+      for (int c = 0; c < KC; ++c) s += dot8(w[r][c], xv[m][c]);
+      acc[m][r] = wave_sum(s);
+    }
+
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int unit = unit0 + r;
+      float *out = a.out + m * a.ldo_r;
+      if (lane == r && unit < a.N) {
+        if constexpr (EPI == EPI_STORE) {
+          out[unit] = acc[m][r];
+        } else if constexpr (EPI == EPI_RESIDUAL) {
+          out[unit] = eadd[m] + acc[m][r];
+        } else if constexpr (EPI == EPI_BIAS) {
+          out[unit] = acc[m][r] + eadd[m];
+        } else {
+          const float g = acc[m][2 * r], u = acc[m][2 * r + 1];
+          out[unit] = g / (1.0f + expf(-g)) * u;
+        }
+      }
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1291,12 +1309,27 @@ __device__ int block_sample(SelectShared &sh, int V, const SamplingParams &sp, f
   return sh.misc[0];
 }
 
+// Ends a frame (advance = 1) or checks the token drawn after the prefill (advance = 0):
+// frame counter, then EOS (the frame's semantic token) or max_frames.
+__device__ __forceinline__ void end_frame(SlotState *st, const SlotParams *prm, int advance) {
+  if (st->done) return;
+  const int f = st->frame + advance;
+  st->frame = f;
+  if (st->semantic == prm->codec_eos)
+    st->done = 1;
+  else if (f >= st->max_frames)
+    st->done = 2;
+}
+
 __global__ __launch_bounds__(1024) void k_select_talker(SelectTalkerArgs a) {
   const int row = blockIdx.x;
   if (a.row_on && !a.row_on[row]) return;
   a.st += row;
   a.prm += row;
-  if (a.after_frame && skip_work(a.st, SKIP_TALKER)) return;
+  if (a.after_frame && skip_work(a.st, SKIP_TALKER)) {  // no Talker step after the last frame
+    if (a.end_frame && threadIdx.x == 0) end_frame(a.st, a.prm, 1);
+    return;
+  }
   a.logits += (size_t)row * a.V;
   if (!a.x_t16) a.x += (size_t)row * a.H;
   a.cp_prefix += (size_t)row * 2 * a.H;
@@ -1346,6 +1379,9 @@ __global__ __launch_bounds__(1024) void k_select_talker(SelectTalkerArgs a) {
     a.cp_prefix[i] = (xv(i) * inv) * a.gamma[i];
     a.cp_prefix[a.H + i] = bf16_to_f32(a.codec_emb[(size_t)tok * a.H + i]);
   }
+  // every thread read the loop state at entry (before the first barrier); thread 0 wrote
+  // the semantic token itself
+  if (a.end_frame && tid == 0) end_frame(a.st, a.prm, a.after_frame);
 }
 
 __global__ __launch_bounds__(1024) void k_select_cp(SelectCpArgs a) {
@@ -1404,20 +1440,6 @@ __global__ __launch_bounds__(1024) void k_sample_draws(const float *logits, int 
 }
 
 // Ends a frame (advance = 1) or checks the token drawn after the prefill (advance = 0).
-// Thread r handles stream row r (rows <= 64).
-__global__ void k_frame_end(SlotState *st, const SlotParams *prm, int advance, int rows, const int32_t *row_on) {
-  const int r = threadIdx.x;
-  if (r >= rows || (row_on && !row_on[r])) return;
-  st += r;
-  prm += r;
-  if (st->done) return;
-  const int f = st->frame + advance;
-  st->frame = f;
-  if (st->semantic == prm->codec_eos)
-    st->done = 1;
-  else if (f >= st->max_frames)
-    st->done = 2;
-}
 
 // dst = src [rows][K] repacked for the skinny GEMM: [rows / 16][K / 32][64 lanes][8], lane
 // j + 16 kb of (tile, step) holding src[16 tile + j][32 step + 8 kb .. + 8].
@@ -1464,6 +1486,12 @@ static void gemv_launch(const GemvArgs &a, hipStream_t s, const LaunchTiming *t)
   if constexpr (EPI == EPI_RESIDUAL && !NORM && KC <= 8) {
     if (a.attn_part) {
       launch_timed(k_gemv<EPI, NORM, KC, RW, NT, true>, grid, dim3(256), 0, s, t, a);
+      return;
+    }
+  }
+  if constexpr (!NT && KC <= 6) {  // two input rows: the CodePredictor's prefix pass
+    if (a.rows == 2) {
+      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, false, 2>, grid, dim3(256), 0, s, t, a);
       return;
     }
   }
@@ -1528,6 +1556,9 @@ static hipError_t gemv_epi(int epi, bool norm, const GemvArgs &a, hipStream_t s,
 hipError_t launch_gemv(int epi, bool norm, bool streaming, const GemvArgs &a, hipStream_t s,
                        const LaunchTiming *t) {
   if (!gemv_supports_k(a.K) || a.N <= 0) return hipErrorInvalidValue;
+  if (a.rows > 1 && (a.rows != 2 || streaming || a.attn_part || a.K > 6 * 512 || a.ldx_r % 4 ||
+                     (epi == EPI_RESIDUAL && !a.ldr_r) || !a.ldo_r))
+    return hipErrorInvalidValue;
   return streaming ? gemv_epi<true>(epi, norm, a, s, t) : gemv_epi<false>(epi, norm, a, s, t);
 }
 
@@ -1711,13 +1742,6 @@ hipError_t launch_sample_draws(const float *logits, int V, const SamplingParams 
   if (V <= 0 || V > kMaxVocab || n <= 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_sample_draws, dim3(n), dim3(1024), 0, s, logits, V, sp, (uint32_t)(seed & 0xffffffffu),
                      (uint32_t)(seed >> 32), kind, out);
-  return hipGetLastError();
-}
-
-hipError_t launch_frame_end(SlotState *st, const SlotParams *prm, int advance, hipStream_t s, int rows,
-                            const int32_t *row_on) {
-  if (rows < 1 || rows > kMaxRows || (rows > 1 && !row_on)) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_frame_end, dim3(1), dim3(64), 0, s, st, prm, advance, rows, row_on);
   return hipGetLastError();
 }
 
