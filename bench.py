@@ -172,6 +172,8 @@ def main() -> int:
     ap.add_argument("--multistream", default="cfg5_0.6b_multistream",
                     help="multi-stream workload reported beside the headline line ('' to skip)")
     ap.add_argument("--multistream-only", action="store_true", help="run only the multi-stream workload")
+    ap.add_argument("--kernel-classes", action="store_true",
+                    help="graph-time every kernel class of q3t_bench_kernel on the workload's model and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -194,6 +196,16 @@ def main() -> int:
     model.write(tmp)
     spec = model.spec
     del model
+    if args.kernel_classes:
+        eng = E.HipTtsEngine(tmp, E.EngineOptions(max_cache_steps=w.max_cache_steps))
+        for k, name in E.HipTtsEngine.KERNELS.items():
+            us, b = eng.bench_kernel(k, 1020)
+            print(json.dumps({"class": k, "kernel": name, "us_per_launch": round(us, 3),
+                              "algorithmic_bytes": int(b), "GBps": round(b / us / 1e3, 1)}))
+        eng.close()
+        import shutil
+        shutil.rmtree(tmp, ignore_errors=True)
+        return 0
     if args.multistream_only:
         print(json.dumps(multistream(E.HipTtsEngine, tmp, args.multistream, args.steps, args.warmup,
                                      not args.eager, args.frames)))
