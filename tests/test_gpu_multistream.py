@@ -170,3 +170,71 @@ def test_cfg5_sixteen_streams_match_oracle(models):
               f"talker logit err {err:.2e}")
         assert err <= LOGIT_TOL
     print(f"{identical}/{w.streams} streams bit-identical over every frame")
+
+
+def test_batched_stream_ends_by_eos_while_others_continue(models, tmp_path):
+    """One stream of a batch hits EOS mid-chunk (a model whose EOS row copies and slightly beats
+    a token the baseline emits); the others run to max_frames.  Every stream equals the
+    single-stream path on the same model."""
+    from q3t import synth
+    from q3t.workloads import WORKLOADS
+    w = WORKLOADS["tiny_greedy"]
+    base, d0 = models.get(w.spec)
+    inp = w.inputs(base)
+    with E.HipTtsEngine(d0, E.EngineOptions(max_cache_steps=w.max_cache_steps)) as eng:
+        sem = eng.generate_codes(inp, E.GenerateOptions.greedy(12)).codes[:, 0].tolist()
+    target = next(t for f, t in enumerate(sem) if f >= 2 and t not in sem[:f])
+    tensors = dict(base.tensors)
+    head = synth.bf16_bits_to_f32(tensors["talker.codec_head.weight"]).copy()
+    head[2150] = head[target] * 1.01
+    tensors["talker.codec_head.weight"] = synth.f32_to_bf16_bits(head)
+    synth.SyntheticModel(base.spec, base.seed, tensors).write(str(tmp_path))
+    mw = MULTI_WORKLOADS["tiny_multistream"]
+    inputs = [inp] + mw.inputs(base)[:2]
+    opts = [E.GenerateOptions.greedy(12), E.GenerateOptions.greedy(10), E.GenerateOptions.greedy(14)]
+    cap = max(mw.max_cache_steps, w.max_cache_steps)
+    with E.HipTtsEngine(str(tmp_path), E.EngineOptions(max_cache_steps=cap)) as eng:
+        ref = [eng.generate_codes(i, o) for i, o in zip(inputs, opts)]
+    assert ref[0].ended_by_eos and 0 < ref[0].frames < 12
+    with E.HipTtsEngine(str(tmp_path), E.EngineOptions(max_cache_steps=cap, max_streams=3)) as eng:
+        s = eng.start_streams(inputs, opts, E.StreamOptions(text_lookahead_tokens=1 << 30))
+        live, last = list(s), {}
+        while live:
+            chunks = eng.next_codes_chunks(live, 5)
+            for x, c in zip(live, chunks):
+                if c is not None:
+                    last[id(x)] = c
+            live = [x for x, c in zip(live, chunks) if c is not None]
+        got = [x.finish_codes() for x in s]
+        assert last[id(s[0])].ended_by_eos and not last[id(s[1])].ended_by_eos
+    for j, (g, r) in enumerate(zip(got, ref)):
+        np.testing.assert_array_equal(g.codes, r.codes, err_msg=f"stream {j}")
+        assert g.ended_by_eos == r.ended_by_eos
+
+
+def test_batched_bf16_kv_tracks_single_stream(models):
+    """bf16 KV caches on the batched path.  The two paths add in different fp32 orders, and a
+    bf16 store can round one ulp apart (0.4%), which the model then amplifies; so the runs are
+    compared on what must hold.  While the token histories agree, the Talker logits agree
+    within the 2e-2 bound.  The first differing frame is no earlier than frame 4."""
+    name = "tiny_multistream"
+    w = MULTI_WORKLOADS[name]
+    model, d = models.get(w.spec, w.weight_seed)
+    r = run_batch(models, name, kv_bf16=True, trace=True)
+    for j, (inp, kw) in enumerate(zip(w.inputs(model), w.options_kwargs())):
+        with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=w.max_cache_steps, kv_bf16=True)) as eng:
+            eng.set_trace(True)
+            st = eng.start_stream(inp, E.GenerateOptions(**kw), E.StreamOptions(text_lookahead_tokens=1 << 30))
+            while st.next_codes_chunk(8) is not None:
+                pass
+            logits = st.talker_logits()
+            codes = st.finish_codes().codes
+        a, b = r["codes"][j], codes
+        n = min(len(a), len(b))
+        diff = np.nonzero((a[:n] != b[:n]).any(1))[0]
+        first = int(diff[0]) if diff.size else n
+        rows = min(first + 1, len(logits), len(r["logits"][j]))
+        err = float(np.abs(r["logits"][j][:rows] - logits[:rows]).max())
+        print(f"stream {j}: first differing frame {first} of {n}, logits over {rows} rows max diff {err:.2e}")
+        assert err <= LOGIT_TOL
+        assert first >= min(4, n)
