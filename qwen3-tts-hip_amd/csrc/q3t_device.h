@@ -73,7 +73,28 @@ struct GemvArgs {
   int32_t attn_part_chunks, attn_chunk, attn_pos_mode, attn_pos_const, attn_q_heads, attn_kv_heads;
   // rows = 2: a second input row x + ldx_r (res + ldr_r, out + ldo_r) against the same weights
   int32_t rows, ldx_r, ldr_r, ldo_r;
+  // Greedy token hand-off between CodePredictor groups (one stream), replacing a token
+  // selection kernel:
+  //  * producer (keys_out set; EPI_STORE): workgroup b also stores to keys_out[b] the order key
+  //    (argmax_key) of its largest output, and the outputs to trace + st->frame * trace_frame
+  //    when trace is set;
+  //  * consumer (keys_in set): the input row is g_emb[tok] (bf16 [*, K]), tok = the token of
+  //    the largest of keys_in[0 .. n_keys).  Workgroup 0 also stores that row to g_cur, adds it
+  //    to g_sum (g_first: assigns it) and writes tok to codes[frame][g_code] (g_first: the
+  //    frame's semantic token to codes[frame][0]), codes rows g_groups wide.
+  uint64_t *keys_out;
+  float *trace;
+  int64_t trace_frame;
+  const uint64_t *keys_in;
+  int32_t n_keys;
+  const uint16_t *g_emb;
+  float *g_cur, *g_sum;
+  int32_t *g_codes;
+  int32_t g_first, g_code, g_groups;
 };
+
+// Most workgroups a hand-off producer may have (keys per group).
+constexpr int kHandoffKeys = 256;
 
 struct AttnArgs {
   const float *qkv;     // [q_heads*d + 2*kv_heads*d] raw projections

@@ -303,7 +303,13 @@ struct Slot {
   hipStream_t stream = nullptr;
   hipGraphExec_t graph = nullptr;
   bool graph_traced = false;
+  bool graph_cp_greedy = false;
   SlotState *h_state = nullptr;  // pinned host mirror
+  // Greedy CodePredictor (the stream's subtalker does not sample): each LM head hands its
+  // argmax to the next group's first GEMV through cp_keys ([groups - 1][kHandoffKeys] order
+  // keys) instead of a token selection kernel.
+  uint64_t *cp_keys = nullptr;
+  bool cp_greedy = false;
 };
 
 // Per-stream device buffers for all slots, laid out as rows: slot i's buffer is
@@ -324,6 +330,7 @@ struct Pools {
         *logits_c = nullptr, *x_c = nullptr, *cp_prefix = nullptr, *cp_in = nullptr, *cur = nullptr,
         *emb_sum = nullptr, *trailing = nullptr, *attn_part = nullptr, *trace_t = nullptr, *trace_c = nullptr;
   int32_t *codes = nullptr;
+  uint64_t *cp_keys = nullptr;                          // [n][groups - 1][kHandoffKeys]
   SlotState *st = nullptr;
   SlotParams *prm = nullptr;
   int32_t *row_on = nullptr;                            // [n] rows a batched launch covers
@@ -383,16 +390,31 @@ struct Engine {
   }
 
   // One decoder-stack step for one position (decode.rs:951-1001 / 1300-1475).
+  // handoff: layer 0's QKV GEMV takes its input row from a hand-off (GemvArgs::keys_in and
+  // the g_* fields of *handoff); `in` is then the row its workgroup 0 stores (g_cur).
   void stack_step(const StackW &w, char *kc, char *vc, const float *in, float *x, Slot &sl, int pos_mode,
-                  int pos_const, int skip, hipStream_t s) {
+                  int pos_const, int skip, hipStream_t s, const GemvArgs *handoff = nullptr) {
     const Dims &d = w.d;
     const bool nt = &w == &talker;
     const size_t cache_layer = (size_t)d.kv_heads * w.cap * d.head_dim * (kv_bf16 ? 2 : 4);
     for (int l = 0; l < d.layers; ++l) {
       const LayerW &L = w.layers[l];
       const float *src = l == 0 ? in : x;
-      gemv(EPI_STORE, true, L.qkv, src, L.g_in, d.eps, nullptr, nullptr, sl.qkv, d.qkv_rows(), d.hidden, skip,
-           sl.st, s, nt);
+      if (l == 0 && handoff) {
+        GemvArgs a = *handoff;
+        a.W = L.qkv;
+        a.gamma = L.g_in;
+        a.eps = d.eps;
+        a.out = sl.qkv;
+        a.N = d.qkv_rows();
+        a.K = d.hidden;
+        a.skip = skip;
+        a.st = sl.st;
+        hip_check(launch_gemv(EPI_STORE, true, nt, a, s), "launch_gemv(hand-off)");
+      } else {
+        gemv(EPI_STORE, true, L.qkv, src, L.g_in, d.eps, nullptr, nullptr, sl.qkv, d.qkv_rows(), d.hidden, skip,
+             sl.st, s, nt);
+      }
       // The Talker's attention spans many chunks: partials, merged by the O projection.  The
       // CodePredictor's 16-row cache is one chunk: direct output.
       const int partial = attn_chunks(w.cap) > 1 ? 1 : 0;
@@ -533,23 +555,65 @@ struct Engine {
       ldin = Hc;
     }
     const float *x_pos1 = cp_prefix_pass(in, ldin, sl, s);
+    // Greedy: groups 0 .. nac-2 hand their token to the next group's first GEMV; the last
+    // group's selection kernel also writes the next Talker input.
+    const bool fused = sl.cp_greedy && handoff_ok();
     for (int g = 0; g < nac; ++g) {
       if (g > 0) {
         const float *in = sl.cur;
+        GemvArgs h{};
+        if (fused) {
+          h.keys_in = sl.cp_keys + (size_t)(g - 1) * kHandoffKeys;
+          h.n_keys = gemv_grid_for(Vc, Hc);
+          h.g_emb = cp_emb + (size_t)(g - 1) * Vc * Ht;
+          h.g_cur = sl.cur;
+          h.g_sum = sl.emb_sum;
+          h.g_codes = sl.codes;
+          h.g_first = g == 1;
+          h.g_code = g;
+          h.g_groups = groups;
+        }
         if (has_proj) {
-          gemv(EPI_BIAS, false, proj_w, sl.cur, nullptr, 0.f, nullptr, proj_b, sl.cp_in + 2 * Hc, Hc, Ht,
-               SKIP_DONE, sl.st, s);
+          GemvArgs a = h;
+          a.W = proj_w;
+          a.x = sl.cur;
+          a.bias = proj_b;
+          a.out = sl.cp_in + 2 * Hc;
+          a.N = Hc;
+          a.K = Ht;
+          a.skip = SKIP_DONE;
+          a.st = sl.st;
+          hip_check(launch_gemv(EPI_BIAS, false, false, a, s), "launch_gemv(projection)");
           in = sl.cp_in + 2 * Hc;
         }
-        stack_step(cp, sl.c_k, sl.c_v, in, sl.x_c, sl, POS_CONST, g + 1, SKIP_DONE, s);
+        stack_step(cp, sl.c_k, sl.c_v, in, sl.x_c, sl, POS_CONST, g + 1, SKIP_DONE, s,
+                   fused && !has_proj ? &h : nullptr);
       }
-      gemv(EPI_STORE, true, lm_heads + (size_t)g * Vc * Hc, g == 0 ? x_pos1 : sl.x_c, c_norm, cd.eps, nullptr,
-           nullptr, sl.logits_c, Vc, Hc, SKIP_DONE, sl.st, s);
-      SelectCpArgs a{sl.logits_c, cp_emb + (size_t)g * Vc * Ht, sl.cur, sl.emb_sum, sl.codes,
-                     trace ? sl.trace_c : nullptr, sl.t_in, codec_emb, sl.trailing, sl.st, sl.prm, Vc, Ht, groups,
-                     g};
-      hip_check(launch_select_cp(a, s), "launch_select_cp");
+      GemvArgs a{lm_heads + (size_t)g * Vc * Hc, g == 0 ? x_pos1 : sl.x_c, c_norm, nullptr, nullptr, sl.logits_c,
+                 Vc, Hc, cd.eps, SKIP_DONE, sl.st};
+      if (fused && g < nac - 1) {
+        a.keys_out = sl.cp_keys + (size_t)g * kHandoffKeys;
+        if (trace) {
+          a.trace = sl.trace_c + (size_t)g * Vc;
+          a.trace_frame = (int64_t)(groups - 1) * Vc;
+        }
+        hip_check(launch_gemv(EPI_STORE, true, false, a, s), "launch_gemv(lm_head hand-off)");
+        continue;
+      }
+      hip_check(launch_gemv(EPI_STORE, true, false, a, s), "launch_gemv(lm_head)");
+      SelectCpArgs sa{sl.logits_c, cp_emb + (size_t)g * Vc * Ht, sl.cur, sl.emb_sum, sl.codes,
+                      trace ? sl.trace_c : nullptr, sl.t_in, codec_emb, sl.trailing, sl.st, sl.prm, Vc, Ht, groups,
+                      g};
+      hip_check(launch_select_cp(sa, s), "launch_select_cp");
     }
+  }
+
+  // The greedy hand-off covers the CodePredictor's shapes: LM heads over K = Hc in 512, 1024
+  // or 2048 with at most kHandoffKeys workgroups, and an input row (Ht wide with the
+  // projection, else Hc) of 512, 1024 or 2048.
+  bool handoff_ok() const {
+    auto k_ok = [](int k) { return k == 512 || k == 1024 || k == 2048; };
+    return k_ok(cd.hidden) && k_ok(talker_hidden) && gemv_grid_for(cd.vocab, cd.hidden) <= kHandoffKeys;
   }
 
   // ----- stream rows: the batched frame over slots 0..rows-1, masked by pools.row_on -----
@@ -751,6 +815,7 @@ void alloc_pools(Engine &e, int n) {
   p.trailing = fz(p.trailing_row);
   p.attn_part = fz(p.part_row);
   p.codes = (int32_t *)zeroed((size_t)p.codes_row * n * 4);
+  p.cp_keys = (uint64_t *)zeroed((size_t)n * (e.groups - 1) * kHandoffKeys * 8);
   p.st = (SlotState *)zeroed(sizeof(SlotState) * n);
   p.prm = (SlotParams *)zeroed(sizeof(SlotParams) * n);
   p.row_on = (int32_t *)zeroed(sizeof(int32_t) * n);
@@ -787,6 +852,7 @@ void alloc_pools(Engine &e, int n) {
     sl.attn_part = p.attn_part + (size_t)i * p.part_row;
     sl.attn_part_chunks = p.part_chunks;
     sl.codes = p.codes + (size_t)i * p.codes_row;
+    sl.cp_keys = p.cp_keys + (size_t)i * (e.groups - 1) * kHandoffKeys;
     sl.st = p.st + i;
     sl.prm = p.prm + i;
     sl.h_state = p.h_states + i;
@@ -806,7 +872,7 @@ void free_pools(Engine &e) {
   void *ptrs[] = {p.t_k,      p.t_v,     p.c_k,   p.c_v,      p.x_t,      p.t_in,    p.qkv,  p.attn,
                   p.act,      p.logits_t, p.logits_c, p.x_c,  p.cp_prefix, p.cp_in,  p.cur,  p.emb_sum,
                   p.trailing, p.attn_part, p.trace_t, p.trace_c, p.codes,  p.st,      p.prm,  p.row_on,
-                  p.px,       p.pqkv,    p.pattn, p.pact,     p.pinv};
+                  p.px,       p.pqkv,    p.pattn, p.pact,     p.pinv,    p.cp_keys};
   for (void *q : ptrs)
     if (q) (void)hipFree(q);
   if (p.h_states) (void)hipHostFree(p.h_states);
@@ -885,7 +951,7 @@ void sync_state(Slot &s) {
 
 void run_frames(Engine &e, Slot &s, int n) {
   if (e.use_graph) {
-    if (!s.graph || s.graph_traced != (bool)e.trace) {
+    if (!s.graph || s.graph_traced != (bool)e.trace || s.graph_cp_greedy != s.cp_greedy) {
       if (s.graph) {
         HIPC(hipGraphExecDestroy(s.graph));
         s.graph = nullptr;
@@ -904,6 +970,7 @@ void run_frames(Engine &e, Slot &s, int n) {
       (void)hipGraphDestroy(g);
       hip_check(err, "hipGraphInstantiate");
       s.graph_traced = (bool)e.trace;
+      s.graph_cp_greedy = s.cp_greedy;
     }
     for (int i = 0; i < n; ++i) HIPC(hipGraphLaunch(s.graph, s.stream));
   } else {
@@ -1172,6 +1239,7 @@ void stage_stream(Engine &e, int slot, int row0, const q3t_stream_input &in, con
   pr.seed_hi = (uint32_t)(o->seed >> 32);
   pr.trace = e.trace;
   pr.codec_eos = e.codec_eos;
+  sl.cp_greedy = !o->subtalker_dosample;
   // Pageable sources: hipMemcpy returns once the host copy is taken.
   HIPC(hipStreamSynchronize(s));
   HIPC(hipMemcpy(sl.st, &st0, sizeof(SlotState), hipMemcpyHostToDevice));
@@ -1409,6 +1477,7 @@ Slot &hook_slot(Engine &e, int prefill_steps, int max_frames) {
   SlotParams pr{};
   pr.repetition_penalty = 1.0f;
   pr.codec_eos = e.codec_eos;
+  s.cp_greedy = true;
   HIPC(hipMemcpy(s.st, &st0, sizeof st0, hipMemcpyHostToDevice));
   HIPC(hipMemcpy(s.prm, &pr, sizeof pr, hipMemcpyHostToDevice));
   return s;

@@ -63,6 +63,45 @@ __device__ __forceinline__ float wave_max(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+// Argmax as a 64-bit maximum: order_key(v, i) = (v's bits mapped to an unsigned order) << 32 |
+// (2^32 - 1 - i), so the largest key is the largest value and, among equal values, the lowest
+// index.  Values that block_argmax never picks (NaN, -inf, -FLT_MAX) map to 0, which is also
+// the empty key; key_token(0) = 0, block_argmax's answer when nothing beats -FLT_MAX.
+__device__ __forceinline__ uint64_t order_key(float v, int idx) {
+  if (!(v > -FLT_MAX)) return 0;
+  uint32_t u = __float_as_uint(v);
+  if (u == 0x80000000u) u = 0;  // -0 ties with +0
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
+}
+
+__device__ __forceinline__ int key_token(uint64_t key) {
+  return key ? (int)(0xffffffffu - (uint32_t)(key & 0xffffffffu)) : 0;
+}
+
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  const int lo = (int)(uint32_t)v, hi = (int)(uint32_t)(v >> 32);
+  const uint32_t plo = (uint32_t)__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROWS, 0xf, false);
+  const uint32_t phi = (uint32_t)__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROWS, 0xf, false);
+  return ((uint64_t)phi << 32) | plo;
+}
+
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// Largest key of the wave, in every lane (same permutation sequence as wave_max).
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  v = umax64(v, dpp_u64<0xB1>(v));
+  v = umax64(v, dpp_u64<0x4E>(v));
+  v = umax64(v, dpp_u64<0x141>(v));
+  v = umax64(v, dpp_u64<0x140>(v));
+  v = umax64(v, dpp_u64<0x142, 0xa>(v));
+  v = umax64(v, dpp_u64<0x143, 0xc>(v));
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 63);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), 63);
+  return ((uint64_t)hi << 32) | lo;
+}
+
 __device__ __forceinline__ bool skip_work(const SlotState *st, int mode) {
   if (mode == SKIP_NEVER) return false;
   if (st->done) return true;
@@ -108,9 +147,12 @@ __device__ void merge_attention(const GemvArgs &a, float *xs);
 // ATTN = the input vector is the merge of attention partials (see merge_attention).
 // MR = input rows (1, or 2: row 1 at x + ldx_r, res + ldr_r, out + ldo_r) against the same
 // weight loads.
-template <int EPI, bool NORM, int KC, int RW, bool NT, bool ATTN = false, int MR = 1>
+// HO = greedy token hand-off (GemvArgs::keys_out / keys_in): 1 producer, 2 consumer.
+template <int EPI, bool NORM, int KC, int RW, bool NT, bool ATTN = false, int MR = 1, int HO = 0>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   static_assert(!ATTN || MR == 1, "the attention merge feeds one row");
+  static_assert(HO == 0 || (MR == 1 && !ATTN), "the hand-off feeds one row");
+  static_assert(HO != 1 || EPI == EPI_STORE, "the hand-off producer stores its outputs");
   if (skip_work(a.st, a.skip)) return;
   constexpr int K = KC * 512;
   constexpr int NR = (EPI == EPI_SWIGLU) ? 2 * RW : RW;
@@ -118,6 +160,18 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   const int wave = threadIdx.x >> 6;
   const int unit0 = (blockIdx.x * 4 + wave) * RW;
   __shared__ float xs[ATTN ? K : 1];
+  __shared__ uint64_t wkeys[HO == 1 ? 4 : 1];
+
+  // Hand-off consumer: the producer's keys are loaded first (4 per lane), so that they are in
+  // flight together with the weights.
+  uint64_t kin[HO == 2 ? 4 : 1];
+  if constexpr (HO == 2) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = lane + 64 * j;
+      kin[j] = a.keys_in[min(i, a.n_keys - 1)];
+    }
+  }
 
   // Load order: activations (and the norm gain), then every weight row of this wave, then
   // nothing else until the arithmetic.  The norm then only waits for the small activation
@@ -127,6 +181,15 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 #pragma unroll
   for (int c = 0; c < KC; ++c) {
     if constexpr (ATTN) break;
+    if constexpr (HO == 2) {
+      if constexpr (NORM) {
+        const float4 *pg = reinterpret_cast<const float4 *>(a.gamma + c * 512 + lane * 8);
+        const float4 g0 = pg[0], g1 = pg[1];
+        gv[c][0] = g0.x; gv[c][1] = g0.y; gv[c][2] = g0.z; gv[c][3] = g0.w;
+        gv[c][4] = g1.x; gv[c][5] = g1.y; gv[c][6] = g1.z; gv[c][7] = g1.w;
+      }
+      continue;
+    }
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       const float4 *px = reinterpret_cast<const float4 *>(a.x + m * a.ldx_r + c * 512 + lane * 8);
@@ -162,6 +225,43 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     for (int c = 0; c < KC; ++c) w[r][c] = load_w<NT>(pw + c * 64);
   }
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (HO == 2) {
+    // Out-of-range key slots repeat the last key, which changes no maximum.
+    const uint64_t best = wave_max_u64(umax64(umax64(kin[0], kin[1]), umax64(kin[2], kin[3])));
+    const int tok = key_token(best);
+    const uint4 *pe = reinterpret_cast<const uint4 *>(a.g_emb + (size_t)tok * K) + lane;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      const uint4 e = pe[c * 64];
+      xv[0][c][0] = bf_lo(e.x); xv[0][c][1] = bf_hi(e.x); xv[0][c][2] = bf_lo(e.y); xv[0][c][3] = bf_hi(e.y);
+      xv[0][c][4] = bf_lo(e.z); xv[0][c][5] = bf_hi(e.z); xv[0][c][6] = bf_lo(e.w); xv[0][c][7] = bf_hi(e.w);
+    }
+    if (blockIdx.x == 0 && wave == 0) {
+      const int frame = a.st->frame;
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        const int i = c * 512 + lane * 8;
+        float4 *pc = reinterpret_cast<float4 *>(a.g_cur + i);
+        float4 *ps = reinterpret_cast<float4 *>(a.g_sum + i);
+        const float *e = xv[0][c];
+        float4 s0 = make_float4(e[0], e[1], e[2], e[3]), s1 = make_float4(e[4], e[5], e[6], e[7]);
+        pc[0] = s0;
+        pc[1] = s1;
+        if (!a.g_first) {
+          const float4 o0 = ps[0], o1 = ps[1];
+          s0 = make_float4(o0.x + e[0], o0.y + e[1], o0.z + e[2], o0.w + e[3]);
+          s1 = make_float4(o1.x + e[4], o1.y + e[5], o1.z + e[6], o1.w + e[7]);
+        }
+        ps[0] = s0;
+        ps[1] = s1;
+      }
+      if (lane == 0) {
+        int32_t *codes = a.g_codes + (size_t)frame * a.g_groups;
+        codes[a.g_code] = tok;
+        if (a.g_first) codes[0] = a.st->semantic;
+      }
+    }
+  }
   if constexpr (ATTN) {
     merge_attention(a, xs);
     __syncthreads();
@@ -198,6 +298,24 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
       for (int c = 0; c < KC; ++c) s += dot8(w[r][c], xv[m][c]);
       acc[m][r] = wave_sum(s);
     }
+
+  if constexpr (HO == 1) {
+    // acc is wave-uniform: the wave's best key, then the workgroup's, in a fixed order.
+    uint64_t best = 0;
+#pragma unroll
+    for (int r = 0; r < RW; ++r)
+      if (unit0 + r < a.N) best = umax64(best, order_key(acc[0][r], unit0 + r));
+    if (lane == 0) wkeys[wave] = best;
+    if (a.trace) {
+      float *tr = a.trace + (size_t)a.st->frame * a.trace_frame;
+#pragma unroll
+      for (int r = 0; r < RW; ++r)
+        if (lane == r && unit0 + r < a.N) tr[unit0 + r] = acc[0][r];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+      a.keys_out[blockIdx.x] = umax64(umax64(wkeys[0], wkeys[1]), umax64(wkeys[2], wkeys[3]));
+  }
 
 #pragma unroll
   for (int m = 0; m < MR; ++m)
@@ -1479,10 +1597,47 @@ static void launch_timed(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_
 // Weight loads in flight per lane are capped at kMaxLoads (4 VGPRs each).
 constexpr int kMaxLoads = 24;
 
+// Rows per wave: spread the matrix over ~256 workgroups (one per CU, one wave per SIMD)
+// with every weight load of the launch issued up front; when that needs more than
+// kMaxLoads loads per lane, use more workgroups instead.  The result is one of 1, 2, 3, 4, 6
+// that fits kMaxLoads.
+static int gemv_rows_per_wave(int N, int KC, int epi) {
+  const int pu = (epi == EPI_SWIGLU) ? 2 : 1;
+  int rw = (N + 1023) / 1024;
+  const int cap_rw = kMaxLoads / (pu * KC);
+  if (rw > cap_rw) rw = std::max(1, cap_rw);
+  if (rw == 5) rw = 6;
+  if (rw > 6) rw = 6;
+  while (rw > 1 && rw * pu * KC > kMaxLoads) rw = rw == 6 ? 4 : rw - 1;
+  return rw;
+}
+
+static int gemv_grid(int N, int K, int epi) {
+  const int units = 4 * gemv_rows_per_wave(N, K / 512, epi);
+  return (N + units - 1) / units;
+}
+
+int gemv_grid_for(int N, int K) { return gemv_grid(N, K, EPI_STORE); }
+
 template <int EPI, bool NORM, int KC, int RW, bool NT>
 static void gemv_launch(const GemvArgs &a, hipStream_t s, const LaunchTiming *t) {
   const int units = 4 * RW;
   const dim3 grid((a.N + units - 1) / units);
+  // Hand-off variants: the CodePredictor's LM heads (producer; store + norm) and the first
+  // GEMV of the next group (consumer; its QKV with norm, or the bias-only input projection).
+  if constexpr (!NT && KC <= 4 && KC != 3 && ((EPI == EPI_STORE && NORM) || (EPI == EPI_BIAS && !NORM))) {
+    if (a.keys_out) {
+      if constexpr (EPI == EPI_STORE) {
+        if (grid.x > (unsigned)kHandoffKeys) return;  // launch_gemv checked the grid
+        launch_timed(k_gemv<EPI, NORM, KC, RW, NT, false, 1, 1>, grid, dim3(256), 0, s, t, a);
+      }
+      return;
+    }
+    if (a.keys_in) {
+      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, false, 1, 2>, grid, dim3(256), 0, s, t, a);
+      return;
+    }
+  }
   if constexpr (EPI == EPI_RESIDUAL && !NORM && KC <= 8) {
     if (a.attn_part) {
       launch_timed(k_gemv<EPI, NORM, KC, RW, NT, true>, grid, dim3(256), 0, s, t, a);
@@ -1500,16 +1655,8 @@ static void gemv_launch(const GemvArgs &a, hipStream_t s, const LaunchTiming *t)
 
 template <int EPI, bool NORM, int KC, bool NT>
 static hipError_t gemv_rw(const GemvArgs &a, hipStream_t s, const LaunchTiming *t) {
-  // Rows per wave: spread the matrix over ~256 workgroups (one per CU, one wave per SIMD)
-  // with every weight load of the launch issued up front; when that needs more than
-  // kMaxLoads loads per lane, use more workgroups instead.
   constexpr int pu = (EPI == EPI_SWIGLU) ? 2 : 1;
-  int rw = (a.N + 1023) / 1024;
-  const int cap_rw = kMaxLoads / (pu * KC);
-  if (rw > cap_rw) rw = std::max(1, cap_rw);
-  if (rw == 5) rw = 6;
-  if (rw > 6) rw = 6;
-  switch (rw) {
+  switch (gemv_rows_per_wave(a.N, KC, EPI)) {
     case 6:
       if constexpr (6 * pu * KC <= kMaxLoads) { gemv_launch<EPI, NORM, KC, 6, NT>(a, s, t); break; }
       [[fallthrough]];
@@ -1556,6 +1703,15 @@ static hipError_t gemv_epi(int epi, bool norm, const GemvArgs &a, hipStream_t s,
 hipError_t launch_gemv(int epi, bool norm, bool streaming, const GemvArgs &a, hipStream_t s,
                        const LaunchTiming *t) {
   if (!gemv_supports_k(a.K) || a.N <= 0) return hipErrorInvalidValue;
+  if (a.keys_out || a.keys_in) {
+    const bool shape_ok = !streaming && a.rows <= 1 && !a.attn_part && !(a.keys_out && a.keys_in) &&
+                          (a.K == 512 || a.K == 1024 || a.K == 2048) && a.st;
+    const bool producer_ok = epi == EPI_STORE && norm && gemv_grid(a.N, a.K, epi) <= kHandoffKeys;
+    const bool consumer_ok = ((epi == EPI_STORE && norm) || (epi == EPI_BIAS && !norm)) && a.n_keys >= 1 &&
+                             a.n_keys <= kHandoffKeys && a.g_emb && a.g_cur && a.g_sum && a.g_codes &&
+                             a.g_code >= 1 && a.g_code < a.g_groups;
+    if (!shape_ok || (a.keys_out ? !producer_ok : !consumer_ok)) return hipErrorInvalidValue;
+  }
   if (a.rows > 1 && (a.rows != 2 || streaming || a.attn_part || a.K > 6 * 512 || a.ldx_r % 4 ||
                      (epi == EPI_RESIDUAL && !a.ldr_r) || !a.ldo_r))
     return hipErrorInvalidValue;

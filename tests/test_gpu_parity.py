@@ -111,6 +111,22 @@ def test_greedy_repetition_penalty_matches_oracle(models):
     check_talker_logits(r["talker_logits"], fx, same)
 
 
+def test_sampled_talker_with_greedy_subtalker_matches_oracle(models):
+    """Talker sampling (top-k 50, T 0.9, penalty 1.05) with a greedy CodePredictor: the greedy
+    groups hand their tokens from one LM head to the next group's first GEMV, while the
+    Talker's token still goes through its sampler."""
+    w = WORKLOADS["tiny_greedy"]
+    model, _ = models.get(w.spec)
+    inputs = w.inputs(model)
+    opts = E.GenerateOptions.greedy(16, do_sample=True, top_k=50, top_p=1.0, temperature=0.9,
+                                    repetition_penalty=1.05, seed=11)
+    r = run(models, "tiny_greedy", options=opts)
+    fx = _as_fixture(_oracle_rollout(model, inputs, opts, w.max_cache_steps))
+    same = check_codes(r["codes"], r["eos"], fx, allow_ties=False)
+    check_talker_logits(r["talker_logits"], fx, same)
+    print(f"sampled Talker + greedy CodePredictor: {same} frames identical")
+
+
 def test_bf16_kv_cache_matches_bf16_oracle(models):
     """KV stored as bf16 (rounded once at the store), against the oracle's bf16-KV model."""
     w = WORKLOADS["tiny_greedy"]
