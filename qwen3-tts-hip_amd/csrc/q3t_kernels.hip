@@ -153,7 +153,6 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   static_assert(!ATTN || MR == 1, "the attention merge feeds one row");
   static_assert(HO == 0 || (MR == 1 && !ATTN), "the hand-off feeds one row");
   static_assert(HO != 1 || EPI == EPI_STORE, "the hand-off producer stores its outputs");
-  if (skip_work(a.st, a.skip)) return;
   constexpr int K = KC * 512;
   constexpr int NR = (EPI == EPI_SWIGLU) ? 2 * RW : RW;
   const int lane = threadIdx.x & 63;
@@ -213,6 +212,9 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     if constexpr (EPI == EPI_RESIDUAL) eadd[m] = a.res[m * a.ldr_r + min(unit0 + min(lane, RW - 1), a.N - 1)];
     if constexpr (EPI == EPI_BIAS) eadd[m] = a.bias[min(unit0 + min(lane, RW - 1), a.N - 1)];
   }
+  // Keep the activation loads ahead of the weight loads in issue order: loads complete in
+  // order, so the norm can then start before the weights have arrived.
+  __builtin_amdgcn_sched_barrier(0);
   // Rows past the end (a partial last workgroup) load the last row instead of branching;
   // their results are never stored.
   uint4 w[NR][KC];
@@ -225,6 +227,10 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
     for (int c = 0; c < KC; ++c) w[r][c] = load_w<NT>(pw + c * 64);
   }
   __builtin_amdgcn_sched_barrier(0);
+  // The stream-state check comes after the loads (every address above is valid whatever the
+  // state), so its round trip overlaps theirs instead of preceding them.  Nothing is stored
+  // before it.
+  if (skip_work(a.st, a.skip)) return;
   if constexpr (HO == 2) {
     // Out-of-range key slots repeat the last key, which changes no maximum.
     const uint64_t best = wave_max_u64(umax64(umax64(kin[0], kin[1]), umax64(kin[2], kin[3])));
@@ -402,12 +408,17 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   static_assert(G >= 1 && G <= 2, "query heads per KV head");
   static_assert(CH % 16 == 0 && CH <= kAttnMaxChunk, "chunk length");
   const int row = blockIdx.z;
-  if (a.row_on && !a.row_on[row]) return;
   const SlotState *st = a.st + row;
-  if (skip_work(st, a.skip)) return;
+  // A position given by the launch needs no state: the row mask and the stream state are
+  // then checked after the loads below are issued (they are valid for any state).
+  const bool frame_pos = a.pos_mode == POS_TALKER_FRAME;
+  if (frame_pos) {
+    if (a.row_on && !a.row_on[row]) return;
+    if (skip_work(st, a.skip)) return;
+  }
   const int h = blockIdx.x;
   const int c = blockIdx.y;
-  const int pos = (a.pos_mode == POS_TALKER_FRAME) ? st->prefill_steps + st->frame : a.pos_const;
+  const int pos = frame_pos ? st->prefill_steps + st->frame : a.pos_const;
   if (pos < 0 || pos >= a.cap) return;  // host validates; never index outside the cache
   const int L = pos + 1;
   const int nchunks = (L + CH - 1) / CH;
@@ -439,12 +450,19 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   // memory round trip.  Rows at or past `pos` are never used from these registers.
   const int vec = wave;
   const bool has_vec = wave < G + 2 && (wave < G || owns_pos);
-  float x0 = 0.f, x1 = 0.f;
+  const float *gain = vec < G ? a.gq : (vec == G ? a.gk : nullptr);
+  float x0 = 0.f, x1 = 0.f, g0 = 0.f, g1 = 0.f;
+  float2 cs = make_float2(0.f, 0.f);
   if (has_vec) {
     const float *src = vec < G ? qkv + (h * G + vec) * D
                                : (vec == G ? qkv + q_out + h * D : qkv + q_out + kv_out + h * D);
     x0 = src[lane];
     x1 = src[lane + 64];
+    if (gain) {
+      g0 = gain[lane];
+      g1 = gain[lane + 64];
+      cs = a.rope[(size_t)pos * (D / 2) + lane];
+    }
   }
   const int tmax = max(pos - 1, 0);
   float kpre[CH / 16][8];
@@ -460,16 +478,18 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
     vpre[i] = KvIo<KVT>::load2(vbase + (size_t)t * D + 2 * lane);
   }
   __builtin_amdgcn_sched_barrier(0);
+  if (!frame_pos) {  // workgroup-uniform: no barrier has been reached yet
+    if (a.row_on && !a.row_on[row]) return;
+    if (skip_work(st, a.skip)) return;
+  }
 
   // 1: q heads (waves 0..G-1); k and v (waves G, G+1) only where row `pos` is stored.
   if (has_vec) {
-    const float2 cs = a.rope[(size_t)pos * (D / 2) + lane];
-    const float *gain = vec < G ? a.gq : (vec == G ? a.gk : nullptr);
     if (gain) {
       const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
       const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
-      x0 = (x0 * inv) * gain[lane];
-      x1 = (x1 * inv) * gain[lane + 64];
+      x0 = (x0 * inv) * g0;
+      x1 = (x1 * inv) * g1;
       const float r0 = x0 * cs.x - x1 * cs.y;
       const float r1 = x1 * cs.x + x0 * cs.y;
       x0 = r0;
