@@ -56,6 +56,24 @@ enum Epilogue : int32_t {
   EPI_BIAS = 3,      // out[n] = acc + bias[n]
 };
 
+// Greedy token hand-off into a CodePredictor group (one stream): the group's input token is
+// the one whose order key is the largest of keys[0 .. n_keys) (the previous group's LM head
+// writes them).  Workgroup 0 of the consuming kernel also stores the group's input row to cur
+// (row tok of cur_table when set, else the embedding row emb[tok]), adds emb[tok] to sum
+// (first: assigns it) and writes the token to codes[frame][code] (first: also the frame's
+// semantic token to codes[frame][0]); codes rows are `groups` wide.
+struct TokenHandoff {
+  const uint64_t *keys;
+  int32_t n_keys;
+  const uint16_t *emb;     // [V][emb_width] bf16
+  int32_t emb_width;
+  const float *cur_table;  // [V][cur_width] or null
+  int32_t cur_width;
+  float *cur, *sum;
+  int32_t *codes;
+  int32_t first, code, groups;
+};
+
 struct GemvArgs {
   const uint16_t *W;  // [rows, K] bf16, row-major (the checkpoint's [out, in] layout)
   const float *x;     // [K]
@@ -73,24 +91,12 @@ struct GemvArgs {
   int32_t attn_part_chunks, attn_chunk, attn_pos_mode, attn_pos_const, attn_q_heads, attn_kv_heads;
   // rows = 2: a second input row x + ldx_r (res + ldr_r, out + ldo_r) against the same weights
   int32_t rows, ldx_r, ldr_r, ldo_r;
-  // Greedy token hand-off between CodePredictor groups (one stream), replacing a token
-  // selection kernel:
-  //  * producer (keys_out set; EPI_STORE): workgroup b also stores to keys_out[b] the order key
-  //    (argmax_key) of its largest output, and the outputs to trace + st->frame * trace_frame
-  //    when trace is set;
-  //  * consumer (keys_in set): the input row is g_emb[tok] (bf16 [*, K]), tok = the token of
-  //    the largest of keys_in[0 .. n_keys).  Workgroup 0 also stores that row to g_cur, adds it
-  //    to g_sum (g_first: assigns it) and writes tok to codes[frame][g_code] (g_first: the
-  //    frame's semantic token to codes[frame][0]), codes rows g_groups wide.
+  // Greedy token hand-off producer (one stream; EPI_STORE), replacing a token selection
+  // kernel: workgroup b also stores to keys_out[b] the order key (order_key) of its largest
+  // output, and the outputs to trace + st->frame * trace_frame when trace is set.
   uint64_t *keys_out;
   float *trace;
   int64_t trace_frame;
-  const uint64_t *keys_in;
-  int32_t n_keys;
-  const uint16_t *g_emb;
-  float *g_cur, *g_sum;
-  int32_t *g_codes;
-  int32_t g_first, g_code, g_groups;
 };
 
 // Most workgroups a hand-off producer may have (keys per group).
@@ -121,6 +127,11 @@ struct AttnArgs {
   int64_t kv_row, part_row;
   const int32_t *row_on;
   int32_t out_t16;      // direct output in T16 (rows <= 16) instead of out + r * ld_out
+  // Greedy hand-off (one stream, one chunk): the raw q/k/v row is qkv_table + tok * ld_table
+  // instead of qkv, tok as TokenHandoff defines it (h.keys set).
+  TokenHandoff h;
+  const float *qkv_table;
+  int64_t ld_table;
 };
 
 // Merge of split-attention partials into attention outputs, one workgroup per stream row.

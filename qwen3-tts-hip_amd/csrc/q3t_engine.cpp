@@ -371,6 +371,10 @@ struct Engine {
   uint16_t *cp_emb = nullptr;    // [groups-1][Vc][Ht]
   uint16_t *proj_w = nullptr;    // [Hc][Ht]
   float *proj_b = nullptr;
+  // Greedy hand-off tables (built at load): for CodePredictor groups 1 .. groups-2, the layer-0
+  // raw q/k/v row of every input token, [groups-2][Vc][qkv_rows], and (projection only) the
+  // projected input row, [groups-2][Vc][Hc].
+  float *cp_qkv_table = nullptr, *cp_in_table = nullptr;
   // Packed copies for the batched frame's skinny GEMMs (multi-stream engines only).
   uint16_t *codec_head_p = nullptr, *lm_heads_p = nullptr, *proj_w_p = nullptr;
   // Batched-frame activations in T16 (16 stream rows): residual streams, attention output,
@@ -390,31 +394,22 @@ struct Engine {
   }
 
   // One decoder-stack step for one position (decode.rs:951-1001 / 1300-1475).
-  // handoff: layer 0's QKV GEMV takes its input row from a hand-off (GemvArgs::keys_in and
-  // the g_* fields of *handoff); `in` is then the row its workgroup 0 stores (g_cur).
+  // handoff: layer 0 takes its raw q/k/v row from qkv_table (row = the handed-off token) in its
+  // attention kernel and runs no QKV GEMV; `in` is then the row that kernel stores
+  // (handoff->cur).
   void stack_step(const StackW &w, char *kc, char *vc, const float *in, float *x, Slot &sl, int pos_mode,
-                  int pos_const, int skip, hipStream_t s, const GemvArgs *handoff = nullptr) {
+                  int pos_const, int skip, hipStream_t s, const TokenHandoff *handoff = nullptr,
+                  const float *qkv_table = nullptr) {
     const Dims &d = w.d;
     const bool nt = &w == &talker;
     const size_t cache_layer = (size_t)d.kv_heads * w.cap * d.head_dim * (kv_bf16 ? 2 : 4);
     for (int l = 0; l < d.layers; ++l) {
       const LayerW &L = w.layers[l];
       const float *src = l == 0 ? in : x;
-      if (l == 0 && handoff) {
-        GemvArgs a = *handoff;
-        a.W = L.qkv;
-        a.gamma = L.g_in;
-        a.eps = d.eps;
-        a.out = sl.qkv;
-        a.N = d.qkv_rows();
-        a.K = d.hidden;
-        a.skip = skip;
-        a.st = sl.st;
-        hip_check(launch_gemv(EPI_STORE, true, nt, a, s), "launch_gemv(hand-off)");
-      } else {
+      const bool table = l == 0 && handoff;
+      if (!table)
         gemv(EPI_STORE, true, L.qkv, src, L.g_in, d.eps, nullptr, nullptr, sl.qkv, d.qkv_rows(), d.hidden, skip,
              sl.st, s, nt);
-      }
       // The Talker's attention spans many chunks: partials, merged by the O projection.  The
       // CodePredictor's 16-row cache is one chunk: direct output.
       const int partial = attn_chunks(w.cap) > 1 ? 1 : 0;
@@ -422,9 +417,22 @@ struct Engine {
                   sl.attn,  d.q_heads, d.kv_heads, w.cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
                   pos_mode, pos_const, skip,    kv_bf16, sl.st,  sl.attn_part, sl.attn_part_chunks,
                   attn_chunk_len(w.cap), partial};
+      if (table) {
+        aa.h = *handoff;
+        aa.qkv_table = qkv_table;
+        aa.ld_table = d.qkv_rows();
+      }
       hip_check(launch_attn_decode(aa, d.head_dim, s), "launch_attn_decode");
+      // Up to kAttnGemvMergeChunks partials are merged inside the O projection; more (caches
+      // past 1024 rows) by the merge kernel first.
+      const bool merge_in_o = partial && attn_chunks(w.cap) <= kAttnGemvMergeChunks;
+      if (partial && !merge_in_o) {
+        AttnMergeArgs ma{sl.attn_part, sl.attn, d.q_heads, d.kv_heads, sl.attn_part_chunks, attn_chunk_len(w.cap),
+                         pos_mode, pos_const, skip, d.q_out(), 0, sl.st, nullptr, 0};
+        hip_check(launch_attn_merge(ma, 1, s), "launch_attn_merge");
+      }
       GemvArgs og{L.o, sl.attn, nullptr, src, nullptr, x, d.hidden, d.q_out(), 0.f, skip, sl.st};
-      if (partial) {
+      if (merge_in_o) {
         og.x = nullptr;
         og.attn_part = sl.attn_part;
         og.attn_part_chunks = sl.attn_part_chunks;
@@ -555,39 +563,41 @@ struct Engine {
       ldin = Hc;
     }
     const float *x_pos1 = cp_prefix_pass(in, ldin, sl, s);
-    // Greedy: groups 0 .. nac-2 hand their token to the next group's first GEMV; the last
+    // Greedy (tables built): groups 0 .. nac-2 hand their token from the LM head to the next
+    // group's layer-0 attention, which reads that token's precomputed q/k/v row; the last
     // group's selection kernel also writes the next Talker input.
-    const bool fused = sl.cp_greedy && handoff_ok();
+    const bool fused = sl.cp_greedy && cp_qkv_table;
     for (int g = 0; g < nac; ++g) {
       if (g > 0) {
         const float *in = sl.cur;
-        GemvArgs h{};
         if (fused) {
-          h.keys_in = sl.cp_keys + (size_t)(g - 1) * kHandoffKeys;
-          h.n_keys = gemv_grid_for(Vc, Hc);
-          h.g_emb = cp_emb + (size_t)(g - 1) * Vc * Ht;
-          h.g_cur = sl.cur;
-          h.g_sum = sl.emb_sum;
-          h.g_codes = sl.codes;
-          h.g_first = g == 1;
-          h.g_code = g;
-          h.g_groups = groups;
+          TokenHandoff t{};
+          t.keys = sl.cp_keys + (size_t)(g - 1) * kHandoffKeys;
+          t.n_keys = gemv_grid_for(Vc, Hc);
+          t.emb = cp_emb + (size_t)(g - 1) * Vc * Ht;
+          t.emb_width = Ht;
+          t.cur = sl.cur;
+          t.sum = sl.emb_sum;
+          t.codes = sl.codes;
+          t.first = g == 1;
+          t.code = g;
+          t.groups = groups;
+          if (has_proj) {  // layer 0's input is the projected row: from its table, to cp_in row 2
+            t.cur_table = cp_in_table + (size_t)(g - 1) * Vc * Hc;
+            t.cur_width = Hc;
+            t.cur = sl.cp_in + 2 * Hc;
+            in = t.cur;
+          }
+          stack_step(cp, sl.c_k, sl.c_v, in, sl.x_c, sl, POS_CONST, g + 1, SKIP_DONE, s, &t,
+                     cp_qkv_table + (size_t)(g - 1) * Vc * cd.qkv_rows());
+        } else {
+          if (has_proj) {
+            gemv(EPI_BIAS, false, proj_w, sl.cur, nullptr, 0.f, nullptr, proj_b, sl.cp_in + 2 * Hc, Hc, Ht,
+                 SKIP_DONE, sl.st, s);
+            in = sl.cp_in + 2 * Hc;
+          }
+          stack_step(cp, sl.c_k, sl.c_v, in, sl.x_c, sl, POS_CONST, g + 1, SKIP_DONE, s);
         }
-        if (has_proj) {
-          GemvArgs a = h;
-          a.W = proj_w;
-          a.x = sl.cur;
-          a.bias = proj_b;
-          a.out = sl.cp_in + 2 * Hc;
-          a.N = Hc;
-          a.K = Ht;
-          a.skip = SKIP_DONE;
-          a.st = sl.st;
-          hip_check(launch_gemv(EPI_BIAS, false, false, a, s), "launch_gemv(projection)");
-          in = sl.cp_in + 2 * Hc;
-        }
-        stack_step(cp, sl.c_k, sl.c_v, in, sl.x_c, sl, POS_CONST, g + 1, SKIP_DONE, s,
-                   fused && !has_proj ? &h : nullptr);
       }
       GemvArgs a{lm_heads + (size_t)g * Vc * Hc, g == 0 ? x_pos1 : sl.x_c, c_norm, nullptr, nullptr, sl.logits_c,
                  Vc, Hc, cd.eps, SKIP_DONE, sl.st};
@@ -609,11 +619,12 @@ struct Engine {
   }
 
   // The greedy hand-off covers the CodePredictor's shapes: LM heads over K = Hc in 512, 1024
-  // or 2048 with at most kHandoffKeys workgroups, and an input row (Ht wide with the
-  // projection, else Hc) of 512, 1024 or 2048.
+  // or 2048 with at most kHandoffKeys workgroups, embedding rows (Ht) of at most 2048, and
+  // table GEMMs the matrix-core prefill path takes (Hc % 32 == 0, q/k/v rows % 128 == 0).
   bool handoff_ok() const {
     auto k_ok = [](int k) { return k == 512 || k == 1024 || k == 2048; };
-    return k_ok(cd.hidden) && k_ok(talker_hidden) && gemv_grid_for(cd.vocab, cd.hidden) <= kHandoffKeys;
+    return k_ok(cd.hidden) && talker_hidden <= 2048 && talker_hidden % 32 == 0 && cd.qkv_rows() % 128 == 0 &&
+           cd.vocab >= 128 && gemv_grid_for(cd.vocab, cd.hidden) <= kHandoffKeys && groups > 2;
   }
 
   // ----- stream rows: the batched frame over slots 0..rows-1, masked by pools.row_on -----
@@ -880,6 +891,51 @@ void free_pools(Engine &e) {
   p = Pools();
 }
 
+// Greedy hand-off tables: layer 0's raw q/k/v row (and, with the projection, its input row)
+// for every token of the embedding tables that feed CodePredictor groups 1 .. groups-2.  The
+// prompt-prefill GEMMs compute them (matrix cores, fp32 activations split into exact bf16
+// terms), so a table row equals the runtime GEMV's result up to fp32 summation order.
+void build_cp_tables(Engine &e) {
+  if (!e.handoff_ok()) return;
+  const Dims &cd = e.cd;
+  const int Vc = cd.vocab, Ht = e.talker_hidden, Hc = cd.hidden, Q = cd.qkv_rows(), n = e.groups - 2;
+  int64_t &t = e.device_bytes;
+  e.cp_qkv_table = dev_alloc<float>((size_t)n * Vc * Q, t);
+  if (e.has_proj) e.cp_in_table = dev_alloc<float>((size_t)n * Vc * Hc, t);
+  int64_t scratch_bytes = 0;
+  float *X = dev_alloc<float>((size_t)Vc * Ht, scratch_bytes);
+  float *inv = nullptr;
+  try {
+    inv = dev_alloc<float>((size_t)Vc, scratch_bytes);
+    for (int g = 1; g <= n; ++g) {
+      hip_check(launch_bf16_to_f32(e.cp_emb + (size_t)(g - 1) * Vc * Ht, X, (size_t)Vc * Ht, nullptr),
+                "launch_bf16_to_f32");
+      const float *src = X;
+      if (e.has_proj) {
+        GemmArgs p{};
+        p.X = X; p.ldx = Ht; p.W = e.proj_w; p.bias = e.proj_b;
+        p.Y = e.cp_in_table + (size_t)(g - 1) * Vc * Hc; p.ldy = Hc;
+        p.M = Vc; p.N = Hc; p.K = Ht;
+        hip_check(launch_gemm(EPI_BIAS, p, nullptr), "launch_gemm(projection table)");
+        src = p.Y;
+      }
+      hip_check(launch_row_rms(src, Hc, Vc, Hc, cd.eps, inv, nullptr), "launch_row_rms(table)");
+      GemmArgs q{};
+      q.X = src; q.ldx = Hc; q.row_scale = inv; q.gamma = e.cp.layers[0].g_in; q.W = e.cp.layers[0].qkv;
+      q.Y = e.cp_qkv_table + (size_t)(g - 1) * Vc * Q; q.ldy = Q;
+      q.M = Vc; q.N = Q; q.K = Hc;
+      hip_check(launch_gemm(EPI_STORE, q, nullptr), "launch_gemm(q/k/v table)");
+    }
+    HIPC(hipDeviceSynchronize());
+  } catch (...) {
+    (void)hipFree(X);
+    if (inv) (void)hipFree(inv);
+    throw;
+  }
+  (void)hipFree(X);
+  (void)hipFree(inv);
+}
+
 // Packed weight copies and T16 activations for the batched frame (engines with more than
 // one stream slot).  Packing runs on the device from the row-major copies.
 void alloc_rows(Engine &e) {
@@ -1138,6 +1194,7 @@ int q3t_engine_create(const q3t_engine_options *opts, q3t_engine **out) {
     try {
       alloc_pools(*e, nslots);
       if (nslots > 1 && e->rows_ok) alloc_rows(*e);
+      build_cp_tables(*e);
     } catch (...) {
       free_pools(*e);
       throw;
@@ -1157,7 +1214,8 @@ int q3t_engine_destroy(q3t_engine *e) {
                     e->cp.rope,     e->codec_head,   e->codec_emb,   e->t_norm,      e->c_norm,
                     e->lm_heads,    e->cp_emb,       e->proj_w,      e->proj_b,      e->talker.mats_p,
                     e->cp.mats_p,   e->codec_head_p, e->lm_heads_p,  e->proj_w_p,    e->bx_t,
-                    e->bx_c,        e->battn,        e->bact,        e->bcp_in};
+                    e->bx_c,        e->battn,        e->bact,        e->bcp_in,      e->cp_qkv_table,
+                    e->cp_in_table};
     for (void *p : ptrs)
       if (p) (void)hipFree(p);
     delete e;
@@ -1602,7 +1660,7 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
           break;
         case 1: {  // O projection + residual (Talker layers merge attention partials first)
           GemvArgs og{W.o, s.attn, nullptr, s.act, nullptr, s.act, d.hidden, d.q_out(), 0.f, SKIP_NEVER, s.st};
-          if (nt) {
+          if (nt && attn_chunks(l.w->cap) <= kAttnGemvMergeChunks) {
             og.x = nullptr;
             og.attn_part = s.attn_part;
             og.attn_part_chunks = s.attn_part_chunks;

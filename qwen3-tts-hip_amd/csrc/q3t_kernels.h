@@ -31,6 +31,9 @@ constexpr int kMaxRows = 16;
 hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t stream,
                               const LaunchTiming *timing = nullptr, int rows = 1);
 hipError_t launch_attn_merge(const AttnMergeArgs &a, int rows, hipStream_t stream);
+// Most attention chunks the O-projection GEMV merges itself (caches up to 8 x 128 rows); the
+// partials of a longer cache are merged by launch_attn_merge first.
+constexpr int kAttnGemvMergeChunks = 8;
 int attn_max_cache_steps(int q_heads, int kv_heads);
 // Key rows per attention workgroup for a cache of `cap` rows, and the resulting number of
 // chunks (partials the workspace must hold per head).
@@ -50,6 +53,9 @@ hipError_t launch_gemm_skinny(int epi, bool norm, const GemmArgs &a, hipStream_t
 hipError_t launch_pack_weights(const uint16_t *src, uint16_t *dst, int rows, int K, hipStream_t stream);
 // inv_rms[m] = 1 / sqrt(mean(X[m]^2) + eps).
 hipError_t launch_row_rms(const float *X, int ldx, int M, int K, float eps, float *inv_rms, hipStream_t stream);
+
+// dst[i] = src[i] (bf16 -> fp32, exact).
+hipError_t launch_bf16_to_f32(const uint16_t *src, float *dst, size_t n, hipStream_t stream);
 
 // Prefill attention: q/k norm + RoPE + KV store for P rows, then causal attention.
 hipError_t launch_prefill_attention(const PrefillAttnArgs &a, hipStream_t stream);

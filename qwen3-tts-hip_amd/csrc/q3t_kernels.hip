@@ -147,30 +147,18 @@ __device__ void merge_attention(const GemvArgs &a, float *xs);
 // ATTN = the input vector is the merge of attention partials (see merge_attention).
 // MR = input rows (1, or 2: row 1 at x + ldx_r, res + ldr_r, out + ldo_r) against the same
 // weight loads.
-// HO = greedy token hand-off (GemvArgs::keys_out / keys_in): 1 producer, 2 consumer.
-template <int EPI, bool NORM, int KC, int RW, bool NT, bool ATTN = false, int MR = 1, int HO = 0>
+// HO = greedy token hand-off producer (GemvArgs::keys_out).
+template <int EPI, bool NORM, int KC, int RW, bool NT, bool ATTN = false, int MR = 1, bool HO = false>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   static_assert(!ATTN || MR == 1, "the attention merge feeds one row");
-  static_assert(HO == 0 || (MR == 1 && !ATTN), "the hand-off feeds one row");
-  static_assert(HO != 1 || EPI == EPI_STORE, "the hand-off producer stores its outputs");
+  static_assert(!HO || (MR == 1 && !ATTN && EPI == EPI_STORE), "the hand-off producer stores one row");
   constexpr int K = KC * 512;
   constexpr int NR = (EPI == EPI_SWIGLU) ? 2 * RW : RW;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int unit0 = (blockIdx.x * 4 + wave) * RW;
   __shared__ float xs[ATTN ? K : 1];
-  __shared__ uint64_t wkeys[HO == 1 ? 4 : 1];
-
-  // Hand-off consumer: the producer's keys are loaded first (4 per lane), so that they are in
-  // flight together with the weights.
-  uint64_t kin[HO == 2 ? 4 : 1];
-  if constexpr (HO == 2) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = lane + 64 * j;
-      kin[j] = a.keys_in[min(i, a.n_keys - 1)];
-    }
-  }
+  __shared__ uint64_t wkeys[HO ? 4 : 1];
 
   // Load order: activations (and the norm gain), then every weight row of this wave, then
   // nothing else until the arithmetic.  The norm then only waits for the small activation
@@ -180,15 +168,6 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 #pragma unroll
   for (int c = 0; c < KC; ++c) {
     if constexpr (ATTN) break;
-    if constexpr (HO == 2) {
-      if constexpr (NORM) {
-        const float4 *pg = reinterpret_cast<const float4 *>(a.gamma + c * 512 + lane * 8);
-        const float4 g0 = pg[0], g1 = pg[1];
-        gv[c][0] = g0.x; gv[c][1] = g0.y; gv[c][2] = g0.z; gv[c][3] = g0.w;
-        gv[c][4] = g1.x; gv[c][5] = g1.y; gv[c][6] = g1.z; gv[c][7] = g1.w;
-      }
-      continue;
-    }
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       const float4 *px = reinterpret_cast<const float4 *>(a.x + m * a.ldx_r + c * 512 + lane * 8);
@@ -231,43 +210,6 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   // state), so its round trip overlaps theirs instead of preceding them.  Nothing is stored
   // before it.
   if (skip_work(a.st, a.skip)) return;
-  if constexpr (HO == 2) {
-    // Out-of-range key slots repeat the last key, which changes no maximum.
-    const uint64_t best = wave_max_u64(umax64(umax64(kin[0], kin[1]), umax64(kin[2], kin[3])));
-    const int tok = key_token(best);
-    const uint4 *pe = reinterpret_cast<const uint4 *>(a.g_emb + (size_t)tok * K) + lane;
-#pragma unroll
-    for (int c = 0; c < KC; ++c) {
-      const uint4 e = pe[c * 64];
-      xv[0][c][0] = bf_lo(e.x); xv[0][c][1] = bf_hi(e.x); xv[0][c][2] = bf_lo(e.y); xv[0][c][3] = bf_hi(e.y);
-      xv[0][c][4] = bf_lo(e.z); xv[0][c][5] = bf_hi(e.z); xv[0][c][6] = bf_lo(e.w); xv[0][c][7] = bf_hi(e.w);
-    }
-    if (blockIdx.x == 0 && wave == 0) {
-      const int frame = a.st->frame;
-#pragma unroll
-      for (int c = 0; c < KC; ++c) {
-        const int i = c * 512 + lane * 8;
-        float4 *pc = reinterpret_cast<float4 *>(a.g_cur + i);
-        float4 *ps = reinterpret_cast<float4 *>(a.g_sum + i);
-        const float *e = xv[0][c];
-        float4 s0 = make_float4(e[0], e[1], e[2], e[3]), s1 = make_float4(e[4], e[5], e[6], e[7]);
-        pc[0] = s0;
-        pc[1] = s1;
-        if (!a.g_first) {
-          const float4 o0 = ps[0], o1 = ps[1];
-          s0 = make_float4(o0.x + e[0], o0.y + e[1], o0.z + e[2], o0.w + e[3]);
-          s1 = make_float4(o1.x + e[4], o1.y + e[5], o1.z + e[6], o1.w + e[7]);
-        }
-        ps[0] = s0;
-        ps[1] = s1;
-      }
-      if (lane == 0) {
-        int32_t *codes = a.g_codes + (size_t)frame * a.g_groups;
-        codes[a.g_code] = tok;
-        if (a.g_first) codes[0] = a.st->semantic;
-      }
-    }
-  }
   if constexpr (ATTN) {
     merge_attention(a, xs);
     __syncthreads();
@@ -305,7 +247,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
       acc[m][r] = wave_sum(s);
     }
 
-  if constexpr (HO == 1) {
+  if constexpr (HO) {
     // acc is wave-uniform: the wave's best key, then the workgroup's, in a fixed order.
     uint64_t best = 0;
 #pragma unroll
@@ -400,9 +342,49 @@ struct KvIo<uint16_t> {
 //      chunks in chunk order after the kernel boundary, so no workgroup fences or waits.
 // ---------------------------------------------------------------------------------------
 constexpr int kAttnMaxChunk = 128;
-constexpr int kAttnMaxChunks = 8;
+constexpr int kAttnMaxChunks = kAttnGemvMergeChunks;
 
-template <int D, int G, typename KVT, int CH>
+// The stores of a TokenHandoff, by one 256-thread workgroup: thread t covers elements
+// 4t .. 4t+3 and 1024 + 4t .. (widths up to 2048).  handoff_load issues every load (the
+// embedding row, the running sum, the table row), handoff_store the sums and stores.
+__device__ __forceinline__ void handoff_load(const TokenHandoff &h, int tok, float4 *e, float4 *sum, float4 *cur) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int i = 4 * (int)threadIdx.x + 1024 * j;
+    e[j] = sum[j] = cur[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (i < h.emb_width) {
+      const uint2 w = *reinterpret_cast<const uint2 *>(h.emb + (size_t)tok * h.emb_width + i);
+      e[j] = make_float4(bf_lo(w.x), bf_hi(w.x), bf_lo(w.y), bf_hi(w.y));
+      if (!h.first) sum[j] = *reinterpret_cast<const float4 *>(h.sum + i);
+    }
+    if (h.cur_table && i < h.cur_width)
+      cur[j] = *reinterpret_cast<const float4 *>(h.cur_table + (size_t)tok * h.cur_width + i);
+  }
+}
+
+__device__ __forceinline__ void handoff_store(const TokenHandoff &h, int tok, const SlotState *st, const float4 *e,
+                                              const float4 *sum, const float4 *cur) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int i = 4 * (int)threadIdx.x + 1024 * j;
+    if (i < h.emb_width) {
+      const float4 s = h.first ? e[j]
+                               : make_float4(sum[j].x + e[j].x, sum[j].y + e[j].y, sum[j].z + e[j].z, sum[j].w + e[j].w);
+      *reinterpret_cast<float4 *>(h.sum + i) = s;
+      if (!h.cur_table) *reinterpret_cast<float4 *>(h.cur + i) = e[j];
+    }
+    if (h.cur_table && i < h.cur_width) *reinterpret_cast<float4 *>(h.cur + i) = cur[j];
+  }
+  if (threadIdx.x == 0) {
+    int32_t *codes = h.codes + (size_t)st->frame * h.groups;
+    codes[h.code] = tok;
+    if (h.first) codes[0] = st->semantic;
+  }
+}
+
+// HO = greedy token hand-off (AttnArgs::h): the q/k/v row comes from a table indexed by the
+// token the previous group's LM head chose; workgroup (0, 0) also does the hand-off's stores.
+template <int D, int G, typename KVT, int CH, bool HO = false>
 __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   static_assert(D == 128, "lane layout assumes head_dim 128");
   static_assert(G >= 1 && G <= 2, "query heads per KV head");
@@ -447,17 +429,24 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
 
   // Loads first: this wave's head vector, then every cached K and V row the workgroup needs
   // (addresses clamped into the cache instead of branching), so the kernel waits on one
-  // memory round trip.  Rows at or past `pos` are never used from these registers.
+  // memory round trip.  Rows at or past `pos` are never used from these registers.  With the
+  // hand-off, the head vector's row is known only once the keys (loaded first) are reduced.
   const int vec = wave;
   const bool has_vec = wave < G + 2 && (wave < G || owns_pos);
   const float *gain = vec < G ? a.gq : (vec == G ? a.gk : nullptr);
   float x0 = 0.f, x1 = 0.f, g0 = 0.f, g1 = 0.f;
   float2 cs = make_float2(0.f, 0.f);
+  const int vec_off = vec < G ? (h * G + vec) * D : (vec == G ? q_out + h * D : q_out + kv_out + h * D);
+  uint64_t kin[HO ? 4 : 1];
+  if constexpr (HO) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) kin[j] = a.h.keys[min(lane + 64 * j, a.h.n_keys - 1)];
+  }
   if (has_vec) {
-    const float *src = vec < G ? qkv + (h * G + vec) * D
-                               : (vec == G ? qkv + q_out + h * D : qkv + q_out + kv_out + h * D);
-    x0 = src[lane];
-    x1 = src[lane + 64];
+    if constexpr (!HO) {
+      x0 = qkv[vec_off + lane];
+      x1 = qkv[vec_off + lane + 64];
+    }
     if (gain) {
       g0 = gain[lane];
       g1 = gain[lane + 64];
@@ -481,6 +470,19 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   if (!frame_pos) {  // workgroup-uniform: no barrier has been reached yet
     if (a.row_on && !a.row_on[row]) return;
     if (skip_work(st, a.skip)) return;
+  }
+  // Hand-off: the token, its q/k/v row, and (workgroup (0, 0)) the rows the hand-off stores,
+  // loaded here and stored after the attention output.
+  int tok = 0;
+  float4 side_e[2], side_s[2], side_c[2];
+  if constexpr (HO) {
+    tok = key_token(wave_max_u64(umax64(umax64(kin[0], kin[1]), umax64(kin[2], kin[3]))));
+    if (has_vec) {
+      const float *src = a.qkv_table + (size_t)tok * a.ld_table + vec_off;
+      x0 = src[lane];
+      x1 = src[lane + 64];
+    }
+    if (h == 0 && c == 0) handoff_load(a.h, tok, side_e, side_s, side_c);
   }
 
   // 1: q heads (waves 0..G-1); k and v (waves G, G+1) only where row `pos` is stored.
@@ -570,6 +572,10 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   }
   __syncthreads();
 
+  if constexpr (HO) {
+    if (h == 0 && c == 0) handoff_store(a.h, tok, st, side_e, side_s, side_c);
+  }
+
   // 3: final output (single chunk) or this chunk's partial.
   const int o = threadIdx.x;  // G * D <= 256 outputs
   if (o >= G * D) return;
@@ -600,12 +606,13 @@ __device__ void merge_attention(const GemvArgs &a, float *xs) {
     const int h = hq / G, g = hq % G;
     const float *p0 = a.attn_part + (((size_t)h * a.attn_part_chunks) * G + g) * (D + 2);
     const size_t stride = (size_t)G * (D + 2);
-    // at most kAttnMaxChunks chunks: every partial is loaded at once (indices clamped), then
-    // the max and the weighted sums in chunk order
+    // at most kAttnMaxChunks chunks: every partial slot is loaded at once (indices clamped
+    // to the workspace, not to the chunks in use, so the loads do not wait for the stream
+    // state), then the max and the weighted sums over the chunks in use, in chunk order
     float mv[kAttnMaxChunks], lv[kAttnMaxChunks], av[kAttnMaxChunks][8];
 #pragma unroll
     for (int c = 0; c < kAttnMaxChunks; ++c) {
-      const float *pc = p0 + min(c, nchunks - 1) * stride;
+      const float *pc = p0 + min(c, a.attn_part_chunks - 1) * stride;
       mv[c] = pc[0];
       lv[c] = pc[1];
 #pragma unroll
@@ -1594,6 +1601,11 @@ __global__ void k_pack_w(const uint16_t *src, uint16_t *dst, int rows, int K) {
       *reinterpret_cast<const uint4 *>(src + (tile * 16 + j) * (size_t)K + step * 32 + kb * 8);
 }
 
+__global__ void k_bf16_to_f32(const uint16_t *src, float *dst, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = bf16_to_f32(src[i]);
+}
+
 }  // namespace
 
 // ---------------------------------------------------------------------------------------
@@ -1643,18 +1655,11 @@ template <int EPI, bool NORM, int KC, int RW, bool NT>
 static void gemv_launch(const GemvArgs &a, hipStream_t s, const LaunchTiming *t) {
   const int units = 4 * RW;
   const dim3 grid((a.N + units - 1) / units);
-  // Hand-off variants: the CodePredictor's LM heads (producer; store + norm) and the first
-  // GEMV of the next group (consumer; its QKV with norm, or the bias-only input projection).
-  if constexpr (!NT && KC <= 4 && KC != 3 && ((EPI == EPI_STORE && NORM) || (EPI == EPI_BIAS && !NORM))) {
+  // Hand-off producer: the CodePredictor's LM heads (store + norm).
+  if constexpr (!NT && KC <= 4 && KC != 3 && EPI == EPI_STORE && NORM) {
     if (a.keys_out) {
-      if constexpr (EPI == EPI_STORE) {
-        if (grid.x > (unsigned)kHandoffKeys) return;  // launch_gemv checked the grid
-        launch_timed(k_gemv<EPI, NORM, KC, RW, NT, false, 1, 1>, grid, dim3(256), 0, s, t, a);
-      }
-      return;
-    }
-    if (a.keys_in) {
-      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, false, 1, 2>, grid, dim3(256), 0, s, t, a);
+      if (grid.x > (unsigned)kHandoffKeys) return;  // launch_gemv checked the grid
+      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, false, 1, true>, grid, dim3(256), 0, s, t, a);
       return;
     }
   }
@@ -1720,17 +1725,19 @@ static hipError_t gemv_epi(int epi, bool norm, const GemvArgs &a, hipStream_t s,
   return hipErrorInvalidValue;
 }
 
+static bool handoff_ok(const TokenHandoff &h) {
+  return h.keys && h.n_keys >= 1 && h.n_keys <= kHandoffKeys && h.emb && h.emb_width > 0 && h.emb_width % 8 == 0 &&
+         h.cur && h.sum && h.codes && h.code >= 1 && h.code < h.groups &&
+         (!h.cur_table || (h.cur_width > 0 && h.cur_width % 4 == 0));
+}
+
 hipError_t launch_gemv(int epi, bool norm, bool streaming, const GemvArgs &a, hipStream_t s,
                        const LaunchTiming *t) {
   if (!gemv_supports_k(a.K) || a.N <= 0) return hipErrorInvalidValue;
-  if (a.keys_out || a.keys_in) {
-    const bool shape_ok = !streaming && a.rows <= 1 && !a.attn_part && !(a.keys_out && a.keys_in) &&
-                          (a.K == 512 || a.K == 1024 || a.K == 2048) && a.st;
-    const bool producer_ok = epi == EPI_STORE && norm && gemv_grid(a.N, a.K, epi) <= kHandoffKeys;
-    const bool consumer_ok = ((epi == EPI_STORE && norm) || (epi == EPI_BIAS && !norm)) && a.n_keys >= 1 &&
-                             a.n_keys <= kHandoffKeys && a.g_emb && a.g_cur && a.g_sum && a.g_codes &&
-                             a.g_code >= 1 && a.g_code < a.g_groups;
-    if (!shape_ok || (a.keys_out ? !producer_ok : !consumer_ok)) return hipErrorInvalidValue;
+  if (a.keys_out) {
+    const bool ok = !streaming && a.rows <= 1 && !a.attn_part && (a.K == 512 || a.K == 1024 || a.K == 2048) &&
+                    a.st && epi == EPI_STORE && norm && gemv_grid(a.N, a.K, epi) <= kHandoffKeys;
+    if (!ok) return hipErrorInvalidValue;
   }
   if (a.rows > 1 && (a.rows != 2 || streaming || a.attn_part || a.K > 6 * 512 || a.ldx_r % 4 ||
                      (epi == EPI_RESIDUAL && !a.ldr_r) || !a.ldo_r))
@@ -1766,6 +1773,22 @@ hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t s, co
   const int nch = (a.cap + a.chunk - 1) / a.chunk;
   if (a.partial_out ? a.part_chunks < nch : nch != 1) return hipErrorInvalidValue;
   const dim3 grid(a.kv_heads, nch, rows), block(256);
+  if (a.h.keys) {
+    // the hand-off: one stream, one chunk of 32 rows, a position given by the launch
+    const int qkv_rows = (a.q_heads + 2 * a.kv_heads) * head_dim;
+    if (rows != 1 || a.partial_out || a.chunk != 32 || a.pos_mode != POS_CONST || !a.qkv_table ||
+        a.ld_table < qkv_rows || !handoff_ok(a.h) || a.h.emb_width > 2048 || a.h.emb_width % 4 ||
+        (a.h.cur_table && a.h.cur_width > 2048) || !a.st)
+      return hipErrorInvalidValue;
+    if (a.kv_bf16) {
+      if (G == 1) launch_timed(k_attn_split<128, 1, uint16_t, 32, true>, grid, block, 0, s, t, a);
+      else launch_timed(k_attn_split<128, 2, uint16_t, 32, true>, grid, block, 0, s, t, a);
+    } else {
+      if (G == 1) launch_timed(k_attn_split<128, 1, float, 32, true>, grid, block, 0, s, t, a);
+      else launch_timed(k_attn_split<128, 2, float, 32, true>, grid, block, 0, s, t, a);
+    }
+    return hipGetLastError();
+  }
 #define Q3T_ATTN_CASE(GG, TT, CC) \
   if (G == GG && a.chunk == CC) {  \
     launch_timed(k_attn_split<128, GG, TT, CC>, grid, block, 0, s, t, a); \
@@ -1861,6 +1884,12 @@ hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
     case EPI_BIAS: return gemm_epi<EPI_BIAS>(a, s);
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_bf16_to_f32(const uint16_t *src, float *dst, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_bf16_to_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, dst, n);
+  return hipGetLastError();
 }
 
 hipError_t launch_row_rms(const float *X, int ldx, int M, int K, float eps, float *inv_rms, hipStream_t s) {

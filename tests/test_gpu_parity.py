@@ -161,6 +161,23 @@ def test_eos_ends_stream_like_the_reference(models, tmp_path):
     assert r["eos"] and r["chunks"][-1].ended_by_eos
 
 
+def test_cache_past_1024_rows_matches_oracle(models):
+    """A 1,109-row prompt in a 1,152-row cache: the Talker's attention spans 9 chunks of 128
+    rows, more than the O projection merges itself, so the merge kernel runs first."""
+    w = WORKLOADS["tiny_greedy"]
+    model, _ = models.get(w.spec)
+    prompt = np.random.default_rng(21).integers(0, 151643, 1100)
+    from q3t import textprep
+    inputs = textprep.TextPrep(model).prepare(prompt)
+    assert inputs.prefill_steps == 1109
+    opts = E.GenerateOptions.greedy(6)
+    r = run(models, "tiny_greedy", options=opts, inputs=inputs, cap=1152)
+    fx = _as_fixture(_oracle_rollout(model, inputs, opts, 1152))
+    same = check_codes(r["codes"], r["eos"], fx)
+    err = check_talker_logits(r["talker_logits"], fx, same)
+    print(f"1152-row cache: {same} frames identical, talker logit err {err:.2e}")
+
+
 def test_capacity_busy_and_exhausted_streams(models):
     w = WORKLOADS["tiny_greedy"]
     model, d = models.get(w.spec)
