@@ -545,7 +545,7 @@ struct Engine {
       PrefillAttnArgs pa{p.pqkv, L.gq, L.gk, w.rope, sl.c_k + l * cache_layer, sl.c_v + l * cache_layer, p.pattn,
                          2, 0, Q, O, d.q_heads, d.kv_heads, w.cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
                          kv_bf16};
-      hip_check(launch_prefill_attention(pa, s), "launch_prefill_attention(cp)");
+      hip_check(launch_prefix_attention(pa, s), "launch_prefix_attention");
       gemv2(EPI_RESIDUAL, false, L.o, p.pattn, O, nullptr, 0.f, src, lds, nullptr, x2, H, H, O, sl, s);
       gemv2(EPI_SWIGLU, true, L.gu, x2, H, L.g_post, d.eps, nullptr, 0, nullptr, p.pact, I, I, H, sl, s);
       gemv2(EPI_RESIDUAL, false, L.down, p.pact, I, nullptr, 0.f, x2, H, nullptr, x2, H, H, I, sl, s);

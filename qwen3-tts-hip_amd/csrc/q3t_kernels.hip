@@ -1170,6 +1170,86 @@ __global__ __launch_bounds__(256) void k_prefill_qkv(PrefillAttnArgs a) {
   }
 }
 
+// Prefill of a few rows at positions 0 .. P-1 (the CodePredictor's 2-row prefix) in one
+// workgroup per KV head: q/k head RMSNorm + RoPE, K/V stores, then each row's causal
+// attention over rows 0..p with the values just stored (rounded to the cache type).  The
+// P * (G + 2) head vectors are spread over the 4 waves, loads first.
+template <int G, typename KVT, int P>
+__global__ __launch_bounds__(256) void k_attn_prefix(PrefillAttnArgs a) {
+  constexpr int D = 128, NV = P * (G + 2), VPW = (NV + 3) / 4;
+  const int h = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ float qs[P][G][D], ks[P][D], vs[P][D];
+  __shared__ float sc[P][G][P];
+  float x0[VPW], x1[VPW], g0[VPW], g1[VPW];
+  float2 cs[VPW];
+#pragma unroll
+  for (int i = 0; i < VPW; ++i) {
+    const int vi = min(wave + 4 * i, NV - 1);  // vector vi: row vi / (G + 2), kind vi % (G + 2)
+    const int p = vi / (G + 2), kind = vi % (G + 2);
+    const int off = kind < G ? (h * G + kind) * D
+                             : (kind == G ? a.q_heads * D + h * D : (a.q_heads + a.kv_heads) * D + h * D);
+    const float *src = a.qkv + (size_t)p * a.ldq + off;
+    x0[i] = src[lane];
+    x1[i] = src[lane + 64];
+    const float *gain = kind < G ? a.gq : a.gk;  // unused for v
+    g0[i] = gain[lane];
+    g1[i] = gain[lane + 64];
+    cs[i] = a.rope[(size_t)p * (D / 2) + lane];
+  }
+#pragma unroll
+  for (int i = 0; i < VPW; ++i) {
+    const int vi = wave + 4 * i;
+    if (vi >= NV) break;  // wave-uniform
+    const int p = vi / (G + 2), kind = vi % (G + 2);
+    float y0 = x0[i], y1 = x1[i];
+    if (kind <= G) {
+      const float ss = wave_sum(fmaf(y0, y0, y1 * y1));
+      const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+      y0 = (y0 * inv) * g0[i];
+      y1 = (y1 * inv) * g1[i];
+      const float r0 = y0 * cs[i].x - y1 * cs[i].y, r1 = y1 * cs[i].x + y0 * cs[i].y;
+      y0 = r0;
+      y1 = r1;
+    }
+    if (kind < G) {
+      qs[p][kind][lane] = y0;
+      qs[p][kind][lane + 64] = y1;
+    } else {
+      KVT *cache = reinterpret_cast<KVT *>(kind == G ? a.kcache : a.vcache) + ((size_t)h * a.cap + p) * D;
+      float *keep = kind == G ? ks[p] : vs[p];
+      keep[lane] = KvIo<KVT>::store(cache + lane, y0);
+      keep[lane + 64] = KvIo<KVT>::store(cache + lane + 64, y1);
+    }
+  }
+  __syncthreads();
+  // scores: 16 lanes per (row, head, key) triple, 8 dims each
+  constexpr int NT = P * G * P;
+  const int sub = lane & 15, grp = (int)threadIdx.x >> 4;
+  for (int tr = grp; tr < NT; tr += 16) {
+    const int p = tr / (G * P), g = (tr / P) % G, t = tr % P;
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc = fmaf(qs[p][g][sub * 8 + j], ks[t][sub * 8 + j], acc);
+    acc = row16_sum(acc);
+    if (sub == 0) sc[p][g][t] = acc * a.scale;
+  }
+  __syncthreads();
+  // outputs: row p, head g, dim d; softmax over keys 0..p in key order
+  for (int o = threadIdx.x; o < P * G * D; o += 256) {
+    const int p = o / (G * D), g = (o / D) % G, d = o % D;
+    float m = -FLT_MAX;
+    for (int t = 0; t <= p; ++t) m = fmaxf(m, sc[p][g][t]);
+    float l = 0.f, acc = 0.f;
+    for (int t = 0; t <= p; ++t) {
+      const float w = expf(sc[p][g][t] - m);
+      l += w;
+      acc = fmaf(w, vs[t][d], acc);
+    }
+    a.out[(size_t)p * a.ldo + (h * G + g) * D + d] = acc / l;
+  }
+}
+
 template <int G, typename KVT>
 __global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs a) {
   constexpr int D = 128, CH = 64;
@@ -1895,6 +1975,21 @@ hipError_t launch_bf16_to_f32(const uint16_t *src, float *dst, size_t n, hipStre
 hipError_t launch_row_rms(const float *X, int ldx, int M, int K, float eps, float *inv_rms, hipStream_t s) {
   if (M <= 0 || K <= 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_row_rms, dim3((M + 3) / 4), dim3(256), 0, s, X, ldx, M, K, eps, inv_rms);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefix_attention(const PrefillAttnArgs &a, hipStream_t s) {
+  if (a.P != 2 || a.pos0 != 0 || a.kv_heads <= 0 || a.q_heads % a.kv_heads || a.cap < 2) return hipErrorInvalidValue;
+  const int G = a.q_heads / a.kv_heads;
+  if (G != 1 && G != 2) return hipErrorInvalidValue;
+  const dim3 grid(a.kv_heads), block(256);
+  if (a.kv_bf16) {
+    if (G == 1) hipLaunchKernelGGL((k_attn_prefix<1, uint16_t, 2>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_attn_prefix<2, uint16_t, 2>), grid, block, 0, s, a);
+  } else {
+    if (G == 1) hipLaunchKernelGGL((k_attn_prefix<1, float, 2>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_attn_prefix<2, float, 2>), grid, block, 0, s, a);
+  }
   return hipGetLastError();
 }
 
