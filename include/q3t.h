@@ -72,6 +72,8 @@ typedef struct {
   int32_t q_heads, kv_heads, head_dim, num_code_groups;
   int32_t codec_eos, max_cache_steps, max_streams;
   int64_t device_bytes; /* device memory held by the engine */
+  int32_t text_vocab;   /* text-embedding rows on the device (0: no device text preparation) */
+  int32_t text_hidden;
 } q3t_engine_info;
 
 /* GeneratedCodesChunk (generation.rs:876-963). */
@@ -136,6 +138,26 @@ int q3t_streams_start(q3t_engine *engine, int32_t n, const q3t_stream_input *inp
  * Streams not listed are untouched. */
 int q3t_streams_next_codes(q3t_engine *engine, q3t_stream *const *streams, int32_t n,
                            int32_t max_chunk_frames, int32_t *codes, q3t_chunk_info *info);
+
+/* TtsTextPrep::prepare_custom_voice_with_lookahead (text.rs:340-382) from content token ids,
+ * on the device: the tokenizer's ids between the chat-template prefix and suffix (text.rs:361)
+ * -> text-embedding rows -> text_projection (fc1, SiLU, fc2) -> plus the codec embedding rows
+ * of the role / think / language / speaker / pad / bos layout (text.rs:516-603).  speaker and
+ * language are the q3t_generate_options enums, resolved through config.json's spk_id and
+ * codec_language_id maps (text.rs:642-653).  The model directory must hold
+ * talker.model.text_embedding.weight (Q3T_ERR_NOT_FOUND otherwise).  prefill must hold
+ * (9 + n_ids) * H floats, trailing (n_ids + 1) * H, tts_pad H; *prefill_steps = 9 + lookahead
+ * rows and *trailing_steps = n_ids - lookahead + 1 (the rest of the content, then tts_eos),
+ * lookahead = min(max(text_lookahead_tokens, 1), n_ids) (0 without content). */
+int q3t_prepare_text(q3t_engine *engine, const int32_t *content_ids, int32_t n_ids, int32_t speaker,
+                     int32_t language, int32_t text_lookahead_tokens, float *prefill, int32_t *prefill_steps,
+                     float *trailing, int32_t *trailing_steps, float *tts_pad);
+
+/* HipTtsEngine::start_stream (generation.rs:421-440) from content token ids: the rows
+ * q3t_prepare_text describes are built on the device straight into the stream's slot (no
+ * host round trip), then as q3t_stream_start.  The speaker and language come from opts. */
+int q3t_stream_start_text(q3t_engine *engine, const int32_t *content_ids, int32_t n_ids,
+                          int32_t text_lookahead_tokens, const q3t_generate_options *opts, q3t_stream **out);
 
 /* Drops the stream and frees its slot (HipTtsStream's Drop). */
 int q3t_stream_destroy(q3t_stream *stream);

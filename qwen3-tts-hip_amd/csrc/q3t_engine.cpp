@@ -16,6 +16,7 @@
 #include <cstdio>
 #include <cstring>
 #include <fstream>
+#include <map>
 #include <memory>
 #include <sstream>
 #include <stdexcept>
@@ -133,6 +134,11 @@ class SafeTensors {
     return out;
   }
   bool has(const std::string &name) const { return header_.has(name); }
+  std::vector<int64_t> shape(const std::string &name) const {
+    std::vector<int64_t> out;
+    for (const json::Value &d : header_.at(name).at("shape").arr) out.push_back(d.integer());
+    return out;
+  }
 
  private:
   struct View {
@@ -375,6 +381,16 @@ struct Engine {
   // raw q/k/v row of every input token, [groups-2][Vc][qkv_rows], and (projection only) the
   // projected input row, [groups-2][Vc][Hc].
   float *cp_qkv_table = nullptr, *cp_in_table = nullptr;
+  // Prompt preparation on the device (text.rs:516-603), when the checkpoint holds
+  // talker.model.text_embedding.weight: the table [text_vocab][text_hidden] and the text
+  // projection fc1 [tp_inter][text_hidden] + bias, fc2 [H][tp_inter] + bias.
+  uint16_t *text_emb = nullptr, *tp_fc1 = nullptr, *tp_fc2 = nullptr;
+  float *tp_b1 = nullptr, *tp_b2 = nullptr;
+  int text_vocab = 0, text_hidden = 0, tp_inter = 0;
+  // Special ids (config.rs:30-44).
+  int tok_im_start = 0, tok_assistant = 0, tok_tts_pad = 0, tok_tts_bos = 0, tok_tts_eos = 0;
+  int codec_pad = 0, codec_bos = 0, codec_think = 0, codec_think_bos = 0, codec_think_eos = 0;
+  std::map<std::string, int> speaker_ids, language_ids;
   // Packed copies for the batched frame's skinny GEMMs (multi-stream engines only).
   uint16_t *codec_head_p = nullptr, *lm_heads_p = nullptr, *proj_w_p = nullptr;
   // Batched-frame activations in T16 (16 stream rows): residual streams, attention output,
@@ -1186,6 +1202,37 @@ int q3t_engine_create(const q3t_engine_options *opts, q3t_engine **out) {
     }
     e->lm_heads = upload_bf16(heads, {Vc, Hc});
     e->cp_emb = upload_bf16(embs, {Vc, Ht});
+    // Special ids and the speaker / language maps (config.rs:47-80).
+    e->tok_im_start = (int)cfg.at("im_start_token_id").integer();
+    e->tok_assistant = (int)cfg.at("assistant_token_id").integer();
+    e->tok_tts_pad = (int)cfg.at("tts_pad_token_id").integer();
+    e->tok_tts_bos = (int)cfg.at("tts_bos_token_id").integer();
+    e->tok_tts_eos = (int)cfg.at("tts_eos_token_id").integer();
+    e->codec_pad = (int)tc.at("codec_pad_id").integer();
+    e->codec_bos = (int)tc.at("codec_bos_id").integer();
+    e->codec_think = (int)tc.at("codec_think_id").integer();
+    e->codec_think_bos = (int)tc.at("codec_think_bos_id").integer();
+    e->codec_think_eos = (int)tc.at("codec_think_eos_id").integer();
+    for (const auto &kv : tc.at("spk_id").obj) e->speaker_ids[kv.first] = (int)kv.second.integer();
+    for (const auto &kv : tc.at("codec_language_id").obj) e->language_ids[kv.first] = (int)kv.second.integer();
+    if (st.has("talker.model.text_embedding.weight")) {
+      // TtsTextPrep::load (text.rs:267-329): table [vocab, text_hidden], fc1 [inter, text_hidden],
+      // fc2 [H, inter].
+      const std::vector<int64_t> ts = st.shape("talker.model.text_embedding.weight");
+      const std::vector<int64_t> f1 = st.shape("talker.text_projection.linear_fc1.weight");
+      const std::vector<int64_t> f2 = st.shape("talker.text_projection.linear_fc2.weight");
+      if (ts.size() != 2 || f1.size() != 2 || f2.size() != 2 || f1[1] != ts[1] || f2[1] != f1[0] || f2[0] != Ht)
+        fail(Q3T_ERR_INVALID, "invalid text embedding / text projection shapes");
+      if (ts[1] % 32 || f1[0] % 32) fail(Q3T_ERR_INVALID, "text widths must be multiples of 32");
+      e->text_vocab = (int)ts[0];
+      e->text_hidden = (int)ts[1];
+      e->tp_inter = (int)f1[0];
+      e->text_emb = upload_bf16({"talker.model.text_embedding.weight"}, ts);
+      e->tp_fc1 = upload_bf16({"talker.text_projection.linear_fc1.weight"}, f1);
+      e->tp_b1 = upload_f32("talker.text_projection.linear_fc1.bias", f1[0]);
+      e->tp_fc2 = upload_bf16({"talker.text_projection.linear_fc2.weight"}, f2);
+      e->tp_b2 = upload_f32("talker.text_projection.linear_fc2.bias", Ht);
+    }
     if (e->has_proj) {
       if (!gemv_supports_k((int)Ht)) fail(Q3T_ERR_INVALID, "projection width %d unsupported", (int)Ht);
       e->proj_w = upload_bf16({"talker.code_predictor.small_to_mtp_projection.weight"}, {Hc, Ht});
@@ -1215,7 +1262,8 @@ int q3t_engine_destroy(q3t_engine *e) {
                     e->lm_heads,    e->cp_emb,       e->proj_w,      e->proj_b,      e->talker.mats_p,
                     e->cp.mats_p,   e->codec_head_p, e->lm_heads_p,  e->proj_w_p,    e->bx_t,
                     e->bx_c,        e->battn,        e->bact,        e->bcp_in,      e->cp_qkv_table,
-                    e->cp_in_table};
+                    e->cp_in_table, e->text_emb,     e->tp_fc1,      e->tp_fc2,      e->tp_b1,
+                    e->tp_b2};
     for (void *p : ptrs)
       if (p) (void)hipFree(p);
     delete e;
@@ -1241,6 +1289,8 @@ int q3t_engine_get_info(const q3t_engine *e, q3t_engine_info *o) {
     o->max_cache_steps = e->cap;
     o->max_streams = (int32_t)e->slots.size();
     o->device_bytes = e->device_bytes;
+    o->text_vocab = e->text_vocab;
+    o->text_hidden = e->text_hidden;
   });
 }
 
@@ -1270,6 +1320,9 @@ void validate_input(const Engine &e, const q3t_stream_input &in, const q3t_gener
 
 // Uploads one stream's inputs (prompt rows into the prefill workspace at row0, trailing
 // rows then tts_pad, loop state, options) onto stream s.
+void stage_state(Engine &e, int slot, int prefill_steps, int trailing_rows, const q3t_generate_options *o,
+                 hipStream_t s);
+
 void stage_stream(Engine &e, int slot, int row0, const q3t_stream_input &in, const q3t_generate_options *o,
                   hipStream_t s) {
   Slot &sl = e.slots[slot];
@@ -1280,13 +1333,20 @@ void stage_stream(Engine &e, int slot, int row0, const q3t_stream_input &in, con
   if (rows > 0)
     HIPC(hipMemcpyAsync(sl.trailing, in.trailing, (size_t)rows * Ht * 4, hipMemcpyHostToDevice, s));
   HIPC(hipMemcpyAsync(sl.trailing + (size_t)rows * Ht, in.tts_pad, (size_t)Ht * 4, hipMemcpyHostToDevice, s));
+  stage_state(e, slot, in.prefill_steps, rows, o, s);
+}
+
+// Loop state and options of a starting stream (its prompt rows are already staged on s).
+void stage_state(Engine &e, int slot, int prefill_steps, int trailing_rows, const q3t_generate_options *o,
+                 hipStream_t s) {
+  Slot &sl = e.slots[slot];
   SlotState st0{};
   st0.frame = 0;
   st0.semantic = -1;
   st0.done = 0;
-  st0.prefill_steps = in.prefill_steps;
+  st0.prefill_steps = prefill_steps;
   st0.max_frames = o->max_frames;
-  st0.trailing_rows = rows;
+  st0.trailing_rows = trailing_rows;
   SlotParams pr{};
   pr.talker = SamplingParams{o->do_sample ? 1 : 0, o->top_k, o->top_p, o->temperature};
   pr.cp = SamplingParams{o->subtalker_dosample ? 1 : 0, o->subtalker_top_k, o->subtalker_top_p,
@@ -1304,6 +1364,113 @@ void stage_stream(Engine &e, int slot, int row0, const q3t_stream_input &in, con
   HIPC(hipMemcpy(sl.prm, &pr, sizeof(SlotParams), hipMemcpyHostToDevice));
 }
 
+// Speaker::config_key / Language::config_key order of the q3t_generate_options enums
+// (text.rs:39-52, 103-116).
+const char *const kSpeakerKeys[] = {"serena", "vivian", "uncle_fu", "ryan", "aiden",
+                                    "ono_anna", "sohee", "eric", "dylan"};
+const char *const kLanguageKeys[] = {"chinese", "english", "japanese", "korean", "german",
+                                     "french", "russian", "portuguese", "spanish", "italian"};
+constexpr int kNewline = 198;  // text.rs:15
+
+int resolve_token(const std::map<std::string, int> &ids, const char *const *keys, int nkeys, int index,
+                  const char *kind) {
+  if (index < 0 || index >= nkeys) fail(Q3T_ERR_INVALID, "unknown %s %d", kind, index);
+  auto it = ids.find(keys[index]);
+  if (it == ids.end()) fail(Q3T_ERR_INVALID, "missing %s token id for %s", kind, keys[index]);  // text.rs:642-653
+  return it->second;
+}
+
+// A prompt's rows as TtsTextPrep::prepare_custom_voice_with_lookahead lays them out
+// (text.rs:340-382, 516-573): the text ids to project, the codec embedding row added to
+// each (-1: none) and each row's destination ((kind << 24) | row: 0 prefill, 1 trailing,
+// 2 tts_pad, 3 dropped).
+struct TextPlan {
+  std::vector<int32_t> ids, codec, dst;
+  int prefill_steps = 0, trailing_steps = 0;
+};
+
+TextPlan plan_text(const Engine &e, const int32_t *content, int n, int speaker, int language, int lookahead,
+                   int trailing_cap) {
+  if (!e.text_emb)
+    fail(Q3T_ERR_NOT_FOUND, "the model has no talker.model.text_embedding.weight: device text preparation "
+                            "needs it");
+  if (n < 0 || (n > 0 && !content)) fail(Q3T_ERR_INVALID, "null or negative content ids");
+  if (lookahead <= 0) fail(Q3T_ERR_INVALID, "text_lookahead_tokens must be non-zero");
+  for (int i = 0; i < n; ++i)
+    if (content[i] < 0 || content[i] >= e.text_vocab)
+      fail(Q3T_ERR_INVALID, "text token %d is out of range for vocab %d", content[i], e.text_vocab);
+  const int spk = resolve_token(e.speaker_ids, kSpeakerKeys, 9, speaker, "speaker");
+  const int lang = resolve_token(e.language_ids, kLanguageKeys, 10, language, "language");
+  for (int c : {spk, lang, e.codec_pad, e.codec_bos, e.codec_think, e.codec_think_bos, e.codec_think_eos})
+    if (c < 0 || c >= e.td.vocab) fail(Q3T_ERR_INVALID, "codec token %d is out of range for vocab %d", c, e.td.vocab);
+  for (int t : {e.tok_im_start, e.tok_assistant, kNewline, e.tok_tts_pad, e.tok_tts_bos, e.tok_tts_eos})
+    if (t < 0 || t >= e.text_vocab) fail(Q3T_ERR_INVALID, "text token %d is out of range for vocab %d", t, e.text_vocab);
+  const int L = n == 0 ? 0 : std::max(1, std::min(lookahead, n));
+  TextPlan p;
+  auto row = [&](int id, int codec, int kind, int r) {
+    p.ids.push_back(id);
+    p.codec.push_back(codec);
+    p.dst.push_back((kind << 24) | r);
+  };
+  // role prefix, then tts_pad x5 / tts_bos over [think, think_bos, language, think_eos,
+  // speaker, pad], then the first L content ids over pad (bos on the last)
+  const int role[3] = {e.tok_im_start, e.tok_assistant, kNewline};
+  for (int i = 0; i < 3; ++i) row(role[i], -1, 0, i);
+  const int codec6[6] = {e.codec_think, e.codec_think_bos, lang, e.codec_think_eos, spk, e.codec_pad};
+  for (int i = 0; i < 6; ++i) row(i < 5 ? e.tok_tts_pad : e.tok_tts_bos, codec6[i], 0, 3 + i);
+  for (int i = 0; i < L; ++i) row(content[i], i + 1 == L ? e.codec_bos : e.codec_pad, 0, 9 + i);
+  p.prefill_steps = 9 + L;
+  // trailing text: the rest of the content, then tts_eos; then the tts_pad row
+  p.trailing_steps = n - L + 1;
+  for (int i = 0; i < p.trailing_steps; ++i) {
+    const int id = i + L < n ? content[i + L] : e.tok_tts_eos;
+    row(id, -1, i < trailing_cap ? 1 : 3, i < trailing_cap ? i : 0);
+  }
+  row(e.tok_tts_pad, -1, 2, 0);
+  return p;
+}
+
+// Runs a TextPlan on stream s: text-embedding gather -> fc1 (+ bias) -> SiLU -> fc2 (+ bias)
+// -> plus codec rows, into prefill / trailing / pad (device pointers).  Synchronous.
+void prepare_text_device(Engine &e, const TextPlan &p, float *prefill, float *trailing, float *pad, hipStream_t s) {
+  const int M = (int)p.ids.size(), H = e.talker_hidden;
+  int64_t bytes = 0;
+  std::vector<void *> owned;
+  auto take = [&](size_t n) {
+    void *q = dev_alloc<char>(n, bytes);
+    owned.push_back(q);
+    return q;
+  };
+  try {
+    int32_t *ids = (int32_t *)take((size_t)M * 4 * 3);
+    int32_t *codec = ids + M, *dst = ids + 2 * M;
+    float *X = (float *)take((size_t)M * e.text_hidden * 4);
+    float *Hd = (float *)take((size_t)M * e.tp_inter * 4);
+    float *Y = (float *)take((size_t)M * H * 4);
+    std::vector<int32_t> host(p.ids);
+    host.insert(host.end(), p.codec.begin(), p.codec.end());
+    host.insert(host.end(), p.dst.begin(), p.dst.end());
+    HIPC(hipMemcpyAsync(ids, host.data(), host.size() * 4, hipMemcpyHostToDevice, s));
+    hip_check(launch_text_gather(e.text_emb, e.text_hidden, ids, M, X, s), "launch_text_gather");
+    GemmArgs g{};
+    g.X = X; g.ldx = e.text_hidden; g.W = e.tp_fc1; g.bias = e.tp_b1; g.Y = Hd; g.ldy = e.tp_inter;
+    g.M = M; g.N = e.tp_inter; g.K = e.text_hidden;
+    hip_check(launch_gemm(EPI_BIAS, g, s), "launch_gemm(text fc1)");
+    hip_check(launch_silu(Hd, (size_t)M * e.tp_inter, s), "launch_silu");
+    g = GemmArgs{};
+    g.X = Hd; g.ldx = e.tp_inter; g.W = e.tp_fc2; g.bias = e.tp_b2; g.Y = Y; g.ldy = H;
+    g.M = M; g.N = H; g.K = e.tp_inter;
+    hip_check(launch_gemm(EPI_BIAS, g, s), "launch_gemm(text fc2)");
+    hip_check(launch_text_assemble(Y, H, M, codec, e.codec_emb, dst, prefill, trailing, pad, s),
+              "launch_text_assemble");
+    HIPC(hipStreamSynchronize(s));
+  } catch (...) {
+    for (void *q : owned) (void)hipFree(q);
+    throw;
+  }
+  for (void *q : owned) (void)hipFree(q);
+}
+
 q3t_stream *new_stream(Engine &e, int slot, int max_frames) {
   Slot &sl = e.slots[slot];
   sl.in_use = true;
@@ -1313,6 +1480,19 @@ q3t_stream *new_stream(Engine &e, int slot, int max_frames) {
   stream->max_frames = max_frames;
   stream->done = sl.h_state->done;
   return stream;
+}
+
+// A stream whose prompt rows (prefill workspace rows 0..P-1) and state are staged: the
+// Talker prefill at positions 0..P-1, the head and the first semantic token with its EOS /
+// max_frames check (talker.rs:207-233).
+q3t_stream *start_staged(Engine &e, int slot, int P, const q3t_generate_options *o) {
+  Slot &s = e.slots[slot];
+  e.prefill_segments({PrefillSeg{slot, 0, P}}, P, s.stream);
+  e.gemv(EPI_STORE, true, e.codec_head, s.x_t, e.t_norm, e.td.eps, nullptr, nullptr, s.logits_t, e.td.vocab,
+         e.td.hidden, SKIP_NEVER, s.st, s.stream);
+  e.select_talker(s, 0, s.stream);
+  sync_state(s);
+  return new_stream(e, slot, o->max_frames);
 }
 
 }  // namespace
@@ -1336,17 +1516,68 @@ int q3t_stream_start(q3t_engine *e, const float *prefill, int32_t P, const float
       }
     if (slot < 0) fail(Q3T_ERR_BUSY, "all %zu stream slots are in use", e->slots.size());
     HIPC(hipSetDevice(e->device));
-    Slot &s = e->slots[slot];
     ensure_trace(*e);
-    stage_stream(*e, slot, 0, in, o, s.stream);
-    // Talker prefill: positions 0..P-1, then the head and the first semantic token
-    // (talker.rs:207-233).
-    e->prefill_segments({PrefillSeg{slot, 0, P}}, P, s.stream);
-    e->gemv(EPI_STORE, true, e->codec_head, s.x_t, e->t_norm, e->td.eps, nullptr, nullptr, s.logits_t, e->td.vocab,
-            e->td.hidden, SKIP_NEVER, s.st, s.stream);
-    e->select_talker(s, 0, s.stream);  // + the EOS / max_frames check of the first token
-    sync_state(s);
-    *out = new_stream(*e, slot, o->max_frames);
+    stage_stream(*e, slot, 0, in, o, e->slots[slot].stream);
+    *out = start_staged(*e, slot, P, o);
+  });
+}
+
+int q3t_prepare_text(q3t_engine *e, const int32_t *content_ids, int32_t n_ids, int32_t speaker, int32_t language,
+                     int32_t text_lookahead_tokens, float *prefill, int32_t *prefill_steps, float *trailing,
+                     int32_t *trailing_steps, float *tts_pad) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || !prefill || !prefill_steps || !trailing || !trailing_steps || !tts_pad)
+      fail(Q3T_ERR_INVALID, "null argument");
+    const TextPlan p = plan_text(*e, content_ids, n_ids, speaker, language, text_lookahead_tokens, n_ids + 1);
+    HIPC(hipSetDevice(e->device));
+    const size_t H = (size_t)e->talker_hidden;
+    int64_t bytes = 0;
+    float *d = dev_alloc<float>((size_t)(p.prefill_steps + p.trailing_steps + 1) * H, bytes);
+    try {
+      float *dt = d + (size_t)p.prefill_steps * H, *dp = dt + (size_t)p.trailing_steps * H;
+      prepare_text_device(*e, p, d, dt, dp, e->pools.stream);
+      HIPC(hipMemcpy(prefill, d, (size_t)p.prefill_steps * H * 4, hipMemcpyDeviceToHost));
+      HIPC(hipMemcpy(trailing, dt, (size_t)p.trailing_steps * H * 4, hipMemcpyDeviceToHost));
+      HIPC(hipMemcpy(tts_pad, dp, H * 4, hipMemcpyDeviceToHost));
+    } catch (...) {
+      (void)hipFree(d);
+      throw;
+    }
+    (void)hipFree(d);
+    *prefill_steps = p.prefill_steps;
+    *trailing_steps = p.trailing_steps;
+  });
+}
+
+int q3t_stream_start_text(q3t_engine *e, const int32_t *content_ids, int32_t n_ids, int32_t text_lookahead_tokens,
+                          const q3t_generate_options *o, q3t_stream **out) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || !out) fail(Q3T_ERR_INVALID, "null engine or output");
+    *out = nullptr;
+    validate_options(o);
+    const TextPlan p =
+        plan_text(*e, content_ids, n_ids, o->speaker, o->language, text_lookahead_tokens, e->cap);
+    if ((int64_t)p.prefill_steps + o->max_frames > e->cap)
+      fail(Q3T_ERR_CAPACITY,
+           "requested %lld cache steps but engine was loaded for %d; call load_with_max_frames with a larger "
+           "max_frames",
+           (long long)p.prefill_steps + o->max_frames, e->cap);
+    int slot = -1;
+    for (size_t i = 0; i < e->slots.size(); ++i)
+      if (!e->slots[i].in_use) {
+        slot = (int)i;
+        break;
+      }
+    if (slot < 0) fail(Q3T_ERR_BUSY, "all %zu stream slots are in use", e->slots.size());
+    HIPC(hipSetDevice(e->device));
+    ensure_trace(*e);
+    Slot &s = e->slots[slot];
+    const int rows = std::min(p.trailing_steps, e->cap);
+    prepare_text_device(*e, p, e->pools.px, s.trailing, s.trailing + (size_t)rows * e->talker_hidden, s.stream);
+    stage_state(*e, slot, p.prefill_steps, rows, o, s.stream);
+    *out = start_staged(*e, slot, p.prefill_steps, o);
   });
 }
 

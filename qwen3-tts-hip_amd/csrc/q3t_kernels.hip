@@ -1681,6 +1681,39 @@ __global__ void k_pack_w(const uint16_t *src, uint16_t *dst, int rows, int K) {
       *reinterpret_cast<const uint4 *>(src + (tile * 16 + j) * (size_t)K + step * 32 + kb * 8);
 }
 
+// ---------------------------------------------------------------------------------------
+// Prompt preparation (text.rs:516-603): text-embedding rows through the text projection
+// (fc1, SiLU, fc2; the GEMMs run on the matrix-core path), plus codec embedding rows, placed
+// into the prefill, trailing-text and tts_pad rows.
+// ---------------------------------------------------------------------------------------
+// X[m] = table[ids[m]] (bf16 -> fp32), one workgroup per row.
+__global__ void k_text_gather(const uint16_t *table, int width, const int32_t *ids, float *X) {
+  const int m = blockIdx.x;
+  const uint16_t *src = table + (size_t)ids[m] * width;
+  float *dst = X + (size_t)m * width;
+  for (int i = threadIdx.x; i < width; i += blockDim.x) dst[i] = bf16_to_f32(src[i]);
+}
+
+// x = x / (1 + e^-x) (text.rs:705-707).
+__global__ void k_silu(float *x, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = x[i] / (1.0f + expf(-x[i]));
+}
+
+// Row m of Y (+ codec_emb[codec[m]] where codec[m] >= 0) to its destination dst[m]:
+// (kind << 24) | row, kind 0 = prefill row, 1 = trailing row, 2 = the tts_pad row, 3 = none.
+__global__ void k_text_assemble(const float *Y, int H, const int32_t *codec, const uint16_t *codec_emb,
+                                const int32_t *dst, float *prefill, float *trailing, float *pad) {
+  const int m = blockIdx.x;
+  const int kind = dst[m] >> 24, row = dst[m] & 0xffffff;
+  if (kind == 3) return;
+  float *out = kind == 0 ? prefill + (size_t)row * H : (kind == 1 ? trailing + (size_t)row * H : pad);
+  const int c = codec[m];
+  const float *y = Y + (size_t)m * H;
+  for (int i = threadIdx.x; i < H; i += blockDim.x)
+    out[i] = c >= 0 ? y[i] + bf16_to_f32(codec_emb[(size_t)c * H + i]) : y[i];
+}
+
 __global__ void k_bf16_to_f32(const uint16_t *src, float *dst, size_t n) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) dst[i] = bf16_to_f32(src[i]);
@@ -1964,6 +1997,25 @@ hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
     case EPI_BIAS: return gemm_epi<EPI_BIAS>(a, s);
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_text_gather(const uint16_t *table, int width, const int32_t *ids, int M, float *X, hipStream_t s) {
+  if (M <= 0 || width <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_text_gather, dim3(M), dim3(256), 0, s, table, width, ids, X);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu(float *x, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_silu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, x, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_text_assemble(const float *Y, int H, int M, const int32_t *codec, const uint16_t *codec_emb,
+                                const int32_t *dst, float *prefill, float *trailing, float *pad, hipStream_t s) {
+  if (M <= 0 || H <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_text_assemble, dim3(M), dim3(256), 0, s, Y, H, codec, codec_emb, dst, prefill, trailing, pad);
+  return hipGetLastError();
 }
 
 hipError_t launch_bf16_to_f32(const uint16_t *src, float *dst, size_t n, hipStream_t s) {

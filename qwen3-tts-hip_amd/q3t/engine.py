@@ -102,7 +102,9 @@ class _EngineInfo(ctypes.Structure):
         "talker_hidden", "talker_intermediate", "talker_layers", "talker_vocab",
         "cp_hidden", "cp_intermediate", "cp_layers", "cp_vocab",
         "q_heads", "kv_heads", "head_dim", "num_code_groups",
-        "codec_eos", "max_cache_steps", "max_streams")] + [("device_bytes", ctypes.c_int64)]
+        "codec_eos", "max_cache_steps", "max_streams")] + [("device_bytes", ctypes.c_int64),
+                                                             ("text_vocab", ctypes.c_int32),
+                                                             ("text_hidden", ctypes.c_int32)]
 
 
 class _ChunkInfo(ctypes.Structure):
@@ -140,6 +142,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                                             f32p, P(_GenerateOptions), P(ctypes.c_void_p)]),
         "q3t_stream_next_codes": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, i32p, P(_ChunkInfo)]),
         "q3t_stream_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+        "q3t_prepare_text": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
+                                            ctypes.c_int32, f32p, i32p, f32p, i32p, f32p]),
+        "q3t_stream_start_text": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32, ctypes.c_int32,
+                                                 P(_GenerateOptions), P(ctypes.c_void_p)]),
         "q3t_streams_start": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, P(_StreamInput), P(_GenerateOptions),
                                              P(ctypes.c_void_p)]),
         "q3t_streams_next_codes": (ctypes.c_int, [ctypes.c_void_p, P(ctypes.c_void_p), ctypes.c_int32,
@@ -440,6 +446,44 @@ class HipTtsEngine:
         inp = self._prepare(inputs, options, stream_options.text_lookahead_tokens)
         return HipTtsStream(self, inp, options, stream_options)
 
+    # -- prompt preparation on the device --------------------------------------------------
+    @property
+    def has_device_text_prep(self) -> bool:
+        """The checkpoint holds the text-embedding table (q3t_prepare_text works)."""
+        return self.info.get("text_vocab", 0) > 0
+
+    def prepare_text(self, content_ids: Sequence[int], speaker: str = "ryan", language: str = "english",
+                     text_lookahead_tokens: int = 1 << 30) -> PreparedInputs:
+        """``TtsTextPrep::prepare_custom_voice_with_lookahead`` (text.rs:340-382) on the device
+        (``q3t_prepare_text``): content ids -> prefill rows, trailing text rows, tts_pad row."""
+        ids = np.ascontiguousarray(np.asarray(content_ids, dtype=np.int64).astype(np.int32))
+        n, H = int(ids.size), self.info["talker_hidden"]
+        opts = GenerateOptions(speaker=speaker, language=language)._c()
+        pre = np.zeros((9 + n, H), np.float32)
+        trail = np.zeros((n + 1, H), np.float32)
+        pad = np.zeros(H, np.float32)
+        P, T = ctypes.c_int32(), ctypes.c_int32()
+        lookahead = min(int(text_lookahead_tokens), 0x7FFFFFFF)
+        _check(_lib.q3t_prepare_text(self._h, _iptr(ids), n, opts.speaker, opts.language, lookahead, _fptr(pre),
+                                     ctypes.byref(P), _fptr(trail), ctypes.byref(T), _fptr(pad)))
+        return PreparedInputs(content_ids=ids.astype(np.int64), prefill=pre[:P.value].copy(),
+                              trailing_text=trail[:T.value].copy(), tts_pad_embed=pad)
+
+    def start_stream_text(self, content_ids: Sequence[int], options: GenerateOptions = GenerateOptions(),
+                          stream_options: StreamOptions = StreamOptions()) -> "HipTtsStream":
+        """``start_stream`` (generation.rs:421-440) with the prompt rows built on the device
+        straight into the stream's slot (``q3t_stream_start_text``)."""
+        stream_options.validate()
+        ids = np.ascontiguousarray(np.asarray(content_ids, dtype=np.int64).astype(np.int32))
+        o = options._c()
+        handle = ctypes.c_void_p()
+        lookahead = min(int(stream_options.text_lookahead_tokens), 0x7FFFFFFF)
+        _check(_lib.q3t_stream_start_text(self._h, _iptr(ids), int(ids.size), lookahead, ctypes.byref(o),
+                                          ctypes.byref(handle)))
+        n = int(ids.size)
+        steps = 9 + (0 if n == 0 else max(1, min(lookahead, n)))
+        return HipTtsStream(self, None, options, stream_options, handle=handle, prefill_steps=steps)
+
     # -- several streams at once (no counterpart in the reference: one stream per engine) --
     def start_streams(self, inputs: List[Inputs], options: List[GenerateOptions],
                       stream_options: StreamOptions = StreamOptions()) -> List["HipTtsStream"]:
@@ -493,8 +537,9 @@ class HipTtsEngine:
 class HipTtsStream:
     """``HipTtsStream`` (generation.rs:145-163, 876-997).  Must not outlive its engine."""
 
-    def __init__(self, engine: HipTtsEngine, inputs: PreparedInputs, options: GenerateOptions,
-                 stream_options: StreamOptions, handle: Optional[ctypes.c_void_p] = None):
+    def __init__(self, engine: HipTtsEngine, inputs: Optional[PreparedInputs], options: GenerateOptions,
+                 stream_options: StreamOptions, handle: Optional[ctypes.c_void_p] = None,
+                 prefill_steps: Optional[int] = None):
         self.engine = engine
         self.inputs = inputs
         self.options = options
@@ -506,7 +551,7 @@ class HipTtsStream:
             _check(_lib.q3t_stream_start(engine._h, _fptr(pre), pre.shape[0], _fptr(trail), trail.shape[0],
                                          _fptr(pad), ctypes.byref(o), ctypes.byref(handle)))
         self._h = handle
-        self.prefill_steps = inputs.prefill_steps
+        self.prefill_steps = inputs.prefill_steps if prefill_steps is None else prefill_steps
         self._codes = []
         self.frame = 0
         self.ended_by_eos = False

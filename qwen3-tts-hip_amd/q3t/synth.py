@@ -236,6 +236,15 @@ def text_embedding_rows(seed: int, rows: np.ndarray, text_hidden: int = TEXT_HID
     return out
 
 
+def text_embedding_block(seed: int, r0: int, r1: int, text_hidden: int = TEXT_HIDDEN) -> np.ndarray:
+    """bf16 bit patterns of table rows r0 .. r1-1 (the values text_embedding_rows returns)."""
+    out = np.empty((r1 - r0, text_hidden), dtype=np.uint16)
+    for r in range(r0, r1):
+        z = _philox(seed, TEXT_EMBEDDING_NAME, r + 1).standard_normal(text_hidden, dtype=np.float32)
+        out[r - r0] = f32_to_bf16_bits(z * np.float32(0.02))
+    return out
+
+
 class SyntheticModel:
     """All path tensors of one synthetic model, as bf16 bit patterns held in memory."""
 
@@ -268,8 +277,12 @@ class SyntheticModel:
             h = zlib.crc32(self.tensors[name].tobytes(), h)
         return f"{h:08x}"
 
-    def write(self, model_dir: str) -> None:
-        """Write config.json + model.safetensors (BF16, [out, in] row-major)."""
+    def write(self, model_dir: str, text_embedding: bool = False) -> None:
+        """Write config.json + model.safetensors (BF16, [out, in] row-major).
+
+        text_embedding=True also writes the full 151,936-row text-embedding table (the rows
+        ``text_embedding_rows`` generates; ~0.6 GB at text_hidden 2048, ~11 s), which device
+        text preparation reads.  It is streamed to the file in row blocks."""
         os.makedirs(model_dir, exist_ok=True)
         with open(os.path.join(model_dir, "config.json"), "w") as f:
             json.dump(self.config(), f, indent=1)
@@ -281,6 +294,12 @@ class SyntheticModel:
             nbytes = int(np.prod(shape)) * 2
             header[name] = {"dtype": "BF16", "shape": list(shape), "data_offsets": [offset, offset + nbytes]}
             offset += nbytes
+        th = self.spec.text_hidden
+        if text_embedding:
+            nbytes = TEXT_VOCAB * th * 2
+            header[TEXT_EMBEDDING_NAME] = {"dtype": "BF16", "shape": [TEXT_VOCAB, th],
+                                           "data_offsets": [offset, offset + nbytes]}
+            offset += nbytes
         blob = json.dumps(header, separators=(",", ":")).encode()
         blob += b" " * ((8 - len(blob) % 8) % 8)
         path = os.path.join(model_dir, "model.safetensors")
@@ -289,6 +308,9 @@ class SyntheticModel:
             f.write(blob)
             for name, _, _ in inv:
                 f.write(np.ascontiguousarray(self.tensors[name]).tobytes())
+            if text_embedding:
+                for r0 in range(0, TEXT_VOCAB, 8192):
+                    f.write(text_embedding_block(self.seed, r0, min(TEXT_VOCAB, r0 + 8192), th).tobytes())
         os.replace(path + ".tmp", path)
 
 

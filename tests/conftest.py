@@ -36,6 +36,16 @@ class _ModelCache:
             self.models[key] = (model, d)
         return self.models[key]
 
+    def get_with_text(self, spec: str, seed: int = 0):
+        """The same model written with its full text-embedding table (device text preparation)."""
+        key = (spec, seed, "text")
+        if key not in self.models:
+            model, _ = self.get(spec, seed)
+            d = os.path.join(self.root, f"{spec}_{seed}_text")
+            model.write(d, text_embedding=True)
+            self.models[key] = (model, d)
+        return self.models[key]
+
     def drop(self, spec: str, seed: int = 0):
         item = self.models.pop((spec, seed), None)
         if item:
