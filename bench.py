@@ -172,6 +172,8 @@ def main() -> int:
     ap.add_argument("--multistream", default="cfg5_0.6b_multistream",
                     help="multi-stream workload reported beside the headline line ('' to skip)")
     ap.add_argument("--multistream-only", action="store_true", help="run only the multi-stream workload")
+    ap.add_argument("--no-text-prep", action="store_true",
+                    help="skip the device prompt-preparation timing (and the text-embedding table it needs)")
     ap.add_argument("--kernel-classes", action="store_true",
                     help="graph-time every kernel class of q3t_bench_kernel on the workload's model and exit")
     args = ap.parse_args()
@@ -193,8 +195,18 @@ def main() -> int:
     model = synth.SyntheticModel.build(w.spec, w.weight_seed)
     inputs = w.inputs(model)
     tmp = tempfile.mkdtemp(prefix="q3t_bench_")
-    model.write(tmp)
+    with_text = not (args.no_text_prep or args.kernel_classes or args.multistream_only)
+    model.write(tmp, text_embedding=with_text)
     spec = model.spec
+    host_prep = None
+    if with_text:
+        from q3t import textprep
+        tp = textprep.TextPrep(model)
+        t0 = time.perf_counter()
+        look = (1 << 30) if w.lookahead is None else w.lookahead
+        for _ in range(3):
+            tp.prepare(w.prompt(), text_lookahead_tokens=look)
+        host_prep = (time.perf_counter() - t0) / 3
     del model
     if args.kernel_classes:
         eng = E.HipTtsEngine(tmp, E.EngineOptions(max_cache_steps=w.max_cache_steps))
@@ -244,6 +256,19 @@ def main() -> int:
     frame_s = elapsed / frames
     roofline = eng.dominant_kernel_roofline(HBM_PEAK_GBPS)
     roofline["traffic"] = measured_traffic(w.name, roofline["kernel"])
+    text_prep = None
+    if with_text:
+        # Prompt preparation of the same prompt on the device (q3t_prepare_text, host copies
+        # and workspace allocation included), against the package's numpy preparation.
+        ids = w.prompt()
+        dev = eng.prepare_text(ids, text_lookahead_tokens=look)
+        assert np.abs(dev.prefill - inputs.prefill).max() < 1e-4
+        t0 = time.perf_counter()
+        for _ in range(20):
+            eng.prepare_text(ids, text_lookahead_tokens=look)
+        text_prep = {"content_ids": int(len(ids)), "rows_projected": int(len(ids)) + 11,
+                     "device_ms": round(1000 * (time.perf_counter() - t0) / 20, 3),
+                     "host_numpy_ms": round(1000 * host_prep, 3)}
     eng.close()
     multi = None
     if args.multistream and w.spec == "0.6b" and w.weight_seed == 0:
@@ -276,6 +301,8 @@ def main() -> int:
     }
     if multi is not None:
         out["multistream"] = multi
+    if text_prep is not None:
+        out["text_prep"] = text_prep
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out))
