@@ -281,7 +281,9 @@ class GeneratedCodesChunk:
     ended_by_eos: bool
 
 
-Inputs = Union[PreparedInputs, Sequence[int]]
+# A prompt: prepared rows, content token ids, or text (tokenized with the model directory's
+# tokenizer files).
+Inputs = Union[PreparedInputs, Sequence[int], str]
 
 
 class HipTtsEngine:
@@ -302,6 +304,11 @@ class HipTtsEngine:
         self.hidden = info.talker_hidden
         self.text_prep = text_prep
         self._streams = 0
+        # TextTokenizer::from_pretrained (text.rs:161-182) when the directory has its files.
+        self.tokenizer = None
+        if any(os.path.exists(os.path.join(model_dir, f)) for f in ("tokenizer.json", "vocab.json")):
+            from .tokenizer import TextTokenizer
+            self.tokenizer = TextTokenizer.from_pretrained(model_dir)
 
     # -- constructors (generation.rs:255-315) ------------------------------------------
     @classmethod
@@ -420,15 +427,38 @@ class HipTtsEngine:
         return out
 
     # -- generation ----------------------------------------------------------------------
+    def content_ids(self, text: str) -> List[int]:
+        """``content_ids_for_text`` (text.rs:384-395) with the model directory's tokenizer."""
+        if self.tokenizer is None:
+            raise InvalidInputError(Q3T_ERR_INVALID, "the model directory has no tokenizer.json or "
+                                                     "vocab.json + merges.txt")
+        return self.tokenizer.content_ids(text)
+
+    def _on_device(self, inputs: Inputs) -> Optional[List[int]]:
+        """Content ids to prepare on the device, or None for host-prepared inputs: text, or ids
+        with no host TextPrep given."""
+        if isinstance(inputs, PreparedInputs):
+            return None
+        if isinstance(inputs, str):
+            return self.content_ids(inputs)
+        return None if self.text_prep is not None else [int(i) for i in inputs]
+
     def _prepare(self, inputs: Inputs, options: GenerateOptions, lookahead: int) -> PreparedInputs:
         if isinstance(inputs, PreparedInputs):
             return inputs
-        if self.text_prep is None:
-            raise InvalidInputError(Q3T_ERR_INVALID, "content ids need a TextPrep; pass PreparedInputs instead")
+        if isinstance(inputs, str) or self.text_prep is None:
+            ids = self._on_device(inputs)
+            return self.prepare_text(ids, options.speaker, options.language, lookahead)
         return self.text_prep.prepare(inputs, options.speaker, options.language, lookahead)
 
     def generate_codes(self, inputs: Inputs, options: GenerateOptions = GenerateOptions()) -> GeneratedCodes:
         """``generate_codes`` (generation.rs:356-371): all text in the prefill, then the rollout."""
+        ids = self._on_device(inputs)
+        if ids is not None:  # prompt rows built on the device, then drained as one chunk
+            with self.start_stream_text(ids, options, StreamOptions(text_lookahead_tokens=0x7FFFFFFF)) as st:
+                chunk = st.next_codes_chunk(max(options.max_frames, 1))
+                codes = chunk.codes if chunk else np.zeros((0, self.code_groups), np.int32)
+                return GeneratedCodes(codes, int(codes.shape[0]), st.ended_by_eos)
         inp = self._prepare(inputs, options, 1 << 30)
         o = options._c()
         pre, trail, pad = _f32(inp.prefill), _f32(inp.trailing_text), _f32(inp.tts_pad_embed)
@@ -443,6 +473,9 @@ class HipTtsEngine:
                      stream_options: StreamOptions = StreamOptions()) -> "HipTtsStream":
         """``start_stream`` (generation.rs:421-440)."""
         stream_options.validate()
+        ids = self._on_device(inputs)
+        if ids is not None:
+            return self.start_stream_text(ids, options, stream_options)
         inp = self._prepare(inputs, options, stream_options.text_lookahead_tokens)
         return HipTtsStream(self, inp, options, stream_options)
 

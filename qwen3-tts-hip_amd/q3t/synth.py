@@ -314,6 +314,64 @@ class SyntheticModel:
         os.replace(path + ".tmp", path)
 
 
+# ----------------------------------------------------------------------------------------
+# synthetic tokenizer files
+# ----------------------------------------------------------------------------------------
+def byte_level_alphabet() -> List[str]:
+    """The 256 byte-level symbols in the GPT-2 / Qwen2 vocabulary order: printable bytes
+    first, then the rest mapped above U+0100 (so byte 10, the newline, is id 198)."""
+    bs = list(range(ord("!"), ord("~") + 1)) + list(range(0xA1, 0xAC + 1)) + list(range(0xAE, 0xFF + 1))
+    cs = list(bs)
+    n = 0
+    for b in range(256):
+        if b not in bs:
+            bs.append(b)
+            cs.append(256 + n)
+            n += 1
+    return [chr(c) for c in cs]
+
+
+# Merges of the synthetic BPE: "assistant" (77091, as the real vocabulary has it) and a few
+# words, so that encoding exercises multi-step merges and the space marker.
+SYNTH_WORDS = {"assistant": TOKENS["assistant_token_id"], "hello": 9707, "\u0120world": 1879,
+               "the": 1782, "\u0120the": 279}
+SPECIAL_TOKENS = {151643: "<|endoftext|>", 151644: "<|im_start|>", 151645: "<|im_end|>"}
+
+
+def write_tokenizer(model_dir: str) -> None:
+    """vocab.json + merges.txt + tokenizer_config.json of a small byte-level BPE with the real
+    vocabulary size (151,643 ids, unused ids filled with unreachable tokens) and the chat
+    specials as added tokens, the files TextTokenizer::from_bpe_files reads (text.rs:195-237)."""
+    alphabet = byte_level_alphabet()
+    vocab = {ch: i for i, ch in enumerate(alphabet)}
+    merges = []
+    next_id = 256
+    for word, wid in SYNTH_WORDS.items():
+        cur = word[0]
+        for k in range(1, len(word)):
+            merges.append(f"{cur} {word[k]}")
+            cur += word[k]
+            if cur not in vocab:
+                if k == len(word) - 1:
+                    vocab[cur] = wid
+                else:
+                    vocab[cur] = next_id
+                    next_id += 1
+    used = set(vocab.values())
+    filler = (i for i in range(151643) if i not in used)
+    for i in filler:
+        vocab[f"<|q3t_unused_{i}|>"] = i
+    os.makedirs(model_dir, exist_ok=True)
+    with open(os.path.join(model_dir, "vocab.json"), "w") as f:
+        json.dump(vocab, f, ensure_ascii=False)
+    with open(os.path.join(model_dir, "merges.txt"), "w") as f:
+        f.write("#version: 0.2\n" + "\n".join(merges) + "\n")
+    added = {str(i): dict(content=c, lstrip=False, normalized=False, rstrip=False, single_word=False, special=True)
+             for i, c in SPECIAL_TOKENS.items()}
+    with open(os.path.join(model_dir, "tokenizer_config.json"), "w") as f:
+        json.dump({"added_tokens_decoder": added}, f)
+
+
 def read_safetensors_bf16(path: str) -> Dict[str, np.ndarray]:
     """Read a BF16 safetensors file into uint16 arrays (memory-mapped)."""
     with open(path, "rb") as f:

@@ -37,12 +37,16 @@ class _ModelCache:
         return self.models[key]
 
     def get_with_text(self, spec: str, seed: int = 0):
-        """The same model written with its full text-embedding table (device text preparation)."""
+        """The same model written with its full text-embedding table and tokenizer files
+        (device text preparation, text inputs)."""
+        from q3t import synth
+
         key = (spec, seed, "text")
         if key not in self.models:
             model, _ = self.get(spec, seed)
             d = os.path.join(self.root, f"{spec}_{seed}_text")
             model.write(d, text_embedding=True)
+            synth.write_tokenizer(d)
             self.models[key] = (model, d)
         return self.models[key]
 

@@ -97,3 +97,28 @@ def test_text_prep_errors(tiny_text, models):
         assert not e2.has_device_text_prep
         with pytest.raises(E.NotFoundError):
             e2.prepare_text([1, 2, 3])
+
+
+def test_generate_codes_from_text(tiny_text, models):
+    """Text in, codes out: the directory's tokenizer, the chat-template slice, device
+    preparation with every content id in the prefill (generate_codes, generation.rs:356-371)."""
+    model, oracle, eng = tiny_text
+    assert eng.tokenizer is not None
+    text = "hello world, hello world!"
+    ids = eng.content_ids(text)
+    assert ids[:2] == [9707, 1879]
+    opts = E.GenerateOptions.greedy(10)
+    a = eng.generate_codes(text, opts)
+    b = eng.generate_codes(ids, opts)            # ids prepared on the device (no host TextPrep given)
+    np.testing.assert_array_equal(a.codes, b.codes)
+    ref_in = oracle.prepare(ids, "ryan", "english", 1 << 30)
+    o = Oracle(model.tensors, model.config(), max_cache_steps=256)
+    oo = OracleOptions(**{k: getattr(opts, k) for k in OracleOptions.__dataclass_fields__})
+    tr = o.rollout(ref_in.prefill, ref_in.trailing_text, ref_in.tts_pad_embed, oo)
+    fx = dict(codes=tr.codes, talker_logits=tr.talker_logits, talker_margins=tr.talker_margins,
+              cp_margins=tr.cp_margins, meta=dict(ended_by_eos=tr.ended_by_eos))
+    same = check_codes(a.codes, a.ended_by_eos, fx)
+    print(f"generate_codes from text: {same} frames identical")
+    with eng.start_stream(text, opts, E.StreamOptions(text_lookahead_tokens=2)) as st:
+        assert st.prefill_steps == 11
+        assert st.next_codes_chunk(4).frames == 4
