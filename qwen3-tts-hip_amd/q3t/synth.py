@@ -315,6 +315,131 @@ class SyntheticModel:
 
 
 # ----------------------------------------------------------------------------------------
+# synthetic speech-tokenizer (codec) checkpoint: speech_tokenizer/model.safetensors
+# ----------------------------------------------------------------------------------------
+# Shapes of the reference's codec decoder (src/audio/codec_hip.rs:18-45, 214-336).
+CODEC = dict(groups=16, codebook=2048, codebook_dim=256, projected=512, pre_conv=1024, hidden=512,
+             layers=8, heads=16, head_dim=64, intermediate=1024, upsample=1024, convnext=4096,
+             decoder_init=1536, blocks=((1536, 768, 8), (768, 384, 5), (384, 192, 4), (192, 96, 3)),
+             final=96)
+
+
+def codec_inventory(c: dict = CODEC) -> List[Tuple[str, Tuple[int, ...], str]]:
+    """(name, shape, kind) of every codec-decoder tensor.  Kinds: fan:N[:g] = N(0, g^2/N) weights
+    (so activations stay O(1) through the ~40 layers; g = 0.25 on the residual units' last
+    convolutions, whose outputs add up over 12 units), bias, gain (1 + N(0, 0.02)), code (codebook
+    sums, N(0, 1)), usage (cluster usage, e^N(0, 0.3)), scale (0.1 + N(0, 0.02): layer scales,
+    ConvNeXt gamma), snake (log alpha / log beta, N(0, 0.1))."""
+    inv = []
+    q = "decoder.quantizer"
+    for name, n in (("rvq_first", 1), ("rvq_rest", c["groups"] - 1)):
+        for i in range(n):
+            p = f"{q}.{name}.vq.layers.{i}._codebook"
+            inv += [(f"{p}.embedding_sum", (c["codebook"], c["codebook_dim"]), "code"),
+                    (f"{p}.cluster_usage", (c["codebook"],), "usage")]
+        inv.append((f"{q}.{name}.output_proj.weight", (c["projected"], c["codebook_dim"], 1),
+                    f"fan:{2 * c['codebook_dim']}"))
+    inv += [("decoder.pre_conv.conv.weight", (c["pre_conv"], c["projected"], 3), f"fan:{3 * c['projected']}"),
+            ("decoder.pre_conv.conv.bias", (c["pre_conv"],), "bias")]
+    t, H, Q, I = "decoder.pre_transformer", c["hidden"], c["heads"] * c["head_dim"], c["intermediate"]
+    inv += [(f"{t}.input_proj.weight", (H, c["pre_conv"]), f"fan:{c['pre_conv']}"),
+            (f"{t}.input_proj.bias", (H,), "bias")]
+    for i in range(c["layers"]):
+        p = f"{t}.layers.{i}"
+        inv += [(f"{p}.input_layernorm.weight", (H,), "gain"),
+                (f"{p}.self_attn.q_proj.weight", (Q, H), f"fan:{H}"),
+                (f"{p}.self_attn.k_proj.weight", (Q, H), f"fan:{H}"),
+                (f"{p}.self_attn.v_proj.weight", (Q, H), f"fan:{H}"),
+                (f"{p}.self_attn.o_proj.weight", (H, Q), f"fan:{Q}"),
+                (f"{p}.self_attn_layer_scale.scale", (H,), "scale"),
+                (f"{p}.post_attention_layernorm.weight", (H,), "gain"),
+                (f"{p}.mlp.gate_proj.weight", (I, H), f"fan:{H}"),
+                (f"{p}.mlp.up_proj.weight", (I, H), f"fan:{H}"),
+                (f"{p}.mlp.down_proj.weight", (H, I), f"fan:{I}"),
+                (f"{p}.mlp_layer_scale.scale", (H,), "scale")]
+    inv += [(f"{t}.norm.weight", (H,), "gain"),
+            (f"{t}.output_proj.weight", (c["pre_conv"], H), f"fan:{H}"),
+            (f"{t}.output_proj.bias", (c["pre_conv"],), "bias")]
+    U, X = c["upsample"], c["convnext"]
+    for i in range(2):
+        p = f"decoder.upsample.{i}"
+        inv += [(f"{p}.0.conv.weight", (U, U, 2), f"fan:{U}"), (f"{p}.0.conv.bias", (U,), "bias"),
+                (f"{p}.1.dwconv.conv.weight", (U, 1, 7), "fan:7"), (f"{p}.1.dwconv.conv.bias", (U,), "bias"),
+                (f"{p}.1.norm.weight", (U,), "gain"), (f"{p}.1.norm.bias", (U,), "bias"),
+                (f"{p}.1.pwconv1.weight", (X, U), f"fan:{U}"), (f"{p}.1.pwconv1.bias", (X,), "bias"),
+                (f"{p}.1.pwconv2.weight", (U, X), f"fan:{X}"), (f"{p}.1.pwconv2.bias", (U,), "bias"),
+                (f"{p}.1.gamma", (U,), "scale")]
+    inv += [("decoder.decoder.0.conv.weight", (c["decoder_init"], c["pre_conv"], 7), f"fan:{7 * c['pre_conv']}"),
+            ("decoder.decoder.0.conv.bias", (c["decoder_init"],), "bias")]
+    for b, (ci, co, stride) in enumerate(c["blocks"]):
+        p = f"decoder.decoder.{b + 1}.block"
+        inv += [(f"{p}.0.alpha", (ci,), "snake"), (f"{p}.0.beta", (ci,), "snake"),
+                (f"{p}.1.conv.weight", (ci, co, 2 * stride), f"fan:{2 * ci}"), (f"{p}.1.conv.bias", (co,), "bias")]
+        for u in range(3):
+            r = f"{p}.{u + 2}"
+            inv += [(f"{r}.act1.alpha", (co,), "snake"), (f"{r}.act1.beta", (co,), "snake"),
+                    (f"{r}.conv1.conv.weight", (co, co, 7), f"fan:{7 * co}"), (f"{r}.conv1.conv.bias", (co,), "bias"),
+                    (f"{r}.act2.alpha", (co,), "snake"), (f"{r}.act2.beta", (co,), "snake"),
+                    (f"{r}.conv2.conv.weight", (co, co, 1), f"fan:{co}:0.25"), (f"{r}.conv2.conv.bias", (co,), "bias")]
+    inv += [("decoder.decoder.5.alpha", (c["final"],), "snake"), ("decoder.decoder.5.beta", (c["final"],), "snake"),
+            ("decoder.decoder.6.conv.weight", (1, c["final"], 7), f"fan:{7 * c['final']}:0.2"),
+            ("decoder.decoder.6.conv.bias", (1,), "bias")]
+    return inv
+
+
+def generate_codec_tensor(seed: int, name: str, shape: Tuple[int, ...], kind: str) -> np.ndarray:
+    """bf16 bit patterns of one synthetic codec tensor (its own Philox stream, as the model's)."""
+    n = int(np.prod(shape))
+    z = _philox(seed, "codec:" + name).standard_normal(n, dtype=np.float32)
+    if kind.startswith("fan:"):
+        parts = kind.split(":")
+        gain = float(parts[2]) if len(parts) > 2 else 1.0
+        z *= np.float32(gain / np.sqrt(float(parts[1])))
+    elif kind == "bias":
+        z *= np.float32(0.02)
+    elif kind == "gain":
+        z = np.float32(1.0) + z * np.float32(0.02)
+    elif kind == "usage":
+        z = np.exp(z * np.float32(0.3)).astype(np.float32)
+    elif kind == "scale":
+        z = np.float32(0.1) + z * np.float32(0.02)
+    elif kind == "snake":
+        z *= np.float32(0.1)
+    elif kind != "code":
+        raise ValueError(f"unknown codec tensor kind {kind}")
+    return f32_to_bf16_bits(z).reshape(shape)
+
+
+def codec_tensors(seed: int = 0) -> Dict[str, np.ndarray]:
+    return {name: generate_codec_tensor(seed, name, shape, kind) for name, shape, kind in codec_inventory()}
+
+
+def write_codec(model_dir: str, seed: int = 0, tensors: Optional[Dict[str, np.ndarray]] = None) -> None:
+    """speech_tokenizer/model.safetensors (BF16) under model_dir, the file the reference's
+    codec loader opens (codec_hip.rs:214-215)."""
+    tensors = tensors if tensors is not None else codec_tensors(seed)
+    d = os.path.join(model_dir, "speech_tokenizer")
+    os.makedirs(d, exist_ok=True)
+    header: Dict[str, dict] = {"__metadata__": {"format": "pt", "q3t_seed": str(seed)}}
+    offset = 0
+    names = [name for name, _, _ in codec_inventory()]
+    for name in names:
+        nbytes = tensors[name].size * 2
+        header[name] = {"dtype": "BF16", "shape": list(tensors[name].shape),
+                        "data_offsets": [offset, offset + nbytes]}
+        offset += nbytes
+    blob = json.dumps(header, separators=(",", ":")).encode()
+    blob += b" " * ((8 - len(blob) % 8) % 8)
+    path = os.path.join(d, "model.safetensors")
+    with open(path + ".tmp", "wb") as f:
+        f.write(struct.pack("<Q", len(blob)))
+        f.write(blob)
+        for name in names:
+            f.write(np.ascontiguousarray(tensors[name]).tobytes())
+    os.replace(path + ".tmp", path)
+
+
+# ----------------------------------------------------------------------------------------
 # synthetic tokenizer files
 # ----------------------------------------------------------------------------------------
 def byte_level_alphabet() -> List[str]:
