@@ -47,7 +47,7 @@ def causal_conv(x: np.ndarray, w: np.ndarray, b: np.ndarray, dilation: int = 1) 
     xp = np.concatenate([np.zeros((pad, in_c)), x], axis=0)
     y = np.tile(b, (T, 1)).astype(np.float64)
     for j in range(k):
-        y += xp[j * dilation:j * dilation + T] @ w[:, :, j].T
+        y += xp[j * dilation:j * dilation + T] @ np.ascontiguousarray(w[:, :, j].T)
     return y
 
 
@@ -57,7 +57,7 @@ def transposed_conv(x: np.ndarray, w: np.ndarray, b: np.ndarray, stride: int) ->
     in_c, out_c, k = w.shape
     y = np.zeros((T * stride + k, out_c))
     for j in range(k):
-        y[j:j + T * stride:stride] += x @ w[:, :, j]
+        y[j:j + T * stride:stride] += x @ np.ascontiguousarray(w[:, :, j])
     return y[:T * stride] + b
 
 
