@@ -74,6 +74,7 @@ typedef struct {
   int64_t device_bytes; /* device memory held by the engine */
   int32_t text_vocab;   /* text-embedding rows on the device (0: no device text preparation) */
   int32_t text_hidden;
+  int32_t samples_per_frame; /* codec samples per frame (1920 at 24 kHz), 0: no codec decoder */
 } q3t_engine_info;
 
 /* GeneratedCodesChunk (generation.rs:876-963). */
@@ -158,6 +159,22 @@ int q3t_prepare_text(q3t_engine *engine, const int32_t *content_ids, int32_t n_i
  * host round trip), then as q3t_stream_start.  The speaker and language come from opts. */
 int q3t_stream_start_text(q3t_engine *engine, const int32_t *content_ids, int32_t n_ids,
                           int32_t text_lookahead_tokens, const q3t_generate_options *opts, q3t_stream **out);
+
+/* HipTtsEngine::decode_codes (generation.rs:619-647): codec frames [frames][num_code_groups]
+ * int32 (frame-major, as the codes calls return them) -> frames * samples_per_frame samples at
+ * 24 kHz in [-1, 1], through the speech tokenizer's decoder (src/audio/codec_hip.rs: RVQ,
+ * pre-conv, 8-layer pre-transformer, two ConvNeXt upsampling stages, four Snake / transposed-
+ * conv decoder blocks).  The model directory must hold speech_tokenizer/model.safetensors
+ * (Q3T_ERR_NOT_FOUND otherwise).  frames = 0 decodes nothing. */
+int q3t_decode_codes(q3t_engine *engine, const int32_t *codes, int32_t frames, float *samples);
+
+/* HipTtsStream::next_audio_chunk (generation.rs:965-989): q3t_stream_next_codes into codes
+ * (max_chunk_frames * num_code_groups), then the chunk's frames decoded together with up to
+ * left_context_frames earlier frames of the stream (StreamOptions::left_context_frames,
+ * default 25), keeping the chunk's own info->frames * samples_per_frame samples in samples
+ * (*n_samples of them).  info->frames = 0: the stream had nothing left. */
+int q3t_stream_next_audio(q3t_stream *stream, int32_t max_chunk_frames, int32_t left_context_frames,
+                          int32_t *codes, float *samples, int32_t *n_samples, q3t_chunk_info *info);
 
 /* Drops the stream and frees its slot (HipTtsStream's Drop). */
 int q3t_stream_destroy(q3t_stream *stream);

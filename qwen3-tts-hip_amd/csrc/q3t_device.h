@@ -54,6 +54,9 @@ enum Epilogue : int32_t {
   EPI_RESIDUAL = 1,  // out[n] = res[n] + acc
   EPI_SWIGLU = 2,    // out[j] = silu(acc_gate_j) * acc_up_j; W holds gate rows then up rows
   EPI_BIAS = 3,      // out[n] = acc + bias[n]
+  // matrix-core GEMMs only (the codec decoder):
+  EPI_AFFINE_RES = 4,  // out[n] = res[n] + (acc + bias[n]) * scale[n] (bias, scale optional)
+  EPI_BIAS_GELU = 5,   // out[n] = gelu(acc + bias[n]), erf form
 };
 
 // Greedy token hand-off into a CodePredictor group (one stream): the group's input token is
@@ -163,7 +166,11 @@ struct GemmArgs {
   float *Y;                // [M][ldy]
   const float *res;        // EPI_RESIDUAL: [M][ldr]
   const float *bias;       // EPI_BIAS: [N]
+  const float *scale;      // EPI_AFFINE_RES: [N] or null
   int32_t M, N, K, ldx, ldy, ldr;
+  // Segmented X rows (matrix-core GEMMs; a dilated convolution's taps): with xseg_len > 0,
+  // element k of row m is X[m * ldx + (k / xseg_len) * xseg_stride + k % xseg_len].
+  int32_t xseg_len, xseg_stride;
   float eps;               // skinny GEMM with a fused RMSNorm
   const int32_t *row_on;   // skinny GEMM: row m is stored only where row_on[m] (null: all rows)
   // skinny GEMM layouts: X / Y / res in T16 (ld ignored) instead of row-major, and W packed

@@ -29,7 +29,9 @@
 #include <unistd.h>
 
 #include "../../include/q3t.h"
+#include "q3t_codec.h"
 #include "q3t_device.h"
+#include "q3t_host.h"
 #include "q3t_json.h"
 #include "q3t_kernels.h"
 
@@ -37,25 +39,6 @@ namespace q3t {
 namespace {
 
 thread_local std::string g_last_error;
-
-struct Failure {
-  int code;
-  std::string msg;
-};
-
-[[noreturn]] void fail(int code, const char *fmt, ...) {
-  char buf[1024];
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(buf, sizeof buf, fmt, ap);
-  va_end(ap);
-  throw Failure{code, buf};
-}
-
-void hip_check(hipError_t e, const char *call) {
-  if (e != hipSuccess) fail(Q3T_ERR_HIP, "%s failed: %s (%d)", call, hipGetErrorString(e), (int)e);
-}
-#define HIPC(x) ::q3t::hip_check((x), #x)
 
 template <typename F>
 int guarded(F &&f) {
@@ -70,116 +53,6 @@ int guarded(F &&f) {
     return Q3T_ERR_INVALID;
   }
 }
-
-uint16_t f32_to_bf16_host(float f) {
-  uint32_t u;
-  memcpy(&u, &f, 4);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-float bf16_to_f32_host(uint16_t b) {
-  const uint32_t u = (uint32_t)b << 16;
-  float f;
-  memcpy(&f, &u, 4);
-  return f;
-}
-
-// ------------------------------------------------------------------------------------
-// safetensors (BF16 or F32 tensors; F32 is rounded to bf16 on load)
-// ------------------------------------------------------------------------------------
-class SafeTensors {
- public:
-  explicit SafeTensors(const std::string &path) : path_(path) {
-    fd_ = open(path.c_str(), O_RDONLY);
-    if (fd_ < 0) fail(Q3T_ERR_NOT_FOUND, "cannot open %s", path.c_str());
-    struct stat sb;
-    fstat(fd_, &sb);
-    size_ = (size_t)sb.st_size;
-    if (size_ < 8) fail(Q3T_ERR_INVALID, "%s is not a safetensors file", path.c_str());
-    base_ = (const uint8_t *)mmap(nullptr, size_, PROT_READ, MAP_PRIVATE, fd_, 0);
-    if (base_ == MAP_FAILED) fail(Q3T_ERR_INVALID, "mmap of %s failed", path.c_str());
-    uint64_t hlen;
-    memcpy(&hlen, base_, 8);
-    if (8 + hlen > size_) fail(Q3T_ERR_INVALID, "%s: header length out of range", path.c_str());
-    header_ = json::parse(std::string((const char *)base_ + 8, hlen));
-    data_ = base_ + 8 + hlen;
-    data_size_ = size_ - 8 - hlen;
-  }
-  ~SafeTensors() {
-    if (base_ && base_ != MAP_FAILED) munmap((void *)base_, size_);
-    if (fd_ >= 0) close(fd_);
-  }
-
-  // Appends the tensor (as bf16) to out, checking its shape.
-  void append_bf16(const std::string &name, const std::vector<int64_t> &shape, std::vector<uint16_t> &out) const {
-    const auto [ptr, dtype, n] = view(name, shape);
-    const size_t at = out.size();
-    out.resize(at + n);
-    if (dtype == "BF16") {
-      memcpy(out.data() + at, ptr, n * 2);
-    } else {
-      const float *f = (const float *)ptr;
-      for (size_t i = 0; i < n; ++i) out[at + i] = f32_to_bf16_host(f[i]);
-    }
-  }
-  std::vector<float> f32(const std::string &name, const std::vector<int64_t> &shape) const {
-    const auto [ptr, dtype, n] = view(name, shape);
-    std::vector<float> out(n);
-    if (dtype == "BF16") {
-      const uint16_t *b = (const uint16_t *)ptr;
-      for (size_t i = 0; i < n; ++i) out[i] = bf16_to_f32_host(b[i]);
-    } else {
-      memcpy(out.data(), ptr, n * 4);
-    }
-    return out;
-  }
-  bool has(const std::string &name) const { return header_.has(name); }
-  std::vector<int64_t> shape(const std::string &name) const {
-    std::vector<int64_t> out;
-    for (const json::Value &d : header_.at(name).at("shape").arr) out.push_back(d.integer());
-    return out;
-  }
-
- private:
-  struct View {
-    const uint8_t *ptr;
-    std::string dtype;
-    size_t n;
-  };
-  View view(const std::string &name, const std::vector<int64_t> &shape) const {
-    if (!header_.has(name)) fail(Q3T_ERR_NOT_FOUND, "tensor %s not found in %s", name.c_str(), path_.c_str());
-    const json::Value &t = header_.at(name);
-    const std::string dtype = t.at("dtype").str;
-    if (dtype != "BF16" && dtype != "F32")
-      fail(Q3T_ERR_INVALID, "%s has dtype %s, expected BF16 or F32", name.c_str(), dtype.c_str());
-    const auto &sh = t.at("shape").arr;
-    bool ok = sh.size() == shape.size();
-    size_t n = 1;
-    for (size_t i = 0; ok && i < sh.size(); ++i) {
-      ok = sh[i].integer() == shape[i];
-      n *= (size_t)shape[i];
-    }
-    if (!ok) {
-      std::string want, got;
-      for (auto d : shape) want += std::to_string(d) + ",";
-      for (auto &d : sh) got += std::to_string(d.integer()) + ",";
-      fail(Q3T_ERR_INVALID, "%s shape [%s] does not match expected [%s]", name.c_str(), got.c_str(), want.c_str());
-    }
-    const auto &off = t.at("data_offsets").arr;
-    const size_t b = (size_t)off[0].integer(), e = (size_t)off[1].integer();
-    const size_t esz = dtype == "BF16" ? 2 : 4;
-    if (e > data_size_ || e - b != n * esz) fail(Q3T_ERR_INVALID, "%s: data offsets out of range", name.c_str());
-    return {data_ + b, dtype, n};
-  }
-
-  std::string path_;
-  int fd_ = -1;
-  size_t size_ = 0;
-  const uint8_t *base_ = nullptr;
-  const uint8_t *data_ = nullptr;
-  size_t data_size_ = 0;
-  json::Value header_;
-};
 
 // ------------------------------------------------------------------------------------
 // model
@@ -208,15 +81,6 @@ Dims dims_from(const json::Value &c) {
   d.eps = (float)c.at("rms_norm_eps").number();
   d.theta = (float)c.at("rope_theta").number();
   return d;
-}
-
-template <typename T>
-T *dev_alloc(size_t n, int64_t &tally) {
-  void *p = nullptr;
-  if (n == 0) n = 1;
-  HIPC(hipMalloc(&p, n * sizeof(T)));
-  tally += (int64_t)(n * sizeof(T));
-  return (T *)p;
 }
 
 struct LayerW {
@@ -391,6 +255,8 @@ struct Engine {
   int tok_im_start = 0, tok_assistant = 0, tok_tts_pad = 0, tok_tts_bos = 0, tok_tts_eos = 0;
   int codec_pad = 0, codec_bos = 0, codec_think = 0, codec_think_bos = 0, codec_think_eos = 0;
   std::map<std::string, int> speaker_ids, language_ids;
+  // Codec decoder (speech_tokenizer/model.safetensors under the model directory), or null.
+  Codec *codec = nullptr;
   // Packed copies for the batched frame's skinny GEMMs (multi-stream engines only).
   uint16_t *codec_head_p = nullptr, *lm_heads_p = nullptr, *proj_w_p = nullptr;
   // Batched-frame activations in T16 (16 stream rows): residual streams, attention output,
@@ -1242,6 +1108,7 @@ int q3t_engine_create(const q3t_engine_options *opts, q3t_engine **out) {
       alloc_pools(*e, nslots);
       if (nslots > 1 && e->rows_ok) alloc_rows(*e);
       build_cp_tables(*e);
+      e->codec = codec_load(dir, &e->device_bytes);
     } catch (...) {
       free_pools(*e);
       throw;
@@ -1257,6 +1124,7 @@ int q3t_engine_destroy(q3t_engine *e) {
     (void)hipSetDevice(e->device);
     (void)hipDeviceSynchronize();
     q3t::free_pools(*e);
+    q3t::codec_free(e->codec);
     void *ptrs[] = {e->talker.mats, e->talker.gains, e->talker.rope, e->cp.mats,     e->cp.gains,
                     e->cp.rope,     e->codec_head,   e->codec_emb,   e->t_norm,      e->c_norm,
                     e->lm_heads,    e->cp_emb,       e->proj_w,      e->proj_b,      e->talker.mats_p,
@@ -1291,6 +1159,7 @@ int q3t_engine_get_info(const q3t_engine *e, q3t_engine_info *o) {
     o->device_bytes = e->device_bytes;
     o->text_vocab = e->text_vocab;
     o->text_hidden = e->text_hidden;
+    o->samples_per_frame = e->codec ? q3t::kCodecSamplesPerFrame : 0;
   });
 }
 
@@ -1695,6 +1564,59 @@ int q3t_stream_next_codes(q3t_stream *sp, int32_t max_chunk, int32_t *codes, q3t
     info->frames = produced;
     info->total_frames = sp->host_frame;
     info->ended_by_eos = sp->done == 1;
+  });
+}
+
+int q3t_decode_codes(q3t_engine *e, const int32_t *codes, int32_t frames, float *samples) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || (frames > 0 && (!codes || !samples))) fail(Q3T_ERR_INVALID, "null argument");
+    if (frames < 0) fail(Q3T_ERR_INVALID, "frame count must not be negative");
+    if (!e->codec) fail(Q3T_ERR_NOT_FOUND, "the model directory has no speech_tokenizer/model.safetensors");
+    if (frames == 0) return;  // decode_codes of no codes: no samples (generation.rs:628-630)
+    HIPC(hipSetDevice(e->device));
+    hipStream_t s = e->pools.stream;
+    int32_t *dc = codec_codes_buffer(*e->codec, (size_t)frames * e->groups);
+    float *ds = codec_samples_buffer(*e->codec, (size_t)frames * kCodecSamplesPerFrame);
+    HIPC(hipMemcpyAsync(dc, codes, (size_t)frames * e->groups * 4, hipMemcpyHostToDevice, s));
+    codec_decode(*e->codec, dc, frames, e->groups, ds, s);
+    HIPC(hipMemcpy(samples, ds, (size_t)frames * kCodecSamplesPerFrame * 4, hipMemcpyDeviceToHost));
+  });
+}
+
+int q3t_stream_next_audio(q3t_stream *sp, int32_t max_chunk, int32_t left_context, int32_t *codes, float *samples,
+                          int32_t *n_samples, q3t_chunk_info *info) {
+  using namespace q3t;
+  if (!sp || !codes || !samples || !n_samples || !info) {
+    g_last_error = "null argument";
+    return Q3T_ERR_INVALID;
+  }
+  if (!sp->engine->codec) {
+    g_last_error = "the model directory has no speech_tokenizer/model.safetensors";
+    return Q3T_ERR_NOT_FOUND;
+  }
+  if (left_context < 0) {
+    g_last_error = "left_context_frames must not be negative";
+    return Q3T_ERR_INVALID;
+  }
+  *n_samples = 0;
+  const int rc = q3t_stream_next_codes(sp, max_chunk, codes, info);
+  if (rc != Q3T_OK || info->frames == 0) return rc;
+  return guarded([&] {
+    // next_audio_chunk (generation.rs:965-989): decode the chunk with up to left_context
+    // earlier frames (the slot keeps every frame's codes on the device) and keep the chunk's
+    // own samples.
+    Engine &e = *sp->engine;
+    HIPC(hipSetDevice(e.device));
+    const int start = info->total_frames - info->frames;
+    const int ctx = std::min(left_context, start);
+    const int n = info->frames + ctx;
+    hipStream_t s = e.slots[sp->slot].stream;
+    float *ds = codec_samples_buffer(*e.codec, (size_t)n * kCodecSamplesPerFrame);
+    codec_decode(*e.codec, e.slots[sp->slot].codes + (size_t)(start - ctx) * e.groups, n, e.groups, ds, s);
+    HIPC(hipMemcpy(samples, ds + (size_t)ctx * kCodecSamplesPerFrame,
+                   (size_t)info->frames * kCodecSamplesPerFrame * 4, hipMemcpyDeviceToHost));
+    *n_samples = info->frames * kCodecSamplesPerFrame;
   });
 }
 

@@ -722,6 +722,32 @@ __device__ __forceinline__ void split_bf16x8(const float *x, bf16x8_t &hi, bf16x
   }
 }
 
+// Offset of X element (m, k) in the matrix-core GEMMs (k a multiple of 4 inside one 32-wide
+// k step, which never straddles an X segment).
+__device__ __forceinline__ size_t gemm_x_offset(const GemmArgs &a, int m, int k) {
+  size_t o = (size_t)m * a.ldx;
+  if (a.xseg_len > 0) o += (size_t)(k / a.xseg_len) * a.xseg_stride + k % a.xseg_len;
+  else o += k;
+  return o;
+}
+
+// Epilogues of the matrix-core GEMMs for element (m, n) with accumulated value v (not SwiGLU).
+template <int EPI>
+__device__ __forceinline__ float gemm_epilogue(const GemmArgs &a, int m, int n, float v) {
+  if constexpr (EPI == EPI_RESIDUAL) v = a.res[(size_t)m * a.ldr + n] + v;
+  if constexpr (EPI == EPI_BIAS) v = v + a.bias[n];
+  if constexpr (EPI == EPI_AFFINE_RES) {
+    if (a.bias) v = v + a.bias[n];
+    if (a.scale) v = v * a.scale[n];
+    v = a.res[(size_t)m * a.ldr + n] + v;
+  }
+  if constexpr (EPI == EPI_BIAS_GELU) {
+    v = v + a.bias[n];
+    v = 0.5f * v * (1.0f + erff(v * 0.7071067811865476f));
+  }
+  return v;
+}
+
 template <int EPI, int MB, int NB>
 __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
   const int lane = threadIdx.x & 63;
@@ -764,7 +790,7 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
     float xa[MB][8];
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
-      const float4 *px = reinterpret_cast<const float4 *>(a.X + (size_t)arow[i] * a.ldx + k);
+      const float4 *px = reinterpret_cast<const float4 *>(a.X + gemm_x_offset(a, arow[i], k));
       const float4 p0 = px[0], p1 = px[1];
       xa[i][0] = p0.x; xa[i][1] = p0.y; xa[i][2] = p0.z; xa[i][3] = p0.w;
       xa[i][4] = p1.x; xa[i][5] = p1.y; xa[i][6] = p1.z; xa[i][7] = p1.w;
@@ -823,10 +849,8 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
         if constexpr (EPI == EPI_SWIGLU) {
           const float u = acc[i][j + NTILE][e];
           v = v / (1.0f + expf(-v)) * u;
-        } else if constexpr (EPI == EPI_RESIDUAL) {
-          v = a.res[(size_t)m * a.ldr + n] + v;
-        } else if constexpr (EPI == EPI_BIAS) {
-          v = v + a.bias[n];
+        } else {
+          v = gemm_epilogue<EPI>(a, m, n, v);
         }
         a.Y[(size_t)m * a.ldy + n] = v;
       }
@@ -887,7 +911,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
     for (int i = 0; i < NA; ++i) {
       const int idx = tid + 256 * i, row = idx / CA, c4 = idx % CA;
       const int m = min(m0 + row, a.M - 1);
-      ra[i] = *reinterpret_cast<const float4 *>(a.X + (size_t)m * a.ldx + k0 + 4 * c4);
+      ra[i] = *reinterpret_cast<const float4 *>(a.X + gemm_x_offset(a, m, k0 + 4 * c4));
       if (a.gamma) rg[i] = *reinterpret_cast<const float4 *>(a.gamma + k0 + 4 * c4);
     }
 #pragma unroll
@@ -979,10 +1003,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int n = nb * 128 + wn * 64 + u * 16 + li;
-          float v = acc[t][u][e];
-          if constexpr (EPI == EPI_RESIDUAL) v = a.res[(size_t)m * a.ldr + n] + v;
-          if constexpr (EPI == EPI_BIAS) v = v + a.bias[n];
-          a.Y[(size_t)m * a.ldy + n] = v;
+          a.Y[(size_t)m * a.ldy + n] = gemm_epilogue<EPI>(a, m, n, acc[t][u][e]);
         }
       }
     }
@@ -1990,11 +2011,15 @@ hipError_t launch_pack_weights(const uint16_t *src, uint16_t *dst, int rows, int
 
 hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t s) {
   if (a.M <= 0 || a.N <= 0 || a.K <= 0 || a.K % 32 || a.ldx % 4) return hipErrorInvalidValue;
+  if (a.xseg_len && (a.xseg_len < 0 || a.xseg_len % 32 || a.K % a.xseg_len || a.xseg_stride % 4))
+    return hipErrorInvalidValue;
   switch (epi) {
     case EPI_STORE: return gemm_epi<EPI_STORE>(a, s);
     case EPI_RESIDUAL: return gemm_epi<EPI_RESIDUAL>(a, s);
     case EPI_SWIGLU: return gemm_epi<EPI_SWIGLU>(a, s);
     case EPI_BIAS: return gemm_epi<EPI_BIAS>(a, s);
+    case EPI_AFFINE_RES: return a.res ? gemm_epi<EPI_AFFINE_RES>(a, s) : hipErrorInvalidValue;
+    case EPI_BIAS_GELU: return a.bias ? gemm_epi<EPI_BIAS_GELU>(a, s) : hipErrorInvalidValue;
   }
   return hipErrorInvalidValue;
 }

@@ -104,7 +104,8 @@ class _EngineInfo(ctypes.Structure):
         "q_heads", "kv_heads", "head_dim", "num_code_groups",
         "codec_eos", "max_cache_steps", "max_streams")] + [("device_bytes", ctypes.c_int64),
                                                              ("text_vocab", ctypes.c_int32),
-                                                             ("text_hidden", ctypes.c_int32)]
+                                                             ("text_hidden", ctypes.c_int32),
+                                                             ("samples_per_frame", ctypes.c_int32)]
 
 
 class _ChunkInfo(ctypes.Structure):
@@ -142,6 +143,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                                             f32p, P(_GenerateOptions), P(ctypes.c_void_p)]),
         "q3t_stream_next_codes": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, i32p, P(_ChunkInfo)]),
         "q3t_stream_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+        "q3t_decode_codes": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32, f32p]),
+        "q3t_stream_next_audio": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, i32p, f32p, i32p,
+                                                 P(_ChunkInfo)]),
         "q3t_prepare_text": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                             ctypes.c_int32, f32p, i32p, f32p, i32p, f32p]),
         "q3t_stream_start_text": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32, ctypes.c_int32,
@@ -264,6 +268,27 @@ class StreamOptions:
     def validate(self) -> None:
         if self.text_lookahead_tokens == 0:
             raise InvalidInputError(Q3T_ERR_INVALID, "text_lookahead_tokens must be non-zero")
+
+
+@dataclasses.dataclass
+class GeneratedAudioChunk:
+    """``GeneratedAudioChunk`` (generation.rs:165-172)."""
+    samples: np.ndarray      # float32, 24 kHz
+    sample_rate: int
+    frames: int
+    total_frames: int
+    ended_by_eos: bool
+
+
+@dataclasses.dataclass
+class GeneratedSpeech:
+    """``GeneratedSpeech`` (generation.rs:94-103)."""
+    text: str
+    frames: int
+    ended_by_eos: bool
+    codes: np.ndarray
+    samples: np.ndarray
+    sample_rate: int
 
 
 @dataclasses.dataclass
@@ -479,6 +504,30 @@ class HipTtsEngine:
         inp = self._prepare(inputs, options, stream_options.text_lookahead_tokens)
         return HipTtsStream(self, inp, options, stream_options)
 
+    # -- codec decoder ----------------------------------------------------------------------
+    @property
+    def has_codec(self) -> bool:
+        """The model directory holds speech_tokenizer/model.safetensors (decode_codes works)."""
+        return self.info.get("samples_per_frame", 0) > 0
+
+    def decode_codes(self, codes: np.ndarray) -> np.ndarray:
+        """``decode_codes`` (generation.rs:619-647): codes [frames, 16] -> float32 samples at 24 kHz."""
+        c = np.ascontiguousarray(np.asarray(codes, dtype=np.int32))
+        if c.size % self.code_groups:
+            raise InvalidInputError(Q3T_ERR_INVALID, f"code length {c.size} is not divisible by {self.code_groups}")
+        frames = c.size // self.code_groups
+        out = np.zeros(frames * max(self.info["samples_per_frame"], 1), dtype=np.float32)
+        _check(_lib.q3t_decode_codes(self._h, _iptr(c), frames, _fptr(out)))
+        return out if frames else np.zeros(0, np.float32)
+
+    def generate(self, inputs: Inputs, options: GenerateOptions = GenerateOptions()) -> "GeneratedSpeech":
+        """``generate`` (generation.rs:317-332): codes, then audio when ``decode_audio``."""
+        g = self.generate_codes(inputs, options)
+        samples = (self.decode_codes(g.codes) if options.decode_audio and g.frames
+                   else np.zeros(0, np.float32))
+        return GeneratedSpeech(inputs if isinstance(inputs, str) else "", g.frames, g.ended_by_eos, g.codes,
+                               samples, SAMPLE_RATE)
+
     # -- prompt preparation on the device --------------------------------------------------
     @property
     def has_device_text_prep(self) -> bool:
@@ -596,6 +645,23 @@ class HipTtsStream:
         info = _ChunkInfo()
         _check(_lib.q3t_stream_next_codes(self._h, max_chunk_frames, _iptr(buf), ctypes.byref(info)))
         return self._accept(buf, info)
+
+    def next_audio_chunk(self, max_chunk_frames: int) -> Optional[GeneratedAudioChunk]:
+        """``next_audio_chunk`` (generation.rs:965-989): the next codes chunk, decoded with up
+        to ``stream_options.left_context_frames`` earlier frames as context."""
+        if max_chunk_frames <= 0:
+            raise InvalidInputError(Q3T_ERR_INVALID, "max_chunk_frames must be non-zero")
+        buf = np.zeros((max_chunk_frames, self.engine.code_groups), dtype=np.int32)
+        samples = np.zeros(max_chunk_frames * max(self.engine.info["samples_per_frame"], 1), dtype=np.float32)
+        n = ctypes.c_int32()
+        info = _ChunkInfo()
+        _check(_lib.q3t_stream_next_audio(self._h, max_chunk_frames, int(self.stream_options.left_context_frames),
+                                          _iptr(buf), _fptr(samples), ctypes.byref(n), ctypes.byref(info)))
+        chunk = self._accept(buf, info)
+        if chunk is None:
+            return None
+        return GeneratedAudioChunk(samples[:n.value].copy(), SAMPLE_RATE, chunk.frames, chunk.total_frames,
+                                   chunk.ended_by_eos)
 
     def _accept(self, buf: np.ndarray, info: _ChunkInfo) -> Optional[GeneratedCodesChunk]:
         self.frame = info.total_frames

@@ -37,8 +37,8 @@ class _ModelCache:
         return self.models[key]
 
     def get_with_text(self, spec: str, seed: int = 0):
-        """The same model written with its full text-embedding table and tokenizer files
-        (device text preparation, text inputs)."""
+        """The same model written with its full text-embedding table, tokenizer files and the
+        speech-tokenizer (codec) checkpoint: device text preparation, text inputs, audio."""
         from q3t import synth
 
         key = (spec, seed, "text")
@@ -47,6 +47,7 @@ class _ModelCache:
             d = os.path.join(self.root, f"{spec}_{seed}_text")
             model.write(d, text_embedding=True)
             synth.write_tokenizer(d)
+            synth.write_codec(d, seed)
             self.models[key] = (model, d)
         return self.models[key]
 
