@@ -172,6 +172,8 @@ def main() -> int:
     ap.add_argument("--multistream", default="cfg5_0.6b_multistream",
                     help="multi-stream workload reported beside the headline line ('' to skip)")
     ap.add_argument("--multistream-only", action="store_true", help="run only the multi-stream workload")
+    ap.add_argument("--no-codec", action="store_true",
+                    help="skip the codec-decoder timing (and the speech-tokenizer checkpoint it needs)")
     ap.add_argument("--no-text-prep", action="store_true",
                     help="skip the device prompt-preparation timing (and the text-embedding table it needs)")
     ap.add_argument("--kernel-classes", action="store_true",
@@ -197,6 +199,9 @@ def main() -> int:
     tmp = tempfile.mkdtemp(prefix="q3t_bench_")
     with_text = not (args.no_text_prep or args.kernel_classes or args.multistream_only)
     model.write(tmp, text_embedding=with_text)
+    with_codec = not (args.no_codec or args.kernel_classes or args.multistream_only)
+    if with_codec:
+        synth.write_codec(tmp, 0)
     spec = model.spec
     host_prep = None
     if with_text:
@@ -228,15 +233,20 @@ def main() -> int:
                                               kv_bf16=args.kv_bf16))
     opts = E.GenerateOptions(**w.options_kwargs())
 
+    last_codes = []
+
     def one_step():
         st = eng.start_stream(inputs, opts)
         n = 0
+        got = []
         while True:
             c = st.next_codes_chunk(w.chunk_frames)
             if c is None:
                 break
             n += c.frames
+            got.append(c.codes)
         st.close()
+        last_codes[:] = got
         return n
 
     for _ in range(args.warmup):
@@ -269,6 +279,29 @@ def main() -> int:
         text_prep = {"content_ids": int(len(ids)), "rows_projected": int(len(ids)) + 11,
                      "device_ms": round(1000 * (time.perf_counter() - t0) / 20, 3),
                      "host_numpy_ms": round(1000 * host_prep, 3)}
+    codec = None
+    if with_codec and eng.has_codec:
+        # Codec decoder on the generation's own codes: one decode of all frames
+        # (generate / decode_codes) and the streaming window (a chunk plus 25 frames of left
+        # context, next_audio_chunk), host copies included.
+        codes = np.concatenate(last_codes)
+        F = codes.shape[0]
+        eng.decode_codes(codes)
+        t0 = time.perf_counter()
+        for _ in range(3):
+            eng.decode_codes(codes)
+        full_s = (time.perf_counter() - t0) / 3
+        win = codes[:w.chunk_frames + 25]
+        eng.decode_codes(win)
+        t0 = time.perf_counter()
+        for _ in range(10):
+            eng.decode_codes(win)
+        win_s = (time.perf_counter() - t0) / 10
+        codec = {"frames": int(F), "decode_ms": round(1000 * full_s, 3),
+                 "decode_rtf": round(full_s / (F * FRAME_SECONDS), 5),
+                 "stream_window_frames": int(win.shape[0]), "stream_chunk_frames": w.chunk_frames,
+                 "stream_window_ms": round(1000 * win_s, 3),
+                 "stream_rtf": round(win_s / (w.chunk_frames * FRAME_SECONDS), 5)}
     eng.close()
     multi = None
     if args.multistream and w.spec == "0.6b" and w.weight_seed == 0:
@@ -303,6 +336,8 @@ def main() -> int:
         out["multistream"] = multi
     if text_prep is not None:
         out["text_prep"] = text_prep
+    if codec is not None:
+        out["codec"] = codec
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out))

@@ -872,7 +872,8 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
 // the previous tile, then into the other LDS buffer (double buffering).  X is scaled by the row's
 // 1/rms and the gain on the way into LDS; its fp32 values become hi/mid/lo bf16 terms after
 // the LDS read, as in k_gemm_mfma.  SwiGLU blocks hold 64 gate rows and the matching 64 up
-// rows (64 outputs).  Requires K % 32 == 0 and N % 128 == 0 (N % 64 for SwiGLU).
+// rows (64 outputs).  Requires K % 32 == 0 (and N % 64 == 0 for SwiGLU); a partial last block
+// of columns computes clamped weight rows and stores only columns below N.
 // ---------------------------------------------------------------------------------------
 template <int EPI>
 __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
@@ -889,10 +890,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
   const int nb = blockIdx.x;
   const int KT = a.K / BK;
 
-  // weight row of block row r
+  // weight row of block row r (a partial last block of a non-SwiGLU GEMM repeats the last row;
+  // its columns are not stored)
   auto wrow = [&](int r) -> int {
     if constexpr (SW) return r < 64 ? nb * 64 + r : a.N + nb * 64 + (r - 64);
-    else return nb * 128 + r;
+    else return min(nb * 128 + r, a.N - 1);
   };
   // per thread and k step: 4 float4 of X (8 lanes x 16 B per 128-byte row), 2 uint4 of W
   // (4 lanes x 16 B per 64-byte row)
@@ -1003,7 +1005,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int n = nb * 128 + wn * 64 + u * 16 + li;
-          a.Y[(size_t)m * a.ldy + n] = gemm_epilogue<EPI>(a, m, n, acc[t][u][e]);
+          if (n < a.N) a.Y[(size_t)m * a.ldy + n] = gemm_epilogue<EPI>(a, m, n, acc[t][u][e]);
         }
       }
     }
@@ -1946,9 +1948,9 @@ static hipError_t gemm_epi(const GemmArgs &a, hipStream_t s) {
   constexpr int NB = 4;
   constexpr int NT = (EPI == EPI_SWIGLU) ? NB / 2 : NB;
   const int cols_per_wg = 4 * 16 * NT;
-  if (a.M >= 128 && a.K % 32 == 0 && a.N % (EPI == EPI_SWIGLU ? 64 : 128) == 0 && a.ldx % 4 == 0) {
+  if (a.M >= 128 && a.K % 32 == 0 && (EPI != EPI_SWIGLU || a.N % 64 == 0) && a.ldx % 4 == 0) {
     const int nout = EPI == EPI_SWIGLU ? 64 : 128;
-    hipLaunchKernelGGL((k_gemm_lds<EPI>), dim3(a.N / nout, (a.M + 127) / 128), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((k_gemm_lds<EPI>), dim3((a.N + nout - 1) / nout, (a.M + 127) / 128), dim3(256), 0, s, a);
   } else if (a.M <= 16) {
     hipLaunchKernelGGL((k_gemm_mfma<EPI, 1, NB>), dim3((a.N + cols_per_wg - 1) / cols_per_wg, (a.M + 15) / 16),
                        dim3(256), 0, s, a);
