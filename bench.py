@@ -158,6 +158,28 @@ def multistream(eng_cls, model_dir: str, name: str, steps: int, warmup: int, use
             "rtf_per_stream": round(el / steps * w.streams / (frames / steps) / FRAME_SECONDS, 5)}
 
 
+def codec_decode_only(E, synth, frames: int, steps: int) -> int:
+    """decode_codes of `frames` random frames, `steps` timed calls after one warmup (the codec
+    decoder alone: profiling runs)."""
+    import numpy as np
+    import shutil
+    tmp = tempfile.mkdtemp(prefix="q3t_codec_")
+    synth.SyntheticModel.build("tiny", 0).write(tmp)
+    synth.write_codec(tmp, 0)
+    eng = E.HipTtsEngine(tmp, E.EngineOptions(max_cache_steps=64))
+    codes = np.random.default_rng(0).integers(0, 2048, (frames, 16)).astype(np.int32)
+    eng.decode_codes(codes)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        eng.decode_codes(codes)
+    dt = (time.perf_counter() - t0) / steps
+    eng.close()
+    shutil.rmtree(tmp, ignore_errors=True)
+    print(json.dumps({"codec_decode_frames": frames, "decode_ms": round(1000 * dt, 3),
+                      "decode_rtf": round(dt / (frames * FRAME_SECONDS), 5), "steps": steps}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -172,6 +194,8 @@ def main() -> int:
     ap.add_argument("--multistream", default="cfg5_0.6b_multistream",
                     help="multi-stream workload reported beside the headline line ('' to skip)")
     ap.add_argument("--multistream-only", action="store_true", help="run only the multi-stream workload")
+    ap.add_argument("--codec-decode", type=int, default=0, metavar="FRAMES",
+                    help="only time decode_codes of FRAMES random frames (tiny model + codec checkpoint) and exit")
     ap.add_argument("--no-codec", action="store_true",
                     help="skip the codec-decoder timing (and the speech-tokenizer checkpoint it needs)")
     ap.add_argument("--no-text-prep", action="store_true",
@@ -189,6 +213,9 @@ def main() -> int:
     from q3t import engine as E
     from q3t import synth
     from q3t.workloads import WORKLOADS
+
+    if args.codec_decode > 0:
+        return codec_decode_only(E, synth, args.codec_decode, max(args.steps, 1))
 
     w = WORKLOADS[args.workload]
     if args.frames > 0:
