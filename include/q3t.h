@@ -45,9 +45,10 @@ typedef struct {
                               1 = bf16 (half the KV bytes, rounded once at the store) */
 } q3t_engine_options;
 
-/* GenerateOptions (generation.rs:40-77), field for field.  speaker / language / decode_audio
- * are carried for API parity; the token loop does not read them (the speaker and language
- * are already encoded in the prefill rows, and waveform decoding is outside this library). */
+/* GenerateOptions (generation.rs:40-77), field for field.  speaker / language (the Speaker /
+ * Language ordinals) choose the codec rows of a prompt that q3t_stream_start_text prepares; with
+ * prepared rows they are already encoded in them.  decode_audio is the caller's: audio comes
+ * from q3t_decode_codes / q3t_stream_next_audio. */
 typedef struct {
   int32_t speaker;
   int32_t language;
