@@ -161,6 +161,26 @@ int q3t_prepare_text(q3t_engine *engine, const int32_t *content_ids, int32_t n_i
 int q3t_stream_start_text(q3t_engine *engine, const int32_t *content_ids, int32_t n_ids,
                           int32_t text_lookahead_tokens, const q3t_generate_options *opts, q3t_stream **out);
 
+/* TtsTextPrep::prepare_voice_clone_xvector_with_lookahead (text.rs:432-490, 507-514): as
+ * q3t_prepare_text with the speaker's codec row replaced by a voice-clone prompt's speaker
+ * embedding (VoiceClonePrompt::speaker_embedding, src/model/voice_clone.rs), embedding_len
+ * floats in host memory; embedding_len must equal the Talker hidden size (Q3T_ERR_INVALID
+ * "speaker embedding length ... does not match model hidden ...", text.rs:445-451).  Only
+ * x-vector prompts exist here; rejecting ICL prompts (text.rs:439-443) is the caller's, who
+ * holds the prompt. */
+int q3t_prepare_text_voice_clone(q3t_engine *engine, const int32_t *content_ids, int32_t n_ids,
+                                 const float *speaker_embedding, int32_t embedding_len, int32_t language,
+                                 int32_t text_lookahead_tokens, float *prefill, int32_t *prefill_steps,
+                                 float *trailing, int32_t *trailing_steps, float *tts_pad);
+
+/* HipTtsEngine::start_voice_clone_stream (generation.rs:442-462) from content token ids: the
+ * rows q3t_prepare_text_voice_clone describes, built on the device into the stream's slot,
+ * then as q3t_stream_start.  opts->speaker is not used; opts->language is. */
+int q3t_stream_start_voice_clone(q3t_engine *engine, const int32_t *content_ids, int32_t n_ids,
+                                 const float *speaker_embedding, int32_t embedding_len,
+                                 int32_t text_lookahead_tokens, const q3t_generate_options *opts,
+                                 q3t_stream **out);
+
 /* HipTtsEngine::decode_codes (generation.rs:619-647): codec frames [frames][num_code_groups]
  * int32 (frame-major, as the codes calls return them) -> frames * samples_per_frame samples at
  * 24 kHz in [-1, 1], through the speech tokenizer's decoder (src/audio/codec_hip.rs: RVQ,

@@ -13,6 +13,8 @@ Sources restated (reference = /root/reference of piedshag/qwen3-tts-hip):
 * codec / text embedding rows and their range checks    src/model/text.rs:605-640
 * speaker / language ids from config.json                src/model/text.rs:492-505, 642-653;
                                                         src/model/config.rs:47-80
+* voice clone (x-vector): the speaker row replaced by    src/model/text.rs:432-490, 507-514;
+  the prompt's speaker embedding                        src/model/voice_clone.rs
 
 Arithmetic is float64 (the reference's is float32 with a sequential fused multiply-add per
 output, bias first); the weights are the bf16 values of the checkpoint.  The text-embedding
@@ -79,16 +81,23 @@ class TextPrepOracle:
                 raise ValueError(f"codec token {t} is out of range for vocab {self.codec_emb.shape[0]}")
         return self.codec_emb[list(tokens)]
 
-    # text.rs:516-573
-    def prefill(self, text_tokens: Sequence[int], speaker: str, language: str) -> np.ndarray:
+    # text.rs:516-573 (speaker: a config key, or an x-vector row of width H)
+    def prefill(self, text_tokens: Sequence[int], speaker, language: str) -> np.ndarray:
         t = self.tok
-        if speaker not in self.speaker_ids:
+        if isinstance(speaker, str) and speaker not in self.speaker_ids:
             raise ValueError(f"missing speaker token id for {speaker}")
         if language not in self.language_ids:
             raise ValueError(f"missing language token id for {language}")
         role = self.projected([t["im_start"], t["assistant"], NEWLINE])
+        spk_id = self.speaker_ids[speaker] if isinstance(speaker, str) else t["codec_pad"]
         codec = self.codec([t["codec_think"], t["codec_think_bos"], self.language_ids[language],
-                            t["codec_think_eos"], self.speaker_ids[speaker], t["codec_pad"], t["codec_bos"]])
+                            t["codec_think_eos"], spk_id, t["codec_pad"], t["codec_bos"]])
+        if not isinstance(speaker, str):
+            xvec = np.asarray(speaker, dtype=np.float64)
+            if xvec.shape != (codec.shape[1],):  # text.rs:445-451, 521-527
+                raise ValueError(f"speaker embedding length {xvec.size} does not match hidden {codec.shape[1]}")
+            codec = codec.copy()
+            codec[4] = xvec
         tts = self.projected([t["tts_pad"]] * 5 + [t["tts_bos"]])
         rows = [role] + [tts[i] + codec[i] for i in range(6)]
         text = self.projected(text_tokens) if len(text_tokens) else np.zeros((0, codec.shape[1]))
@@ -96,8 +105,8 @@ class TextPrepOracle:
             rows.append(text[i] + codec[6 if i + 1 == len(text_tokens) else 5])
         return np.vstack([np.atleast_2d(r) for r in rows])
 
-    # text.rs:340-382
-    def prepare(self, content_ids: Sequence[int], speaker: str = "ryan", language: str = "english",
+    # text.rs:340-382; text.rs:432-490 with an x-vector as `speaker`
+    def prepare(self, content_ids: Sequence[int], speaker="ryan", language: str = "english",
                 text_lookahead_tokens: int = 1) -> Prepared:
         if text_lookahead_tokens == 0:
             raise ValueError("text_lookahead_tokens must be non-zero")

@@ -1251,15 +1251,18 @@ int resolve_token(const std::map<std::string, int> &ids, const char *const *keys
 
 // A prompt's rows as TtsTextPrep::prepare_custom_voice_with_lookahead lays them out
 // (text.rs:340-382, 516-573): the text ids to project, the codec embedding row added to
-// each (-1: none) and each row's destination ((kind << 24) | row: 0 prefill, 1 trailing,
-// 2 tts_pad, 3 dropped).
+// each (-1: none, kTextSpeakerRow: the voice-clone speaker embedding) and each row's
+// destination ((kind << 24) | row: 0 prefill, 1 trailing, 2 tts_pad, 3 dropped).  With a
+// speaker embedding (xvec, H floats) the speaker's codec row is that embedding instead
+// (prepare_voice_clone_xvector_with_lookahead, text.rs:432-490, 507-514).
 struct TextPlan {
   std::vector<int32_t> ids, codec, dst;
+  std::vector<float> xvec;
   int prefill_steps = 0, trailing_steps = 0;
 };
 
 TextPlan plan_text(const Engine &e, const int32_t *content, int n, int speaker, int language, int lookahead,
-                   int trailing_cap) {
+                   int trailing_cap, const float *xvec = nullptr, int xvec_len = 0) {
   if (!e.text_emb)
     fail(Q3T_ERR_NOT_FOUND, "the model has no talker.model.text_embedding.weight: device text preparation "
                             "needs it");
@@ -1268,7 +1271,9 @@ TextPlan plan_text(const Engine &e, const int32_t *content, int n, int speaker, 
   for (int i = 0; i < n; ++i)
     if (content[i] < 0 || content[i] >= e.text_vocab)
       fail(Q3T_ERR_INVALID, "text token %d is out of range for vocab %d", content[i], e.text_vocab);
-  const int spk = resolve_token(e.speaker_ids, kSpeakerKeys, 9, speaker, "speaker");
+  if (xvec && xvec_len != e.talker_hidden)  // text.rs:445-451
+    fail(Q3T_ERR_INVALID, "speaker embedding length %d does not match model hidden %d", xvec_len, e.talker_hidden);
+  const int spk = xvec ? e.codec_pad : resolve_token(e.speaker_ids, kSpeakerKeys, 9, speaker, "speaker");
   const int lang = resolve_token(e.language_ids, kLanguageKeys, 10, language, "language");
   for (int c : {spk, lang, e.codec_pad, e.codec_bos, e.codec_think, e.codec_think_bos, e.codec_think_eos})
     if (c < 0 || c >= e.td.vocab) fail(Q3T_ERR_INVALID, "codec token %d is out of range for vocab %d", c, e.td.vocab);
@@ -1285,7 +1290,9 @@ TextPlan plan_text(const Engine &e, const int32_t *content, int n, int speaker, 
   // speaker, pad], then the first L content ids over pad (bos on the last)
   const int role[3] = {e.tok_im_start, e.tok_assistant, kNewline};
   for (int i = 0; i < 3; ++i) row(role[i], -1, 0, i);
-  const int codec6[6] = {e.codec_think, e.codec_think_bos, lang, e.codec_think_eos, spk, e.codec_pad};
+  const int codec6[6] = {e.codec_think, e.codec_think_bos, lang, e.codec_think_eos, xvec ? kTextSpeakerRow : spk,
+                         e.codec_pad};
+  if (xvec) p.xvec.assign(xvec, xvec + xvec_len);
   for (int i = 0; i < 6; ++i) row(i < 5 ? e.tok_tts_pad : e.tok_tts_bos, codec6[i], 0, 3 + i);
   for (int i = 0; i < L; ++i) row(content[i], i + 1 == L ? e.codec_bos : e.codec_pad, 0, 9 + i);
   p.prefill_steps = 9 + L;
@@ -1316,6 +1323,11 @@ void prepare_text_device(Engine &e, const TextPlan &p, float *prefill, float *tr
     float *X = (float *)take((size_t)M * e.text_hidden * 4);
     float *Hd = (float *)take((size_t)M * e.tp_inter * 4);
     float *Y = (float *)take((size_t)M * H * 4);
+    float *xvec = nullptr;
+    if (!p.xvec.empty()) {
+      xvec = (float *)take(p.xvec.size() * 4);
+      HIPC(hipMemcpyAsync(xvec, p.xvec.data(), p.xvec.size() * 4, hipMemcpyHostToDevice, s));
+    }
     std::vector<int32_t> host(p.ids);
     host.insert(host.end(), p.codec.begin(), p.codec.end());
     host.insert(host.end(), p.dst.begin(), p.dst.end());
@@ -1330,7 +1342,7 @@ void prepare_text_device(Engine &e, const TextPlan &p, float *prefill, float *tr
     g.X = Hd; g.ldx = e.tp_inter; g.W = e.tp_fc2; g.bias = e.tp_b2; g.Y = Y; g.ldy = H;
     g.M = M; g.N = H; g.K = e.tp_inter;
     hip_check(launch_gemm(EPI_BIAS, g, s), "launch_gemm(text fc2)");
-    hip_check(launch_text_assemble(Y, H, M, codec, e.codec_emb, dst, prefill, trailing, pad, s),
+    hip_check(launch_text_assemble(Y, H, M, codec, e.codec_emb, xvec, dst, prefill, trailing, pad, s),
               "launch_text_assemble");
     HIPC(hipStreamSynchronize(s));
   } catch (...) {
@@ -1391,6 +1403,63 @@ int q3t_stream_start(q3t_engine *e, const float *prefill, int32_t P, const float
   });
 }
 
+}  // extern "C"
+
+namespace q3t {
+namespace {
+
+// q3t_prepare_text / q3t_prepare_text_voice_clone: runs the plan into a device staging
+// buffer and copies its rows to the caller's host arrays.
+void prepare_text_to_host(Engine *e, const TextPlan &p, float *prefill, int32_t *prefill_steps, float *trailing,
+                          int32_t *trailing_steps, float *tts_pad) {
+  HIPC(hipSetDevice(e->device));
+  const size_t H = (size_t)e->talker_hidden;
+  int64_t bytes = 0;
+  float *d = dev_alloc<float>((size_t)(p.prefill_steps + p.trailing_steps + 1) * H, bytes);
+  try {
+    float *dt = d + (size_t)p.prefill_steps * H, *dp = dt + (size_t)p.trailing_steps * H;
+    prepare_text_device(*e, p, d, dt, dp, e->pools.stream);
+    HIPC(hipMemcpy(prefill, d, (size_t)p.prefill_steps * H * 4, hipMemcpyDeviceToHost));
+    HIPC(hipMemcpy(trailing, dt, (size_t)p.trailing_steps * H * 4, hipMemcpyDeviceToHost));
+    HIPC(hipMemcpy(tts_pad, dp, H * 4, hipMemcpyDeviceToHost));
+  } catch (...) {
+    (void)hipFree(d);
+    throw;
+  }
+  (void)hipFree(d);
+  *prefill_steps = p.prefill_steps;
+  *trailing_steps = p.trailing_steps;
+}
+
+// q3t_stream_start_text / q3t_stream_start_voice_clone: the plan's rows built straight into a
+// free slot, then the prefill and the first semantic token.
+q3t_stream *start_text_stream(Engine *e, const TextPlan &p, const q3t_generate_options *o) {
+  if ((int64_t)p.prefill_steps + o->max_frames > e->cap)
+    fail(Q3T_ERR_CAPACITY,
+         "requested %lld cache steps but engine was loaded for %d; call load_with_max_frames with a larger "
+         "max_frames",
+         (long long)p.prefill_steps + o->max_frames, e->cap);
+  int slot = -1;
+  for (size_t i = 0; i < e->slots.size(); ++i)
+    if (!e->slots[i].in_use) {
+      slot = (int)i;
+      break;
+    }
+  if (slot < 0) fail(Q3T_ERR_BUSY, "all %zu stream slots are in use", e->slots.size());
+  HIPC(hipSetDevice(e->device));
+  ensure_trace(*e);
+  Slot &s = e->slots[slot];
+  const int rows = std::min(p.trailing_steps, e->cap);
+  prepare_text_device(*e, p, e->pools.px, s.trailing, s.trailing + (size_t)rows * e->talker_hidden, s.stream);
+  stage_state(*e, slot, p.prefill_steps, rows, o, s.stream);
+  return start_staged(*e, slot, p.prefill_steps, o);
+}
+
+}  // namespace
+}  // namespace q3t
+
+extern "C" {
+
 int q3t_prepare_text(q3t_engine *e, const int32_t *content_ids, int32_t n_ids, int32_t speaker, int32_t language,
                      int32_t text_lookahead_tokens, float *prefill, int32_t *prefill_steps, float *trailing,
                      int32_t *trailing_steps, float *tts_pad) {
@@ -1399,23 +1468,21 @@ int q3t_prepare_text(q3t_engine *e, const int32_t *content_ids, int32_t n_ids, i
     if (!e || !prefill || !prefill_steps || !trailing || !trailing_steps || !tts_pad)
       fail(Q3T_ERR_INVALID, "null argument");
     const TextPlan p = plan_text(*e, content_ids, n_ids, speaker, language, text_lookahead_tokens, n_ids + 1);
-    HIPC(hipSetDevice(e->device));
-    const size_t H = (size_t)e->talker_hidden;
-    int64_t bytes = 0;
-    float *d = dev_alloc<float>((size_t)(p.prefill_steps + p.trailing_steps + 1) * H, bytes);
-    try {
-      float *dt = d + (size_t)p.prefill_steps * H, *dp = dt + (size_t)p.trailing_steps * H;
-      prepare_text_device(*e, p, d, dt, dp, e->pools.stream);
-      HIPC(hipMemcpy(prefill, d, (size_t)p.prefill_steps * H * 4, hipMemcpyDeviceToHost));
-      HIPC(hipMemcpy(trailing, dt, (size_t)p.trailing_steps * H * 4, hipMemcpyDeviceToHost));
-      HIPC(hipMemcpy(tts_pad, dp, H * 4, hipMemcpyDeviceToHost));
-    } catch (...) {
-      (void)hipFree(d);
-      throw;
-    }
-    (void)hipFree(d);
-    *prefill_steps = p.prefill_steps;
-    *trailing_steps = p.trailing_steps;
+    prepare_text_to_host(e, p, prefill, prefill_steps, trailing, trailing_steps, tts_pad);
+  });
+}
+
+int q3t_prepare_text_voice_clone(q3t_engine *e, const int32_t *content_ids, int32_t n_ids,
+                                 const float *speaker_embedding, int32_t embedding_len, int32_t language,
+                                 int32_t text_lookahead_tokens, float *prefill, int32_t *prefill_steps,
+                                 float *trailing, int32_t *trailing_steps, float *tts_pad) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || !speaker_embedding || !prefill || !prefill_steps || !trailing || !trailing_steps || !tts_pad)
+      fail(Q3T_ERR_INVALID, "null argument");
+    const TextPlan p = plan_text(*e, content_ids, n_ids, 0, language, text_lookahead_tokens, n_ids + 1,
+                                 speaker_embedding, embedding_len);
+    prepare_text_to_host(e, p, prefill, prefill_steps, trailing, trailing_steps, tts_pad);
   });
 }
 
@@ -1426,27 +1493,22 @@ int q3t_stream_start_text(q3t_engine *e, const int32_t *content_ids, int32_t n_i
     if (!e || !out) fail(Q3T_ERR_INVALID, "null engine or output");
     *out = nullptr;
     validate_options(o);
-    const TextPlan p =
-        plan_text(*e, content_ids, n_ids, o->speaker, o->language, text_lookahead_tokens, e->cap);
-    if ((int64_t)p.prefill_steps + o->max_frames > e->cap)
-      fail(Q3T_ERR_CAPACITY,
-           "requested %lld cache steps but engine was loaded for %d; call load_with_max_frames with a larger "
-           "max_frames",
-           (long long)p.prefill_steps + o->max_frames, e->cap);
-    int slot = -1;
-    for (size_t i = 0; i < e->slots.size(); ++i)
-      if (!e->slots[i].in_use) {
-        slot = (int)i;
-        break;
-      }
-    if (slot < 0) fail(Q3T_ERR_BUSY, "all %zu stream slots are in use", e->slots.size());
-    HIPC(hipSetDevice(e->device));
-    ensure_trace(*e);
-    Slot &s = e->slots[slot];
-    const int rows = std::min(p.trailing_steps, e->cap);
-    prepare_text_device(*e, p, e->pools.px, s.trailing, s.trailing + (size_t)rows * e->talker_hidden, s.stream);
-    stage_state(*e, slot, p.prefill_steps, rows, o, s.stream);
-    *out = start_staged(*e, slot, p.prefill_steps, o);
+    const TextPlan p = plan_text(*e, content_ids, n_ids, o->speaker, o->language, text_lookahead_tokens, e->cap);
+    *out = start_text_stream(e, p, o);
+  });
+}
+
+int q3t_stream_start_voice_clone(q3t_engine *e, const int32_t *content_ids, int32_t n_ids,
+                                 const float *speaker_embedding, int32_t embedding_len,
+                                 int32_t text_lookahead_tokens, const q3t_generate_options *o, q3t_stream **out) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || !out || !speaker_embedding) fail(Q3T_ERR_INVALID, "null argument");
+    *out = nullptr;
+    validate_options(o);
+    const TextPlan p = plan_text(*e, content_ids, n_ids, 0, o->language, text_lookahead_tokens, e->cap,
+                                 speaker_embedding, embedding_len);
+    *out = start_text_stream(e, p, o);
   });
 }
 

@@ -59,8 +59,12 @@ hipError_t launch_row_rms(const float *X, int ldx, int M, int K, float eps, floa
 // kind 0 prefill row, 1 trailing row, 2 the tts_pad row, 3 dropped.  The host validates ids.
 hipError_t launch_text_gather(const uint16_t *table, int width, const int32_t *ids, int M, float *X, hipStream_t stream);
 hipError_t launch_silu(float *x, size_t n, hipStream_t stream);
+// codec[m] value that adds the H-float row `xvec` (a voice-clone speaker embedding) instead of
+// a codec embedding row.
+constexpr int32_t kTextSpeakerRow = -2;
 hipError_t launch_text_assemble(const float *Y, int H, int M, const int32_t *codec, const uint16_t *codec_emb,
-                                const int32_t *dst, float *prefill, float *trailing, float *pad, hipStream_t stream);
+                                const float *xvec, const int32_t *dst, float *prefill, float *trailing, float *pad,
+                                hipStream_t stream);
 
 // dst[i] = src[i] (bf16 -> fp32, exact).
 hipError_t launch_bf16_to_f32(const uint16_t *src, float *dst, size_t n, hipStream_t stream);

@@ -1723,16 +1723,22 @@ __global__ void k_silu(float *x, size_t n) {
   if (i < n) x[i] = x[i] / (1.0f + expf(-x[i]));
 }
 
-// Row m of Y (+ codec_emb[codec[m]] where codec[m] >= 0) to its destination dst[m]:
-// (kind << 24) | row, kind 0 = prefill row, 1 = trailing row, 2 = the tts_pad row, 3 = none.
+// Row m of Y (+ codec_emb[codec[m]] where codec[m] >= 0, + xvec where codec[m] ==
+// kTextSpeakerRow) to its destination dst[m]: (kind << 24) | row, kind 0 = prefill row,
+// 1 = trailing row, 2 = the tts_pad row, 3 = none.
 __global__ void k_text_assemble(const float *Y, int H, const int32_t *codec, const uint16_t *codec_emb,
-                                const int32_t *dst, float *prefill, float *trailing, float *pad) {
+                                const float *xvec, const int32_t *dst, float *prefill, float *trailing,
+                                float *pad) {
   const int m = blockIdx.x;
   const int kind = dst[m] >> 24, row = dst[m] & 0xffffff;
   if (kind == 3) return;
   float *out = kind == 0 ? prefill + (size_t)row * H : (kind == 1 ? trailing + (size_t)row * H : pad);
   const int c = codec[m];
   const float *y = Y + (size_t)m * H;
+  if (c == kTextSpeakerRow) {
+    for (int i = threadIdx.x; i < H; i += blockDim.x) out[i] = y[i] + xvec[i];
+    return;
+  }
   for (int i = threadIdx.x; i < H; i += blockDim.x)
     out[i] = c >= 0 ? y[i] + bf16_to_f32(codec_emb[(size_t)c * H + i]) : y[i];
 }
@@ -2039,9 +2045,11 @@ hipError_t launch_silu(float *x, size_t n, hipStream_t s) {
 }
 
 hipError_t launch_text_assemble(const float *Y, int H, int M, const int32_t *codec, const uint16_t *codec_emb,
-                                const int32_t *dst, float *prefill, float *trailing, float *pad, hipStream_t s) {
+                                const float *xvec, const int32_t *dst, float *prefill, float *trailing, float *pad,
+                                hipStream_t s) {
   if (M <= 0 || H <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_text_assemble, dim3(M), dim3(256), 0, s, Y, H, codec, codec_emb, dst, prefill, trailing, pad);
+  hipLaunchKernelGGL(k_text_assemble, dim3(M), dim3(256), 0, s, Y, H, codec, codec_emb, xvec, dst, prefill, trailing,
+                     pad);
   return hipGetLastError();
 }
 

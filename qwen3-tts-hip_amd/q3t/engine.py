@@ -10,15 +10,18 @@ reference (Rust)                            here
 frames`` / ``load_with_options`` (255-315)  / ``load_with_options``
 ``generate_codes`` (356-371)                ``HipTtsEngine.generate_codes``
 ``start_stream`` (421-440)                  ``HipTtsEngine.start_stream``
+``generate_voice_clone[_codes]`` (334-393)  ``HipTtsEngine.generate_voice_clone[_codes]``
+``start_voice_clone_stream`` (442-462)      ``HipTtsEngine.start_voice_clone_stream``
 ``HipTtsStream::next_codes_chunk`` (876-)   ``HipTtsStream.next_codes_chunk``
 ``HipTtsStream::finish_codes`` (991-997)    ``HipTtsStream.finish_codes``
 ``GenerateOptions`` / ``StreamOptions``     same names, same defaults (40-92)
 ``Error::InvalidInput`` / ``Error::Hip``    ``InvalidInputError`` / ``HipError``
 =========================================  =============================================
 
-The reference takes text and tokenizes it; no tokenizer ships offline, so these calls
-take a :class:`q3t.textprep.PreparedInputs` (the reference's ``TtsPreparedInputs``) or a
-sequence of content token ids together with a :class:`q3t.textprep.TextPrep`.
+The generation calls take text (tokenized with the model directory's tokenizer files, as
+the reference does), a sequence of content token ids (prepared on the device, or by a
+:class:`q3t.textprep.TextPrep` given to the engine), or a
+:class:`q3t.textprep.PreparedInputs` (the reference's ``TtsPreparedInputs``).
 
 There is no CPU fallback: if ``libq3t.so`` is missing or the GPU call fails, the call
 raises.
@@ -33,6 +36,7 @@ from typing import List, Optional, Sequence, Union
 import numpy as np
 
 from .textprep import PreparedInputs, TextPrep
+from .voice_clone import VoiceClonePrompt
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libq3t.so")
@@ -150,6 +154,12 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                                             ctypes.c_int32, f32p, i32p, f32p, i32p, f32p]),
         "q3t_stream_start_text": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32, ctypes.c_int32,
                                                  P(_GenerateOptions), P(ctypes.c_void_p)]),
+        "q3t_prepare_text_voice_clone": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32, f32p, ctypes.c_int32,
+                                                        ctypes.c_int32, ctypes.c_int32, f32p, i32p, f32p, i32p,
+                                                        f32p]),
+        "q3t_stream_start_voice_clone": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32, f32p,
+                                                        ctypes.c_int32, ctypes.c_int32, P(_GenerateOptions),
+                                                        P(ctypes.c_void_p)]),
         "q3t_streams_start": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, P(_StreamInput), P(_GenerateOptions),
                                              P(ctypes.c_void_p)]),
         "q3t_streams_next_codes": (ctypes.c_int, [ctypes.c_void_p, P(ctypes.c_void_p), ctypes.c_int32,
@@ -565,6 +575,71 @@ class HipTtsEngine:
         n = int(ids.size)
         steps = 9 + (0 if n == 0 else max(1, min(lookahead, n)))
         return HipTtsStream(self, None, options, stream_options, handle=handle, prefill_steps=steps)
+
+    # -- voice clone (x-vector prompts) ----------------------------------------------------
+    def _voice_clone_args(self, inputs: Union[str, Sequence[int]], prompt: VoiceClonePrompt):
+        if isinstance(inputs, PreparedInputs):
+            raise InvalidInputError(Q3T_ERR_INVALID, "voice clone calls take text or content token ids")
+        prompt.check_x_vector_only()
+        ids = self.content_ids(inputs) if isinstance(inputs, str) else [int(i) for i in inputs]
+        ids = np.ascontiguousarray(np.asarray(ids, dtype=np.int64).astype(np.int32))
+        emb = np.ascontiguousarray(np.asarray(prompt.speaker_embedding, dtype=np.float32).reshape(-1))
+        return ids, emb
+
+    def prepare_voice_clone_text(self, inputs: Union[str, Sequence[int]], prompt: VoiceClonePrompt,
+                                 language: str = "english", text_lookahead_tokens: int = 1 << 30) -> PreparedInputs:
+        """``TtsTextPrep::prepare_voice_clone_xvector_with_lookahead`` (text.rs:432-490) on the
+        device (``q3t_prepare_text_voice_clone``)."""
+        ids, emb = self._voice_clone_args(inputs, prompt)
+        n, H = int(ids.size), self.info["talker_hidden"]
+        lang = GenerateOptions(language=language)._c().language
+        pre = np.zeros((9 + n, H), np.float32)
+        trail = np.zeros((n + 1, H), np.float32)
+        pad = np.zeros(H, np.float32)
+        P, T = ctypes.c_int32(), ctypes.c_int32()
+        lookahead = min(int(text_lookahead_tokens), 0x7FFFFFFF)
+        _check(_lib.q3t_prepare_text_voice_clone(self._h, _iptr(ids), n, _fptr(emb), int(emb.size), lang, lookahead,
+                                                 _fptr(pre), ctypes.byref(P), _fptr(trail), ctypes.byref(T),
+                                                 _fptr(pad)))
+        return PreparedInputs(content_ids=ids.astype(np.int64), prefill=pre[:P.value].copy(),
+                              trailing_text=trail[:T.value].copy(), tts_pad_embed=pad)
+
+    def start_voice_clone_stream(self, inputs: Union[str, Sequence[int]], prompt: VoiceClonePrompt,
+                                 options: GenerateOptions = GenerateOptions(),
+                                 stream_options: StreamOptions = StreamOptions()) -> "HipTtsStream":
+        """``start_voice_clone_stream`` (generation.rs:442-462): the prompt rows with the
+        prompt's speaker embedding, built on the device into the stream's slot
+        (``q3t_stream_start_voice_clone``).  ``options.speaker`` is not used."""
+        options.validate()  # generation.rs:450-451: options, stream options, then the prompt
+        stream_options.validate()
+        ids, emb = self._voice_clone_args(inputs, prompt)
+        o = options._c()
+        handle = ctypes.c_void_p()
+        lookahead = min(int(stream_options.text_lookahead_tokens), 0x7FFFFFFF)
+        _check(_lib.q3t_stream_start_voice_clone(self._h, _iptr(ids), int(ids.size), _fptr(emb), int(emb.size),
+                                                 lookahead, ctypes.byref(o), ctypes.byref(handle)))
+        n = int(ids.size)
+        steps = 9 + (0 if n == 0 else max(1, min(lookahead, n)))
+        return HipTtsStream(self, None, options, stream_options, handle=handle, prefill_steps=steps)
+
+    def generate_voice_clone_codes(self, inputs: Union[str, Sequence[int]], prompt: VoiceClonePrompt,
+                                   options: GenerateOptions = GenerateOptions()) -> GeneratedCodes:
+        """``generate_voice_clone_codes`` (generation.rs:373-393): all text in the prefill, then
+        the rollout."""
+        with self.start_voice_clone_stream(inputs, prompt, options,
+                                           StreamOptions(text_lookahead_tokens=0x7FFFFFFF)) as st:
+            chunk = st.next_codes_chunk(max(options.max_frames, 1))
+            codes = chunk.codes if chunk else np.zeros((0, self.code_groups), np.int32)
+            return GeneratedCodes(codes, int(codes.shape[0]), st.ended_by_eos)
+
+    def generate_voice_clone(self, inputs: Union[str, Sequence[int]], prompt: VoiceClonePrompt,
+                             options: GenerateOptions = GenerateOptions()) -> "GeneratedSpeech":
+        """``generate_voice_clone`` (generation.rs:334-354): codes, then audio when ``decode_audio``."""
+        g = self.generate_voice_clone_codes(inputs, prompt, options)
+        samples = (self.decode_codes(g.codes) if options.decode_audio and g.frames
+                   else np.zeros(0, np.float32))
+        return GeneratedSpeech(inputs if isinstance(inputs, str) else "", g.frames, g.ended_by_eos, g.codes,
+                               samples, SAMPLE_RATE)
 
     # -- several streams at once (no counterpart in the reference: one stream per engine) --
     def start_streams(self, inputs: List[Inputs], options: List[GenerateOptions],

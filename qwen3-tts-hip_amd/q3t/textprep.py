@@ -1,9 +1,9 @@
 """Host-side prompt preparation: token ids -> the [P, H] prefill, trailing text rows and tts_pad row.
 
 This runs on the CPU before the token loop, as it does in the reference
-(src/model/text.rs:340-382, :516-603).  There is no tokenizer offline, so callers pass
-content token ids directly (the ids between the chat-template prefix and suffix,
-text.rs:361).  Layout of the prefill (text.rs:516-573):
+(src/model/text.rs:340-382, :516-603); HipTtsEngine.prepare_text does the same on the GPU.
+Callers pass content token ids (the ids between the chat-template prefix and suffix,
+text.rs:361), which q3t.tokenizer produces from text.  Layout of the prefill (text.rs:516-573):
 
     3 rows   text_proj([im_start, assistant, "\\n"])
     6 rows   text_proj([pad, pad, pad, pad, pad, bos])[i] + codec_emb([think, think_bos,

@@ -82,3 +82,22 @@ def test_agrees_with_host_preparation(tiny):
     np.testing.assert_allclose(host.prefill, ref.prefill, rtol=0, atol=1e-6)
     np.testing.assert_allclose(host.trailing_text, ref.trailing_text, rtol=0, atol=1e-6)
     np.testing.assert_allclose(host.tts_pad_embed, ref.tts_pad_embed, rtol=0, atol=1e-6)
+
+
+def test_voice_clone_replaces_the_speaker_row(tiny):
+    """prepare_voice_clone_xvector_with_lookahead (text.rs:432-490): the custom-voice layout with
+    the speaker's codec row (prefill row 7) replaced by the prompt's x-vector."""
+    model, o = tiny
+    content = [5, 99, 1234]
+    H = model.spec.talker.hidden
+    xvec = np.random.default_rng(4).standard_normal(H) * 0.05
+    vc = o.prepare(content, xvec, "english", text_lookahead_tokens=8)
+    cv = o.prepare(content, "ryan", "english", text_lookahead_tokens=8)
+    spk = model.config()["talker_config"]["spk_id"]["ryan"]
+    codec = model.f32("talker.model.codec_embedding.weight").astype(np.float64)
+    diff = vc.prefill - cv.prefill
+    np.testing.assert_allclose(diff[7], xvec - codec[spk], rtol=0, atol=1e-14)
+    np.testing.assert_array_equal(np.delete(diff, 7, axis=0), 0)
+    np.testing.assert_array_equal(vc.trailing_text, cv.trailing_text)
+    with pytest.raises(ValueError, match="speaker embedding length"):
+        o.prepare(content, xvec[:-1], "english")
