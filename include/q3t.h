@@ -181,6 +181,36 @@ int q3t_stream_start_voice_clone(q3t_engine *engine, const int32_t *content_ids,
                                  int32_t text_lookahead_tokens, const q3t_generate_options *opts,
                                  q3t_stream **out);
 
+/* Text streams: text that arrives while audio is produced (PollingTextStream,
+ * generation.rs:176-211, 1093-1437).  The caller keeps the reference's token queue and its
+ * start / resume / flush rules (TextStreamOptions, generation.rs:212-228); the device holds the
+ * prompt rows and the trailing text rows.
+ *
+ * q3t_text_stream_start: try_start_generation (generation.rs:1280-1358) once enough content ids
+ * are queued: the prefill of custom_voice_prefill_from_content_tokens (text.rs:397-404) with every
+ * one of the n_ids >= 1 ids in it (codec bos on the last), or, with a non-null
+ * speaker_embedding of embedding_len floats, voice_clone_xvector_prefill_from_content_tokens
+ * (text.rs:406-418); then the Talker prefill and the first semantic token.  The stream's
+ * trailing text starts empty and open: q3t_stream_next_codes / q3t_stream_next_audio run frame
+ * f (f + 1 < max_frames) only once trailing row f has been pushed, and return frames = 0 with
+ * ended_by_eos = 0 and total_frames < max_frames when the next frame waits for text (the
+ * reference's IncrementalAudio::NeedMoreText).  Open streams are not accepted by
+ * q3t_streams_next_codes. */
+int q3t_text_stream_start(q3t_engine *engine, const int32_t *content_ids, int32_t n_ids,
+                          const float *speaker_embedding, int32_t embedding_len,
+                          const q3t_generate_options *opts, q3t_stream **out);
+
+/* The next n content ids popped from the caller's queue, in order: each becomes the next
+ * trailing text row, projected on the device (next_trailing_buffer, generation.rs:1367-1369).
+ * Q3T_ERR_INVALID "cannot push text after finish_text" once the text is finished
+ * (generation.rs:1108-1116). */
+int q3t_text_stream_push(q3t_stream *stream, const int32_t *content_ids, int32_t n);
+
+/* finish_text (generation.rs:1118-1129): the tts_eos row follows the last pushed row, then every
+ * later frame reads tts_pad (generation.rs:1371-1386), and the frames no longer wait for text.
+ * A second call does nothing. */
+int q3t_text_stream_finish(q3t_stream *stream);
+
 /* HipTtsEngine::decode_codes (generation.rs:619-647): codec frames [frames][num_code_groups]
  * int32 (frame-major, as the codes calls return them) -> frames * samples_per_frame samples at
  * 24 kHz in [-1, 1], through the speech tokenizer's decoder (src/audio/codec_hip.rs: RVQ,

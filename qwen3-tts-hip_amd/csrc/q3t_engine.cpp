@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstddef>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -635,6 +636,10 @@ struct Stream {
   int host_frame = 0;  // frames already handed to the caller
   int done = 0;
   int max_frames = 0;
+  // Open text input (q3t_text_stream_start): text_rows trailing rows have been pushed; until
+  // q3t_text_stream_finish a frame that needs row text_rows or later does not run.
+  bool text_open = false;
+  int text_rows = 0;
 };
 
 namespace {
@@ -1261,13 +1266,18 @@ struct TextPlan {
   int prefill_steps = 0, trailing_steps = 0;
 };
 
+//
+// open_text: the prefill of a text stream (custom_voice_prefill_from_content_tokens,
+// text.rs:396-430): every id in the prefill and no trailing text, which the stream's pushes
+// supply.
 TextPlan plan_text(const Engine &e, const int32_t *content, int n, int speaker, int language, int lookahead,
-                   int trailing_cap, const float *xvec = nullptr, int xvec_len = 0) {
+                   int trailing_cap, const float *xvec = nullptr, int xvec_len = 0, bool open_text = false) {
   if (!e.text_emb)
     fail(Q3T_ERR_NOT_FOUND, "the model has no talker.model.text_embedding.weight: device text preparation "
                             "needs it");
   if (n < 0 || (n > 0 && !content)) fail(Q3T_ERR_INVALID, "null or negative content ids");
   if (lookahead <= 0) fail(Q3T_ERR_INVALID, "text_lookahead_tokens must be non-zero");
+  if (open_text && n == 0) fail(Q3T_ERR_INVALID, "a text stream starts with at least one content token");
   for (int i = 0; i < n; ++i)
     if (content[i] < 0 || content[i] >= e.text_vocab)
       fail(Q3T_ERR_INVALID, "text token %d is out of range for vocab %d", content[i], e.text_vocab);
@@ -1297,12 +1307,27 @@ TextPlan plan_text(const Engine &e, const int32_t *content, int n, int speaker, 
   for (int i = 0; i < L; ++i) row(content[i], i + 1 == L ? e.codec_bos : e.codec_pad, 0, 9 + i);
   p.prefill_steps = 9 + L;
   // trailing text: the rest of the content, then tts_eos; then the tts_pad row
-  p.trailing_steps = n - L + 1;
+  p.trailing_steps = open_text ? 0 : n - L + 1;
   for (int i = 0; i < p.trailing_steps; ++i) {
     const int id = i + L < n ? content[i + L] : e.tok_tts_eos;
     row(id, -1, i < trailing_cap ? 1 : 3, i < trailing_cap ? i : 0);
   }
   row(e.tok_tts_pad, -1, 2, 0);
+  return p;
+}
+
+// Trailing text rows of an open text stream: id i projected into trailing row first_row + i
+// (projected_text_embedding_for_token of each popped token, generation.rs:1367-1369).
+TextPlan plan_trailing_rows(const Engine &e, const int32_t *ids, int n, int first_row) {
+  TextPlan p;
+  for (int i = 0; i < n; ++i) {
+    if (ids[i] < 0 || ids[i] >= e.text_vocab)
+      fail(Q3T_ERR_INVALID, "text token %d is out of range for vocab %d", ids[i], e.text_vocab);
+    p.ids.push_back(ids[i]);
+    p.codec.push_back(-1);
+    p.dst.push_back((1 << 24) | (first_row + i));
+  }
+  p.trailing_steps = n;
   return p;
 }
 
@@ -1431,9 +1456,11 @@ void prepare_text_to_host(Engine *e, const TextPlan &p, float *prefill, int32_t 
   *trailing_steps = p.trailing_steps;
 }
 
-// q3t_stream_start_text / q3t_stream_start_voice_clone: the plan's rows built straight into a
-// free slot, then the prefill and the first semantic token.
-q3t_stream *start_text_stream(Engine *e, const TextPlan &p, const q3t_generate_options *o) {
+// q3t_stream_start_text / q3t_stream_start_voice_clone / q3t_text_stream_start: the plan's rows
+// built straight into a free slot, then the prefill and the first semantic token.  An open
+// text stream keeps the tts_pad row in the last trailing row (cap) and lets frame f read row f
+// until q3t_text_stream_finish.
+q3t_stream *start_text_stream(Engine *e, const TextPlan &p, const q3t_generate_options *o, bool open_text = false) {
   if ((int64_t)p.prefill_steps + o->max_frames > e->cap)
     fail(Q3T_ERR_CAPACITY,
          "requested %lld cache steps but engine was loaded for %d; call load_with_max_frames with a larger "
@@ -1449,10 +1476,12 @@ q3t_stream *start_text_stream(Engine *e, const TextPlan &p, const q3t_generate_o
   HIPC(hipSetDevice(e->device));
   ensure_trace(*e);
   Slot &s = e->slots[slot];
-  const int rows = std::min(p.trailing_steps, e->cap);
+  const int rows = open_text ? e->cap : std::min(p.trailing_steps, e->cap);
   prepare_text_device(*e, p, e->pools.px, s.trailing, s.trailing + (size_t)rows * e->talker_hidden, s.stream);
   stage_state(*e, slot, p.prefill_steps, rows, o, s.stream);
-  return start_staged(*e, slot, p.prefill_steps, o);
+  q3t_stream *out = start_staged(*e, slot, p.prefill_steps, o);
+  out->text_open = open_text;
+  return out;
 }
 
 }  // namespace
@@ -1512,6 +1541,66 @@ int q3t_stream_start_voice_clone(q3t_engine *e, const int32_t *content_ids, int3
   });
 }
 
+int q3t_text_stream_start(q3t_engine *e, const int32_t *content_ids, int32_t n_ids, const float *speaker_embedding,
+                          int32_t embedding_len, const q3t_generate_options *o, q3t_stream **out) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || !out) fail(Q3T_ERR_INVALID, "null engine or output");
+    *out = nullptr;
+    validate_options(o);
+    const TextPlan p = plan_text(*e, content_ids, n_ids, o->speaker, o->language, std::max(n_ids, 1), e->cap,
+                                 speaker_embedding, speaker_embedding ? embedding_len : 0, true);
+    *out = start_text_stream(e, p, o, true);
+  });
+}
+
+int q3t_text_stream_push(q3t_stream *sp, const int32_t *ids, int32_t n) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!sp || (n > 0 && !ids)) fail(Q3T_ERR_INVALID, "null argument");
+    if (n < 0) fail(Q3T_ERR_INVALID, "token count must not be negative");
+    if (!sp->text_open) fail(Q3T_ERR_INVALID, "cannot push text after finish_text");  // generation.rs:1108-1116
+    Engine &e = *sp->engine;
+    // Rows at max_frames or later are never read (frame f reads row f only when f + 1 < max_frames).
+    const int keep = std::max(0, std::min(n, sp->max_frames - sp->text_rows));
+    const TextPlan p = plan_trailing_rows(e, ids, n, sp->text_rows);  // checks every id
+    if (keep > 0) {
+      TextPlan q = p;
+      q.ids.resize(keep);
+      q.codec.resize(keep);
+      q.dst.resize(keep);
+      HIPC(hipSetDevice(e.device));
+      prepare_text_device(e, q, nullptr, e.slots[sp->slot].trailing, nullptr, e.slots[sp->slot].stream);
+    }
+    sp->text_rows = std::min<int64_t>((int64_t)sp->text_rows + n, sp->max_frames);
+  });
+}
+
+int q3t_text_stream_finish(q3t_stream *sp) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!sp) fail(Q3T_ERR_INVALID, "null argument");
+    if (!sp->text_open) return;  // finish_text after finish_text is a no-op (generation.rs:1118-1121)
+    Engine &e = *sp->engine;
+    Slot &s = e.slots[sp->slot];
+    const size_t H = (size_t)e.talker_hidden;
+    const int R = std::min(sp->text_rows, sp->max_frames);
+    HIPC(hipSetDevice(e.device));
+    // tts_eos after the last pushed row, then tts_pad for every later frame (generation.rs:1371-1386)
+    if (R < sp->max_frames) {
+      const TextPlan p = plan_trailing_rows(e, &e.tok_tts_eos, 1, R);
+      prepare_text_device(e, p, nullptr, s.trailing, nullptr, s.stream);
+    }
+    const int T = std::min(R + 1, sp->max_frames);
+    HIPC(hipMemcpyAsync(s.trailing + (size_t)T * H, s.trailing + (size_t)e.cap * H, H * 4, hipMemcpyDeviceToDevice,
+                        s.stream));
+    HIPC(hipStreamSynchronize(s.stream));
+    const int32_t rows = T;
+    HIPC(hipMemcpy((char *)s.st + offsetof(SlotState, trailing_rows), &rows, sizeof(rows), hipMemcpyHostToDevice));
+    sp->text_open = false;
+  });
+}
+
 int q3t_streams_start(q3t_engine *e, int32_t n, const q3t_stream_input *inputs, const q3t_generate_options *opts,
                       q3t_stream **out) {
   return guarded([&] {
@@ -1566,6 +1655,8 @@ int q3t_streams_next_codes(q3t_engine *e, q3t_stream *const *streams, int32_t n,
       q3t_stream *sp = streams[j];
       if (!sp || sp->engine != e) fail(Q3T_ERR_INVALID, "stream %d is null or belongs to another engine", j);
       if (seen[sp->slot]++) fail(Q3T_ERR_INVALID, "stream %d is listed twice", j);
+      if (sp->text_open)
+        fail(Q3T_ERR_INVALID, "stream %d has open text input; advance it with q3t_stream_next_codes", j);
       info[j].frames = 0;
       info[j].total_frames = sp->host_frame;
       info[j].ended_by_eos = sp->done == 1;
@@ -1613,7 +1704,13 @@ int q3t_stream_next_codes(q3t_stream *sp, int32_t max_chunk, int32_t *codes, q3t
     info->ended_by_eos = sp->done == 1;
     if (sp->done || sp->host_frame >= sp->max_frames) return;
     HIPC(hipSetDevice(e.device));
-    const int n = std::min(max_chunk, sp->max_frames - sp->host_frame);
+    int n = std::min(max_chunk, sp->max_frames - sp->host_frame);
+    // Open text: frame f (f + 1 < max_frames) reads trailing row f, which must have been pushed;
+    // frames = 0 without the end flags is the reference's NeedMoreText (generation.rs:1150-1158,
+    // 1200-1208).
+    if (sp->text_open && sp->text_rows < sp->max_frames - 1)
+      n = std::min(n, std::max(0, sp->text_rows - sp->host_frame));
+    if (n == 0) return;
     run_frames(e, s, n);
     sync_state(s);
     const int produced = s.h_state->frame - sp->host_frame;

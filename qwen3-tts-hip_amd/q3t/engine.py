@@ -12,6 +12,9 @@ frames`` / ``load_with_options`` (255-315)  / ``load_with_options``
 ``start_stream`` (421-440)                  ``HipTtsEngine.start_stream``
 ``generate_voice_clone[_codes]`` (334-393)  ``HipTtsEngine.generate_voice_clone[_codes]``
 ``start_voice_clone_stream`` (442-462)      ``HipTtsEngine.start_voice_clone_stream``
+``start_[voice_clone_]text_stream[_polling]`` ``HipTtsEngine.start_[voice_clone_]text_stream[_polling]``
+(463-511), ``PollingTextStream``,           (:mod:`q3t.text_stream`)
+``HipTextStream``, ``TextStreamInput``
 ``HipTtsStream::next_codes_chunk`` (876-)   ``HipTtsStream.next_codes_chunk``
 ``HipTtsStream::finish_codes`` (991-997)    ``HipTtsStream.finish_codes``
 ``GenerateOptions`` / ``StreamOptions``     same names, same defaults (40-92)
@@ -160,6 +163,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "q3t_stream_start_voice_clone": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32, f32p,
                                                         ctypes.c_int32, ctypes.c_int32, P(_GenerateOptions),
                                                         P(ctypes.c_void_p)]),
+        "q3t_text_stream_start": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32, f32p, ctypes.c_int32,
+                                                 P(_GenerateOptions), P(ctypes.c_void_p)]),
+        "q3t_text_stream_push": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32]),
+        "q3t_text_stream_finish": (ctypes.c_int, [ctypes.c_void_p]),
         "q3t_streams_start": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, P(_StreamInput), P(_GenerateOptions),
                                              P(ctypes.c_void_p)]),
         "q3t_streams_next_codes": (ctypes.c_int, [ctypes.c_void_p, P(ctypes.c_void_p), ctypes.c_int32,
@@ -640,6 +647,31 @@ class HipTtsEngine:
                    else np.zeros(0, np.float32))
         return GeneratedSpeech(inputs if isinstance(inputs, str) else "", g.frames, g.ended_by_eos, g.codes,
                                samples, SAMPLE_RATE)
+
+    # -- text streams (text pushed while audio is produced) ---------------------------------
+    def start_text_stream_polling(self, options: GenerateOptions = GenerateOptions(), stream_options=None):
+        """``start_text_stream_polling`` (generation.rs:475-483)."""
+        from .text_stream import PollingTextStream, TextStreamOptions
+        return PollingTextStream(self, options, stream_options or TextStreamOptions())
+
+    def start_text_stream(self, options: GenerateOptions = GenerateOptions(), stream_options=None):
+        """``start_text_stream`` (generation.rs:463-473): (TextStreamInput, HipTextStream)."""
+        from .text_stream import HipTextStream
+        st = HipTextStream(self.start_text_stream_polling(options, stream_options))
+        return st._input(), st
+
+    def start_voice_clone_text_stream_polling(self, prompt: VoiceClonePrompt,
+                                              options: GenerateOptions = GenerateOptions(), stream_options=None):
+        """``start_voice_clone_text_stream_polling`` (generation.rs:496-511)."""
+        from .text_stream import PollingTextStream, TextStreamOptions
+        return PollingTextStream(self, options, stream_options or TextStreamOptions(), prompt)
+
+    def start_voice_clone_text_stream(self, prompt: VoiceClonePrompt, options: GenerateOptions = GenerateOptions(),
+                                      stream_options=None):
+        """``start_voice_clone_text_stream`` (generation.rs:485-494)."""
+        from .text_stream import HipTextStream
+        st = HipTextStream(self.start_voice_clone_text_stream_polling(prompt, options, stream_options))
+        return st._input(), st
 
     # -- several streams at once (no counterpart in the reference: one stream per engine) --
     def start_streams(self, inputs: List[Inputs], options: List[GenerateOptions],
