@@ -75,6 +75,9 @@ struct TokenHandoff {
   float *cur, *sum;
   int32_t *codes;
   int32_t first, code, groups;
+  // Stream rows (grid z of the attention): row r reads keys + r * keys_row and stores to
+  // sum + r * sum_row, cur + r * cur_row, codes + r * codes_row (all 0 for one stream).
+  int64_t keys_row, sum_row, cur_row, codes_row;
 };
 
 struct GemvArgs {
@@ -130,8 +133,8 @@ struct AttnArgs {
   int64_t kv_row, part_row;
   const int32_t *row_on;
   int32_t out_t16;      // direct output in T16 (rows <= 16) instead of out + r * ld_out
-  // Greedy hand-off (one stream, one chunk): the raw q/k/v row is qkv_table + tok * ld_table
-  // instead of qkv, tok as TokenHandoff defines it (h.keys set).
+  // Greedy hand-off (one chunk; one stream or stream rows): the raw q/k/v row is
+  // qkv_table + tok * ld_table instead of qkv, tok as TokenHandoff defines it (h.keys set).
   TokenHandoff h;
   const float *qkv_table;
   int64_t ld_table;
@@ -176,6 +179,10 @@ struct GemmArgs {
   // skinny GEMM layouts: X / Y / res in T16 (ld ignored) instead of row-major, and W packed
   // as [N/16][K/32][64 lanes][8] (each k step of a 16-column tile is 1 KiB contiguous).
   int32_t x_t16, y_t16, r_t16, w_packed;
+  // skinny GEMM, EPI_STORE: instead of Y, each workgroup (16 columns) stores every row's
+  // largest order key (value, lowest column) at keys_out[m * keys_row + blockIdx.x].
+  uint64_t *keys_out;
+  int64_t keys_row;
 };
 
 // Prompt prefill attention over rows at positions pos0 .. pos0 + P - 1.

@@ -210,9 +210,10 @@ struct Pools {
   SlotState *h_states = nullptr;                        // pinned [n]
   int32_t *h_row_on = nullptr;                          // pinned [n]
   hipStream_t stream = nullptr;                         // batched work
-  hipGraphExec_t graph = nullptr;                       // batched frame, keyed by (rows, traced)
+  hipGraphExec_t graph = nullptr;                       // batched frame, keyed by (rows, traced, fused)
   int graph_rows = 0;
   bool graph_traced = false;
+  bool graph_fused = false;
 };
 
 constexpr int kRowsAttnChunk = 32;
@@ -510,6 +511,12 @@ struct Engine {
            cd.vocab >= 128 && gemv_grid_for(cd.vocab, cd.hidden) <= kHandoffKeys && groups > 2;
   }
 
+  // The batched frame's hand-off: tables built, no Talker -> CodePredictor projection (layer
+  // 0's input row would be T16), LM heads of whole 16-column tiles, no logit tracing.
+  bool rows_handoff_ok() const {
+    return cp_qkv_table && !has_proj && !trace && cd.vocab % 16 == 0 && cd.vocab / 16 <= kHandoffKeys;
+  }
+
   // ----- stream rows: the batched frame over slots 0..rows-1, masked by pools.row_on -----
 
   // An activation operand of the batched frame: row-major with leading dimension ld, or a
@@ -522,7 +529,8 @@ struct Engine {
 
   // Skinny matrix-core GEMM over the stream rows, packed weights Wp.
   void rgemm(int epi, bool norm, const uint16_t *Wp, Act X, const float *gamma, float eps, Act res,
-             const float *bias, Act Y, int N, int K, int rows, hipStream_t s) {
+             const float *bias, Act Y, int N, int K, int rows, hipStream_t s, uint64_t *keys_out = nullptr,
+             int64_t keys_row = 0) {
     GemmArgs g{};
     g.X = X.p; g.ldx = X.ld < 0 ? K : X.ld; g.x_t16 = X.ld < 0;
     g.gamma = gamma; g.eps = eps; g.W = Wp; g.w_packed = 1;
@@ -530,13 +538,16 @@ struct Engine {
     g.bias = bias;
     g.Y = const_cast<float *>(Y.p); g.ldy = Y.ld < 0 ? N : Y.ld; g.y_t16 = Y.ld < 0;
     g.M = rows; g.N = N; g.K = K; g.row_on = pools.row_on;
+    g.keys_out = keys_out; g.keys_row = keys_row;
     hip_check(launch_gemm_skinny(epi, norm, g, s), "launch_gemm_skinny");
   }
 
   // One decoder-stack step of every stream row (each at its own position and cache).  The
-  // residual stream x is a T16 block; `in` feeds layer 0.
+  // residual stream x is a T16 block; `in` feeds layer 0.  With a hand-off, layer 0's
+  // attention takes each row's q/k/v from qkv_table at its token and stores `in` itself.
   void rows_stack_step(const StackW &w, char *kc, char *vc, size_t kv_row, Act in, float *x, int rows, int pos_mode,
-                       int pos_const, int skip, hipStream_t s) {
+                       int pos_const, int skip, hipStream_t s, const TokenHandoff *handoff = nullptr,
+                       const float *qkv_table = nullptr) {
     const Dims &d = w.d;
     Pools &p = pools;
     const int H = d.hidden;
@@ -548,8 +559,10 @@ struct Engine {
     for (int l = 0; l < d.layers; ++l) {
       const LayerW &L = w.layers[l];
       const Act src = l == 0 ? in : t16(x);
-      rgemm(EPI_STORE, true, L.qkv_p, src, L.g_in, d.eps, none, nullptr, Act{p.qkv, p.s_qkv}, d.qkv_rows(), H,
-            rows, s);
+      const bool table = l == 0 && handoff;
+      if (!table)
+        rgemm(EPI_STORE, true, L.qkv_p, src, L.g_in, d.eps, none, nullptr, Act{p.qkv, p.s_qkv}, d.qkv_rows(), H,
+              rows, s);
       AttnArgs aa{p.qkv,    L.gq,    L.gk,     w.rope,  kc + l * cache_layer, vc + l * cache_layer,
                   battn,    d.q_heads, d.kv_heads, w.cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
                   pos_mode, pos_const, skip,    kv_bf16, p.st,   p.attn_part, nch,
@@ -560,6 +573,11 @@ struct Engine {
       aa.part_row = p.part_row;
       aa.row_on = p.row_on;
       aa.out_t16 = 1;
+      if (table) {
+        aa.h = *handoff;
+        aa.qkv_table = qkv_table;
+        aa.ld_table = d.qkv_rows();
+      }
       hip_check(launch_attn_decode(aa, d.head_dim, s, nullptr, rows), "launch_attn_decode(rows)");
       if (partial) {
         AttnMergeArgs m{p.attn_part, battn,     d.q_heads, d.kv_heads, nch,        chunk,
@@ -589,9 +607,15 @@ struct Engine {
   // enqueue_frame for stream rows 0..rows-1 at once: the weights of every pass are read
   // once for all rows (skinny matrix-core GEMMs); attention, selection and the loop state
   // are per row.  Rows that have ended or are masked out keep their state.
-  void enqueue_rows_frame(int rows, hipStream_t s) {
+  //
+  // fused (every live row greedy in the CodePredictor, rows_handoff_ok()): groups 0 .. nac-2
+  // hand their tokens over as the single-stream frame does (per-row argmax keys from the LM
+  // head, q/k/v table rows in the next group's layer-0 attention); only the last group runs
+  // the selection kernel.
+  void enqueue_rows_frame(int rows, bool fused, hipStream_t s) {
     Pools &p = pools;
     const int Ht = talker_hidden, Hc = cd.hidden, Vc = cd.vocab, nac = groups - 1;
+    const int64_t keys_row = (int64_t)(groups - 1) * kHandoffKeys;
     const Act none{nullptr, 0};
     const size_t hc16 = (size_t)16 * Hc;
     Act in0{p.cp_prefix, 2 * Ht}, in1{p.cp_prefix + Ht, 2 * Ht};
@@ -604,13 +628,36 @@ struct Engine {
     rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in0, bx_c, rows, POS_CONST, 0, SKIP_DONE, s);
     rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in1, bx_c, rows, POS_CONST, 1, SKIP_DONE, s);
     for (int g = 0; g < nac; ++g) {
-      if (g > 0) {
+      if (g > 0 && fused) {
+        TokenHandoff t{};
+        t.keys = p.cp_keys + (size_t)(g - 1) * kHandoffKeys;
+        t.keys_row = keys_row;
+        t.n_keys = (Vc + 15) / 16;
+        t.emb = cp_emb + (size_t)(g - 1) * Vc * Ht;
+        t.emb_width = Ht;
+        t.cur = p.cur;
+        t.cur_row = Ht;
+        t.sum = p.emb_sum;
+        t.sum_row = Ht;
+        t.codes = p.codes;
+        t.codes_row = p.codes_row;
+        t.first = g == 1;
+        t.code = g;
+        t.groups = groups;
+        rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, Act{p.cur, Ht}, bx_c, rows, POS_CONST, g + 1, SKIP_DONE, s, &t,
+                        cp_qkv_table + (size_t)(g - 1) * Vc * cd.qkv_rows());
+      } else if (g > 0) {
         Act in{p.cur, Ht};
         if (has_proj) {
           rgemm(EPI_BIAS, false, proj_w_p, in, nullptr, 0.f, none, proj_b, t16(bcp_in + 2 * hc16), Hc, Ht, rows, s);
           in = t16(bcp_in + 2 * hc16);
         }
         rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in, bx_c, rows, POS_CONST, g + 1, SKIP_DONE, s);
+      }
+      if (fused && g < nac - 1) {
+        rgemm(EPI_STORE, true, lm_heads_p + (size_t)g * Vc * Hc, t16(bx_c), c_norm, cd.eps, none, nullptr,
+              Act{p.logits_c, Vc}, Vc, Hc, rows, s, p.cp_keys + (size_t)g * kHandoffKeys, keys_row);
+        continue;
       }
       rgemm(EPI_STORE, true, lm_heads_p + (size_t)g * Vc * Hc, t16(bx_c), c_norm, cd.eps, none, nullptr,
             Act{p.logits_c, Vc}, Vc, Hc, rows, s);
@@ -922,10 +969,10 @@ void run_frames(Engine &e, Slot &s, int n) {
 }
 
 // n batched frames over stream rows 0..rows-1 (pools.row_on already on the device).
-void run_rows_frames(Engine &e, int rows, int n) {
+void run_rows_frames(Engine &e, int rows, int n, bool fused) {
   Pools &p = e.pools;
   if (e.use_graph) {
-    if (!p.graph || p.graph_rows != rows || p.graph_traced != (bool)e.trace) {
+    if (!p.graph || p.graph_rows != rows || p.graph_traced != (bool)e.trace || p.graph_fused != fused) {
       if (p.graph) {
         HIPC(hipGraphExecDestroy(p.graph));
         p.graph = nullptr;
@@ -933,7 +980,7 @@ void run_rows_frames(Engine &e, int rows, int n) {
       hipGraph_t g;
       HIPC(hipStreamBeginCapture(p.stream, hipStreamCaptureModeThreadLocal));
       try {
-        e.enqueue_rows_frame(rows, p.stream);
+        e.enqueue_rows_frame(rows, fused, p.stream);
       } catch (...) {
         (void)hipStreamEndCapture(p.stream, &g);
         if (g) (void)hipGraphDestroy(g);
@@ -945,10 +992,11 @@ void run_rows_frames(Engine &e, int rows, int n) {
       hip_check(err, "hipGraphInstantiate");
       p.graph_rows = rows;
       p.graph_traced = (bool)e.trace;
+      p.graph_fused = fused;
     }
     for (int i = 0; i < n; ++i) HIPC(hipGraphLaunch(p.graph, p.stream));
   } else {
-    for (int i = 0; i < n; ++i) e.enqueue_rows_frame(rows, p.stream);
+    for (int i = 0; i < n; ++i) e.enqueue_rows_frame(rows, fused, p.stream);
   }
 }
 
@@ -1669,8 +1717,10 @@ int q3t_streams_next_codes(q3t_engine *e, q3t_stream *const *streams, int32_t n,
     HIPC(hipSetDevice(e->device));
     Pools &p = e->pools;
     const int rows = set_rows(*e, on, p.stream);
+    bool fused = e->rows_handoff_ok();
+    for (int slot : on) fused = fused && e->slots[slot].cp_greedy;
     // Streams that need fewer frames than nrun reach max_frames on the device and stop there.
-    run_rows_frames(*e, rows, nrun);
+    run_rows_frames(*e, rows, nrun, fused);
     HIPC(hipMemcpyAsync(p.h_states, p.st, sizeof(SlotState) * rows, hipMemcpyDeviceToHost, p.stream));
     HIPC(hipStreamSynchronize(p.stream));
     for (int j = 0; j < n; ++j) {

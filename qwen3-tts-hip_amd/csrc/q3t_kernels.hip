@@ -347,7 +347,8 @@ constexpr int kAttnMaxChunks = kAttnGemvMergeChunks;
 // The stores of a TokenHandoff, by one 256-thread workgroup: thread t covers elements
 // 4t .. 4t+3 and 1024 + 4t .. (widths up to 2048).  handoff_load issues every load (the
 // embedding row, the running sum, the table row), handoff_store the sums and stores.
-__device__ __forceinline__ void handoff_load(const TokenHandoff &h, int tok, float4 *e, float4 *sum, float4 *cur) {
+__device__ __forceinline__ void handoff_load(const TokenHandoff &h, int row, int tok, float4 *e, float4 *sum,
+                                             float4 *cur) {
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int i = 4 * (int)threadIdx.x + 1024 * j;
@@ -355,28 +356,29 @@ __device__ __forceinline__ void handoff_load(const TokenHandoff &h, int tok, flo
     if (i < h.emb_width) {
       const uint2 w = *reinterpret_cast<const uint2 *>(h.emb + (size_t)tok * h.emb_width + i);
       e[j] = make_float4(bf_lo(w.x), bf_hi(w.x), bf_lo(w.y), bf_hi(w.y));
-      if (!h.first) sum[j] = *reinterpret_cast<const float4 *>(h.sum + i);
+      if (!h.first) sum[j] = *reinterpret_cast<const float4 *>(h.sum + row * h.sum_row + i);
     }
     if (h.cur_table && i < h.cur_width)
       cur[j] = *reinterpret_cast<const float4 *>(h.cur_table + (size_t)tok * h.cur_width + i);
   }
 }
 
-__device__ __forceinline__ void handoff_store(const TokenHandoff &h, int tok, const SlotState *st, const float4 *e,
-                                              const float4 *sum, const float4 *cur) {
+__device__ __forceinline__ void handoff_store(const TokenHandoff &h, int row, int tok, const SlotState *st,
+                                              const float4 *e, const float4 *sum, const float4 *cur) {
+  float *hsum = h.sum + row * h.sum_row, *hcur = h.cur + row * h.cur_row;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int i = 4 * (int)threadIdx.x + 1024 * j;
     if (i < h.emb_width) {
       const float4 s = h.first ? e[j]
                                : make_float4(sum[j].x + e[j].x, sum[j].y + e[j].y, sum[j].z + e[j].z, sum[j].w + e[j].w);
-      *reinterpret_cast<float4 *>(h.sum + i) = s;
-      if (!h.cur_table) *reinterpret_cast<float4 *>(h.cur + i) = e[j];
+      *reinterpret_cast<float4 *>(hsum + i) = s;
+      if (!h.cur_table) *reinterpret_cast<float4 *>(hcur + i) = e[j];
     }
-    if (h.cur_table && i < h.cur_width) *reinterpret_cast<float4 *>(h.cur + i) = cur[j];
+    if (h.cur_table && i < h.cur_width) *reinterpret_cast<float4 *>(hcur + i) = cur[j];
   }
   if (threadIdx.x == 0) {
-    int32_t *codes = h.codes + (size_t)st->frame * h.groups;
+    int32_t *codes = h.codes + row * h.codes_row + (size_t)st->frame * h.groups;
     codes[h.code] = tok;
     if (h.first) codes[0] = st->semantic;
   }
@@ -439,8 +441,9 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   const int vec_off = vec < G ? (h * G + vec) * D : (vec == G ? q_out + h * D : q_out + kv_out + h * D);
   uint64_t kin[HO ? 4 : 1];
   if constexpr (HO) {
+    const uint64_t *keys = a.h.keys + row * a.h.keys_row;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) kin[j] = a.h.keys[min(lane + 64 * j, a.h.n_keys - 1)];
+    for (int j = 0; j < 4; ++j) kin[j] = keys[min(lane + 64 * j, a.h.n_keys - 1)];
   }
   if (has_vec) {
     if constexpr (!HO) {
@@ -482,7 +485,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
       x0 = src[lane];
       x1 = src[lane + 64];
     }
-    if (h == 0 && c == 0) handoff_load(a.h, tok, side_e, side_s, side_c);
+    if (h == 0 && c == 0) handoff_load(a.h, row, tok, side_e, side_s, side_c);
   }
 
   // 1: q heads (waves 0..G-1); k and v (waves G, G+1) only where row `pos` is stored.
@@ -573,7 +576,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   __syncthreads();
 
   if constexpr (HO) {
-    if (h == 0 && c == 0) handoff_store(a.h, tok, st, side_e, side_s, side_c);
+    if (h == 0 && c == 0) handoff_store(a.h, row, tok, st, side_e, side_s, side_c);
   }
 
   // 3: final output (single chunk) or this chunk's partial.
@@ -1013,8 +1016,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
 
 __device__ const int32_t kAllRowsOn[16] = {1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1};
 
-template <int EPI, bool NORM, int KS>  // KS = 32-wide k steps per wave = K / (16 * 32)
+// KEYS (EPI_STORE): store per-row argmax keys (GemmArgs::keys_out) instead of Y.
+template <int EPI, bool NORM, int KS, bool KEYS = false>  // KS = 32-wide k steps per wave = K / (16 * 32)
 __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
+  static_assert(!KEYS || EPI == EPI_STORE, "keys replace the plain store");
   constexpr int T = (EPI == EPI_SWIGLU) ? 2 : 1;
   constexpr int KW = KS * 32;  // k range per wave
   const int lane = threadIdx.x & 63;
@@ -1128,6 +1133,19 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
 #pragma unroll
     for (int w = 1; w < 16; ++w) sacc += part[w][t][ol][oe];
     v[t] = sacc;
+  }
+  if constexpr (KEYS) {
+    // The 16 columns of row om sit in lanes oe + 4c (c = 0..15) of one wave: their largest
+    // key, in every one of those lanes, then stored by lane oe.
+    uint64_t key = (om < a.M && on < a.N) ? order_key(v[0], on) : 0;
+#pragma unroll
+    for (int m = 4; m < 64; m <<= 1) {
+      const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)key, m, 64);
+      const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(key >> 32), m, 64);
+      key = umax64(key, ((uint64_t)hi << 32) | lo);
+    }
+    if ((ol & 15) == 0 && om < a.M && oflag) a.keys_out[om * a.keys_row + blockIdx.x] = key;
+    return;
   }
   if (om >= a.M || on >= a.N || !oflag) return;
   float y = v[0];
@@ -1916,11 +1934,16 @@ hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t s, co
   if (a.partial_out ? a.part_chunks < nch : nch != 1) return hipErrorInvalidValue;
   const dim3 grid(a.kv_heads, nch, rows), block(256);
   if (a.h.keys) {
-    // the hand-off: one stream, one chunk of 32 rows, a position given by the launch
+    // the hand-off: one chunk of 32 rows, a position given by the launch; stream rows store
+    // through their own slices (no overlap between rows)
     const int qkv_rows = (a.q_heads + 2 * a.kv_heads) * head_dim;
-    if (rows != 1 || a.partial_out || a.chunk != 32 || a.pos_mode != POS_CONST || !a.qkv_table ||
-        a.ld_table < qkv_rows || !handoff_ok(a.h) || a.h.emb_width > 2048 || a.h.emb_width % 4 ||
-        (a.h.cur_table && a.h.cur_width > 2048) || !a.st)
+    const TokenHandoff &h = a.h;
+    const bool rows_ok = rows == 1 || (h.keys_row >= h.n_keys && h.sum_row >= h.emb_width &&
+                                       h.cur_row >= (h.cur_table ? h.cur_width : h.emb_width) &&
+                                       h.codes_row >= h.groups);
+    if (!rows_ok || a.partial_out || a.chunk != 32 || a.pos_mode != POS_CONST || !a.qkv_table ||
+        a.ld_table < qkv_rows || !handoff_ok(h) || h.emb_width > 2048 || h.emb_width % 4 ||
+        (h.cur_table && h.cur_width > 2048) || !a.st)
       return hipErrorInvalidValue;
     if (a.kv_bf16) {
       if (G == 1) launch_timed(k_attn_split<128, 1, uint16_t, 32, true>, grid, block, 0, s, t, a);
@@ -1992,6 +2015,18 @@ static hipError_t skinny_ks(const GemmArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// The greedy hand-off producer (LM heads over stream rows): per-row argmax keys, no Y.
+static hipError_t skinny_keys(const GemmArgs &a, hipStream_t s) {
+  const dim3 grid((a.N + 15) / 16), block(1024);
+  switch (a.K / 512) {
+    case 1: hipLaunchKernelGGL((k_gemm_skinny<EPI_STORE, true, 1, true>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_gemm_skinny<EPI_STORE, true, 2, true>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_gemm_skinny<EPI_STORE, true, 4, true>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 bool gemm_skinny_supports(int M, int K, bool norm) {
   return M >= 1 && M <= 16 && gemv_supports_k(K) && (!norm || K <= 2048);
 }
@@ -2001,6 +2036,10 @@ hipError_t launch_gemm_skinny(int epi, bool norm, const GemmArgs &a, hipStream_t
     return hipErrorInvalidValue;
   // T16 output / residual needs N % 32 (whole k steps); packed weights need whole 16-column tiles.
   if (((a.y_t16 || a.r_t16) && a.N % 32) || (a.w_packed && a.N % 16)) return hipErrorInvalidValue;
+  if (a.keys_out) {
+    if (epi != EPI_STORE || !norm || a.keys_row < (a.N + 15) / 16) return hipErrorInvalidValue;
+    return skinny_keys(a, s);
+  }
   switch (epi) {
     case EPI_STORE: return norm ? skinny_ks<EPI_STORE, true>(a, s) : skinny_ks<EPI_STORE, false>(a, s);
     case EPI_RESIDUAL: return norm ? hipErrorInvalidValue : skinny_ks<EPI_RESIDUAL, false>(a, s);

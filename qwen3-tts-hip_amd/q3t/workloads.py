@@ -130,6 +130,9 @@ MULTI_WORKLOADS: Dict[str, MultiWorkload] = {w.name: w for w in [
     MultiWorkload("cfg5_0.6b_multistream", "0.6b", 16, (16, 512), (64, 240), 2),
     # small shapes: ragged greedy + sampled streams for quick parity runs
     MultiWorkload("tiny_multistream", "tiny", 6, (4, 40), (8, 24), 5, chunk_frames=5, sampled_every=3),
+    # every stream greedy: the batched frame's token hand-off (no CodePredictor selection
+    # kernels before the last group)
+    MultiWorkload("tiny_multistream_greedy", "tiny", 5, (4, 40), (8, 24), 7, chunk_frames=5),
     # the Talker -> CodePredictor projection (1.7B layout) on the batched path
     MultiWorkload("tinyproj_multistream", "tiny-proj", 3, (4, 24), (6, 14), 6, chunk_frames=4, sampled_every=2),
 ]}

@@ -84,7 +84,7 @@ def test_tiny_multistream_matches_oracle(models):
         assert err <= LOGIT_TOL
 
 
-@pytest.mark.parametrize("name", ["tiny_multistream", "tinyproj_multistream"])
+@pytest.mark.parametrize("name", ["tiny_multistream", "tinyproj_multistream", "tiny_multistream_greedy"])
 def test_multistream_equals_single_stream_path(models, name):
     r = run_batch(models, name)
     for j in range(MULTI_WORKLOADS[name].streams):
@@ -92,9 +92,20 @@ def test_multistream_equals_single_stream_path(models, name):
         np.testing.assert_array_equal(r["codes"][j], g.codes, err_msg=f"stream {j}")
 
 
-def test_multistream_graph_replay_equals_eager(models):
-    a = run_batch(models, "tiny_multistream", use_graph=True)
-    b = run_batch(models, "tiny_multistream", use_graph=False)
+@pytest.mark.parametrize("name", ["tiny_multistream", "tiny_multistream_greedy"])
+def test_multistream_graph_replay_equals_eager(models, name):
+    a = run_batch(models, name, use_graph=True)
+    b = run_batch(models, name, use_graph=False)
+    for j, (x, y) in enumerate(zip(a["codes"], b["codes"])):
+        np.testing.assert_array_equal(x, y, err_msg=f"stream {j}")
+
+
+def test_greedy_batch_hand_off_matches_traced_batch(models):
+    """All-greedy batches hand tokens over between CodePredictor groups without selection
+    kernels; with logit tracing on the batch takes the selection kernels instead.  Both give
+    the same codes."""
+    a = run_batch(models, "tiny_multistream_greedy")
+    b = run_batch(models, "tiny_multistream_greedy", trace=True)
     for j, (x, y) in enumerate(zip(a["codes"], b["codes"])):
         np.testing.assert_array_equal(x, y, err_msg=f"stream {j}")
 
