@@ -142,6 +142,55 @@ __device__ __forceinline__ uint4 load_w(const u32x4 *p) {
 // NT = streaming (non-temporal) weight loads: used for the Talker, whose weights are read once
 // per frame, so that they do not displace the CodePredictor weights that every frame rereads
 // 15 times from the last-level cache.
+// The partials one thread merges (8 output elements at `base`, every chunk slot), loaded
+// without waiting for the stream state: indices are clamped to the workspace, not to the
+// chunks in use.
+struct MergeRegs {
+  float mv[kAttnGemvMergeChunks], lv[kAttnGemvMergeChunks], av[kAttnGemvMergeChunks][8];
+};
+
+__device__ __forceinline__ void merge_load(const GemvArgs &a, int base, MergeRegs &r) {
+  constexpr int D = 128;
+  const int G = a.attn_q_heads / a.attn_kv_heads;
+  const int hq = base / D, d0 = base % D;
+  const int h = hq / G, g = hq % G;
+  const float *p0 = a.attn_part + (((size_t)h * a.attn_part_chunks) * G + g) * (D + 2);
+  const size_t stride = (size_t)G * (D + 2);
+#pragma unroll
+  for (int c = 0; c < kAttnGemvMergeChunks; ++c) {
+    const float *pc = p0 + min(c, a.attn_part_chunks - 1) * stride;
+    r.mv[c] = pc[0];
+    r.lv[c] = pc[1];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r.av[c][j] = pc[2 + d0 + j];  // records are 130 floats: not 16-B aligned
+  }
+}
+
+// The max and the weighted sums over the chunks in use, in chunk order, into xs[base ..].
+__device__ __forceinline__ void merge_finish(const GemvArgs &a, int base, const MergeRegs &r, float *xs) {
+  const int pos = (a.attn_pos_mode == POS_TALKER_FRAME) ? a.st->prefill_steps + a.st->frame : a.attn_pos_const;
+  const int nchunks = (pos + a.attn_chunk) / a.attn_chunk;  // ceil((pos + 1) / chunk)
+  const float *mv = r.mv, *lv = r.lv;
+  const float(*av)[8] = r.av;
+  {
+    float M = -FLT_MAX;
+#pragma unroll
+    for (int c = 0; c < kAttnGemvMergeChunks; ++c)
+      if (c < nchunks) M = fmaxf(M, mv[c]);
+    float den = 0.f, num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < kAttnGemvMergeChunks; ++c)
+      if (c < nchunks) {
+        const float w = expf(mv[c] - M);
+        den = fmaf(w, lv[c], den);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) num[j] = fmaf(w, av[c][j], num[j]);
+      }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xs[base + j] = num[j] / den;
+  }
+}
+
 __device__ void merge_attention(const GemvArgs &a, float *xs);
 
 // ATTN = the input vector is the merge of attention partials (see merge_attention).
@@ -165,6 +214,13 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   // loads while the whole launch's weights are in flight (one DRAM round trip per launch).
   float xv[MR][KC][8];
   float gv[NORM ? KC : 1][8];
+  // Attention input over K <= 2048 (one 8-element slice per thread): its partials are loaded
+  // first, ahead of the weights and of the stream-state check.
+  constexpr bool ATTN_EARLY = ATTN && K <= 256 * 8;
+  MergeRegs mregs;
+  if constexpr (ATTN_EARLY) {
+    if (threadIdx.x * 8 < K) merge_load(a, threadIdx.x * 8, mregs);
+  }
 #pragma unroll
   for (int c = 0; c < KC; ++c) {
     if constexpr (ATTN) break;
@@ -210,7 +266,14 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   // state), so its round trip overlaps theirs instead of preceding them.  Nothing is stored
   // before it.
   if (skip_work(a.st, a.skip)) return;
-  if constexpr (ATTN) {
+  if constexpr (ATTN_EARLY) {
+    if (threadIdx.x * 8 < K) merge_finish(a, threadIdx.x * 8, mregs, xs);
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xv[0][c][j] = xs[c * 512 + lane * 8 + j];
+  } else if constexpr (ATTN) {
     merge_attention(a, xs);
     __syncthreads();
 #pragma unroll
@@ -600,42 +663,10 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
 // Merges the attention partials of all query heads into xs[q_heads * D] (LDS), in chunk
 // order: out = sum_c e^(m_c - M) acc_c / sum_c e^(m_c - M) l_c.  256 threads, 8 dims each.
 __device__ void merge_attention(const GemvArgs &a, float *xs) {
-  constexpr int D = 128;
-  const int pos = (a.attn_pos_mode == POS_TALKER_FRAME) ? a.st->prefill_steps + a.st->frame : a.attn_pos_const;
-  const int nchunks = (pos + a.attn_chunk) / a.attn_chunk;  // ceil((pos + 1) / chunk)
-  const int G = a.attn_q_heads / a.attn_kv_heads;
   for (int base = threadIdx.x * 8; base < a.K; base += 256 * 8) {
-    const int hq = base / D, d0 = base % D;
-    const int h = hq / G, g = hq % G;
-    const float *p0 = a.attn_part + (((size_t)h * a.attn_part_chunks) * G + g) * (D + 2);
-    const size_t stride = (size_t)G * (D + 2);
-    // at most kAttnMaxChunks chunks: every partial slot is loaded at once (indices clamped
-    // to the workspace, not to the chunks in use, so the loads do not wait for the stream
-    // state), then the max and the weighted sums over the chunks in use, in chunk order
-    float mv[kAttnMaxChunks], lv[kAttnMaxChunks], av[kAttnMaxChunks][8];
-#pragma unroll
-    for (int c = 0; c < kAttnMaxChunks; ++c) {
-      const float *pc = p0 + min(c, a.attn_part_chunks - 1) * stride;
-      mv[c] = pc[0];
-      lv[c] = pc[1];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) av[c][j] = pc[2 + d0 + j];  // records are 130 floats: not 16-B aligned
-    }
-    float M = -FLT_MAX;
-#pragma unroll
-    for (int c = 0; c < kAttnMaxChunks; ++c)
-      if (c < nchunks) M = fmaxf(M, mv[c]);
-    float den = 0.f, num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < kAttnMaxChunks; ++c)
-      if (c < nchunks) {
-        const float w = expf(mv[c] - M);
-        den = fmaf(w, lv[c], den);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) num[j] = fmaf(w, av[c][j], num[j]);
-      }
-#pragma unroll
-    for (int j = 0; j < 8; ++j) xs[base + j] = num[j] / den;
+    MergeRegs r;
+    merge_load(a, base, r);
+    merge_finish(a, base, r, xs);
   }
 }
 
