@@ -227,6 +227,25 @@ int q3t_decode_codes(q3t_engine *engine, const int32_t *codes, int32_t frames, f
 int q3t_stream_next_audio(q3t_stream *stream, int32_t max_chunk_frames, int32_t left_context_frames,
                           int32_t *codes, float *samples, int32_t *n_samples, q3t_chunk_info *info);
 
+/* GenerationProfile (generation.rs:104-125) as the device measures it, in seconds of GPU time
+ * between hipEvents: the upload of the prompt rows, the Talker prefill with the first token,
+ * the CodePredictor passes (its token selection and the next Talker input, the reference's
+ * build_step_input, included) and the Talker decode steps (codec head, token selection and the
+ * CodePredictor prefix, the reference's prepare_code_predictor_prefix, included). */
+typedef struct {
+  double upload_seconds, prefill_seconds, code_predictor_seconds, talker_decode_seconds;
+} q3t_profile;
+
+/* generate_codes_profiled's rollout (generation.rs:395-419, 751-874): q3t_stream_start and
+ * q3t_stream_next_codes that also add their phases' GPU time to *profile.  Frames run one at
+ * a time without the frame graph (events between the phases), so they are slower than
+ * q3t_stream_next_codes; the codes are the same. */
+int q3t_stream_start_profiled(q3t_engine *engine, const float *prefill, int32_t prefill_steps,
+                              const float *trailing, int32_t trailing_steps, const float *tts_pad,
+                              const q3t_generate_options *opts, q3t_stream **out, q3t_profile *profile);
+int q3t_stream_next_codes_profiled(q3t_stream *stream, int32_t max_chunk_frames, int32_t *codes,
+                                   q3t_chunk_info *info, q3t_profile *profile);
+
 /* Drops the stream and frees its slot (HipTtsStream's Drop). */
 int q3t_stream_destroy(q3t_stream *stream);
 

@@ -391,6 +391,10 @@ struct Engine {
   // CodePredictor groups 0..14, the next Talker step, token selection, frame bookkeeping.
   void enqueue_frame(Slot &sl, hipStream_t s) {
     enqueue_code_predictor(sl, s);
+    enqueue_talker_decode(sl, s);
+  }
+
+  void enqueue_talker_decode(Slot &sl, hipStream_t s) {
     stack_step(talker, sl.t_k, sl.t_v, sl.t_in, sl.x_t, sl, POS_TALKER_FRAME, 0, SKIP_TALKER, s);
     gemv(EPI_STORE, true, codec_head, sl.x_t, t_norm, td.eps, nullptr, nullptr, sl.logits_t, td.vocab, td.hidden,
          SKIP_TALKER, sl.st, s, true);
@@ -934,6 +938,23 @@ void ensure_trace(Engine &e) {
   }
 }
 
+// hipEvents that free themselves.
+struct Events {
+  std::vector<hipEvent_t> ev;
+  explicit Events(int n) : ev(n, nullptr) {
+    for (auto &x : ev) HIPC(hipEventCreate(&x));
+  }
+  ~Events() {
+    for (auto x : ev)
+      if (x) (void)hipEventDestroy(x);
+  }
+  double seconds(int a, int b) const {
+    float ms = 0.f;
+    HIPC(hipEventElapsedTime(&ms, ev[a], ev[b]));
+    return ms * 1e-3;
+  }
+};
+
 void sync_state(Slot &s) {
   HIPC(hipMemcpyAsync(s.h_state, s.st, sizeof(SlotState), hipMemcpyDeviceToHost, s.stream));
   HIPC(hipStreamSynchronize(s.stream));
@@ -1476,6 +1497,37 @@ int q3t_stream_start(q3t_engine *e, const float *prefill, int32_t P, const float
   });
 }
 
+int q3t_stream_start_profiled(q3t_engine *e, const float *prefill, int32_t P, const float *trailing, int32_t T,
+                              const float *tts_pad, const q3t_generate_options *o, q3t_stream **out,
+                              q3t_profile *prof) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || !out || !prof) fail(Q3T_ERR_INVALID, "null argument");
+    *out = nullptr;
+    const q3t_stream_input in{prefill, P, trailing, T, tts_pad};
+    validate_input(*e, in, o);
+    int slot = -1;
+    for (size_t i = 0; i < e->slots.size(); ++i)
+      if (!e->slots[i].in_use) {
+        slot = (int)i;
+        break;
+      }
+    if (slot < 0) fail(Q3T_ERR_BUSY, "all %zu stream slots are in use", e->slots.size());
+    HIPC(hipSetDevice(e->device));
+    ensure_trace(*e);
+    hipStream_t s = e->slots[slot].stream;
+    Events ev(3);
+    HIPC(hipEventRecord(ev.ev[0], s));
+    stage_stream(*e, slot, 0, in, o, s);
+    HIPC(hipEventRecord(ev.ev[1], s));
+    *out = start_staged(*e, slot, P, o);
+    HIPC(hipEventRecord(ev.ev[2], s));
+    HIPC(hipEventSynchronize(ev.ev[2]));
+    prof->upload_seconds += ev.seconds(0, 1);
+    prof->prefill_seconds += ev.seconds(1, 2);
+  });
+}
+
 }  // extern "C"
 
 namespace q3t {
@@ -1742,37 +1794,90 @@ int q3t_streams_next_codes(q3t_engine *e, q3t_stream *const *streams, int32_t n,
   });
 }
 
+}  // extern "C"
+
+namespace q3t {
+namespace {
+
+// The frames a next_codes call may run (0: none, the stream has ended or waits for text);
+// fills info for the no-frames case.
+int frames_to_run(q3t_stream *sp, int max_chunk, int32_t *codes, q3t_chunk_info *info) {
+  if (!sp || !info || (max_chunk > 0 && !codes)) fail(Q3T_ERR_INVALID, "null argument");
+  if (max_chunk <= 0) fail(Q3T_ERR_INVALID, "max_chunk_frames must be non-zero");
+  info->frames = 0;
+  info->total_frames = sp->host_frame;
+  info->ended_by_eos = sp->done == 1;
+  if (sp->done || sp->host_frame >= sp->max_frames) return 0;
+  int n = std::min(max_chunk, sp->max_frames - sp->host_frame);
+  // Open text: frame f (f + 1 < max_frames) reads trailing row f, which must have been pushed;
+  // frames = 0 without the end flags is the reference's NeedMoreText (generation.rs:1150-1158,
+  // 1200-1208).
+  if (sp->text_open && sp->text_rows < sp->max_frames - 1)
+    n = std::min(n, std::max(0, sp->text_rows - sp->host_frame));
+  return n;
+}
+
+// After up to n frames ran: the new codes to the caller, the host's view of the stream.
+void collect_frames(q3t_stream *sp, int n, int32_t *codes, q3t_chunk_info *info) {
+  Engine &e = *sp->engine;
+  Slot &s = e.slots[sp->slot];
+  sync_state(s);
+  const int produced = s.h_state->frame - sp->host_frame;
+  if (produced < 0 || produced > n) fail(Q3T_ERR_HIP, "device loop state is inconsistent");
+  if (produced > 0)
+    HIPC(hipMemcpy(codes, s.codes + (size_t)sp->host_frame * e.groups, (size_t)produced * e.groups * 4,
+                   hipMemcpyDeviceToHost));
+  sp->host_frame += produced;
+  sp->done = s.h_state->done;
+  info->frames = produced;
+  info->total_frames = sp->host_frame;
+  info->ended_by_eos = sp->done == 1;
+}
+
+
+}  // namespace
+}  // namespace q3t
+
+extern "C" {
+
 int q3t_stream_next_codes(q3t_stream *sp, int32_t max_chunk, int32_t *codes, q3t_chunk_info *info) {
   return guarded([&] {
     using namespace q3t;
-    if (!sp || !info || (max_chunk > 0 && !codes)) fail(Q3T_ERR_INVALID, "null argument");
-    if (max_chunk <= 0) fail(Q3T_ERR_INVALID, "max_chunk_frames must be non-zero");
+    const int n = frames_to_run(sp, max_chunk, codes, info);
+    if (n == 0) return;
+    Engine &e = *sp->engine;
+    HIPC(hipSetDevice(e.device));
+    run_frames(e, e.slots[sp->slot], n);
+    collect_frames(sp, n, codes, info);
+  });
+}
+
+int q3t_stream_next_codes_profiled(q3t_stream *sp, int32_t max_chunk, int32_t *codes, q3t_chunk_info *info,
+                                   q3t_profile *prof) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!prof) fail(Q3T_ERR_INVALID, "null argument");
+    const int n = frames_to_run(sp, max_chunk, codes, info);
+    if (n == 0) return;
     Engine &e = *sp->engine;
     Slot &s = e.slots[sp->slot];
-    info->frames = 0;
-    info->total_frames = sp->host_frame;
-    info->ended_by_eos = sp->done == 1;
-    if (sp->done || sp->host_frame >= sp->max_frames) return;
     HIPC(hipSetDevice(e.device));
-    int n = std::min(max_chunk, sp->max_frames - sp->host_frame);
-    // Open text: frame f (f + 1 < max_frames) reads trailing row f, which must have been pushed;
-    // frames = 0 without the end flags is the reference's NeedMoreText (generation.rs:1150-1158,
-    // 1200-1208).
-    if (sp->text_open && sp->text_rows < sp->max_frames - 1)
-      n = std::min(n, std::max(0, sp->text_rows - sp->host_frame));
-    if (n == 0) return;
-    run_frames(e, s, n);
-    sync_state(s);
-    const int produced = s.h_state->frame - sp->host_frame;
-    if (produced < 0 || produced > n) fail(Q3T_ERR_HIP, "device loop state is inconsistent");
-    if (produced > 0)
-      HIPC(hipMemcpy(codes, s.codes + (size_t)sp->host_frame * e.groups, (size_t)produced * e.groups * 4,
-                     hipMemcpyDeviceToHost));
-    sp->host_frame += produced;
-    sp->done = s.h_state->done;
-    info->frames = produced;
-    info->total_frames = sp->host_frame;
-    info->ended_by_eos = sp->done == 1;
+    Events ev(3);
+    int ran = 0;
+    // One frame at a time (rollout_profiled, generation.rs:751-874): a frame after the end of
+    // the stream is not run, so that it adds no time.
+    while (ran < n && !s.h_state->done) {
+      HIPC(hipEventRecord(ev.ev[0], s.stream));
+      e.enqueue_code_predictor(s, s.stream);
+      HIPC(hipEventRecord(ev.ev[1], s.stream));
+      e.enqueue_talker_decode(s, s.stream);
+      HIPC(hipEventRecord(ev.ev[2], s.stream));
+      sync_state(s);
+      prof->code_predictor_seconds += ev.seconds(0, 1);
+      prof->talker_decode_seconds += ev.seconds(1, 2);
+      ++ran;
+    }
+    collect_frames(sp, n, codes, info);
   });
 }
 

@@ -120,6 +120,11 @@ class _ChunkInfo(ctypes.Structure):
                 ("ended_by_eos", ctypes.c_int32)]
 
 
+class _Profile(ctypes.Structure):
+    _fields_ = [("upload_seconds", ctypes.c_double), ("prefill_seconds", ctypes.c_double),
+                ("code_predictor_seconds", ctypes.c_double), ("talker_decode_seconds", ctypes.c_double)]
+
+
 class _StreamInput(ctypes.Structure):
     _fields_ = [("prefill", ctypes.POINTER(ctypes.c_float)), ("prefill_steps", ctypes.c_int32),
                 ("trailing", ctypes.POINTER(ctypes.c_float)), ("trailing_steps", ctypes.c_int32),
@@ -150,6 +155,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                                             f32p, P(_GenerateOptions), P(ctypes.c_void_p)]),
         "q3t_stream_next_codes": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, i32p, P(_ChunkInfo)]),
         "q3t_stream_destroy": (ctypes.c_int, [ctypes.c_void_p]),
+        "q3t_stream_start_profiled": (ctypes.c_int, [ctypes.c_void_p, f32p, ctypes.c_int32, f32p, ctypes.c_int32,
+                                                     f32p, P(_GenerateOptions), P(ctypes.c_void_p), P(_Profile)]),
+        "q3t_stream_next_codes_profiled": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, i32p, P(_ChunkInfo),
+                                                          P(_Profile)]),
         "q3t_decode_codes": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32, f32p]),
         "q3t_stream_next_audio": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, i32p, f32p, i32p,
                                                  P(_ChunkInfo)]),
@@ -299,13 +308,51 @@ class GeneratedAudioChunk:
 
 @dataclasses.dataclass
 class GeneratedSpeech:
-    """``GeneratedSpeech`` (generation.rs:94-103)."""
+    """``GeneratedSpeech`` (generation.rs:94-103, 1521-1553)."""
     text: str
     frames: int
     ended_by_eos: bool
     codes: np.ndarray
     samples: np.ndarray
     sample_rate: int
+
+    def audio_seconds(self) -> float:
+        return self.samples.size / float(self.sample_rate)
+
+    def to_wav_bytes(self, gain: float = 1.0) -> bytes:
+        from .wav import wav_bytes
+        return wav_bytes(self.samples, self.sample_rate, gain)
+
+    def write_wav(self, path, gain: float = 1.0) -> None:
+        from .wav import write_wav
+        write_wav(path, self.samples, self.sample_rate, gain)
+
+
+@dataclasses.dataclass
+class GenerationProfile:
+    """``GenerationProfile`` (generation.rs:104-125).  prepare_text_seconds is host time; the
+    rest is GPU time between events.  The CodePredictor prefix (prepare_prefix) is built by
+    the Talker's token selection and the next Talker input (build_step_input) by the last
+    CodePredictor selection, so their time is inside talker_decode_seconds and
+    code_predictor_seconds and those two fields stay 0."""
+    prepare_text_seconds: float = 0.0
+    upload_seconds: float = 0.0
+    prefill_seconds: float = 0.0
+    prepare_prefix_seconds: float = 0.0
+    code_predictor_seconds: float = 0.0
+    build_step_input_seconds: float = 0.0
+    talker_decode_seconds: float = 0.0
+
+    def total_seconds(self) -> float:
+        return (self.prepare_text_seconds + self.upload_seconds + self.prefill_seconds + self.prepare_prefix_seconds
+                + self.code_predictor_seconds + self.build_step_input_seconds + self.talker_decode_seconds)
+
+
+@dataclasses.dataclass
+class ProfiledGeneratedCodes:
+    """``ProfiledGeneratedCodes`` (generation.rs:127-131)."""
+    codes: "GeneratedCodes"
+    profile: GenerationProfile
 
 
 @dataclasses.dataclass
@@ -510,6 +557,33 @@ class HipTtsEngine:
                                        _fptr(pad), ctypes.byref(o), _iptr(codes), ctypes.byref(frames),
                                        ctypes.byref(eos)))
         return GeneratedCodes(codes[:frames.value].copy(), frames.value, bool(eos.value))
+
+    def generate_codes_profiled(self, inputs: Inputs,
+                                options: GenerateOptions = GenerateOptions()) -> ProfiledGeneratedCodes:
+        """``generate_codes_profiled`` (generation.rs:395-419): generate_codes with the time of
+        each phase.  Frames run one at a time without the frame graph."""
+        import time
+        options.validate()
+        t0 = time.perf_counter()
+        inp = self._prepare(inputs, options, 1 << 30)
+        prof = GenerationProfile(prepare_text_seconds=time.perf_counter() - t0)
+        p = _Profile()
+        o = options._c()
+        pre, trail, pad = _f32(inp.prefill), _f32(inp.trailing_text), _f32(inp.tts_pad_embed)
+        handle = ctypes.c_void_p()
+        _check(_lib.q3t_stream_start_profiled(self._h, _fptr(pre), pre.shape[0], _fptr(trail), trail.shape[0],
+                                              _fptr(pad), ctypes.byref(o), ctypes.byref(handle), ctypes.byref(p)))
+        try:
+            n = max(options.max_frames, 1)
+            codes = np.zeros((n, self.code_groups), dtype=np.int32)
+            info = _ChunkInfo()
+            _check(_lib.q3t_stream_next_codes_profiled(handle, n, _iptr(codes), ctypes.byref(info), ctypes.byref(p)))
+        finally:
+            _check(_lib.q3t_stream_destroy(handle))
+        prof.upload_seconds, prof.prefill_seconds = p.upload_seconds, p.prefill_seconds
+        prof.code_predictor_seconds, prof.talker_decode_seconds = p.code_predictor_seconds, p.talker_decode_seconds
+        g = GeneratedCodes(codes[:info.frames].copy(), int(info.frames), bool(info.ended_by_eos))
+        return ProfiledGeneratedCodes(g, prof)
 
     def start_stream(self, inputs: Inputs, options: GenerateOptions = GenerateOptions(),
                      stream_options: StreamOptions = StreamOptions()) -> "HipTtsStream":

@@ -74,6 +74,32 @@ def test_chunking_and_generate_codes_agree(models):
     assert g.frames == len(ref) and not g.ended_by_eos
 
 
+@pytest.mark.parametrize("name", ["tiny_greedy", "tiny_sampled"])
+def test_generate_codes_profiled(models, name):
+    """generate_codes_profiled (generation.rs:395-419): the same codes as generate_codes, and
+    a time for every phase the device measures."""
+    w = WORKLOADS[name]
+    model, d = models.get(w.spec)
+    opts = E.GenerateOptions(**w.options_kwargs())
+    print(f"[gpu] generate_codes_profiled {name}", flush=True)
+    with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=w.max_cache_steps)) as eng:
+        g = eng.generate_codes(w.inputs(model), opts)
+        p = eng.generate_codes_profiled(w.inputs(model), opts)
+        again = eng.generate_codes(w.inputs(model), opts)  # the slot is free again
+    np.testing.assert_array_equal(p.codes.codes, g.codes)
+    np.testing.assert_array_equal(again.codes, g.codes)
+    assert (p.codes.frames, p.codes.ended_by_eos) == (g.frames, g.ended_by_eos)
+    prof = p.profile
+    assert prof.upload_seconds > 0 and prof.prefill_seconds > 0
+    assert prof.code_predictor_seconds > 0 and prof.talker_decode_seconds > 0
+    assert prof.prepare_prefix_seconds == 0 and prof.build_step_input_seconds == 0
+    assert prof.total_seconds() == pytest.approx(
+        prof.prepare_text_seconds + prof.upload_seconds + prof.prefill_seconds + prof.code_predictor_seconds
+        + prof.talker_decode_seconds)
+    print(f"{name}: {p.codes.frames} frames; code predictor {1e3 * prof.code_predictor_seconds:.2f} ms, "
+          f"talker {1e3 * prof.talker_decode_seconds:.2f} ms, prefill {1e3 * prof.prefill_seconds:.3f} ms")
+
+
 def test_graph_replay_is_bitwise_equal_to_eager(models):
     a = run(models, "tiny_sampled", use_graph=True)
     b = run(models, "tiny_sampled", use_graph=False)
