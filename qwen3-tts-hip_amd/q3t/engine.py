@@ -56,6 +56,27 @@ Q3T_OK, Q3T_ERR_INVALID, Q3T_ERR_HIP, Q3T_ERR_CAPACITY, Q3T_ERR_NOT_FOUND, Q3T_E
 SPEAKERS = ["serena", "vivian", "uncle_fu", "ryan", "aiden", "ono_anna", "sohee", "eric", "dylan"]
 LANGUAGES = ["chinese", "english", "japanese", "korean", "german", "french", "russian",
              "portuguese", "spanish", "italian"]
+_SPEAKER_ALIASES = {"unclefu": "uncle_fu", "onoanna": "ono_anna"}
+_LANGUAGE_ALIASES = {"zh": "chinese", "en": "english", "ja": "japanese", "ko": "korean", "de": "german",
+                     "fr": "french", "ru": "russian", "pt": "portuguese", "es": "spanish", "it": "italian"}
+
+
+def parse_speaker(value: str) -> int:
+    """``Speaker::from_str`` (text.rs:137-153): case-insensitive name -> the enum ordinal."""
+    v = str(value).lower()
+    v = _SPEAKER_ALIASES.get(v, v)
+    if v not in SPEAKERS:
+        raise InvalidInputError(Q3T_ERR_INVALID, f"unknown speaker {value}")
+    return SPEAKERS.index(v)
+
+
+def parse_language(value: str) -> int:
+    """``Language::from_str`` (text.rs:75-93): case-insensitive name or ISO code -> ordinal."""
+    v = str(value).lower()
+    v = _LANGUAGE_ALIASES.get(v, v)
+    if v not in LANGUAGES:
+        raise InvalidInputError(Q3T_ERR_INVALID, f"unknown language {value}")
+    return LANGUAGES.index(v)
 
 
 class Q3tError(RuntimeError):
@@ -262,8 +283,8 @@ class GenerateOptions:
 
     def _c(self) -> _GenerateOptions:
         o = _GenerateOptions()
-        o.speaker = SPEAKERS.index(self.speaker.lower()) if self.speaker.lower() in SPEAKERS else -1
-        o.language = LANGUAGES.index(self.language.lower()) if self.language.lower() in LANGUAGES else -1
+        o.speaker = parse_speaker(self.speaker)
+        o.language = parse_language(self.language)
         o.max_frames = int(self.max_frames)
         o.decode_audio = int(bool(self.decode_audio))
         o.do_sample = int(bool(self.do_sample))
