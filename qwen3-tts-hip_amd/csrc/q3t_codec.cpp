@@ -71,6 +71,10 @@ struct Codec {
   float *fin_a = nullptr, *fin_b = nullptr, *fin_w = nullptr, *fin_bias = nullptr;  // fin_w [7][96]
   float *ws = nullptr;  // decode workspace, grown to the largest frame count seen
   size_t ws_floats = 0;
+  // K-split partial sums of the GEMMs that would otherwise run as few workgroups (short
+  // windows: a streaming chunk decodes ~31 frames)
+  float *split_ws = nullptr;
+  static constexpr int64_t kSplitFloats = (int64_t)4 << 20;
   int32_t *codes_ws = nullptr;  // staging for host codes
   size_t codes_ws_n = 0;
   float *samples_ws = nullptr;  // staging for samples copied to the host
@@ -242,6 +246,8 @@ Codec *codec_load(const std::string &model_dir, int64_t *device_bytes) {
       c->fin_w = c->upload(r);
     }
     c->fin_bias = up_f32("decoder.decoder.6.conv.bias", 1);
+    c->split_ws = dev_alloc<float>((size_t)Codec::kSplitFloats, c->bytes);
+    c->allocs.push_back(c->split_ws);
   } catch (...) {
     codec_free(c);
     throw;
@@ -321,6 +327,7 @@ void codec_decode(Codec &c, const int32_t *codes, int F, int groups, float *samp
     g.X = X; g.ldx = ldx; g.W = W; g.Y = Y; g.ldy = ldy; g.M = M; g.N = N; g.K = K;
     g.bias = bias; g.res = res; g.ldr = ldr; g.scale = scale; g.row_scale = row_scale; g.gamma = gamma;
     g.xseg_len = seg_len; g.xseg_stride = seg_stride;
+    g.split_ws = c.split_ws; g.split_cap = Codec::kSplitFloats;
     hip_check(launch_gemm(epi, g, s), "launch_gemm(codec)");
   };
 

@@ -247,6 +247,9 @@ struct Engine {
   // raw q/k/v row of every input token, [groups-2][Vc][qkv_rows], and (projection only) the
   // projected input row, [groups-2][Vc][Hc].
   float *cp_qkv_table = nullptr, *cp_in_table = nullptr;
+  // K-split partial sums of prompt-prefill and text-projection GEMMs over few rows
+  static constexpr int64_t kSplitFloats = (int64_t)4 << 20;
+  float *split_ws = nullptr;
   // Prompt preparation on the device (text.rs:516-603), when the checkpoint holds
   // talker.model.text_embedding.weight: the table [text_vocab][text_hidden] and the text
   // projection fc1 [tp_inter][text_hidden] + bias, fc2 [H][tp_inter] + bias.
@@ -351,6 +354,7 @@ struct Engine {
       GemmArgs g{};
       g.X = p.px; g.ldx = H; g.row_scale = p.pinv; g.gamma = L.g_in;
       g.W = L.qkv; g.Y = p.pqkv; g.ldy = Q; g.M = M; g.N = Q; g.K = H;
+      g.split_ws = split_ws; g.split_cap = kSplitFloats;
       hip_check(launch_gemm(EPI_STORE, g, s), "launch_gemm(qkv)");
       for (const PrefillSeg &sg : segs) {
         const Slot &sl = slots[sg.slot];
@@ -362,6 +366,7 @@ struct Engine {
       g = GemmArgs{};
       g.X = p.pattn; g.ldx = O; g.W = L.o; g.res = p.px; g.ldr = H; g.Y = p.px; g.ldy = H;
       g.M = M; g.N = H; g.K = O;
+      g.split_ws = split_ws; g.split_cap = kSplitFloats;
       hip_check(launch_gemm(EPI_RESIDUAL, g, s), "launch_gemm(o)");
       hip_check(launch_row_rms(p.px, H, M, H, d.eps, p.pinv, s), "launch_row_rms");
       g = GemmArgs{};
@@ -371,6 +376,7 @@ struct Engine {
       g = GemmArgs{};
       g.X = p.pact; g.ldx = I; g.W = L.down; g.res = p.px; g.ldr = H; g.Y = p.px; g.ldy = H;
       g.M = M; g.N = H; g.K = I;
+      g.split_ws = split_ws; g.split_cap = kSplitFloats;
       hip_check(launch_gemm(EPI_RESIDUAL, g, s), "launch_gemm(down)");
     }
     for (const PrefillSeg &sg : segs)
@@ -1181,6 +1187,7 @@ int q3t_engine_create(const q3t_engine_options *opts, q3t_engine **out) {
     try {
       alloc_pools(*e, nslots);
       if (nslots > 1 && e->rows_ok) alloc_rows(*e);
+      e->split_ws = dev_alloc<float>((size_t)Engine::kSplitFloats, e->device_bytes);
       build_cp_tables(*e);
       e->codec = codec_load(dir, &e->device_bytes);
     } catch (...) {
@@ -1205,7 +1212,7 @@ int q3t_engine_destroy(q3t_engine *e) {
                     e->cp.mats_p,   e->codec_head_p, e->lm_heads_p,  e->proj_w_p,    e->bx_t,
                     e->bx_c,        e->battn,        e->bact,        e->bcp_in,      e->cp_qkv_table,
                     e->cp_in_table, e->text_emb,     e->tp_fc1,      e->tp_fc2,      e->tp_b1,
-                    e->tp_b2};
+                    e->tp_b2,       e->split_ws};
     for (void *p : ptrs)
       if (p) (void)hipFree(p);
     delete e;
@@ -1430,11 +1437,13 @@ void prepare_text_device(Engine &e, const TextPlan &p, float *prefill, float *tr
     GemmArgs g{};
     g.X = X; g.ldx = e.text_hidden; g.W = e.tp_fc1; g.bias = e.tp_b1; g.Y = Hd; g.ldy = e.tp_inter;
     g.M = M; g.N = e.tp_inter; g.K = e.text_hidden;
+    g.split_ws = e.split_ws; g.split_cap = Engine::kSplitFloats;
     hip_check(launch_gemm(EPI_BIAS, g, s), "launch_gemm(text fc1)");
     hip_check(launch_silu(Hd, (size_t)M * e.tp_inter, s), "launch_silu");
     g = GemmArgs{};
     g.X = Hd; g.ldx = e.tp_inter; g.W = e.tp_fc2; g.bias = e.tp_b2; g.Y = Y; g.ldy = H;
     g.M = M; g.N = H; g.K = e.tp_inter;
+    g.split_ws = e.split_ws; g.split_cap = Engine::kSplitFloats;
     hip_check(launch_gemm(EPI_BIAS, g, s), "launch_gemm(text fc2)");
     hip_check(launch_text_assemble(Y, H, M, codec, e.codec_emb, xvec, dst, prefill, trailing, pad, s),
               "launch_text_assemble");

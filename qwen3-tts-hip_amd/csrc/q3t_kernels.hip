@@ -792,6 +792,9 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
   const int m0 = blockIdx.y * 16 * MB;
   const int n0 = (blockIdx.x * 4 + wave) * 16 * NTILE;  // first output column of this wave
   if (n0 >= a.N) return;
+  // split z of gridDim.z: k steps [kt0, kt1) of 32
+  const int KT = a.K / 32, nsplit = gridDim.z, z = blockIdx.z;
+  const int kt0 = (int)((int64_t)KT * z / nsplit), kt1 = (int)((int64_t)KT * (z + 1) / nsplit);
 
   f32x4_t acc[MB][NB];
 #pragma unroll
@@ -819,7 +822,7 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
     wrow[j] = min(col, lim - 1);
   }
 
-  for (int k0 = 0; k0 < a.K; k0 += 32) {
+  for (int k0 = kt0 * 32; k0 < kt1 * 32; k0 += 32) {
     const int k = k0 + 8 * kb;
     float xa[MB][8];
 #pragma unroll
@@ -884,6 +887,10 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
           const float u = acc[i][j + NTILE][e];
           v = v / (1.0f + expf(-v)) * u;
         } else {
+          if (nsplit > 1) {
+            a.split_ws[((size_t)z * a.M + m) * a.N + n] = v;
+            continue;
+          }
           v = gemm_epilogue<EPI>(a, m, n, v);
         }
         a.Y[(size_t)m * a.ldy + n] = v;
@@ -922,7 +929,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
   const int li = lane & 15, kb = lane >> 4;
   const int m0 = blockIdx.y * BM;
   const int nb = blockIdx.x;
-  const int KT = a.K / BK;
+  // split z of gridDim.z: k tiles [kt0, kt1)
+  const int KT = a.K / BK, nsplit = gridDim.z, z = blockIdx.z;
+  const int kt0 = (int)((int64_t)KT * z / nsplit), kt1 = (int)((int64_t)KT * (z + 1) / nsplit);
 
   // weight row of block row r (a partial last block of a non-SwiGLU GEMM repeats the last row;
   // its columns are not stored)
@@ -987,12 +996,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) acc[t][u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  gload(0);
+  gload(kt0 * BK);
   sstore(0);
   __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < KT) gload((kt + 1) * BK);
+  for (int kt = kt0; kt < kt1; ++kt) {
+    const int buf = (kt - kt0) & 1;
+    if (kt + 1 < kt1) gload((kt + 1) * BK);
 #pragma unroll
     for (int ks = 0; ks < BK / 32; ++ks) {
       bf16x8_t bq[4];
@@ -1017,7 +1026,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
           for (int u = 0; u < 4; ++u)
             acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aq[q][t], bq[u], acc[t][u], 0, 0, 0);
     }
-    if (kt + 1 < KT) sstore(buf ^ 1);
+    if (kt + 1 < kt1) sstore(buf ^ 1);
     __syncthreads();
   }
 
@@ -1039,7 +1048,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int n = nb * 128 + wn * 64 + u * 16 + li;
-          if (n < a.N) a.Y[(size_t)m * a.ldy + n] = gemm_epilogue<EPI>(a, m, n, acc[t][u][e]);
+          if (n >= a.N) continue;
+          if (nsplit > 1) a.split_ws[((size_t)z * a.M + m) * a.N + n] = acc[t][u][e];
+          else a.Y[(size_t)m * a.ldy + n] = gemm_epilogue<EPI>(a, m, n, acc[t][u][e]);
         }
       }
     }
@@ -2001,6 +2012,27 @@ hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t s, co
   return hipErrorInvalidValue;
 }
 
+// Sum of the K splits in split order, then the epilogue: Y[m][n] = f(sum_z ws[z][m][n]).
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm_split_reduce(GemmArgs a, int nsplit) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t mn = (size_t)a.M * a.N;
+  if (i >= mn) return;
+  float v = a.split_ws[i];
+  for (int z = 1; z < nsplit; ++z) v += a.split_ws[(size_t)z * mn + i];
+  const int m = (int)(i / a.N), n = (int)(i % a.N);
+  a.Y[(size_t)m * a.ldy + n] = gemm_epilogue<EPI>(a, m, n, v);
+}
+
+// K splits for a launch of `blocks` workgroups: enough to reach ~256 workgroups, at least
+// 4 k steps of 32 per split, at most 16 splits, within the workspace.
+static int gemm_splits(const GemmArgs &a, int blocks, bool swiglu) {
+  if (!a.split_ws || swiglu || blocks >= 128) return 1;
+  int sp = std::min(std::min((256 + blocks - 1) / blocks, a.K / 32 / 4), 16);
+  while (sp > 1 && (int64_t)sp * a.M * a.N > a.split_cap) --sp;
+  return std::max(sp, 1);
+}
+
 template <int EPI>
 static hipError_t gemm_epi(const GemmArgs &a, hipStream_t s) {
   // 16-row tiles for short M (batched decode), 32-row tiles otherwise; 64 output columns
@@ -2008,15 +2040,29 @@ static hipError_t gemm_epi(const GemmArgs &a, hipStream_t s) {
   constexpr int NB = 4;
   constexpr int NT = (EPI == EPI_SWIGLU) ? NB / 2 : NB;
   const int cols_per_wg = 4 * 16 * NT;
+  dim3 grid;
+  int path;
   if (a.M >= 128 && a.K % 32 == 0 && (EPI != EPI_SWIGLU || a.N % 64 == 0) && a.ldx % 4 == 0) {
     const int nout = EPI == EPI_SWIGLU ? 64 : 128;
-    hipLaunchKernelGGL((k_gemm_lds<EPI>), dim3((a.N + nout - 1) / nout, (a.M + 127) / 128), dim3(256), 0, s, a);
+    grid = dim3((a.N + nout - 1) / nout, (a.M + 127) / 128);
+    path = 0;
   } else if (a.M <= 16) {
-    hipLaunchKernelGGL((k_gemm_mfma<EPI, 1, NB>), dim3((a.N + cols_per_wg - 1) / cols_per_wg, (a.M + 15) / 16),
-                       dim3(256), 0, s, a);
+    grid = dim3((a.N + cols_per_wg - 1) / cols_per_wg, (a.M + 15) / 16);
+    path = 1;
   } else {
-    hipLaunchKernelGGL((k_gemm_mfma<EPI, 2, NB>), dim3((a.N + cols_per_wg - 1) / cols_per_wg, (a.M + 31) / 32),
-                       dim3(256), 0, s, a);
+    grid = dim3((a.N + cols_per_wg - 1) / cols_per_wg, (a.M + 31) / 32);
+    path = 2;
+  }
+  grid.z = gemm_splits(a, (int)(grid.x * grid.y), EPI == EPI_SWIGLU);
+  if (path == 0) hipLaunchKernelGGL((k_gemm_lds<EPI>), grid, dim3(256), 0, s, a);
+  else if (path == 1) hipLaunchKernelGGL((k_gemm_mfma<EPI, 1, NB>), grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL((k_gemm_mfma<EPI, 2, NB>), grid, dim3(256), 0, s, a);
+  if constexpr (EPI != EPI_SWIGLU) {
+    if (grid.z > 1) {
+      const size_t mn = (size_t)a.M * a.N;
+      hipLaunchKernelGGL((k_gemm_split_reduce<EPI>), dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, a,
+                         (int)grid.z);
+    }
   }
   return hipGetLastError();
 }
