@@ -13,6 +13,8 @@ Prints one JSON line.  Besides the contract fields it carries:
   frame_algorithmic_GBps         bytes one frame must move (weights + KV) / frame time
   roofline                       the dominant kernel, timed live with HIP events
   multistream                    BASELINE config 5 (16 streams together) on the same model
+  sampled                        BASELINE config 3 (sampling on both heads) on the same model
+  first_audio                    time from start_stream to the first audio chunk
   cpu_baseline                   the float32 CPU oracle on BASELINE config 1 (bounded sample)
 """
 from __future__ import annotations
@@ -230,6 +232,8 @@ def main() -> int:
     if with_codec:
         synth.write_codec(tmp, 0)
     spec = model.spec
+    w3 = WORKLOADS["cfg3_0.6b_sampled"]
+    inputs3 = w3.inputs(model) if (w3.spec, w3.weight_seed) == (w.spec, w.weight_seed) and args.frames == 0 else None
     host_prep = None
     if with_text:
         from q3t import textprep
@@ -329,6 +333,39 @@ def main() -> int:
                  "stream_window_frames": int(win.shape[0]), "stream_chunk_frames": w.chunk_frames,
                  "stream_window_ms": round(1000 * win_s, 3),
                  "stream_rtf": round(win_s / (w.chunk_frames * FRAME_SECONDS), 5)}
+    sampled = None
+    if inputs3 is not None:
+        # BASELINE config 3 on the same weights: top-k 50 / top-p 1.0 / T 0.9 / repetition
+        # penalty 1.05 on the Talker, sampling in every CodePredictor group (no token hand-off).
+        o3 = E.GenerateOptions(**w3.options_kwargs())
+
+        def one3():
+            with eng.start_stream(inputs3, o3) as st3:
+                n3 = 0
+                while (c3 := st3.next_codes_chunk(w3.chunk_frames)) is not None:
+                    n3 += c3.frames
+            return n3
+        one3()
+        eng.synchronize()
+        t0 = time.perf_counter()
+        n3 = one3()
+        eng.synchronize()
+        el3 = time.perf_counter() - t0
+        sampled = {"workload": w3.name, "frames": n3, "value": round(n3 / el3, 2), "unit": "frames/s",
+                   "rtf": round(el3 / (n3 * FRAME_SECONDS), 5)}
+    first_audio = None
+    if with_codec and eng.has_codec:
+        # start_stream (prefill + first token) through the first next_audio_chunk (chunk_frames
+        # frames, decoded), host-prepared prompt rows.
+        def first():
+            t0 = time.perf_counter()
+            with eng.start_stream(inputs, opts) as st:
+                c = st.next_audio_chunk(w.chunk_frames)
+            return time.perf_counter() - t0, c.frames
+        first()
+        ts = [first()[0] for _ in range(5)]
+        first_audio = {"chunk_frames": w.chunk_frames, "ms": round(1000 * min(ts), 3),
+                       "ms_median": round(1000 * sorted(ts)[2], 3)}
     eng.close()
     multi = None
     if args.multistream and w.spec == "0.6b" and w.weight_seed == 0:
@@ -365,6 +402,10 @@ def main() -> int:
         out["text_prep"] = text_prep
     if codec is not None:
         out["codec"] = codec
+    if sampled is not None:
+        out["sampled"] = sampled
+    if first_audio is not None:
+        out["first_audio"] = first_audio
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out))

@@ -1462,6 +1462,7 @@ struct SelectShared {
   float sv[kMaxVocab];
   int si[kMaxVocab];
   uint32_t hist[256];
+  uint32_t whist[16][256];  // per-wave histograms of a radix pass
   float wv[16];
   int wi[16];
   int misc[8];
@@ -1509,21 +1510,42 @@ __device__ int block_argmax(SelectShared &sh, int V) {
   return sh.misc[0];
 }
 
+// Inclusive prefix sums across a wave (lane order).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t o = (uint32_t)__shfl_up((int)v, d, 64);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float wave_incl_scan(float v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const float o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
 // Top-k / temperature / top-p sampling over the finite entries of lg[0..V).
 // k-th largest found by an 8-bit radix select on order keys; the candidates are ranked by
-// (value desc, index asc); inverse CDF over the kept prefix with target = u * sum(p).
+// (value desc, index asc); inverse CDF over the kept prefix with target = u * sum(p).  The
+// bin scans and the CDF are wave-parallel prefix sums.
 __device__ int block_sample(SelectShared &sh, int V, const SamplingParams &sp, float u) {
-  const int tid = threadIdx.x;
-  if (tid == 0) {
-    sh.misc[1] = 0;  // finite count
-    sh.misc[2] = 0;  // candidate count
-  }
-  __syncthreads();
+  const int tid = threadIdx.x, wave = tid >> 6;
+  if (tid == 0) sh.misc[2] = 0;  // candidate count
   int local = 0;
   for (int i = tid; i < V; i += 1024) local += isfinite(sh.lg[i]) ? 1 : 0;
-  if (local) atomicAdd(&sh.misc[1], local);
+  local = (int)wave_incl_scan((uint32_t)local);  // lane 63: the wave's count
+  if ((tid & 63) == 63) sh.wi[wave] = local;
   __syncthreads();
-  const int n_finite = sh.misc[1];
+  int n_finite = 0;
+#pragma unroll
+  for (int w = 0; w < 16; ++w) n_finite += sh.wi[w];
   if (n_finite == 0) return 0;
   const int k_eff = (sp.top_k > 0 && sp.top_k < n_finite) ? sp.top_k : n_finite;
 
@@ -1532,27 +1554,53 @@ __device__ int block_sample(SelectShared &sh, int V, const SamplingParams &sp, f
     uint32_t prefix = 0, mask = 0;
     int remaining = k_eff;
     for (int shift = 24; shift >= 0; shift -= 8) {
-      if (tid < 256) sh.hist[tid] = 0;
+      // each wave counts into its own histogram (keys of a pass share few digits, so one
+      // shared histogram serialises on its hot bins), then the 16 are added per bin
+#pragma unroll
+      for (int j = 0; j < 4; ++j) (&sh.whist[0][0])[tid + 1024 * j] = 0;
       __syncthreads();
       for (int i = tid; i < V; i += 1024) {
         const float v = sh.lg[i];
         if (!isfinite(v)) continue;
         const uint32_t key = order_key(v);
-        if ((key & mask) == prefix) atomicAdd(&sh.hist[(key >> shift) & 255u], 1u);
+        if ((key & mask) == prefix) atomicAdd(&sh.whist[wave][(key >> shift) & 255u], 1u);
       }
       __syncthreads();
-      if (tid == 0) {
-        int cum = 0, sel = 0;
-        for (int b = 255; b >= 0; --b) {
-          const int c = (int)sh.hist[b];
-          if (cum + c >= remaining) {
-            sel = b;
-            break;
-          }
-          cum += c;
+      if (tid < 256) {
+        uint32_t t = 0;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) t += sh.whist[w][tid];
+        sh.hist[tid] = t;
+      }
+      __syncthreads();
+      if (tid < 64) {
+        // bins from the top: lane l holds 255 - 4l - j, j = 0..3; the first bin where the count
+        // of keys in it and above reaches `remaining` is the k-th largest key's digit
+        const int lane = tid;
+        uint32_t c[4], tot = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          c[j] = sh.hist[255 - 4 * lane - j];
+          tot += c[j];
         }
-        sh.misc[3] = remaining - cum;
-        sh.umisc[0] = prefix | ((uint32_t)sel << shift);
+        uint32_t run = wave_incl_scan(tot) - tot;  // keys in the bins of earlier lanes
+        int found = -1;
+        uint32_t at = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (found < 0 && run + c[j] >= (uint32_t)remaining) {
+            found = j;
+            at = run;
+          }
+          run += c[j];
+        }
+        const uint64_t hit = __ballot(found >= 0);
+        const int first = hit ? __ffsll((unsigned long long)hit) - 1 : 63;
+        if (lane == first) {
+          const int sel = found >= 0 ? 255 - 4 * lane - found : 0;
+          sh.misc[3] = remaining - (int)(found >= 0 ? at : run);
+          sh.umisc[0] = prefix | ((uint32_t)sel << shift);
+        }
       }
       __syncthreads();
       remaining = sh.misc[3];
@@ -1587,34 +1635,37 @@ __device__ int block_sample(SelectShared &sh, int V, const SamplingParams &sp, f
     }
   }
   __syncthreads();
-  if (tid == 0) {
+  // cv[i] = sum of p over ranks 0..i, p = exp((v - vmax) / T): wave 0, 64 ranks per step
+  if (tid < 64) {
     const float vmax = sh.sv[0];
-    float sum = 0.f;
-    for (int i = 0; i < k_eff; ++i) {
-      const float p = expf((sh.sv[i] - vmax) / sp.temperature);
-      sum += p;
-      sh.cv[i] = sum;  // running prefix sums
+    float carry = 0.f;
+    for (int base = 0; base < k_eff; base += 64) {
+      const int i = base + tid;
+      const float p = i < k_eff ? expf((sh.sv[i] - vmax) / sp.temperature) : 0.f;
+      const float c = wave_incl_scan(p) + carry;
+      if (i < k_eff) sh.cv[i] = c;
+      carry = __shfl(c, 63, 64);
     }
-    int kept = k_eff;
-    if (sp.top_p < 1.0f) {
-      const float cut = sp.top_p * sum;
-      for (int i = 0; i < k_eff; ++i)
-        if (sh.cv[i] >= cut) {
-          kept = i + 1;
-          break;
-        }
+    if (tid == 0) {
+      sh.misc[4] = k_eff;  // kept = first rank reaching top_p * sum, plus one
+      sh.misc[5] = 0x7fffffff;
     }
-    const float target = u * sh.cv[kept - 1];
-    int pick = kept - 1;
-    for (int i = 0; i < kept; ++i)
-      if (target <= sh.cv[i]) {
-        pick = i;
-        break;
-      }
-    sh.misc[0] = sh.si[pick];
   }
   __syncthreads();
-  return sh.misc[0];
+  const float total = sh.cv[k_eff - 1];
+  if (sp.top_p < 1.0f) {
+    const float cut = sp.top_p * total;
+    for (int i = tid; i < k_eff; i += 1024)
+      if (sh.cv[i] >= cut) atomicMin(&sh.misc[4], i + 1);
+  }
+  __syncthreads();
+  const int kept = sh.misc[4];
+  const float target = u * sh.cv[kept - 1];
+  for (int i = tid; i < kept; i += 1024)
+    if (target <= sh.cv[i]) atomicMin(&sh.misc[5], i);
+  __syncthreads();
+  const int pick = sh.misc[5] == 0x7fffffff ? kept - 1 : sh.misc[5];
+  return sh.si[pick];
 }
 
 // Ends a frame (advance = 1) or checks the token drawn after the prefill (advance = 0):
