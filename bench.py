@@ -14,6 +14,7 @@ Prints one JSON line.  Besides the contract fields it carries:
   roofline                       the dominant kernel, timed live with HIP events
   multistream                    BASELINE config 5 (16 streams together) on the same model
   sampled                        BASELINE config 3 (sampling on both heads) on the same model
+  cfg4                           BASELINE config 4 (1.7B, 480 frames, KV 512), one generation
   first_audio                    time from start_stream to the first audio chunk
   cpu_baseline                   the float32 CPU oracle on BASELINE config 1 (bounded sample)
 """
@@ -160,6 +161,43 @@ def multistream(eng_cls, model_dir: str, name: str, steps: int, warmup: int, use
             "rtf_per_stream": round(el / steps * w.streams / (frames / steps) / FRAME_SECONDS, 5)}
 
 
+def big_model_line(E, synth, w, use_graph: bool) -> dict:
+    """the 1.7B-shaped model (Talker hidden 2048, the 2048 -> 1024
+    projection into the CodePredictor), greedy, 128-token prompt, 480 frames, KV 512; one
+    warmup generation, then one timed."""
+    import shutil
+    model = synth.SyntheticModel.build(w.spec, w.weight_seed)
+    inputs = w.inputs(model)
+    tmp = tempfile.mkdtemp(prefix="q3t_bench4_")
+    model.write(tmp)
+    spec = model.spec
+    del model
+    try:
+        eng = E.HipTtsEngine(tmp, E.EngineOptions(max_cache_steps=w.max_cache_steps, use_graph=use_graph))
+        opts = E.GenerateOptions(**w.options_kwargs())
+
+        def one():
+            with eng.start_stream(inputs, opts) as st:
+                n = 0
+                while (c := st.next_codes_chunk(w.chunk_frames)) is not None:
+                    n += c.frames
+            return n
+        one()
+        eng.synchronize()
+        t0 = time.perf_counter()
+        n = one()
+        eng.synchronize()
+        el = time.perf_counter() - t0
+        eng.close()
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    fb = frame_bytes(spec, inputs.prefill_steps + (n - 1) / 2.0, 4)
+    return {"workload": w.name, "frames": n, "value": round(n / el, 2), "unit": "frames/s",
+            "rtf": round(el / (n * FRAME_SECONDS), 5), "frame_ms": round(1000 * el / n, 4),
+            "frame_algorithmic_GBps": round(fb / (el / n) / 1e9, 1), "prefill_steps": inputs.prefill_steps,
+            "kv_capacity": w.max_cache_steps}
+
+
 def codec_decode_only(E, synth, frames: int, steps: int) -> int:
     """decode_codes of `frames` random frames, `steps` timed calls after one warmup (the codec
     decoder alone: profiling runs)."""
@@ -202,6 +240,7 @@ def main() -> int:
                     help="skip the codec-decoder timing (and the speech-tokenizer checkpoint it needs)")
     ap.add_argument("--no-text-prep", action="store_true",
                     help="skip the device prompt-preparation timing (and the text-embedding table it needs)")
+    ap.add_argument("--no-cfg4", action="store_true", help="skip the 1.7B (config 4) generation")
     ap.add_argument("--kernel-classes", action="store_true",
                     help="graph-time every kernel class of q3t_bench_kernel on the workload's model and exit")
     args = ap.parse_args()
@@ -367,6 +406,9 @@ def main() -> int:
         first_audio = {"chunk_frames": w.chunk_frames, "ms": round(1000 * min(ts), 3),
                        "ms_median": round(1000 * sorted(ts)[2], 3)}
     eng.close()
+    cfg4 = None
+    if not args.no_cfg4 and w.name == "cfg2_0.6b_greedy" and args.frames == 0:
+        cfg4 = big_model_line(E, synth, WORKLOADS["cfg4_1.7b_greedy"], not args.eager)
     multi = None
     if args.multistream and w.spec == "0.6b" and w.weight_seed == 0:
         multi = multistream(E.HipTtsEngine, tmp, args.multistream, max(1, min(args.steps, 2)), 1, not args.eager)
@@ -404,6 +446,8 @@ def main() -> int:
         out["codec"] = codec
     if sampled is not None:
         out["sampled"] = sampled
+    if cfg4 is not None:
+        out["cfg4"] = cfg4
     if first_audio is not None:
         out["first_audio"] = first_audio
     if not args.no_cpu_baseline:
