@@ -17,8 +17,8 @@ struct LaunchTiming {
 hipError_t launch_gemv(int epi, bool norm, bool streaming, const GemvArgs &a, hipStream_t stream,
                        const LaunchTiming *timing = nullptr);
 bool gemv_supports_k(int K);
-// Workgroups of a store (or bias) GEMV launch of N outputs over K: the number of order keys a
-// hand-off producer writes.
+// Workgroups of a store (or bias) GEMV launch of N outputs over K with cache-resident (not
+// streamed) weights: the number of order keys a hand-off producer writes.
 int gemv_grid_for(int N, int K);
 
 // Most stream rows one batched launch covers (skinny GEMM rows, select workgroups).

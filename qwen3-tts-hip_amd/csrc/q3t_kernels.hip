@@ -1879,30 +1879,39 @@ static void launch_timed(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_
     hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
 }
 
-// Weight loads in flight per lane are capped at kMaxLoads (4 VGPRs each).
+// Weight loads in flight per lane are capped at kMaxLoads (4 VGPRs each) for streamed
+// weights, and at kMaxLoadsCached for cache-resident ones.
 constexpr int kMaxLoads = 24;
+constexpr int kMaxLoadsCached = 4;
 
 // Rows per wave: spread the matrix over ~256 workgroups (one per CU, one wave per SIMD)
-// with every weight load of the launch issued up front; when that needs more than
-// kMaxLoads loads per lane, use more workgroups instead.  The result is one of 1, 2, 3, 4, 6
-// that fits kMaxLoads.
-static int gemv_rows_per_wave(int N, int KC, int epi) {
+// with every weight load of the launch issued up front; when that needs more than the load
+// cap per lane, use more workgroups instead.  The result is one of 1, 2, 3, 4, 6 that fits
+// the cap (or 1).
+// The cap depends on where the weights come from.  Streamed (non-temporal, read once per
+// frame from HBM) matrices keep up to 24 loads per lane.  The CodePredictor's matrices, reread
+// from the last-level cache 15 times per frame, do better with more workgroups and fewer
+// loads each: its gate/up GEMV at 3 workgroups per CU with 4 loads per lane instead of 1
+// with 12 took the 0.6B frame from 524 to 535 frames/s and the 1.7B frame from 435 to 448;
+// the same cap on the streamed Talker matrices cost the 1.7B frame 3%.
+static int gemv_rows_per_wave(int N, int KC, int epi, bool streaming) {
   const int pu = (epi == EPI_SWIGLU) ? 2 : 1;
+  const int cap = streaming ? kMaxLoads : kMaxLoadsCached;
   int rw = (N + 1023) / 1024;
-  const int cap_rw = kMaxLoads / (pu * KC);
+  const int cap_rw = cap / (pu * KC);
   if (rw > cap_rw) rw = std::max(1, cap_rw);
   if (rw == 5) rw = 6;
   if (rw > 6) rw = 6;
-  while (rw > 1 && rw * pu * KC > kMaxLoads) rw = rw == 6 ? 4 : rw - 1;
+  while (rw > 1 && rw * pu * KC > cap) rw = rw == 6 ? 4 : rw - 1;
   return rw;
 }
 
-static int gemv_grid(int N, int K, int epi) {
-  const int units = 4 * gemv_rows_per_wave(N, K / 512, epi);
+static int gemv_grid(int N, int K, int epi, bool streaming) {
+  const int units = 4 * gemv_rows_per_wave(N, K / 512, epi, streaming);
   return (N + units - 1) / units;
 }
 
-int gemv_grid_for(int N, int K) { return gemv_grid(N, K, EPI_STORE); }
+int gemv_grid_for(int N, int K) { return gemv_grid(N, K, EPI_STORE, false); }
 
 template <int EPI, bool NORM, int KC, int RW, bool NT>
 static void gemv_launch(const GemvArgs &a, hipStream_t s, const LaunchTiming *t) {
@@ -1934,7 +1943,7 @@ static void gemv_launch(const GemvArgs &a, hipStream_t s, const LaunchTiming *t)
 template <int EPI, bool NORM, int KC, bool NT>
 static hipError_t gemv_rw(const GemvArgs &a, hipStream_t s, const LaunchTiming *t) {
   constexpr int pu = (EPI == EPI_SWIGLU) ? 2 : 1;
-  switch (gemv_rows_per_wave(a.N, KC, EPI)) {
+  switch (gemv_rows_per_wave(a.N, KC, EPI, NT)) {
     case 6:
       if constexpr (6 * pu * KC <= kMaxLoads) { gemv_launch<EPI, NORM, KC, 6, NT>(a, s, t); break; }
       [[fallthrough]];
@@ -1989,7 +1998,7 @@ hipError_t launch_gemv(int epi, bool norm, bool streaming, const GemvArgs &a, hi
   if (!gemv_supports_k(a.K) || a.N <= 0) return hipErrorInvalidValue;
   if (a.keys_out) {
     const bool ok = !streaming && a.rows <= 1 && !a.attn_part && (a.K == 512 || a.K == 1024 || a.K == 2048) &&
-                    a.st && epi == EPI_STORE && norm && gemv_grid(a.N, a.K, epi) <= kHandoffKeys;
+                    a.st && epi == EPI_STORE && norm && gemv_grid(a.N, a.K, epi, false) <= kHandoffKeys;
     if (!ok) return hipErrorInvalidValue;
   }
   if (a.rows > 1 && (a.rows != 2 || streaming || a.attn_part || a.K > 6 * 512 || a.ldx_r % 4 ||
