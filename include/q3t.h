@@ -300,7 +300,9 @@ int q3t_engine_synchronize(q3t_engine *engine);
  *          4: Talker attention over a full cache  5: CodePredictor attention (positions 0..15)
  *          6: greedy CodePredictor selection     7: Talker attention at half the cache
  *          8: CodePredictor LM-head GEMV
- * Slot 0 must not hold a stream. */
+ *          9: CodePredictor attention with the O projection fused (when the model has it)
+ * Class 2 runs the CodePredictor's gate/up as frames do (summing the fused projection's
+ * per-head partials when the model has it). Slot 0 must not hold a stream. */
 int q3t_bench_kernel(q3t_engine *engine, int32_t kernel, int32_t iters, double *avg_us,
                      double *bytes_per_launch);
 

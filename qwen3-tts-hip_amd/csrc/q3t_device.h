@@ -103,6 +103,13 @@ struct GemvArgs {
   uint64_t *keys_out;
   float *trace;
   int64_t trace_frame;
+  // Input = x + parts[0] + parts[1] + ... + parts[n_parts - 1] (in that order), each part at
+  // parts + p * ld_parts, when parts is set (the fused attention + O projection's per-head
+  // shares; gate/up with RMSNorm only, K of 512 or 1024).  Workgroup 0 also stores that sum
+  // to x_store.
+  const float *parts;
+  int32_t n_parts, ld_parts;
+  float *x_store;
 };
 
 // Most workgroups a hand-off producer may have (keys per group).
@@ -138,6 +145,11 @@ struct AttnArgs {
   TokenHandoff h;
   const float *qkv_table;
   int64_t ld_table;
+  // Fused output projection (launch_attn_oproj): wo [wo_rows][q_heads*d] bf16; opart
+  // [kv_heads][wo_rows] receives each KV head's share of wo * attn.
+  const uint16_t *wo;
+  int32_t wo_rows;
+  float *opart;
 };
 
 // Merge of split-attention partials into attention outputs, one workgroup per stream row.

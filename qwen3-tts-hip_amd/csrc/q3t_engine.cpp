@@ -167,6 +167,9 @@ struct Slot {
   float *trailing;
   float *attn_part;      // attention partials [kv_heads][chunks][G][2 + head_dim]
   int attn_part_chunks = 0;
+  // The CodePredictor's fused attention + O projection: per-KV-head shares of the projection
+  // [kv_heads][hidden], and the residual row they sum to (stored by the gate/up GEMV).
+  float *opart = nullptr, *x_mid = nullptr;
   int32_t *codes;
   SlotState *st;
   SlotParams *prm;
@@ -199,7 +202,8 @@ struct Pools {
   char *t_k = nullptr, *t_v = nullptr, *c_k = nullptr, *c_v = nullptr;
   float *x_t = nullptr, *t_in = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits_t = nullptr,
         *logits_c = nullptr, *x_c = nullptr, *cp_prefix = nullptr, *cp_in = nullptr, *cur = nullptr,
-        *emb_sum = nullptr, *trailing = nullptr, *attn_part = nullptr, *trace_t = nullptr, *trace_c = nullptr;
+        *emb_sum = nullptr, *trailing = nullptr, *attn_part = nullptr, *trace_t = nullptr, *trace_c = nullptr,
+        *opart = nullptr, *x_mid = nullptr;
   int32_t *codes = nullptr;
   uint64_t *cp_keys = nullptr;                          // [n][groups - 1][kHandoffKeys]
   SlotState *st = nullptr;
@@ -280,6 +284,15 @@ struct Engine {
     hip_check(launch_gemv(epi, norm, nt, a, s, timing), "launch_gemv");
   }
 
+  // The CodePredictor's attention fits one 32-row chunk, so its O projection can be fused
+  // into the attention kernel (launch_attn_oproj) with the residual summed by the gate/up
+  // GEMV: one launch fewer per layer.
+  bool oproj_ok(const StackW &w) const {
+    const Dims &d = w.d;
+    return &w == &cp && w.cap <= 32 && attn_chunk_len(w.cap) == 32 && d.kv_heads <= 8 &&
+           (d.hidden == 512 || d.hidden == 1024);
+  }
+
   // One decoder-stack step for one position (decode.rs:951-1001 / 1300-1475).
   // handoff: layer 0 takes its raw q/k/v row from qkv_table (row = the handed-off token) in its
   // attention kernel and runs no QKV GEMV; `in` is then the row that kernel stores
@@ -289,6 +302,7 @@ struct Engine {
                   const float *qkv_table = nullptr) {
     const Dims &d = w.d;
     const bool nt = &w == &talker;
+    const bool fuse_o = oproj_ok(w);
     const size_t cache_layer = (size_t)d.kv_heads * w.cap * d.head_dim * (kv_bf16 ? 2 : 4);
     for (int l = 0; l < d.layers; ++l) {
       const LayerW &L = w.layers[l];
@@ -297,6 +311,31 @@ struct Engine {
       if (!table)
         gemv(EPI_STORE, true, L.qkv, src, L.g_in, d.eps, nullptr, nullptr, sl.qkv, d.qkv_rows(), d.hidden, skip,
              sl.st, s, nt);
+      if (fuse_o) {
+        // Attention and the O projection in one kernel (K split by KV head), the residual
+        // sum in the gate/up GEMV, which also stores it (x_mid) for the down GEMV.
+        AttnArgs aa{sl.qkv,   L.gq,      L.gk,       w.rope,  kc + l * cache_layer, vc + l * cache_layer,
+                    nullptr,  d.q_heads, d.kv_heads, w.cap,   d.eps, 1.0f / std::sqrt((float)d.head_dim),
+                    pos_mode, pos_const, skip,       kv_bf16, sl.st, nullptr, 0, 32, 0};
+        if (table) {
+          aa.h = *handoff;
+          aa.qkv_table = qkv_table;
+          aa.ld_table = d.qkv_rows();
+        }
+        aa.wo = L.o;
+        aa.wo_rows = d.hidden;
+        aa.opart = sl.opart;
+        hip_check(launch_attn_oproj(aa, d.head_dim, s), "launch_attn_oproj");
+        GemvArgs gu{L.gu, src, L.g_post, nullptr, nullptr, sl.act, d.intermediate, d.hidden, d.eps, skip, sl.st};
+        gu.parts = sl.opart;
+        gu.n_parts = d.kv_heads;
+        gu.ld_parts = d.hidden;
+        gu.x_store = sl.x_mid;
+        hip_check(launch_gemv(EPI_SWIGLU, true, false, gu, s), "launch_gemv(gate/up, partial sum)");
+        gemv(EPI_RESIDUAL, false, L.down, sl.act, nullptr, 0.f, sl.x_mid, nullptr, x, d.hidden, d.intermediate, skip,
+             sl.st, s, nt);
+        continue;
+      }
       // The Talker's attention spans many chunks: partials, merged by the O projection.  The
       // CodePredictor's 16-row cache is one chunk: direct output.
       const int partial = attn_chunks(w.cap) > 1 ? 1 : 0;
@@ -769,6 +808,8 @@ void alloc_pools(Engine &e, int n) {
   p.emb_sum = fz(Ht);
   p.trailing = fz(p.trailing_row);
   p.attn_part = fz(p.part_row);
+  p.opart = fz((size_t)cd.kv_heads * Hc);
+  p.x_mid = fz(Hc);
   p.codes = (int32_t *)zeroed((size_t)p.codes_row * n * 4);
   p.cp_keys = (uint64_t *)zeroed((size_t)n * (e.groups - 1) * kHandoffKeys * 8);
   p.st = (SlotState *)zeroed(sizeof(SlotState) * n);
@@ -806,6 +847,8 @@ void alloc_pools(Engine &e, int n) {
     sl.trailing = p.trailing + (size_t)i * p.trailing_row;
     sl.attn_part = p.attn_part + (size_t)i * p.part_row;
     sl.attn_part_chunks = p.part_chunks;
+    sl.opart = p.opart + (size_t)i * cd.kv_heads * Hc;
+    sl.x_mid = p.x_mid + (size_t)i * Hc;
     sl.codes = p.codes + (size_t)i * p.codes_row;
     sl.cp_keys = p.cp_keys + (size_t)i * (e.groups - 1) * kHandoffKeys;
     sl.st = p.st + i;
@@ -827,7 +870,7 @@ void free_pools(Engine &e) {
   void *ptrs[] = {p.t_k,      p.t_v,     p.c_k,   p.c_v,      p.x_t,      p.t_in,    p.qkv,  p.attn,
                   p.act,      p.logits_t, p.logits_c, p.x_c,  p.cp_prefix, p.cp_in,  p.cur,  p.emb_sum,
                   p.trailing, p.attn_part, p.trace_t, p.trace_c, p.codes,  p.st,      p.prm,  p.row_on,
-                  p.px,       p.pqkv,    p.pattn, p.pact,     p.pinv,    p.cp_keys};
+                  p.px,       p.pqkv,    p.pattn, p.pact,     p.pinv,    p.cp_keys, p.opart, p.x_mid};
   for (void *q : ptrs)
     if (q) (void)hipFree(q);
   if (p.h_states) (void)hipHostFree(p.h_states);
@@ -2087,7 +2130,8 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
     using namespace q3t;
     if (!e || !avg_us || !bytes) fail(Q3T_ERR_INVALID, "null argument");
     if (iters <= 0 || iters > 8192) fail(Q3T_ERR_INVALID, "iters must be in 1..8192");
-    if (kernel < 0 || kernel > 8) fail(Q3T_ERR_INVALID, "unknown kernel class %d", kernel);
+    if (kernel < 0 || kernel > 9) fail(Q3T_ERR_INVALID, "unknown kernel class %d", kernel);
+    if (kernel == 9 && !e->oproj_ok(e->cp)) fail(Q3T_ERR_INVALID, "the model's CodePredictor has no fused O projection");
     Slot &s = e->slots[0];
     if (s.in_use) fail(Q3T_ERR_BUSY, "stream slot 0 is in use");
     HIPC(hipSetDevice(e->device));
@@ -2103,7 +2147,7 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
       for (int l = 0; l < td.layers; ++l) seq.push_back({&e->talker, l});
       for (int g = 0; g < e->groups - 1; ++g)
         for (int l = 0; l < cd.layers; ++l) seq.push_back({&e->cp, l});
-    } else if (kernel == 5) {  // CodePredictor attention: positions 0..groups-1, each over 5 layers
+    } else if (kernel == 5 || kernel == 9) {  // CodePredictor attention: positions 0..groups-1, each over 5 layers
       for (int p = 0; p < e->groups; ++p)
         for (int l = 0; l < cd.layers; ++l) seq.push_back({&e->cp, l});
     } else if (kernel == 6 || kernel == 8) {  // one per CodePredictor group
@@ -2150,11 +2194,20 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
           b = 2.0 * d.hidden * d.q_out() + 4.0 * (d.q_out() + 2 * d.hidden);
           break;
         }
-        case 2:  // gate/up projection with the post-attention RMSNorm prologue and SwiGLU
-          e->gemv(EPI_SWIGLU, true, W.gu, xin, W.g_post, d.eps, nullptr, nullptr, s.act, d.intermediate, d.hidden,
-                  SKIP_NEVER, s.st, s.stream, nt);
+        case 2: {  // gate/up projection with the post-attention RMSNorm prologue and SwiGLU; the
+                   // CodePredictor's (fused O projection) also sums the per-head partials into x
+          GemvArgs gu{W.gu, xin, W.g_post, nullptr, nullptr, s.act, d.intermediate, d.hidden, d.eps, SKIP_NEVER, s.st};
           b = 2.0 * 2 * d.intermediate * d.hidden + 4.0 * (2 * d.hidden + d.intermediate);
+          if (e->oproj_ok(*l.w)) {
+            gu.parts = s.opart;
+            gu.n_parts = d.kv_heads;
+            gu.ld_parts = d.hidden;
+            gu.x_store = s.x_mid;
+            b += 4.0 * (d.kv_heads + 1) * d.hidden;
+          }
+          hip_check(launch_gemv(EPI_SWIGLU, true, nt, gu, s.stream), "launch_gemv");
           break;
+        }
         case 3:  // down projection + residual
           e->gemv(EPI_RESIDUAL, false, W.down, s.act, nullptr, 0.f, s.attn, nullptr, s.attn, d.hidden,
                   d.intermediate, SKIP_NEVER, s.st, s.stream, nt);
@@ -2201,6 +2254,21 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
                       attn_chunk_len(l.w->cap), attn_chunks(l.w->cap) > 1 ? 1 : 0};
           hip_check(launch_attn_decode(aa, d.head_dim, s.stream), "launch_attn_decode");
           b = 2.0 * esz * d.kv_heads * d.head_dim * (l.w->cap / 2 + 1) + 4.0 * (d.qkv_rows() + d.q_out());
+          break;
+        }
+        case 9: {  // CodePredictor attention with the O projection fused (per-head partials)
+          const size_t esz = e->kv_bf16 ? 2 : 4;
+          const size_t layer_bytes = (size_t)d.kv_heads * l.w->cap * d.head_dim * esz;
+          const int pos = (i / d.layers) % e->groups;
+          AttnArgs aa{s.qkv, W.gq, W.gk, l.w->rope, s.c_k + layer_bytes * l.layer, s.c_v + layer_bytes * l.layer,
+                      nullptr, d.q_heads, d.kv_heads, l.w->cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
+                      POS_CONST, pos, SKIP_NEVER, e->kv_bf16, s.st, nullptr, 0, 32, 0};
+          aa.wo = W.o;
+          aa.wo_rows = d.hidden;
+          aa.opart = s.opart;
+          hip_check(launch_attn_oproj(aa, d.head_dim, s.stream), "launch_attn_oproj");
+          b = 2.0 * esz * d.kv_heads * d.head_dim * (pos + 1) + 4.0 * d.qkv_rows() + 2.0 * d.hidden * d.q_out() +
+              4.0 * d.kv_heads * d.hidden;
           break;
         }
         case 8: {  // CodePredictor LM head (final norm prologue)

@@ -193,21 +193,45 @@ __device__ __forceinline__ void merge_finish(const GemvArgs &a, int base, const 
 
 __device__ void merge_attention(const GemvArgs &a, float *xs);
 
-// ATTN = the input vector is the merge of attention partials (see merge_attention).
+// Most per-head partials a GEMV input sums (GemvArgs::parts): the KV heads of a layer.
+constexpr int kMaxParts = 8;
+
+// The input vector of k_gemv: IN_X = x; IN_ATTN = the merge of attention partials (see
+// merge_attention); IN_PARTS = x plus the per-head partials of the fused attention + O
+// projection (GemvArgs::parts), summed through LDS.
+constexpr int IN_X = 0, IN_ATTN = 1, IN_PARTS = 2;
+
 // MR = input rows (1, or 2: row 1 at x + ldx_r, res + ldr_r, out + ldo_r) against the same
 // weight loads.
 // HO = greedy token hand-off producer (GemvArgs::keys_out).
-template <int EPI, bool NORM, int KC, int RW, bool NT, bool ATTN = false, int MR = 1, bool HO = false>
+template <int EPI, bool NORM, int KC, int RW, bool NT, int IN = IN_X, int MR = 1, bool HO = false>
 __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
+  constexpr bool ATTN = IN == IN_ATTN;
+  constexpr bool PARTS = IN == IN_PARTS;
   static_assert(!ATTN || MR == 1, "the attention merge feeds one row");
-  static_assert(!HO || (MR == 1 && !ATTN && EPI == EPI_STORE), "the hand-off producer stores one row");
+  static_assert(!PARTS || (MR == 1 && (KC == 1 || KC == 2)), "the partial sum feeds one row of K <= 1024");
+  static_assert(!HO || (MR == 1 && IN == IN_X && EPI == EPI_STORE), "the hand-off producer stores one row");
   constexpr int K = KC * 512;
   constexpr int NR = (EPI == EPI_SWIGLU) ? 2 * RW : RW;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int unit0 = (blockIdx.x * 4 + wave) * RW;
-  __shared__ float xs[ATTN ? K : 1];
+  __shared__ float xs[(ATTN || PARTS) ? K : 1];
   __shared__ uint64_t wkeys[HO ? 4 : 1];
+  // IN_PARTS: thread t sums elements 4t .. 4t+3 of x and of every part (K <= 1024).
+  constexpr int PJ = 1;
+  float4 px_[PJ], pp_[PARTS ? kMaxParts : 1][PJ];
+  if constexpr (PARTS) {
+#pragma unroll
+    for (int j = 0; j < PJ; ++j) {
+      const int i = 4 * (int)threadIdx.x + 1024 * j;
+      if (i >= K) break;  // K = 512: threads 128 .. 255 (whole waves) have nothing to sum
+      px_[j] = *reinterpret_cast<const float4 *>(a.x + i);
+#pragma unroll
+      for (int p = 0; p < kMaxParts; ++p)
+        pp_[p][j] = *reinterpret_cast<const float4 *>(a.parts + (size_t)min(p, a.n_parts - 1) * a.ld_parts + i);
+    }
+  }
 
   // Load order: activations (and the norm gain), then every weight row of this wave, then
   // nothing else until the arithmetic.  The norm then only waits for the small activation
@@ -223,7 +247,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   }
 #pragma unroll
   for (int c = 0; c < KC; ++c) {
-    if constexpr (ATTN) break;
+    if constexpr (ATTN || PARTS) break;
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       const float4 *px = reinterpret_cast<const float4 *>(a.x + m * a.ldx_r + c * 512 + lane * 8);
@@ -231,7 +255,10 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
       xv[m][c][0] = p0.x; xv[m][c][1] = p0.y; xv[m][c][2] = p0.z; xv[m][c][3] = p0.w;
       xv[m][c][4] = p1.x; xv[m][c][5] = p1.y; xv[m][c][6] = p1.z; xv[m][c][7] = p1.w;
     }
-    if constexpr (NORM) {
+  }
+  if constexpr (NORM) {
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
       const float4 *pg = reinterpret_cast<const float4 *>(a.gamma + c * 512 + lane * 8);
       const float4 g0 = pg[0], g1 = pg[1];
       gv[c][0] = g0.x; gv[c][1] = g0.y; gv[c][2] = g0.z; gv[c][3] = g0.w;
@@ -266,6 +293,29 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   // state), so its round trip overlaps theirs instead of preceding them.  Nothing is stored
   // before it.
   if (skip_work(a.st, a.skip)) return;
+  if constexpr (PARTS) {
+#pragma unroll
+    for (int j = 0; j < PJ; ++j) {
+      const int i = 4 * (int)threadIdx.x + 1024 * j;
+      if (i >= K) break;
+      float4 v = px_[j];
+#pragma unroll
+      for (int p = 0; p < kMaxParts; ++p)
+        if (p < a.n_parts) {
+          v.x += pp_[p][j].x;
+          v.y += pp_[p][j].y;
+          v.z += pp_[p][j].z;
+          v.w += pp_[p][j].w;
+        }
+      *reinterpret_cast<float4 *>(xs + i) = v;
+      if (a.x_store && blockIdx.x == 0) *reinterpret_cast<float4 *>(a.x_store + i) = v;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xv[0][c][j] = xs[c * 512 + lane * 8 + j];
+  }
   if constexpr (ATTN_EARLY) {
     if (threadIdx.x * 8 < K) merge_finish(a, threadIdx.x * 8, mregs, xs);
     __syncthreads();
@@ -362,6 +412,7 @@ struct KvIo<float> {
     *p = x;
     return x;
   }
+  __device__ static float round(float x) { return x; }
 
   __device__ static void load8(const float *p, float *o) {
     const float4 a = reinterpret_cast<const float4 *>(p)[0];
@@ -379,6 +430,7 @@ struct KvIo<uint16_t> {
     *p = b;
     return bf16_to_f32(b);
   }
+  __device__ static float round(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
   __device__ static void load8(const uint16_t *p, float *o) {
     const uint4 w = *reinterpret_cast<const uint4 *>(p);
@@ -449,11 +501,20 @@ __device__ __forceinline__ void handoff_store(const TokenHandoff &h, int row, in
 
 // HO = greedy token hand-off (AttnArgs::h): the q/k/v row comes from a table indexed by the
 // token the previous group's LM head chose; workgroup (0, 0) also does the hand-off's stores.
-template <int D, int G, typename KVT, int CH, bool HO = false>
+// OPROJ = the output projection fused in, its K dimension split by KV head (one chunk, one
+// stream): grid (kv_heads, wo_rows / kOprojRows).  Workgroup (h, b) computes KV head h's
+// attention (every b alike), then opart[h][r] = sum over head h's G * D columns of
+// wo[r][.] * attn for its kOprojRows rows r.  The consumer adds the kv_heads partials to the
+// residual in head order (k_gemv with GemvArgs::parts).  Only b = 0 stores the K/V row at
+// `pos` (and, with HO, the hand-off's rows); the others round it as the store would.
+constexpr int kOprojRows = 32;
+
+template <int D, int G, typename KVT, int CH, bool HO = false, bool OPROJ = false>
 __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   static_assert(D == 128, "lane layout assumes head_dim 128");
   static_assert(G >= 1 && G <= 2, "query heads per KV head");
   static_assert(CH % 16 == 0 && CH <= kAttnMaxChunk, "chunk length");
+  static_assert(!OPROJ || CH == 32, "the fused projection covers one 32-row chunk");
   const int row = blockIdx.z;
   const SlotState *st = a.st + row;
   // A position given by the launch needs no state: the row mask and the stream state are
@@ -464,7 +525,8 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
     if (skip_work(st, a.skip)) return;
   }
   const int h = blockIdx.x;
-  const int c = blockIdx.y;
+  const int c = OPROJ ? 0 : blockIdx.y;
+  const int rb = OPROJ ? blockIdx.y : 0;  // output row block of the fused projection
   const int pos = frame_pos ? st->prefill_steps + st->frame : a.pos_const;
   if (pos < 0 || pos >= a.cap) return;  // host validates; never index outside the cache
   const int L = pos + 1;
@@ -491,6 +553,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   __shared__ float sc[G][CH];
   __shared__ float red[4][G][D];
   __shared__ float stat[G][2];
+  __shared__ float ao[OPROJ ? G * D : 1];
 
   // Loads first: this wave's head vector, then every cached K and V row the workgroup needs
   // (addresses clamped into the cache instead of branching), so the kernel waits on one
@@ -532,6 +595,20 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
     const int t = min(t0 + wave + 4 * i, tmax);
     vpre[i] = KvIo<KVT>::load2(vbase + (size_t)t * D + 2 * lane);
   }
+  // The fused projection's weights: wave w takes rows rb * kOprojRows + w * kOprojRows / 4 ..;
+  // a row's G * D bf16 of head h are LPR lanes x 8, so one 16-byte load per lane covers RPL
+  // rows.
+  constexpr int LPR = G * D / 8;
+  constexpr int RPL = 64 / LPR;
+  constexpr int NWO = OPROJ ? kOprojRows / 4 / RPL : 1;
+  uint4 wo[NWO];
+  if constexpr (OPROJ) {
+#pragma unroll
+    for (int i = 0; i < NWO; ++i) {
+      const int r = rb * kOprojRows + wave * (kOprojRows / 4) + i * RPL + lane / LPR;
+      wo[i] = *reinterpret_cast<const uint4 *>(a.wo + (size_t)r * q_out + h * G * D + (lane % LPR) * 8);
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
   if (!frame_pos) {  // workgroup-uniform: no barrier has been reached yet
     if (a.row_on && !a.row_on[row]) return;
@@ -548,7 +625,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
       x0 = src[lane];
       x1 = src[lane + 64];
     }
-    if (h == 0 && c == 0) handoff_load(a.h, row, tok, side_e, side_s, side_c);
+    if (h == 0 && c == 0 && rb == 0) handoff_load(a.h, row, tok, side_e, side_s, side_c);
   }
 
   // 1: q heads (waves 0..G-1); k and v (waves G, G+1) only where row `pos` is stored.
@@ -570,8 +647,13 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
       KVT *cache = (vec == G) ? kcache : vcache;
       float *keep = (vec == G) ? ks : vs;
       const size_t row = ((size_t)h * a.cap + pos) * D;
-      keep[lane] = KvIo<KVT>::store(cache + row + lane, x0);
-      keep[lane + 64] = KvIo<KVT>::store(cache + row + lane + 64, x1);
+      if (rb == 0) {
+        keep[lane] = KvIo<KVT>::store(cache + row + lane, x0);
+        keep[lane + 64] = KvIo<KVT>::store(cache + row + lane + 64, x1);
+      } else {
+        keep[lane] = KvIo<KVT>::round(x0);
+        keep[lane + 64] = KvIo<KVT>::round(x1);
+      }
     }
   }
   __syncthreads();
@@ -639,7 +721,26 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   __syncthreads();
 
   if constexpr (HO) {
-    if (h == 0 && c == 0) handoff_store(a.h, row, tok, st, side_e, side_s, side_c);
+    if (h == 0 && c == 0 && rb == 0) handoff_store(a.h, row, tok, st, side_e, side_s, side_c);
+  }
+
+  if constexpr (OPROJ) {
+    // 3': this head's attention output to LDS, then its slice of the projection.
+    const int o = threadIdx.x;
+    if (o < G * D) {
+      const int g_o = o / D, d_o = o % D;
+      const float v_o = ((red[0][g_o][d_o] + red[1][g_o][d_o]) + red[2][g_o][d_o]) + red[3][g_o][d_o];
+      ao[o] = v_o / stat[g_o][1];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NWO; ++i) {
+      const int r = rb * kOprojRows + wave * (kOprojRows / 4) + i * RPL + lane / LPR;
+      float sum = row16_sum(dot8(wo[i], ao + (lane % LPR) * 8));
+      if constexpr (LPR == 32) sum += __shfl_xor(sum, 16);
+      if (lane % LPR == 0) a.opart[(size_t)h * a.wo_rows + r] = sum;
+    }
+    return;
   }
 
   // 3: final output (single chunk) or this chunk's partial.
@@ -1921,23 +2022,30 @@ static void gemv_launch(const GemvArgs &a, hipStream_t s, const LaunchTiming *t)
   if constexpr (!NT && KC <= 4 && KC != 3 && EPI == EPI_STORE && NORM) {
     if (a.keys_out) {
       if (grid.x > (unsigned)kHandoffKeys) return;  // launch_gemv checked the grid
-      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, false, 1, true>, grid, dim3(256), 0, s, t, a);
+      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_X, 1, true>, grid, dim3(256), 0, s, t, a);
       return;
     }
   }
   if constexpr (EPI == EPI_RESIDUAL && !NORM && KC <= 8) {
     if (a.attn_part) {
-      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, true>, grid, dim3(256), 0, s, t, a);
+      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_ATTN>, grid, dim3(256), 0, s, t, a);
+      return;
+    }
+  }
+  // The per-head partials of the fused attention + O projection: the CodePredictor's gate/up.
+  if constexpr (EPI == EPI_SWIGLU && NORM && !NT && (KC == 1 || KC == 2)) {
+    if (a.parts) {
+      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_PARTS>, grid, dim3(256), 0, s, t, a);
       return;
     }
   }
   if constexpr (!NT && KC <= 6) {  // two input rows: the CodePredictor's prefix pass
     if (a.rows == 2) {
-      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, false, 2>, grid, dim3(256), 0, s, t, a);
+      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_X, 2>, grid, dim3(256), 0, s, t, a);
       return;
     }
   }
-  launch_timed(k_gemv<EPI, NORM, KC, RW, NT, false>, grid, dim3(256), 0, s, t, a);
+  launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_X>, grid, dim3(256), 0, s, t, a);
 }
 
 template <int EPI, bool NORM, int KC, bool NT>
@@ -2003,6 +2111,10 @@ hipError_t launch_gemv(int epi, bool norm, bool streaming, const GemvArgs &a, hi
   }
   if (a.rows > 1 && (a.rows != 2 || streaming || a.attn_part || a.K > 6 * 512 || a.ldx_r % 4 ||
                      (epi == EPI_RESIDUAL && !a.ldr_r) || !a.ldo_r))
+    return hipErrorInvalidValue;
+  if (a.parts && (epi != EPI_SWIGLU || !norm || streaming || a.rows > 1 || a.attn_part || a.keys_out ||
+                  (a.K != 512 && a.K != 1024) || a.n_parts < 1 || a.n_parts > kMaxParts ||
+                  a.ld_parts < a.K || a.ld_parts % 4 || !a.x))
     return hipErrorInvalidValue;
   return streaming ? gemv_epi<true>(epi, norm, a, s, t) : gemv_epi<false>(epi, norm, a, s, t);
 }
@@ -2070,6 +2182,38 @@ hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t s, co
   }
 #undef Q3T_ATTN_CASE
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_attn_oproj(const AttnArgs &a, int head_dim, hipStream_t s, const LaunchTiming *t) {
+  if (head_dim != 128 || a.kv_heads <= 0 || a.q_heads % a.kv_heads || a.kv_heads > kMaxParts) return hipErrorInvalidValue;
+  const int G = a.q_heads / a.kv_heads;
+  if (G < 1 || G > 2 || a.cap < 1 || a.cap > 32 || a.chunk != 32 || a.partial_out || a.row_on ||
+      a.pos_mode != POS_CONST || !a.wo || !a.opart || a.wo_rows <= 0 || a.wo_rows % kOprojRows || !a.st)
+    return hipErrorInvalidValue;
+  const dim3 grid(a.kv_heads, a.wo_rows / kOprojRows, 1), block(256);
+  if (a.h.keys) {
+    const int qkv_rows = (a.q_heads + 2 * a.kv_heads) * head_dim;
+    const TokenHandoff &h = a.h;
+    if (!a.qkv_table || a.ld_table < qkv_rows || !handoff_ok(h) || h.emb_width > 2048 || h.emb_width % 4 ||
+        (h.cur_table && h.cur_width > 2048))
+      return hipErrorInvalidValue;
+    if (a.kv_bf16) {
+      if (G == 1) launch_timed(k_attn_split<128, 1, uint16_t, 32, true, true>, grid, block, 0, s, t, a);
+      else launch_timed(k_attn_split<128, 2, uint16_t, 32, true, true>, grid, block, 0, s, t, a);
+    } else {
+      if (G == 1) launch_timed(k_attn_split<128, 1, float, 32, true, true>, grid, block, 0, s, t, a);
+      else launch_timed(k_attn_split<128, 2, float, 32, true, true>, grid, block, 0, s, t, a);
+    }
+    return hipGetLastError();
+  }
+  if (a.kv_bf16) {
+    if (G == 1) launch_timed(k_attn_split<128, 1, uint16_t, 32, false, true>, grid, block, 0, s, t, a);
+    else launch_timed(k_attn_split<128, 2, uint16_t, 32, false, true>, grid, block, 0, s, t, a);
+  } else {
+    if (G == 1) launch_timed(k_attn_split<128, 1, float, 32, false, true>, grid, block, 0, s, t, a);
+    else launch_timed(k_attn_split<128, 2, float, 32, false, true>, grid, block, 0, s, t, a);
+  }
+  return hipGetLastError();
 }
 
 // Sum of the K splits in split order, then the epilogue: Y[m][n] = f(sum_z ws[z][m][n]).

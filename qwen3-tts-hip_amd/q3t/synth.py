@@ -137,6 +137,12 @@ SPECS: Dict[str, ModelSpec] = {
                            StackShape(1024, 1536, 2, 8, 4, 128, 3072),
                            StackShape(512, 1024, 2, 4, 2, 128, 2048),
                            text_proj_intermediate=512),
+    # One query head per KV head in both stacks, and a 512 -> 1024 projection into the
+    # CodePredictor (the real models have two query heads per KV head).
+    "tiny-g1": ModelSpec("tiny-g1",
+                         StackShape(512, 1024, 2, 4, 4, 128, 3072),
+                         StackShape(1024, 1024, 2, 8, 8, 128, 2048),
+                         text_proj_intermediate=512),
 }
 
 

@@ -92,3 +92,20 @@ def test_hooks_need_a_free_slot(models):
         st.close()
         with pytest.raises(E.CapacityError):
             eng.debug_talker_step(np.zeros(512, np.float32), w.max_cache_steps)
+
+
+def test_kernel_timing_hook_covers_every_class(models):
+    """q3t_bench_kernel (the roofline report's timer) runs every kernel class of the 0.6B model
+    as a captured graph and reports a positive time and the algorithmic bytes of one launch."""
+    w = WORKLOADS["cfg2_0.6b_greedy"]
+    _, d = models.get(w.spec, w.weight_seed)
+    with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=w.max_cache_steps)) as eng:
+        for k, name in E.HipTtsEngine.KERNELS.items():
+            us, b = eng.bench_kernel(k, 64)
+            print(f"  class {k} {name}: {us:.3f} us, {b:.0f} B")
+            assert 0.0 < us < 1000.0 and b > 0.0, name
+        # class 2 sums the fused projection's 8 per-head partials in its 75 CodePredictor launches
+        _, b2 = eng.bench_kernel(2, 103)
+        assert b2 > 2 * 2 * 3072 * 1024
+        with pytest.raises(E.Q3tError):
+            eng.bench_kernel(10, 8)

@@ -153,6 +153,24 @@ def test_sampled_talker_with_greedy_subtalker_matches_oracle(models):
     print(f"sampled Talker + greedy CodePredictor: {same} frames identical")
 
 
+@pytest.mark.parametrize("sampled", [False, True])
+def test_one_query_head_per_kv_head_matches_oracle(models, sampled):
+    """A model with one query head per KV head in both stacks and a 512 -> 1024 projection into
+    the CodePredictor: its fused attention + O projection with 1 query head per KV head, after a
+    token hand-off (greedy) and after a sampled group."""
+    from q3t import textprep
+    model, d = models.get("tiny-g1")
+    inputs = textprep.TextPrep(model).prepare(np.random.default_rng(5).integers(0, 151643, 20))
+    kw = dict(subtalker_dosample=True, subtalker_top_k=50, subtalker_top_p=0.9, subtalker_temperature=0.9,
+              seed=3) if sampled else {}
+    opts = E.GenerateOptions.greedy(12, **kw)
+    r = run(models, "tiny_greedy", options=opts, inputs=inputs, model_dir=d, cap=64)
+    fx = _as_fixture(_oracle_rollout(model, inputs, opts, 64))
+    same = check_codes(r["codes"], r["eos"], fx, allow_ties=not sampled)
+    err = check_talker_logits(r["talker_logits"], fx, same)
+    print(f"tiny-g1 sampled={sampled}: {same} frames identical, talker logit err {err:.2e}")
+
+
 def test_bf16_kv_cache_matches_bf16_oracle(models):
     """KV stored as bf16 (rounded once at the store), against the oracle's bf16-KV model."""
     w = WORKLOADS["tiny_greedy"]
