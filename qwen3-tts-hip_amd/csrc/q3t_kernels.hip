@@ -201,13 +201,19 @@ constexpr int kMaxParts = 8;
 // projection (GemvArgs::parts), summed through LDS.
 constexpr int IN_X = 0, IN_ATTN = 1, IN_PARTS = 2;
 
+// Waves per workgroup of the IN_PARTS form: every workgroup sums the partials into LDS, so
+// it runs the launch's waves in fewer, larger workgroups (the partials are read from L2 once
+// per workgroup).
+constexpr int kPartsWaves = 12;
+
 // MR = input rows (1, or 2: row 1 at x + ldx_r, res + ldr_r, out + ldo_r) against the same
 // weight loads.
 // HO = greedy token hand-off producer (GemvArgs::keys_out).
 template <int EPI, bool NORM, int KC, int RW, bool NT, int IN = IN_X, int MR = 1, bool HO = false>
-__global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
+__global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gemv(GemvArgs a) {
   constexpr bool ATTN = IN == IN_ATTN;
   constexpr bool PARTS = IN == IN_PARTS;
+  constexpr int WPB = PARTS ? kPartsWaves : 4;
   static_assert(!ATTN || MR == 1, "the attention merge feeds one row");
   static_assert(!PARTS || (MR == 1 && (KC == 1 || KC == 2)), "the partial sum feeds one row of K <= 1024");
   static_assert(!HO || (MR == 1 && IN == IN_X && EPI == EPI_STORE), "the hand-off producer stores one row");
@@ -215,7 +221,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
   constexpr int NR = (EPI == EPI_SWIGLU) ? 2 * RW : RW;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int unit0 = (blockIdx.x * 4 + wave) * RW;
+  const int unit0 = (blockIdx.x * WPB + wave) * RW;
   __shared__ float xs[(ATTN || PARTS) ? K : 1];
   __shared__ uint64_t wkeys[HO ? 4 : 1];
   // IN_PARTS: thread t sums elements 4t .. 4t+3 of x and of every part (K <= 1024).
@@ -225,7 +231,7 @@ __global__ __launch_bounds__(256) void k_gemv(GemvArgs a) {
 #pragma unroll
     for (int j = 0; j < PJ; ++j) {
       const int i = 4 * (int)threadIdx.x + 1024 * j;
-      if (i >= K) break;  // K = 512: threads 128 .. 255 (whole waves) have nothing to sum
+      if (i >= K) break;  // threads past K / 4 (whole waves) have nothing to sum
       px_[j] = *reinterpret_cast<const float4 *>(a.x + i);
 #pragma unroll
       for (int p = 0; p < kMaxParts; ++p)
@@ -2035,7 +2041,8 @@ static void gemv_launch(const GemvArgs &a, hipStream_t s, const LaunchTiming *t)
   // The per-head partials of the fused attention + O projection: the CodePredictor's gate/up.
   if constexpr (EPI == EPI_SWIGLU && NORM && !NT && (KC == 1 || KC == 2)) {
     if (a.parts) {
-      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_PARTS>, grid, dim3(256), 0, s, t, a);
+      const dim3 grid_p((a.N + kPartsWaves * RW - 1) / (kPartsWaves * RW));
+      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_PARTS>, grid_p, dim3(64 * kPartsWaves), 0, s, t, a);
       return;
     }
   }
