@@ -241,6 +241,7 @@ def main() -> int:
     ap.add_argument("--no-text-prep", action="store_true",
                     help="skip the device prompt-preparation timing (and the text-embedding table it needs)")
     ap.add_argument("--no-cfg4", action="store_true", help="skip the 1.7B (config 4) generation")
+    ap.add_argument("--no-sampled", action="store_true", help="skip the sampled (config 3) generation")
     ap.add_argument("--kernel-classes", action="store_true",
                     help="graph-time every kernel class of q3t_bench_kernel on the workload's model and exit")
     args = ap.parse_args()
@@ -272,7 +273,8 @@ def main() -> int:
         synth.write_codec(tmp, 0)
     spec = model.spec
     w3 = WORKLOADS["cfg3_0.6b_sampled"]
-    inputs3 = w3.inputs(model) if (w3.spec, w3.weight_seed) == (w.spec, w.weight_seed) and args.frames == 0 else None
+    inputs3 = (w3.inputs(model) if (w3.spec, w3.weight_seed) == (w.spec, w.weight_seed) and args.frames == 0
+               and not args.no_sampled else None)
     host_prep = None
     if with_text:
         from q3t import textprep
