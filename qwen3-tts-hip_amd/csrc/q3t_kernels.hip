@@ -731,7 +731,9 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   }
 
   if constexpr (OPROJ) {
-    // 3': this head's attention output to LDS, then its slice of the projection.
+    // 3': this head's attention output to LDS, then its slice of the projection.  Rows of
+    // LPR = 32 lanes are summed across their two 16-lane rows by row_bcast:15 (a VALU lane
+    // permute), which leaves each row's sum in lanes 16..31 (and 48..63).
     const int o = threadIdx.x;
     if (o < G * D) {
       const int g_o = o / D, d_o = o % D;
@@ -743,8 +745,8 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
     for (int i = 0; i < NWO; ++i) {
       const int r = rb * kOprojRows + wave * (kOprojRows / 4) + i * RPL + lane / LPR;
       float sum = row16_sum(dot8(wo[i], ao + (lane % LPR) * 8));
-      if constexpr (LPR == 32) sum += __shfl_xor(sum, 16);
-      if (lane % LPR == 0) a.opart[(size_t)h * a.wo_rows + r] = sum;
+      if constexpr (LPR == 32) sum += dpp_f<0x142, 0xa>(sum, 0.f);
+      if (lane % LPR == LPR - 1) a.opart[(size_t)h * a.wo_rows + r] = sum;
     }
     return;
   }
