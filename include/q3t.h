@@ -301,8 +301,10 @@ int q3t_engine_synchronize(q3t_engine *engine);
  *          6: greedy CodePredictor selection     7: Talker attention at half the cache
  *          8: CodePredictor LM-head GEMV
  *          9: CodePredictor attention with the O projection fused (when the model has it)
- * Class 2 runs the CodePredictor's gate/up as frames do (summing the fused projection's
- * per-head partials when the model has it). Slot 0 must not hold a stream. */
+ * Classes 1 and 2 run as frames do: where the model splits an O projection by KV head (the
+ * 0.6B Talker's), class 1 is that per-head projection and class 2 (gate/up) sums its shares;
+ * class 2 also sums the CodePredictor's fused projection shares. Slot 0 must not hold a
+ * stream. */
 int q3t_bench_kernel(q3t_engine *engine, int32_t kernel, int32_t iters, double *avg_us,
                      double *bytes_per_launch);
 

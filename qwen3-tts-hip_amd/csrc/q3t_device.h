@@ -104,9 +104,9 @@ struct GemvArgs {
   float *trace;
   int64_t trace_frame;
   // Input = x + parts[0] + parts[1] + ... + parts[n_parts - 1] (in that order), each part at
-  // parts + p * ld_parts, when parts is set (the fused attention + O projection's per-head
-  // shares; gate/up with RMSNorm only, K of 512 or 1024).  Workgroup 0 also stores that sum
-  // to x_store.
+  // parts + p * ld_parts, when parts is set (a head-split O projection's per-head shares;
+  // gate/up with RMSNorm only, K of 512 or 1024).  Workgroup 0 also stores that sum to
+  // x_store.
   const float *parts;
   int32_t n_parts, ld_parts;
   float *x_store;

@@ -167,7 +167,8 @@ struct Slot {
   float *trailing;
   float *attn_part;      // attention partials [kv_heads][chunks][G][2 + head_dim]
   int attn_part_chunks = 0;
-  // The CodePredictor's fused attention + O projection: per-KV-head shares of the projection
+  // Head-split O projections (the CodePredictor's fused into its attention, the 0.6B
+  // Talker's after its split attention): per-KV-head shares of the projection
   // [kv_heads][hidden], and the residual row they sum to (stored by the gate/up GEMV).
   float *opart = nullptr, *x_mid = nullptr;
   int32_t *codes;
@@ -198,7 +199,7 @@ struct Pools {
   // The batched frame splits the Talker's attention into shorter chunks (more workgroups,
   // fewer bytes each) than one stream can: its partials are merged by k_attn_merge.
   int rows_chunk = 0, rows_part_chunks = 0;
-  int64_t part_row = 0, trailing_row = 0, codes_row = 0, trace_t_row = 0, trace_c_row = 0;
+  int64_t part_row = 0, trailing_row = 0, codes_row = 0, trace_t_row = 0, trace_c_row = 0, s_opart = 0;
   char *t_k = nullptr, *t_v = nullptr, *c_k = nullptr, *c_v = nullptr;
   float *x_t = nullptr, *t_in = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits_t = nullptr,
         *logits_c = nullptr, *x_c = nullptr, *cp_prefix = nullptr, *cp_in = nullptr, *cur = nullptr,
@@ -293,6 +294,16 @@ struct Engine {
            (d.hidden == 512 || d.hidden == 1024);
   }
 
+  // The Talker's split attention (partials) feeds an O projection split by KV head
+  // (launch_oproj_heads) whose shares the gate/up GEMV sums into the residual, when its
+  // hidden size takes the partial-sum GEMV (512 or 1024: the 0.6B Talker).  Each O workgroup
+  // then merges one head's partials instead of all of them.
+  bool talker_heads_o(const StackW &w) const {
+    const Dims &d = w.d;
+    return &w == &talker && attn_chunks(w.cap) > 1 && attn_chunks(w.cap) <= kAttnGemvMergeChunks &&
+           d.kv_heads <= 8 && (d.hidden == 512 || d.hidden == 1024);
+  }
+
   // One decoder-stack step for one position (decode.rs:951-1001 / 1300-1475).
   // handoff: layer 0 takes its raw q/k/v row from qkv_table (row = the handed-off token) in its
   // attention kernel and runs no QKV GEMV; `in` is then the row that kernel stores
@@ -349,6 +360,26 @@ struct Engine {
         aa.ld_table = d.qkv_rows();
       }
       hip_check(launch_attn_decode(aa, d.head_dim, s), "launch_attn_decode");
+      if (talker_heads_o(w)) {
+        GemvArgs og{L.o, nullptr, nullptr, nullptr, nullptr, sl.opart, d.hidden, d.q_out(), 0.f, skip, sl.st};
+        og.attn_part = sl.attn_part;
+        og.attn_part_chunks = sl.attn_part_chunks;
+        og.attn_chunk = attn_chunk_len(w.cap);
+        og.attn_pos_mode = pos_mode;
+        og.attn_pos_const = pos_const;
+        og.attn_q_heads = d.q_heads;
+        og.attn_kv_heads = d.kv_heads;
+        hip_check(launch_oproj_heads(og, s), "launch_oproj_heads");
+        GemvArgs gu{L.gu, src, L.g_post, nullptr, nullptr, sl.act, d.intermediate, d.hidden, d.eps, skip, sl.st};
+        gu.parts = sl.opart;
+        gu.n_parts = d.kv_heads;
+        gu.ld_parts = d.hidden;
+        gu.x_store = sl.x_mid;
+        hip_check(launch_gemv(EPI_SWIGLU, true, nt, gu, s), "launch_gemv(gate/up, partial sum)");
+        gemv(EPI_RESIDUAL, false, L.down, sl.act, nullptr, 0.f, sl.x_mid, nullptr, x, d.hidden, d.intermediate, skip,
+             sl.st, s, nt);
+        continue;
+      }
       // Up to kAttnGemvMergeChunks partials are merged inside the O projection; more (caches
       // past 1024 rows) by the merge kernel first.
       const bool merge_in_o = partial && attn_chunks(w.cap) <= kAttnGemvMergeChunks;
@@ -808,8 +839,9 @@ void alloc_pools(Engine &e, int n) {
   p.emb_sum = fz(Ht);
   p.trailing = fz(p.trailing_row);
   p.attn_part = fz(p.part_row);
-  p.opart = fz((size_t)cd.kv_heads * Hc);
-  p.x_mid = fz(Hc);
+  p.s_opart = std::max((int64_t)cd.kv_heads * Hc, (int64_t)td.kv_heads * Ht);
+  p.opart = fz((size_t)p.s_opart);
+  p.x_mid = fz(std::max(Hc, Ht));
   p.codes = (int32_t *)zeroed((size_t)p.codes_row * n * 4);
   p.cp_keys = (uint64_t *)zeroed((size_t)n * (e.groups - 1) * kHandoffKeys * 8);
   p.st = (SlotState *)zeroed(sizeof(SlotState) * n);
@@ -847,8 +879,8 @@ void alloc_pools(Engine &e, int n) {
     sl.trailing = p.trailing + (size_t)i * p.trailing_row;
     sl.attn_part = p.attn_part + (size_t)i * p.part_row;
     sl.attn_part_chunks = p.part_chunks;
-    sl.opart = p.opart + (size_t)i * cd.kv_heads * Hc;
-    sl.x_mid = p.x_mid + (size_t)i * Hc;
+    sl.opart = p.opart + (size_t)i * p.s_opart;
+    sl.x_mid = p.x_mid + (size_t)i * std::max(Hc, Ht);
     sl.codes = p.codes + (size_t)i * p.codes_row;
     sl.cp_keys = p.cp_keys + (size_t)i * (e.groups - 1) * kHandoffKeys;
     sl.st = p.st + i;
@@ -2178,8 +2210,25 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
                   SKIP_NEVER, s.st, s.stream, nt);
           b = 2.0 * d.qkv_rows() * d.hidden + 4.0 * (d.hidden * 2 + d.qkv_rows());
           break;
-        case 1: {  // O projection + residual (Talker layers merge attention partials first)
+        case 1: {  // O projection + residual (Talker layers merge attention partials first; split
+                   // by KV head into per-head shares where frames run it that way)
           GemvArgs og{W.o, s.attn, nullptr, s.act, nullptr, s.act, d.hidden, d.q_out(), 0.f, SKIP_NEVER, s.st};
+          if (e->talker_heads_o(*l.w)) {
+            og.x = nullptr;
+            og.res = nullptr;
+            og.out = s.opart;
+            og.attn_part = s.attn_part;
+            og.attn_part_chunks = s.attn_part_chunks;
+            og.attn_chunk = attn_chunk_len(l.w->cap);
+            og.attn_pos_mode = POS_CONST;
+            og.attn_pos_const = l.w->cap / 2;
+            og.attn_q_heads = d.q_heads;
+            og.attn_kv_heads = d.kv_heads;
+            hip_check(launch_oproj_heads(og, s.stream), "launch_oproj_heads");
+            b = 2.0 * d.hidden * d.q_out() + 4.0 * (d.kv_heads * d.hidden) +
+                4.0 * d.q_heads * (d.head_dim + 2) * std::min(attn_chunks(l.w->cap), (l.w->cap / 2) / attn_chunk_len(l.w->cap) + 1);
+            break;
+          }
           if (nt && attn_chunks(l.w->cap) <= kAttnGemvMergeChunks) {
             og.x = nullptr;
             og.attn_part = s.attn_part;
@@ -2198,7 +2247,7 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
                    // CodePredictor's (fused O projection) also sums the per-head partials into x
           GemvArgs gu{W.gu, xin, W.g_post, nullptr, nullptr, s.act, d.intermediate, d.hidden, d.eps, SKIP_NEVER, s.st};
           b = 2.0 * 2 * d.intermediate * d.hidden + 4.0 * (2 * d.hidden + d.intermediate);
-          if (e->oproj_ok(*l.w)) {
+          if (e->oproj_ok(*l.w) || e->talker_heads_o(*l.w)) {
             gu.parts = s.opart;
             gu.n_parts = d.kv_heads;
             gu.ld_parts = d.hidden;

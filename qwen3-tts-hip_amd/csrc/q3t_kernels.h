@@ -38,6 +38,12 @@ hipError_t launch_attn_merge(const AttnMergeArgs &a, int rows, hipStream_t strea
 // or 2 query heads per KV head.
 hipError_t launch_attn_oproj(const AttnArgs &a, int head_dim, hipStream_t stream,
                              const LaunchTiming *timing = nullptr);
+// The O projection of one stream's split attention with its K split by KV head: a.out[h][r]
+// (a.out + h * a.N + r) = KV head h's share of (a.W * attn)[r], attn being the merge of the
+// partials a.attn_part (GemvArgs attention-merge fields; at most kAttnGemvMergeChunks
+// chunks).  a.W is [a.N][a.K] bf16 with a.K = q_heads * 128 and a.N a multiple of 32; the
+// weights are streamed.  The gate/up GEMV adds the shares to the residual (GemvArgs::parts).
+hipError_t launch_oproj_heads(const GemvArgs &a, hipStream_t stream, const LaunchTiming *timing = nullptr);
 // Most attention chunks the O-projection GEMV merges itself (caches up to 8 x 128 rows); the
 // partials of a longer cache are merged by launch_attn_merge first.
 constexpr int kAttnGemvMergeChunks = 8;

@@ -779,6 +779,70 @@ __device__ void merge_attention(const GemvArgs &a, float *xs) {
   }
 }
 
+// The Talker's O projection with its K split by KV head (one stream): workgroup (h, b)
+// merges the split-attention partials of KV head h's G query heads (chunk order, the same
+// arithmetic as merge_finish), then multiplies the merged head outputs by head h's G * D
+// columns of W (a.W, [N][K]) for output rows kOprojRows * b ..: out[h][r] = that share of
+// (W attn)[r].  The gate/up GEMV adds the kv_heads shares to the residual
+// (GemvArgs::parts).  Every load (partials of every chunk slot, the weight slice) is issued
+// before the stream state is read.
+template <int G>
+__global__ __launch_bounds__(256) void k_oproj_heads(GemvArgs a) {
+  constexpr int D = 128;
+  constexpr int LPR = G * D / 8;  // lanes per weight row slice
+  constexpr int RPL = 64 / LPR;   // rows per 16-byte load
+  constexpr int NWO = kOprojRows / 4 / RPL;
+  const int h = blockIdx.x, rb = blockIdx.y;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ float ao[G * D];
+  // thread t < G * D: element d of query head g of KV head h
+  const int t = threadIdx.x, g = t / D, d = t % D;
+  const bool has = t < G * D;
+  float mv[kAttnGemvMergeChunks], lv[kAttnGemvMergeChunks], av[kAttnGemvMergeChunks];
+  const float *p0 = a.attn_part + (((size_t)h * a.attn_part_chunks) * G + (has ? g : 0)) * (D + 2);
+  const size_t stride = (size_t)G * (D + 2);
+#pragma unroll
+  for (int c = 0; c < kAttnGemvMergeChunks; ++c) {
+    const float *pc = p0 + min(c, a.attn_part_chunks - 1) * stride;
+    mv[c] = pc[0];
+    lv[c] = pc[1];
+    av[c] = pc[2 + d];
+  }
+  uint4 wo[NWO];
+#pragma unroll
+  for (int i = 0; i < NWO; ++i) {
+    const int r = rb * kOprojRows + wave * (kOprojRows / 4) + i * RPL + lane / LPR;
+    wo[i] = load_w<true>(reinterpret_cast<const u32x4 *>(a.W + (size_t)r * a.K + h * G * D + (lane % LPR) * 8));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (skip_work(a.st, a.skip)) return;
+  const int pos = (a.attn_pos_mode == POS_TALKER_FRAME) ? a.st->prefill_steps + a.st->frame : a.attn_pos_const;
+  const int nchunks = (pos + a.attn_chunk) / a.attn_chunk;  // ceil((pos + 1) / chunk)
+  if (has) {
+    float M = -FLT_MAX;
+#pragma unroll
+    for (int c = 0; c < kAttnGemvMergeChunks; ++c)
+      if (c < nchunks) M = fmaxf(M, mv[c]);
+    float den = 0.f, num = 0.f;
+#pragma unroll
+    for (int c = 0; c < kAttnGemvMergeChunks; ++c)
+      if (c < nchunks) {
+        const float w = expf(mv[c] - M);
+        den = fmaf(w, lv[c], den);
+        num = fmaf(w, av[c], num);
+      }
+    ao[t] = num / den;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < NWO; ++i) {
+    const int r = rb * kOprojRows + wave * (kOprojRows / 4) + i * RPL + lane / LPR;
+    float sum = row16_sum(dot8(wo[i], ao + (lane % LPR) * 8));
+    if constexpr (LPR == 32) sum += dpp_f<0x142, 0xa>(sum, 0.f);
+    if (lane % LPR == LPR - 1) a.out[(size_t)h * a.N + r] = sum;
+  }
+}
+
 // Stream-row form of merge_attention for the batched frame: workgroup (h, r) merges KV head
 // h's G query heads of row r (thread = one output element), in chunk order as in
 // merge_attention.
@@ -2040,8 +2104,9 @@ static void gemv_launch(const GemvArgs &a, hipStream_t s, const LaunchTiming *t)
       return;
     }
   }
-  // The per-head partials of the fused attention + O projection: the CodePredictor's gate/up.
-  if constexpr (EPI == EPI_SWIGLU && NORM && !NT && (KC == 1 || KC == 2)) {
+  // The per-head partials of a head-split O projection: the gate/up GEMV after it (one
+  // output per wave, launched with RW = 1).
+  if constexpr (EPI == EPI_SWIGLU && NORM && RW == 1 && (KC == 1 || KC == 2)) {
     if (a.parts) {
       const dim3 grid_p((a.N + kPartsWaves * RW - 1) / (kPartsWaves * RW));
       launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_PARTS>, grid_p, dim3(64 * kPartsWaves), 0, s, t, a);
@@ -2060,6 +2125,10 @@ static void gemv_launch(const GemvArgs &a, hipStream_t s, const LaunchTiming *t)
 template <int EPI, bool NORM, int KC, bool NT>
 static hipError_t gemv_rw(const GemvArgs &a, hipStream_t s, const LaunchTiming *t) {
   constexpr int pu = (EPI == EPI_SWIGLU) ? 2 : 1;
+  if (a.parts) {  // kPartsWaves-wave workgroups, one output per wave
+    gemv_launch<EPI, NORM, KC, 1, NT>(a, s, t);
+    return hipGetLastError();
+  }
   switch (gemv_rows_per_wave(a.N, KC, EPI, NT)) {
     case 6:
       if constexpr (6 * pu * KC <= kMaxLoads) { gemv_launch<EPI, NORM, KC, 6, NT>(a, s, t); break; }
@@ -2121,7 +2190,7 @@ hipError_t launch_gemv(int epi, bool norm, bool streaming, const GemvArgs &a, hi
   if (a.rows > 1 && (a.rows != 2 || streaming || a.attn_part || a.K > 6 * 512 || a.ldx_r % 4 ||
                      (epi == EPI_RESIDUAL && !a.ldr_r) || !a.ldo_r))
     return hipErrorInvalidValue;
-  if (a.parts && (epi != EPI_SWIGLU || !norm || streaming || a.rows > 1 || a.attn_part || a.keys_out ||
+  if (a.parts && (epi != EPI_SWIGLU || !norm || a.rows > 1 || a.attn_part || a.keys_out ||
                   (a.K != 512 && a.K != 1024) || a.n_parts < 1 || a.n_parts > kMaxParts ||
                   a.ld_parts < a.K || a.ld_parts % 4 || !a.x))
     return hipErrorInvalidValue;
@@ -2191,6 +2260,21 @@ hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t s, co
   }
 #undef Q3T_ATTN_CASE
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_oproj_heads(const GemvArgs &a, hipStream_t s, const LaunchTiming *t) {
+  constexpr int D = 128;
+  if (!a.W || !a.out || !a.attn_part || !a.st || a.attn_kv_heads <= 0 || a.attn_kv_heads > kMaxParts ||
+      a.attn_q_heads % a.attn_kv_heads || a.K != a.attn_q_heads * D || a.N <= 0 || a.N % kOprojRows ||
+      a.attn_part_chunks < 1 || a.attn_part_chunks > kAttnGemvMergeChunks || a.attn_chunk <= 0 ||
+      (a.attn_pos_mode != POS_TALKER_FRAME && a.attn_pos_mode != POS_CONST))
+    return hipErrorInvalidValue;
+  const int G = a.attn_q_heads / a.attn_kv_heads;
+  const dim3 grid(a.attn_kv_heads, a.N / kOprojRows);
+  if (G == 1) launch_timed(k_oproj_heads<1>, grid, dim3(256), 0, s, t, a);
+  else if (G == 2) launch_timed(k_oproj_heads<2>, grid, dim3(256), 0, s, t, a);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 hipError_t launch_attn_oproj(const AttnArgs &a, int head_dim, hipStream_t s, const LaunchTiming *t) {
