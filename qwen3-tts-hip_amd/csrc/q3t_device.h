@@ -110,6 +110,8 @@ struct GemvArgs {
   const float *parts;
   int32_t n_parts, ld_parts;
   float *x_store;
+  // rows = 2 with parts: row 1's parts at parts + ldp_r, its sum stored at x_store + ldxs_r
+  int32_t ldp_r, ldxs_r;
 };
 
 // Most workgroups a hand-off producer may have (keys per group).
@@ -212,6 +214,12 @@ struct PrefillAttnArgs {
   int32_t P, pos0, ldq, ldo, q_heads, kv_heads, cap;
   float eps, scale;
   int32_t kv_bf16;
+  // launch_prefix_attention with the output projection fused (wo set): wo [wo_rows][q_heads*d]
+  // bf16; row p's per-KV-head shares at opart + p * opart_row + h * wo_rows.
+  const uint16_t *wo;
+  int32_t wo_rows;
+  float *opart;
+  int64_t opart_row;
 };
 
 struct SelectTalkerArgs {

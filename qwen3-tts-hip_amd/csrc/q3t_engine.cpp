@@ -509,6 +509,29 @@ struct Engine {
       PrefillAttnArgs pa{p.pqkv, L.gq, L.gk, w.rope, sl.c_k + l * cache_layer, sl.c_v + l * cache_layer, p.pattn,
                          2, 0, Q, O, d.q_heads, d.kv_heads, w.cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
                          kv_bf16};
+      if (oproj_ok(w)) {
+        // The O projection fused into the attention (per-head shares of both rows in pattn),
+        // the residual sum in the two-row gate/up GEMV, which stores it to px rows 2, 3.
+        float *x_mid2 = x2 + 2 * H;
+        pa.wo = L.o;
+        pa.wo_rows = H;
+        pa.opart = p.pattn;
+        pa.opart_row = (int64_t)d.kv_heads * H;
+        hip_check(launch_prefix_attention(pa, s), "launch_prefix_attention(o projection)");
+        GemvArgs gu{L.gu, src, L.g_post, nullptr, nullptr, p.pact, I, H, d.eps, SKIP_DONE, sl.st};
+        gu.rows = 2;
+        gu.ldx_r = lds;
+        gu.ldo_r = I;
+        gu.parts = p.pattn;
+        gu.n_parts = d.kv_heads;
+        gu.ld_parts = H;
+        gu.ldp_r = d.kv_heads * H;
+        gu.x_store = x_mid2;
+        gu.ldxs_r = H;
+        hip_check(launch_gemv(EPI_SWIGLU, true, false, gu, s), "launch_gemv(2 rows, partial sum)");
+        gemv2(EPI_RESIDUAL, false, L.down, p.pact, I, nullptr, 0.f, x_mid2, H, nullptr, x2, H, H, I, sl, s);
+        continue;
+      }
       hip_check(launch_prefix_attention(pa, s), "launch_prefix_attention");
       gemv2(EPI_RESIDUAL, false, L.o, p.pattn, O, nullptr, 0.f, src, lds, nullptr, x2, H, H, O, sl, s);
       gemv2(EPI_SWIGLU, true, L.gu, x2, H, L.g_post, d.eps, nullptr, 0, nullptr, p.pact, I, I, H, sl, s);

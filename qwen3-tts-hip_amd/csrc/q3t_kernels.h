@@ -85,6 +85,8 @@ hipError_t launch_bf16_to_f32(const uint16_t *src, float *dst, size_t n, hipStre
 // Prefill attention: q/k norm + RoPE + KV store for P rows, then causal attention.
 hipError_t launch_prefill_attention(const PrefillAttnArgs &a, hipStream_t stream);
 // The same for P = 2 rows at positions 0 and 1 (the CodePredictor's prefix) in one launch.
+// With a.wo set, the output projection is fused in as in launch_attn_oproj: row p's per-KV-head
+// shares go to a.opart + p * a.opart_row (a.out unused).
 hipError_t launch_prefix_attention(const PrefillAttnArgs &a, hipStream_t stream);
 
 // Token selection, one workgroup per stream row (rows > 1 needs row_on and the row strides).

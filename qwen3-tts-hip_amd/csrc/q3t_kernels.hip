@@ -215,27 +215,30 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
   constexpr bool PARTS = IN == IN_PARTS;
   constexpr int WPB = PARTS ? kPartsWaves : 4;
   static_assert(!ATTN || MR == 1, "the attention merge feeds one row");
-  static_assert(!PARTS || (MR == 1 && (KC == 1 || KC == 2)), "the partial sum feeds one row of K <= 1024");
+  static_assert(!PARTS || (KC == 1 || KC == 2), "the partial sum feeds rows of K <= 1024");
   static_assert(!HO || (MR == 1 && IN == IN_X && EPI == EPI_STORE), "the hand-off producer stores one row");
   constexpr int K = KC * 512;
   constexpr int NR = (EPI == EPI_SWIGLU) ? 2 * RW : RW;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int unit0 = (blockIdx.x * WPB + wave) * RW;
-  __shared__ float xs[(ATTN || PARTS) ? K : 1];
+  __shared__ float xs[PARTS ? MR : 1][(ATTN || PARTS) ? K : 1];
   __shared__ uint64_t wkeys[HO ? 4 : 1];
-  // IN_PARTS: thread t sums elements 4t .. 4t+3 of x and of every part (K <= 1024).
-  constexpr int PJ = 1;
-  float4 px_[PJ], pp_[PARTS ? kMaxParts : 1][PJ];
+  // IN_PARTS: thread t sums elements 4t .. 4t+3 of x and of every part (K <= 1024), for each
+  // input row m (x + m * ldx_r, parts + m * ldp_r).
+  constexpr int PR = PARTS ? MR : 1;
+  float4 px_[PR], pp_[PARTS ? kMaxParts : 1][PR];
   if constexpr (PARTS) {
+    const int i = 4 * (int)threadIdx.x;
+    if (i < K) {  // threads past K / 4 (whole waves) have nothing to sum
 #pragma unroll
-    for (int j = 0; j < PJ; ++j) {
-      const int i = 4 * (int)threadIdx.x + 1024 * j;
-      if (i >= K) break;  // threads past K / 4 (whole waves) have nothing to sum
-      px_[j] = *reinterpret_cast<const float4 *>(a.x + i);
+      for (int m = 0; m < PR; ++m) {
+        px_[m] = *reinterpret_cast<const float4 *>(a.x + m * a.ldx_r + i);
 #pragma unroll
-      for (int p = 0; p < kMaxParts; ++p)
-        pp_[p][j] = *reinterpret_cast<const float4 *>(a.parts + (size_t)min(p, a.n_parts - 1) * a.ld_parts + i);
+        for (int p = 0; p < kMaxParts; ++p)
+          pp_[p][m] = *reinterpret_cast<const float4 *>(a.parts + (size_t)m * a.ldp_r +
+                                                        (size_t)min(p, a.n_parts - 1) * a.ld_parts + i);
+      }
     }
   }
 
@@ -300,42 +303,45 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
   // before it.
   if (skip_work(a.st, a.skip)) return;
   if constexpr (PARTS) {
+    const int i = 4 * (int)threadIdx.x;
+    if (i < K) {
 #pragma unroll
-    for (int j = 0; j < PJ; ++j) {
-      const int i = 4 * (int)threadIdx.x + 1024 * j;
-      if (i >= K) break;
-      float4 v = px_[j];
+      for (int m = 0; m < PR; ++m) {
+        float4 v = px_[m];
 #pragma unroll
-      for (int p = 0; p < kMaxParts; ++p)
-        if (p < a.n_parts) {
-          v.x += pp_[p][j].x;
-          v.y += pp_[p][j].y;
-          v.z += pp_[p][j].z;
-          v.w += pp_[p][j].w;
-        }
-      *reinterpret_cast<float4 *>(xs + i) = v;
-      if (a.x_store && blockIdx.x == 0) *reinterpret_cast<float4 *>(a.x_store + i) = v;
+        for (int p = 0; p < kMaxParts; ++p)
+          if (p < a.n_parts) {
+            v.x += pp_[p][m].x;
+            v.y += pp_[p][m].y;
+            v.z += pp_[p][m].z;
+            v.w += pp_[p][m].w;
+          }
+        *reinterpret_cast<float4 *>(&xs[m][i]) = v;
+        if (a.x_store && blockIdx.x == 0) *reinterpret_cast<float4 *>(a.x_store + m * a.ldxs_r + i) = v;
+      }
     }
     __syncthreads();
 #pragma unroll
-    for (int c = 0; c < KC; ++c)
+    for (int m = 0; m < PR; ++m)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) xv[0][c][j] = xs[c * 512 + lane * 8 + j];
+      for (int c = 0; c < KC; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xv[m][c][j] = xs[m][c * 512 + lane * 8 + j];
   }
   if constexpr (ATTN_EARLY) {
-    if (threadIdx.x * 8 < K) merge_finish(a, threadIdx.x * 8, mregs, xs);
+    if (threadIdx.x * 8 < K) merge_finish(a, threadIdx.x * 8, mregs, xs[0]);
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < KC; ++c)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) xv[0][c][j] = xs[c * 512 + lane * 8 + j];
+      for (int j = 0; j < 8; ++j) xv[0][c][j] = xs[0][c * 512 + lane * 8 + j];
   } else if constexpr (ATTN) {
-    merge_attention(a, xs);
+    merge_attention(a, xs[0]);
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < KC; ++c)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) xv[0][c][j] = xs[c * 512 + lane * 8 + j];
+      for (int j = 0; j < 8; ++j) xv[0][c][j] = xs[0][c * 512 + lane * 8 + j];
   }
 
   if constexpr (NORM) {
@@ -1430,13 +1436,29 @@ __global__ __launch_bounds__(256) void k_prefill_qkv(PrefillAttnArgs a) {
 // workgroup per KV head: q/k head RMSNorm + RoPE, K/V stores, then each row's causal
 // attention over rows 0..p with the values just stored (rounded to the cache type).  The
 // P * (G + 2) head vectors are spread over the 4 waves, loads first.
-template <int G, typename KVT, int P>
+// OPROJ: the output projection fused in as in k_attn_split (grid (kv_heads, wo_rows / 32));
+// row p's per-head shares go to opart + p * opart_row + h * wo_rows.  Only row block 0 stores
+// the K/V rows.
+template <int G, typename KVT, int P, bool OPROJ = false>
 __global__ __launch_bounds__(256) void k_attn_prefix(PrefillAttnArgs a) {
   constexpr int D = 128, NV = P * (G + 2), VPW = (NV + 3) / 4;
   const int h = blockIdx.x;
+  const int rb = OPROJ ? blockIdx.y : 0;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   __shared__ float qs[P][G][D], ks[P][D], vs[P][D];
   __shared__ float sc[P][G][P];
+  __shared__ float ao[OPROJ ? P : 1][G * D];
+  constexpr int LPR = G * D / 8;
+  constexpr int RPL = 64 / LPR;
+  constexpr int NWO = OPROJ ? kOprojRows / 4 / RPL : 1;
+  uint4 wo[NWO];
+  if constexpr (OPROJ) {
+#pragma unroll
+    for (int i = 0; i < NWO; ++i) {
+      const int r = rb * kOprojRows + wave * (kOprojRows / 4) + i * RPL + lane / LPR;
+      wo[i] = *reinterpret_cast<const uint4 *>(a.wo + (size_t)r * a.q_heads * D + h * G * D + (lane % LPR) * 8);
+    }
+  }
   float x0[VPW], x1[VPW], g0[VPW], g1[VPW];
   float2 cs[VPW];
 #pragma unroll
@@ -1474,8 +1496,13 @@ __global__ __launch_bounds__(256) void k_attn_prefix(PrefillAttnArgs a) {
     } else {
       KVT *cache = reinterpret_cast<KVT *>(kind == G ? a.kcache : a.vcache) + ((size_t)h * a.cap + p) * D;
       float *keep = kind == G ? ks[p] : vs[p];
-      keep[lane] = KvIo<KVT>::store(cache + lane, y0);
-      keep[lane + 64] = KvIo<KVT>::store(cache + lane + 64, y1);
+      if (rb == 0) {
+        keep[lane] = KvIo<KVT>::store(cache + lane, y0);
+        keep[lane + 64] = KvIo<KVT>::store(cache + lane + 64, y1);
+      } else {
+        keep[lane] = KvIo<KVT>::round(y0);
+        keep[lane + 64] = KvIo<KVT>::round(y1);
+      }
     }
   }
   __syncthreads();
@@ -1502,7 +1529,23 @@ __global__ __launch_bounds__(256) void k_attn_prefix(PrefillAttnArgs a) {
       l += w;
       acc = fmaf(w, vs[t][d], acc);
     }
-    a.out[(size_t)p * a.ldo + (h * G + g) * D + d] = acc / l;
+    if constexpr (OPROJ)
+      ao[p][g * D + d] = acc / l;
+    else
+      a.out[(size_t)p * a.ldo + (h * G + g) * D + d] = acc / l;
+  }
+  if constexpr (OPROJ) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NWO; ++i) {
+      const int r = rb * kOprojRows + wave * (kOprojRows / 4) + i * RPL + lane / LPR;
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        float sum = row16_sum(dot8(wo[i], ao[p] + (lane % LPR) * 8));
+        if constexpr (LPR == 32) sum += dpp_f<0x142, 0xa>(sum, 0.f);
+        if (lane % LPR == LPR - 1) a.opart[p * a.opart_row + (size_t)h * a.wo_rows + r] = sum;
+      }
+    }
   }
 }
 
@@ -2109,6 +2152,12 @@ static void gemv_launch(const GemvArgs &a, hipStream_t s, const LaunchTiming *t)
   if constexpr (EPI == EPI_SWIGLU && NORM && RW == 1 && (KC == 1 || KC == 2)) {
     if (a.parts) {
       const dim3 grid_p((a.N + kPartsWaves * RW - 1) / (kPartsWaves * RW));
+      if constexpr (!NT) {
+        if (a.rows == 2) {  // the CodePredictor's prefix pass
+          launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_PARTS, 2>, grid_p, dim3(64 * kPartsWaves), 0, s, t, a);
+          return;
+        }
+      }
       launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_PARTS>, grid_p, dim3(64 * kPartsWaves), 0, s, t, a);
       return;
     }
@@ -2190,7 +2239,10 @@ hipError_t launch_gemv(int epi, bool norm, bool streaming, const GemvArgs &a, hi
   if (a.rows > 1 && (a.rows != 2 || streaming || a.attn_part || a.K > 6 * 512 || a.ldx_r % 4 ||
                      (epi == EPI_RESIDUAL && !a.ldr_r) || !a.ldo_r))
     return hipErrorInvalidValue;
-  if (a.parts && (epi != EPI_SWIGLU || !norm || a.rows > 1 || a.attn_part || a.keys_out ||
+  if (a.parts && a.rows == 2 && (a.ldp_r % 4 || a.ldp_r < a.n_parts * a.ld_parts || (a.x_store && a.ldxs_r < a.K) ||
+                                 a.ldxs_r % 4))
+    return hipErrorInvalidValue;
+  if (a.parts && (epi != EPI_SWIGLU || !norm || a.attn_part || a.keys_out ||
                   (a.K != 512 && a.K != 1024) || a.n_parts < 1 || a.n_parts > kMaxParts ||
                   a.ld_parts < a.K || a.ld_parts % 4 || !a.x))
     return hipErrorInvalidValue;
@@ -2482,6 +2534,20 @@ hipError_t launch_prefix_attention(const PrefillAttnArgs &a, hipStream_t s) {
   if (a.P != 2 || a.pos0 != 0 || a.kv_heads <= 0 || a.q_heads % a.kv_heads || a.cap < 2) return hipErrorInvalidValue;
   const int G = a.q_heads / a.kv_heads;
   if (G != 1 && G != 2) return hipErrorInvalidValue;
+  if (a.wo) {  // fused output projection
+    if (!a.opart || a.wo_rows <= 0 || a.wo_rows % kOprojRows || a.kv_heads > kMaxParts ||
+        a.opart_row < (int64_t)a.kv_heads * a.wo_rows)
+      return hipErrorInvalidValue;
+    const dim3 grid_o(a.kv_heads, a.wo_rows / kOprojRows), block_o(256);
+    if (a.kv_bf16) {
+      if (G == 1) hipLaunchKernelGGL((k_attn_prefix<1, uint16_t, 2, true>), grid_o, block_o, 0, s, a);
+      else hipLaunchKernelGGL((k_attn_prefix<2, uint16_t, 2, true>), grid_o, block_o, 0, s, a);
+    } else {
+      if (G == 1) hipLaunchKernelGGL((k_attn_prefix<1, float, 2, true>), grid_o, block_o, 0, s, a);
+      else hipLaunchKernelGGL((k_attn_prefix<2, float, 2, true>), grid_o, block_o, 0, s, a);
+    }
+    return hipGetLastError();
+  }
   const dim3 grid(a.kv_heads), block(256);
   if (a.kv_bf16) {
     if (G == 1) hipLaunchKernelGGL((k_attn_prefix<1, uint16_t, 2>), grid, block, 0, s, a);
