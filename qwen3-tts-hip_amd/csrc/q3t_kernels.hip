@@ -852,49 +852,45 @@ __global__ __launch_bounds__(256) void k_oproj_heads(GemvArgs a) {
 // Stream-row form of merge_attention for the batched frame: workgroup (h, r) merges KV head
 // h's G query heads of row r (thread = one output element), in chunk order as in
 // merge_attention.
+// NC = chunk slots loaded (a power of two >= part_chunks): every partial of every slot is
+// loaded before the stream state is read, so the merge waits on one memory round trip.
+template <int NC>
 __global__ __launch_bounds__(256) void k_attn_merge(AttnMergeArgs a) {
   constexpr int D = 128;
   const int h = blockIdx.x;
   const int row = blockIdx.y;
-  if (a.row_on && !a.row_on[row]) return;
-  const SlotState *st = a.st + row;
-  if (skip_work(st, a.skip)) return;
   const int G = a.q_heads / a.kv_heads;
   if ((int)threadIdx.x >= G * D) return;
   const int g = threadIdx.x / D, d = threadIdx.x % D;
-  const int pos = (a.pos_mode == POS_TALKER_FRAME) ? st->prefill_steps + st->frame : a.pos_const;
-  const int nchunks = min((pos + a.chunk) / a.chunk, a.part_chunks);
   const float *p0 = a.part + row * a.part_row + (((size_t)h * a.part_chunks) * G + g) * (D + 2);
   const size_t stride = (size_t)G * (D + 2);
-  // Loads in blocks of 8 chunks (indices clamped), so a block costs one memory round trip;
-  // max, then the weighted sums in chunk order.
+  float mv[NC], lv[NC], av[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const float *pc = p0 + min(c, a.part_chunks - 1) * stride;
+    mv[c] = pc[0];
+    lv[c] = pc[1];
+    av[c] = pc[2 + d];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (a.row_on && !a.row_on[row]) return;
+  const SlotState *st = a.st + row;
+  if (skip_work(st, a.skip)) return;
+  const int pos = (a.pos_mode == POS_TALKER_FRAME) ? st->prefill_steps + st->frame : a.pos_const;
+  const int nchunks = min((pos + a.chunk) / a.chunk, a.part_chunks);
+  // max, then the weighted sums in chunk order
   float M = -FLT_MAX;
-  for (int c0 = 0; c0 < nchunks; c0 += 8) {
-    float mv[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) mv[j] = p0[min(c0 + j, nchunks - 1) * stride];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (c0 + j < nchunks) M = fmaxf(M, mv[j]);
-  }
+  for (int c = 0; c < NC; ++c)
+    if (c < nchunks) M = fmaxf(M, mv[c]);
   float den = 0.f, num = 0.f;
-  for (int c0 = 0; c0 < nchunks; c0 += 8) {
-    float mv[8], lv[8], av[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float *pc = p0 + min(c0 + j, nchunks - 1) * stride;
-      mv[j] = pc[0];
-      lv[j] = pc[1];
-      av[j] = pc[2 + d];
+  for (int c = 0; c < NC; ++c)
+    if (c < nchunks) {
+      const float w = expf(mv[c] - M);
+      den = fmaf(w, lv[c], den);
+      num = fmaf(w, av[c], num);
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (c0 + j < nchunks) {
-        const float w = expf(mv[j] - M);
-        den = fmaf(w, lv[j], den);
-        num = fmaf(w, av[j], num);
-      }
-  }
   const int k = (h * G + g) * D + d;
   a.out[a.out_t16 ? t16_index(row, k) : (size_t)row * a.ld_out + k] = num / den;
 }
@@ -2581,8 +2577,12 @@ hipError_t launch_attn_merge(const AttnMergeArgs &a, int rows, hipStream_t s) {
   if (rows < 1 || rows > kMaxRows || a.kv_heads <= 0 || a.q_heads % a.kv_heads || a.chunk <= 0 ||
       a.part_chunks <= 0 || a.q_heads * 128 > a.ld_out || (rows > 1 && (!a.row_on || a.part_row <= 0)))
     return hipErrorInvalidValue;
-  if ((a.q_heads / a.kv_heads) * 128 > 256) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_attn_merge, dim3(a.kv_heads, rows), dim3(256), 0, s, a);
+  if ((a.q_heads / a.kv_heads) * 128 > 256 || a.part_chunks > 64) return hipErrorInvalidValue;
+  const dim3 grid(a.kv_heads, rows), block(256);
+  if (a.part_chunks <= 8) hipLaunchKernelGGL(k_attn_merge<8>, grid, block, 0, s, a);
+  else if (a.part_chunks <= 16) hipLaunchKernelGGL(k_attn_merge<16>, grid, block, 0, s, a);
+  else if (a.part_chunks <= 32) hipLaunchKernelGGL(k_attn_merge<32>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(k_attn_merge<64>, grid, block, 0, s, a);
   return hipGetLastError();
 }
 
