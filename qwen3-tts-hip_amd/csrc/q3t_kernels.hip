@@ -1675,6 +1675,7 @@ struct SelectShared {
   int si[kMaxVocab];
   uint32_t hist[256];
   uint32_t whist[16][256];  // per-wave histograms of a radix pass
+  uint32_t skey[64];        // the keys of a radix bin resolved directly
   float wv[16];
   int wi[16];
   int misc[8];
@@ -1812,13 +1813,43 @@ __device__ int block_sample(SelectShared &sh, int V, const SamplingParams &sp, f
           const int sel = found >= 0 ? 255 - 4 * lane - found : 0;
           sh.misc[3] = remaining - (int)(found >= 0 ? at : run);
           sh.umisc[0] = prefix | ((uint32_t)sel << shift);
+          uint32_t nb = 0;  // keys in the selected bin
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (j == found) nb = c[j];
+          sh.misc[6] = found >= 0 ? (int)nb : 1 << 30;
+          sh.misc[7] = 0;
         }
       }
       __syncthreads();
       remaining = sh.misc[3];
       prefix = sh.umisc[0];
       mask |= 255u << shift;
+      const int nbin = sh.misc[6];
       __syncthreads();
+      if (shift > 0 && nbin <= 64) {
+        // Few keys share the prefix: collect them and take the remaining-th largest directly
+        // (the same key the later passes would reach).  Ranks are unique: ties by slot.
+        for (int i = tid; i < V; i += 1024) {
+          const float v = sh.lg[i];
+          if (!isfinite(v)) continue;
+          const uint32_t key = order_key(v);
+          if ((key & mask) == prefix) sh.skey[atomicAdd(&sh.misc[7], 1)] = key;
+        }
+        __syncthreads();
+        if (tid < nbin) {
+          const uint32_t kt = sh.skey[tid];
+          int rank = 0;
+          for (int o = 0; o < nbin; ++o) {
+            const uint32_t ko = sh.skey[o];
+            rank += (ko > kt || (ko == kt && o < tid)) ? 1 : 0;
+          }
+          if (rank == remaining - 1) sh.umisc[0] = kt;
+        }
+        __syncthreads();
+        prefix = sh.umisc[0];
+        break;
+      }
     }
     thresh = prefix;
   }
