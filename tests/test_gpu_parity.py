@@ -222,6 +222,23 @@ def test_cache_past_1024_rows_matches_oracle(models):
     print(f"1152-row cache: {same} frames identical, talker logit err {err:.2e}")
 
 
+def test_cache_of_33_chunks_matches_oracle(models):
+    """A 4,107-row prompt in a 4,224-row cache: 33 key chunks of 128 rows, merged by the merge
+    kernel's 64-slot form before the O projection."""
+    w = WORKLOADS["tiny_greedy"]
+    model, _ = models.get(w.spec)
+    prompt = np.random.default_rng(22).integers(0, 151643, 4098)
+    from q3t import textprep
+    inputs = textprep.TextPrep(model).prepare(prompt)
+    assert inputs.prefill_steps == 4107
+    opts = E.GenerateOptions.greedy(4)
+    r = run(models, "tiny_greedy", options=opts, inputs=inputs, cap=4224)
+    fx = _as_fixture(_oracle_rollout(model, inputs, opts, 4224))
+    same = check_codes(r["codes"], r["eos"], fx)
+    err = check_talker_logits(r["talker_logits"], fx, same)
+    print(f"4224-row cache: {same} frames identical, talker logit err {err:.2e}")
+
+
 def test_capacity_busy_and_exhausted_streams(models):
     w = WORKLOADS["tiny_greedy"]
     model, d = models.get(w.spec)
