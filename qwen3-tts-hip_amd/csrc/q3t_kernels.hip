@@ -1667,7 +1667,7 @@ __device__ __forceinline__ uint32_t order_key(float f) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-struct SelectShared {
+struct alignas(16) SelectShared {
   float lg[kMaxVocab];
   float cv[kMaxVocab];
   int ci[kMaxVocab];
@@ -1766,12 +1766,13 @@ __device__ int block_sample(SelectShared &sh, int V, const SamplingParams &sp, f
   if (k_eff < n_finite) {
     uint32_t prefix = 0, mask = 0;
     int remaining = k_eff;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-      // each wave counts into its own histogram (keys of a pass share few digits, so one
-      // shared histogram serialises on its hot bins), then the 16 are added per bin
+    // each wave counts into its own histogram (keys of a pass share few digits, so one shared
+    // histogram serialises on its hot bins), then the 16 are added per bin by the thread
+    // that also clears that bin for the next pass
 #pragma unroll
-      for (int j = 0; j < 4; ++j) (&sh.whist[0][0])[tid + 1024 * j] = 0;
-      __syncthreads();
+    for (int j = 0; j < 4; ++j) (&sh.whist[0][0])[tid + 1024 * j] = 0;
+    __syncthreads();
+    for (int shift = 24; shift >= 0; shift -= 8) {
       for (int i = tid; i < V; i += 1024) {
         const float v = sh.lg[i];
         if (!isfinite(v)) continue;
@@ -1782,7 +1783,10 @@ __device__ int block_sample(SelectShared &sh, int V, const SamplingParams &sp, f
       if (tid < 256) {
         uint32_t t = 0;
 #pragma unroll
-        for (int w = 0; w < 16; ++w) t += sh.whist[w][tid];
+        for (int w = 0; w < 16; ++w) {
+          t += sh.whist[w][tid];
+          sh.whist[w][tid] = 0;
+        }
         sh.hist[tid] = t;
       }
       __syncthreads();
@@ -1822,11 +1826,11 @@ __device__ int block_sample(SelectShared &sh, int V, const SamplingParams &sp, f
         }
       }
       __syncthreads();
+      // read by every thread; the next writes to these come after two more barriers
       remaining = sh.misc[3];
       prefix = sh.umisc[0];
       mask |= 255u << shift;
       const int nbin = sh.misc[6];
-      __syncthreads();
       if (shift > 0 && nbin <= 64) {
         // Few keys share the prefix: collect them and take the remaining-th largest directly
         // (the same key the later passes would reach).  Ranks are unique: ties by slot.
@@ -1864,13 +1868,25 @@ __device__ int block_sample(SelectShared &sh, int V, const SamplingParams &sp, f
   }
   __syncthreads();
   const int n_cand = sh.misc[2];
+  // pad to a multiple of 4 with entries that never outrank a candidate, then rank each
+  // candidate against the others four at a time
+  const int n_pad = (n_cand + 3) & ~3;  // <= kMaxVocab
+  if (tid < n_pad - n_cand) {
+    sh.cv[n_cand + tid] = -INFINITY;
+    sh.ci[n_cand + tid] = 0x7fffffff;
+  }
+  __syncthreads();
   for (int c = tid; c < n_cand; c += 1024) {
     const float v = sh.cv[c];
     const int idx = sh.ci[c];
     int rank = 0;
-    for (int o = 0; o < n_cand; ++o) {
-      const float ov = sh.cv[o];
-      rank += (ov > v || (ov == v && sh.ci[o] < idx)) ? 1 : 0;
+    for (int o = 0; o < n_pad; o += 4) {
+      const float4 ov = *reinterpret_cast<const float4 *>(&sh.cv[o]);
+      const int4 oi = *reinterpret_cast<const int4 *>(&sh.ci[o]);
+      rank += (ov.x > v || (ov.x == v && oi.x < idx)) ? 1 : 0;
+      rank += (ov.y > v || (ov.y == v && oi.y < idx)) ? 1 : 0;
+      rank += (ov.z > v || (ov.z == v && oi.z < idx)) ? 1 : 0;
+      rank += (ov.w > v || (ov.w == v && oi.w < idx)) ? 1 : 0;
     }
     if (rank < k_eff) {
       sh.sv[rank] = v;
