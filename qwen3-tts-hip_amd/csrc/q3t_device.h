@@ -78,6 +78,10 @@ struct TokenHandoff {
   // Stream rows (grid z of the attention): row r reads keys + r * keys_row and stores to
   // sum + r * sum_row, cur + r * cur_row, codes + r * codes_row (all 0 for one stream).
   int64_t keys_row, sum_row, cur_row, codes_row;
+  // One stream, token chosen by a selection kernel (sampled groups): the token is read from
+  // tok_in instead of reduced from keys, and the selection kernel has done the stores above
+  // (only the table row is taken).
+  const int32_t *tok_in;
 };
 
 struct GemvArgs {
@@ -262,6 +266,7 @@ struct SelectCpArgs {
   // trailing + r * their row strides; st + r, prm + r.
   int64_t codes_row, trace_row, trailing_row;
   const int32_t *row_on;
+  int32_t *tok_out;           // one stream: the chosen token is also stored here (or null)
 };
 
 }  // namespace q3t

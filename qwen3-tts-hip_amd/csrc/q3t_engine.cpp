@@ -185,6 +185,7 @@ struct Slot {
   // keys) instead of a token selection kernel.
   uint64_t *cp_keys = nullptr;
   bool cp_greedy = false;
+  int32_t *tok_cur = nullptr;  // the token the last CodePredictor selection kernel chose
 };
 
 // Per-stream device buffers for all slots, laid out as rows: slot i's buffer is
@@ -207,6 +208,7 @@ struct Pools {
         *opart = nullptr, *x_mid = nullptr;
   int32_t *codes = nullptr;
   uint64_t *cp_keys = nullptr;                          // [n][groups - 1][kHandoffKeys]
+  int32_t *tok_cur = nullptr;                           // [n]
   SlotState *st = nullptr;
   SlotParams *prm = nullptr;
   int32_t *row_on = nullptr;                            // [n] rows a batched launch covers
@@ -554,6 +556,9 @@ struct Engine {
     // group's layer-0 attention, which reads that token's precomputed q/k/v row; the last
     // group's selection kernel also writes the next Talker input.
     const bool fused = sl.cp_greedy && cp_qkv_table;
+    // Sampled groups take the tables too (the token from the selection kernel), when the
+    // model has no projection and the attention has the fused O projection.
+    const bool sampled_tables = !fused && cp_qkv_table && !has_proj && oproj_ok(cp);
     for (int g = 0; g < nac; ++g) {
       if (g > 0) {
         const float *in = sl.cur;
@@ -575,6 +580,13 @@ struct Engine {
             t.cur = sl.cp_in + 2 * Hc;
             in = t.cur;
           }
+          stack_step(cp, sl.c_k, sl.c_v, in, sl.x_c, sl, POS_CONST, g + 1, SKIP_DONE, s, &t,
+                     cp_qkv_table + (size_t)(g - 1) * Vc * cd.qkv_rows());
+        } else if (sampled_tables) {
+          // the previous group's selection kernel chose the token (tok_cur) and stored its
+          // embedding row (cur): layer 0 takes the token's q/k/v table row
+          TokenHandoff t{};
+          t.tok_in = sl.tok_cur;
           stack_step(cp, sl.c_k, sl.c_v, in, sl.x_c, sl, POS_CONST, g + 1, SKIP_DONE, s, &t,
                      cp_qkv_table + (size_t)(g - 1) * Vc * cd.qkv_rows());
         } else {
@@ -601,6 +613,7 @@ struct Engine {
       SelectCpArgs sa{sl.logits_c, cp_emb + (size_t)g * Vc * Ht, sl.cur, sl.emb_sum, sl.codes,
                       trace ? sl.trace_c : nullptr, sl.t_in, codec_emb, sl.trailing, sl.st, sl.prm, Vc, Ht, groups,
                       g};
+      sa.tok_out = sl.tok_cur;
       hip_check(launch_select_cp(sa, s), "launch_select_cp");
     }
   }
@@ -867,6 +880,7 @@ void alloc_pools(Engine &e, int n) {
   p.x_mid = fz(std::max(Hc, Ht));
   p.codes = (int32_t *)zeroed((size_t)p.codes_row * n * 4);
   p.cp_keys = (uint64_t *)zeroed((size_t)n * (e.groups - 1) * kHandoffKeys * 8);
+  p.tok_cur = (int32_t *)zeroed((size_t)n * 4);
   p.st = (SlotState *)zeroed(sizeof(SlotState) * n);
   p.prm = (SlotParams *)zeroed(sizeof(SlotParams) * n);
   p.row_on = (int32_t *)zeroed(sizeof(int32_t) * n);
@@ -906,6 +920,7 @@ void alloc_pools(Engine &e, int n) {
     sl.x_mid = p.x_mid + (size_t)i * std::max(Hc, Ht);
     sl.codes = p.codes + (size_t)i * p.codes_row;
     sl.cp_keys = p.cp_keys + (size_t)i * (e.groups - 1) * kHandoffKeys;
+    sl.tok_cur = p.tok_cur + i;
     sl.st = p.st + i;
     sl.prm = p.prm + i;
     sl.h_state = p.h_states + i;
@@ -925,7 +940,7 @@ void free_pools(Engine &e) {
   void *ptrs[] = {p.t_k,      p.t_v,     p.c_k,   p.c_v,      p.x_t,      p.t_in,    p.qkv,  p.attn,
                   p.act,      p.logits_t, p.logits_c, p.x_c,  p.cp_prefix, p.cp_in,  p.cur,  p.emb_sum,
                   p.trailing, p.attn_part, p.trace_t, p.trace_c, p.codes,  p.st,      p.prm,  p.row_on,
-                  p.px,       p.pqkv,    p.pattn, p.pact,     p.pinv,    p.cp_keys, p.opart, p.x_mid};
+                  p.px,       p.pqkv,    p.pattn, p.pact,     p.pinv,    p.cp_keys, p.opart, p.x_mid, p.tok_cur};
   for (void *q : ptrs)
     if (q) (void)hipFree(q);
   if (p.h_states) (void)hipHostFree(p.h_states);

@@ -578,10 +578,15 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   float2 cs = make_float2(0.f, 0.f);
   const int vec_off = vec < G ? (h * G + vec) * D : (vec == G ? q_out + h * D : q_out + kv_out + h * D);
   uint64_t kin[HO ? 4 : 1];
+  int tok_in = 0;
   if constexpr (HO) {
-    const uint64_t *keys = a.h.keys + row * a.h.keys_row;
+    if (a.h.tok_in) {
+      tok_in = *a.h.tok_in;
+    } else {
+      const uint64_t *keys = a.h.keys + row * a.h.keys_row;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) kin[j] = keys[min(lane + 64 * j, a.h.n_keys - 1)];
+      for (int j = 0; j < 4; ++j) kin[j] = keys[min(lane + 64 * j, a.h.n_keys - 1)];
+    }
   }
   if (has_vec) {
     if constexpr (!HO) {
@@ -631,13 +636,13 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   int tok = 0;
   float4 side_e[2], side_s[2], side_c[2];
   if constexpr (HO) {
-    tok = key_token(wave_max_u64(umax64(umax64(kin[0], kin[1]), umax64(kin[2], kin[3]))));
+    tok = a.h.tok_in ? tok_in : key_token(wave_max_u64(umax64(umax64(kin[0], kin[1]), umax64(kin[2], kin[3]))));
     if (has_vec) {
       const float *src = a.qkv_table + (size_t)tok * a.ld_table + vec_off;
       x0 = src[lane];
       x1 = src[lane + 64];
     }
-    if (h == 0 && c == 0 && rb == 0) handoff_load(a.h, row, tok, side_e, side_s, side_c);
+    if (h == 0 && c == 0 && rb == 0 && !a.h.tok_in) handoff_load(a.h, row, tok, side_e, side_s, side_c);
   }
 
   // 1: q heads (waves 0..G-1); k and v (waves G, G+1) only where row `pos` is stored.
@@ -733,7 +738,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   __syncthreads();
 
   if constexpr (HO) {
-    if (h == 0 && c == 0 && rb == 0) handoff_store(a.h, row, tok, st, side_e, side_s, side_c);
+    if (h == 0 && c == 0 && rb == 0 && !a.h.tok_in) handoff_store(a.h, row, tok, st, side_e, side_s, side_c);
   }
 
   if constexpr (OPROJ) {
@@ -2031,6 +2036,7 @@ __global__ __launch_bounds__(1024) void k_select_cp(SelectCpArgs a) {
   if (tid == 0) {
     a.codes[(size_t)frame * a.groups + 1 + a.group] = tok;
     if (a.group == 0) a.codes[(size_t)frame * a.groups] = semantic;
+    if (a.tok_out) *a.tok_out = tok;
   }
   const bool last = a.group == a.groups - 2;
   const int trow = min(frame, a.st->trailing_rows);
@@ -2379,11 +2385,14 @@ hipError_t launch_attn_oproj(const AttnArgs &a, int head_dim, hipStream_t s, con
       a.pos_mode != POS_CONST || !a.wo || !a.opart || a.wo_rows <= 0 || a.wo_rows % kOprojRows || !a.st)
     return hipErrorInvalidValue;
   const dim3 grid(a.kv_heads, a.wo_rows / kOprojRows, 1), block(256);
-  if (a.h.keys) {
+  if (a.h.keys || a.h.tok_in) {
     const int qkv_rows = (a.q_heads + 2 * a.kv_heads) * head_dim;
     const TokenHandoff &h = a.h;
-    if (!a.qkv_table || a.ld_table < qkv_rows || !handoff_ok(h) || h.emb_width > 2048 || h.emb_width % 4 ||
-        (h.cur_table && h.cur_width > 2048))
+    if (!a.qkv_table || a.ld_table < qkv_rows) return hipErrorInvalidValue;
+    // tok_in: the token's table row only (the caller validates the token's range: the
+    // selection kernel that stores it draws from the table's vocabulary)
+    if (h.tok_in ? (h.keys != nullptr || h.cur_table != nullptr)
+                 : (!handoff_ok(h) || h.emb_width > 2048 || h.emb_width % 4 || (h.cur_table && h.cur_width > 2048)))
       return hipErrorInvalidValue;
     if (a.kv_bf16) {
       if (G == 1) launch_timed(k_attn_split<128, 1, uint16_t, 32, true, true>, grid, block, 0, s, t, a);
@@ -2644,7 +2653,8 @@ hipError_t launch_select_talker(const SelectTalkerArgs &a, hipStream_t s, int ro
 hipError_t launch_select_cp(const SelectCpArgs &a, hipStream_t s, int rows) {
   if (a.Vc > kMaxVocab) return hipErrorInvalidValue;
   if (rows < 1 || rows > kMaxRows ||
-      (rows > 1 && (!a.row_on || a.codes_row <= 0 || a.trailing_row <= 0 || (a.trace && a.trace_row <= 0))))
+      (rows > 1 && (!a.row_on || a.codes_row <= 0 || a.trailing_row <= 0 || (a.trace && a.trace_row <= 0) ||
+                    a.tok_out)))
     return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_select_cp, dim3(rows), dim3(1024), 0, s, a);
   return hipGetLastError();
