@@ -102,6 +102,15 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return ((uint64_t)hi << 32) | lo;
 }
 
+// Whether a kernel skips an ended stream's work: SKIP_DONE once it has ended, SKIP_TALKER
+// also for the Talker step after its last frame.
+__device__ __forceinline__ bool skip_state(const SlotState &sv, int mode) {
+  if (mode == SKIP_NEVER) return false;
+  if (sv.done) return true;
+  if (mode == SKIP_TALKER && sv.frame + 1 >= sv.max_frames) return true;
+  return false;
+}
+
 __device__ __forceinline__ bool skip_work(const SlotState *st, int mode) {
   if (mode == SKIP_NEVER) return false;
   if (st->done) return true;
@@ -532,14 +541,19 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   // A position given by the launch needs no state: the row mask and the stream state are
   // then checked after the loads below are issued (they are valid for any state).
   const bool frame_pos = a.pos_mode == POS_TALKER_FRAME;
+  int frame = 0, prefill_steps = 0;
   if (frame_pos) {
-    if (a.row_on && !a.row_on[row]) return;
-    if (skip_work(st, a.skip)) return;
+    // the row mask and the state in one round trip (both addresses are known)
+    const int on = a.row_on ? a.row_on[row] : 1;
+    const SlotState sv = *st;
+    if (!on || skip_state(sv, a.skip)) return;
+    frame = sv.frame;
+    prefill_steps = sv.prefill_steps;
   }
   const int h = blockIdx.x;
   const int c = OPROJ ? 0 : blockIdx.y;
   const int rb = OPROJ ? blockIdx.y : 0;  // output row block of the fused projection
-  const int pos = frame_pos ? st->prefill_steps + st->frame : a.pos_const;
+  const int pos = frame_pos ? prefill_steps + frame : a.pos_const;
   if (pos < 0 || pos >= a.cap) return;  // host validates; never index outside the cache
   const int L = pos + 1;
   const int nchunks = (L + CH - 1) / CH;
