@@ -11,12 +11,13 @@ import numpy as np
 import pytest
 import torch
 
+import hf_ref
 from oracle import model as om
 from q3t import synth
 
-# transformers' eager attention takes its softmax in float32 (the rest is float64 here), which
-# leaves ~1e-8 differences; a wrong sign, index or operand order shows up as O(0.1).
-HF_TOL = 1e-7
+# float64 throughout (tests/hf_ref.py): agreement is ~1e-14; a wrong sign, index or operand
+# order shows up as O(0.1).
+HF_TOL = 1e-10
 
 SHAPE = synth.StackShape(hidden=64, intermediate=96, layers=3, q_heads=4, kv_heads=2, head_dim=16,
                          vocab=32, rope_theta=1e4)
@@ -28,40 +29,8 @@ def _tensors(seed=3):
 
 
 def _hf_model(tensors):
-    from transformers.models.qwen3 import modeling_qwen3 as mq
-
-    cfg = mq.Qwen3Config(hidden_size=SHAPE.hidden, intermediate_size=SHAPE.intermediate,
-                         num_hidden_layers=SHAPE.layers, num_attention_heads=SHAPE.q_heads,
-                         num_key_value_heads=SHAPE.kv_heads, head_dim=SHAPE.head_dim,
-                         rms_norm_eps=SHAPE.rms_eps, vocab_size=SHAPE.vocab, max_position_embeddings=256,
-                         rope_parameters={"rope_type": "default", "rope_theta": SHAPE.rope_theta},
-                         attention_bias=False, attn_implementation="eager")
-    hf = mq.Qwen3Model(cfg).to(torch.float64).eval()
-    sd = {k[2:]: torch.from_numpy(synth.bf16_bits_to_f32(v).astype(np.float64))
-          for k, v in tensors.items() if k.startswith("m.")}
-    sd["embed_tokens.weight"] = torch.zeros(SHAPE.vocab, SHAPE.hidden, dtype=torch.float64)
-    missing, unexpected = hf.load_state_dict(sd, strict=False)
-    assert not unexpected
-    assert all("rotary" in m or "embed" in m for m in missing), missing
-
-    # transformers evaluates the RoPE angles in float32; supply the same angles in float64
-    # (HF's layout: cos/sin of cat(freqs, freqs)) so the comparison is exact to ~1e-12.
-    def rotary64(x, position_ids):
-        inv = 1.0 / (SHAPE.rope_theta ** (torch.arange(0, SHAPE.head_dim, 2, dtype=torch.float64) / SHAPE.head_dim))
-        freqs = position_ids[..., None].to(torch.float64) * inv
-        emb = torch.cat([freqs, freqs], dim=-1)
-        return emb.cos(), emb.sin()
-
-    hf.rotary_emb.forward = rotary64
-
-    # Qwen3RMSNorm casts its input to float32; evaluate the same formula in float64.
-    def norm64(self, h):
-        return self.weight * (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + self.variance_epsilon))
-
-    for mod in hf.modules():
-        if isinstance(mod, mq.Qwen3RMSNorm):
-            mod.forward = norm64.__get__(mod)
-    return hf
+    return hf_ref.qwen3_model(tensors, "m", SHAPE.hidden, SHAPE.intermediate, SHAPE.layers, SHAPE.q_heads,
+                              SHAPE.kv_heads, SHAPE.head_dim, SHAPE.rms_eps, SHAPE.rope_theta)
 
 
 def _oracle_stack(tensors, cap=64, dtype=np.float64):
