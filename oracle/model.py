@@ -25,6 +25,7 @@ position.  RoPE angles are ``pos * theta**(-2i/d)`` computed in float64.
 from __future__ import annotations
 
 import dataclasses
+import time
 from typing import Dict, List, Optional, Sequence
 
 import numpy as np
@@ -341,12 +342,14 @@ class Oracle:
     # -- frame loop -----------------------------------------------------------------------
     def rollout(self, prefill: np.ndarray, trailing_text: np.ndarray, tts_pad: np.ndarray,
                 opts: GenerateOptions, keep_cp_logits: int = 0,
-                forced_codes: Optional[np.ndarray] = None) -> RolloutTrace:
+                forced_codes: Optional[np.ndarray] = None, timings: Optional[dict] = None) -> RolloutTrace:
         """``HipTtsEngine::rollout`` (generation.rs:657-749).
 
         ``forced_codes`` ([F, 16]) teacher-forces the chosen tokens: logits are still
         computed from the oracle's own state, but the loop continues with the forced
-        tokens, so a GPU run can be checked step by step even past a near-tie.
+        tokens, so a GPU run can be checked step by step even past a near-tie.  ``timings``,
+        when given, receives the seconds of the prefill (``prefill_s``) and of the frames
+        after it (``frames_s``), the split the reference's GenerationProfile reports.
         """
         opts.validate()
         P = int(prefill.shape[0])
@@ -356,6 +359,7 @@ class Oracle:
             raise ValueError(f"requested {P + opts.max_frames} cache steps but engine was loaded for "
                              f"{self.max_cache_steps}")
         tcfg, ccfg = opts.talker_sampling(), opts.subtalker_sampling()
+        t0 = time.perf_counter()
         self.talker.reset()
         logits = self.prefill(prefill)
         u = philox.sampler_uniform(opts.seed, 0, 0) if tcfg.do_sample else None
@@ -363,6 +367,7 @@ class Oracle:
         if forced_codes is not None and len(forced_codes):
             semantic = int(forced_codes[0][0])
         t_logits, t_margins, t_hidden = [logits], [margin], [self.hidden.copy()]
+        t1 = time.perf_counter()
         codes, cp_margins, cp_logits, history = [], [], [], []
         ended = False
         for frame in range(opts.max_frames):
@@ -392,6 +397,9 @@ class Oracle:
                 t_logits.append(logits)
                 t_margins.append(margin)
                 t_hidden.append(self.hidden.copy())
+        if timings is not None:
+            timings["prefill_s"] = t1 - t0
+            timings["frames_s"] = time.perf_counter() - t1
         return RolloutTrace(
             codes=np.asarray(codes, dtype=np.int32).reshape(-1, self.num_code_groups),
             ended_by_eos=ended,

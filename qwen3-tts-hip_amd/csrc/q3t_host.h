@@ -58,26 +58,34 @@ inline float bf16_to_f32_host(uint16_t b) {
 // ------------------------------------------------------------------------------------
 class SafeTensors {
  public:
+  // The file stays mapped for the object's lifetime.  A constructor that throws releases the
+  // mapping and the descriptor itself (the destructor does not run then).
   explicit SafeTensors(const std::string &path) : path_(path) {
     fd_ = open(path.c_str(), O_RDONLY);
     if (fd_ < 0) fail(Q3T_ERR_NOT_FOUND, "cannot open %s", path.c_str());
-    struct stat sb;
-    fstat(fd_, &sb);
-    size_ = (size_t)sb.st_size;
-    if (size_ < 8) fail(Q3T_ERR_INVALID, "%s is not a safetensors file", path.c_str());
-    base_ = (const uint8_t *)mmap(nullptr, size_, PROT_READ, MAP_PRIVATE, fd_, 0);
-    if (base_ == MAP_FAILED) fail(Q3T_ERR_INVALID, "mmap of %s failed", path.c_str());
-    uint64_t hlen;
-    memcpy(&hlen, base_, 8);
-    if (8 + hlen > size_) fail(Q3T_ERR_INVALID, "%s: header length out of range", path.c_str());
-    header_ = json::parse(std::string((const char *)base_ + 8, hlen));
-    data_ = base_ + 8 + hlen;
-    data_size_ = size_ - 8 - hlen;
+    try {
+      struct stat sb;
+      if (fstat(fd_, &sb) != 0) fail(Q3T_ERR_INVALID, "cannot stat %s", path.c_str());
+      size_ = (size_t)sb.st_size;
+      if (size_ < 8) fail(Q3T_ERR_INVALID, "%s is not a safetensors file", path.c_str());
+      void *m = mmap(nullptr, size_, PROT_READ, MAP_PRIVATE, fd_, 0);
+      if (m == MAP_FAILED) fail(Q3T_ERR_INVALID, "mmap of %s failed", path.c_str());
+      base_ = (const uint8_t *)m;
+      uint64_t hlen;
+      memcpy(&hlen, base_, 8);
+      if (hlen > size_ - 8) fail(Q3T_ERR_INVALID, "%s: header length out of range", path.c_str());
+      header_ = json::parse(std::string((const char *)base_ + 8, (size_t)hlen));
+      data_ = base_ + 8 + hlen;
+      data_size_ = size_ - 8 - (size_t)hlen;
+      validate_header();
+    } catch (...) {
+      release();
+      throw;
+    }
   }
-  ~SafeTensors() {
-    if (base_ && base_ != MAP_FAILED) munmap((void *)base_, size_);
-    if (fd_ >= 0) close(fd_);
-  }
+  ~SafeTensors() { release(); }
+  SafeTensors(const SafeTensors &) = delete;
+  SafeTensors &operator=(const SafeTensors &) = delete;
 
   // Appends the tensor (as bf16) to out, checking its shape.
   void append_bf16(const std::string &name, const std::vector<int64_t> &shape, std::vector<uint16_t> &out) const {
@@ -87,16 +95,22 @@ class SafeTensors {
     if (dtype == "BF16") {
       memcpy(out.data() + at, ptr, n * 2);
     } else {
-      const float *f = (const float *)ptr;
-      for (size_t i = 0; i < n; ++i) out[at + i] = f32_to_bf16_host(f[i]);
+      for (size_t i = 0; i < n; ++i) {
+        float f;
+        memcpy(&f, ptr + 4 * i, 4);  // data offsets need not be 4-byte aligned
+        out[at + i] = f32_to_bf16_host(f);
+      }
     }
   }
   std::vector<float> f32(const std::string &name, const std::vector<int64_t> &shape) const {
     const auto [ptr, dtype, n] = view(name, shape);
     std::vector<float> out(n);
     if (dtype == "BF16") {
-      const uint16_t *b = (const uint16_t *)ptr;
-      for (size_t i = 0; i < n; ++i) out[i] = bf16_to_f32_host(b[i]);
+      for (size_t i = 0; i < n; ++i) {
+        uint16_t b;
+        memcpy(&b, ptr + 2 * i, 2);
+        out[i] = bf16_to_f32_host(b);
+      }
     } else {
       memcpy(out.data(), ptr, n * 4);
     }
@@ -135,10 +149,49 @@ class SafeTensors {
       fail(Q3T_ERR_INVALID, "%s shape [%s] does not match expected [%s]", name.c_str(), got.c_str(), want.c_str());
     }
     const auto &off = t.at("data_offsets").arr;
-    const size_t b = (size_t)off[0].integer(), e = (size_t)off[1].integer();
-    const size_t esz = dtype == "BF16" ? 2 : 4;
-    if (e > data_size_ || e - b != n * esz) fail(Q3T_ERR_INVALID, "%s: data offsets out of range", name.c_str());
+    if (off.size() != 2) fail(Q3T_ERR_INVALID, "%s: data_offsets must hold two integers", name.c_str());
+    const int64_t b = off[0].integer(), e = off[1].integer();
+    const uint64_t esz = dtype == "BF16" ? 2 : 4;
+    if (b < 0 || e < b || (uint64_t)e > (uint64_t)data_size_ || (uint64_t)(e - b) != (uint64_t)n * esz)
+      fail(Q3T_ERR_INVALID, "%s: data offsets [%lld, %lld) do not hold %zu elements inside the %zu data bytes",
+           name.c_str(), (long long)b, (long long)e, n, data_size_);
     return {data_ + b, dtype, n};
+  }
+  // Every entry of the header (the format's optional __metadata__ aside) must describe a
+  // byte range inside the data section that holds exactly its shape's elements, so no later
+  // view can point outside the mapping.
+  void validate_header() const {
+    if (header_.kind != json::Value::Object) fail(Q3T_ERR_INVALID, "%s: header is not an object", path_.c_str());
+    for (const auto &kv : header_.obj) {
+      if (kv.first == "__metadata__") continue;
+      const json::Value &t = kv.second;
+      const std::string &dtype = t.at("dtype").str;
+      uint64_t esz = 0;
+      if (dtype == "BF16" || dtype == "F16" || dtype == "I16" || dtype == "U16") esz = 2;
+      else if (dtype == "F32" || dtype == "I32" || dtype == "U32") esz = 4;
+      else if (dtype == "F64" || dtype == "I64" || dtype == "U64") esz = 8;
+      else if (dtype == "BOOL" || dtype == "U8" || dtype == "I8") esz = 1;
+      else fail(Q3T_ERR_INVALID, "%s: tensor %s has unknown dtype %s", path_.c_str(), kv.first.c_str(), dtype.c_str());
+      uint64_t n = 1;
+      for (const json::Value &d : t.at("shape").arr) {
+        const int64_t x = d.integer();
+        if (x < 0 || (x > 0 && n > (UINT64_MAX / 8) / (uint64_t)x))
+          fail(Q3T_ERR_INVALID, "%s: tensor %s has an invalid shape", path_.c_str(), kv.first.c_str());
+        n *= (uint64_t)x;
+      }
+      const auto &off = t.at("data_offsets").arr;
+      if (off.size() != 2) fail(Q3T_ERR_INVALID, "%s: data_offsets must hold two integers", kv.first.c_str());
+      const int64_t b = off[0].integer(), e = off[1].integer();
+      if (b < 0 || e < b || (uint64_t)e > (uint64_t)data_size_ || (uint64_t)(e - b) != n * esz)
+        fail(Q3T_ERR_INVALID, "%s: data offsets [%lld, %lld) do not hold %llu elements inside the %zu data bytes",
+             kv.first.c_str(), (long long)b, (long long)e, (unsigned long long)n, data_size_);
+    }
+  }
+  void release() {
+    if (base_) munmap((void *)base_, size_);
+    if (fd_ >= 0) close(fd_);
+    base_ = nullptr;
+    fd_ = -1;
   }
 
   std::string path_;

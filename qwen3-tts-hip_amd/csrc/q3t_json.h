@@ -30,7 +30,14 @@ struct Value {
     if (kind != Number) throw std::runtime_error("json: expected a number");
     return num;
   }
-  int64_t integer() const { return (int64_t)number(); }
+  // An integral number within +-2^53 (exact in a double); anything else is an error, so a
+  // crafted header cannot reach an out-of-range conversion.
+  int64_t integer() const {
+    const double x = number();
+    if (!(x >= -9007199254740992.0 && x <= 9007199254740992.0) || x != (double)(int64_t)x)
+      throw std::runtime_error("json: expected an integer");
+    return (int64_t)x;
+  }
 };
 
 class Parser {

@@ -3,9 +3,11 @@
     python tests/golden/make_golden.py [workload ...]
 
 Each fixture holds one oracle rollout of a workload from q3t/workloads.py: the codes,
-the raw Talker logits (float16; the parity tolerance is 2e-2), the top-2 margins of every
-argmax (for the near-tie policy) and the first frames' CodePredictor logits, plus the
-weight checksum so a test can tell that it rebuilt the same synthetic model.
+the raw Talker logits (every row as float16 for the 2e-2 bound, and the first rows again as
+float32 so the measured error is not the fixture's rounding), the top-2 margins of every
+argmax (printed when a parity check fails) and the first frames' CodePredictor logits
+(float32), plus the weight checksum so a test can tell that it rebuilt the same synthetic
+model.
 
 A multi-stream workload (MULTI_WORKLOADS) holds one independent single-stream rollout per
 stream (streams do not interact), with the first Talker logit rows of each.
@@ -30,6 +32,7 @@ from q3t.workloads import MULTI_WORKLOADS, WORKLOADS  # noqa: E402
 
 # Talker-logit rows kept per fixture (the codes and margins are always complete).
 MAX_LOGIT_ROWS = 256
+F32_LOGIT_ROWS = 48
 CP_LOGIT_FRAMES = 2
 MULTI_LOGIT_ROWS = 4
 
@@ -51,8 +54,9 @@ def make(name: str) -> str:
     np.savez_compressed(
         path, meta=np.array(json.dumps(meta)), codes=tr.codes,
         talker_logits=tr.talker_logits[:MAX_LOGIT_ROWS].astype(np.float16),
+        talker_logits_f32=tr.talker_logits[:F32_LOGIT_ROWS].astype(np.float32),
         talker_margins=tr.talker_margins, cp_margins=tr.cp_margins,
-        cp_logits=np.asarray(tr.cp_logits, dtype=np.float16),
+        cp_logits=np.asarray(tr.cp_logits, dtype=np.float32),
         prefill_sum=np.array([float(np.sum(inputs.prefill, dtype=np.float64))]))
     print(f"{name}: {tr.frames} frames, eos={tr.ended_by_eos}, {meta['seconds']} s -> {path}", flush=True)
     return path
@@ -118,7 +122,7 @@ def make_multi(name: str) -> str:
         arrays[f"codes_{j}"] = tr.codes
         arrays[f"talker_margins_{j}"] = tr.talker_margins
         arrays[f"cp_margins_{j}"] = tr.cp_margins
-        arrays[f"talker_logits_{j}"] = tr.talker_logits[:MULTI_LOGIT_ROWS].astype(np.float16)
+        arrays[f"talker_logits_{j}"] = tr.talker_logits[:MULTI_LOGIT_ROWS].astype(np.float32)
         frames.append(tr.frames)
         eos.append(bool(tr.ended_by_eos))
         print(f"  stream {j}: P={inp.prefill_steps} frames={tr.frames} ({time.time() - t0:.0f} s)", flush=True)
@@ -133,7 +137,7 @@ def make_multi(name: str) -> str:
 
 
 if __name__ == "__main__":
-    names = sys.argv[1:] or ([n for n in WORKLOADS if not n.startswith("cfg1")] + list(MULTI_WORKLOADS) +
+    names = sys.argv[1:] or (list(WORKLOADS) + list(MULTI_WORKLOADS) +
                              [f"hooks_{s}" for s in HOOK_WORKLOADS])
     for n in names:
         if n.startswith("hooks_"):

@@ -115,3 +115,32 @@ def test_null_arguments():
     assert lib.q3t_generate_options_validate(None) == E.Q3T_ERR_INVALID
     assert lib.q3t_engine_destroy(None) == E.Q3T_OK
     assert lib.q3t_stream_destroy(None) == E.Q3T_OK
+
+
+def _weights_file(tmp_path, header, data=b"\0" * 64, hlen=None):
+    import struct
+    h = json.dumps(header).encode()
+    (tmp_path / "model.safetensors").write_bytes(struct.pack("<Q", len(h) if hlen is None else hlen) + h + data)
+
+
+@pytest.mark.parametrize("header,hlen,match", [
+    ({"a": {"dtype": "BF16", "shape": [4], "data_offsets": [-8, 0]}}, None, "data offsets"),
+    ({"a": {"dtype": "BF16", "shape": [4], "data_offsets": [8, 0]}}, None, "data offsets"),
+    ({"a": {"dtype": "BF16", "shape": [40], "data_offsets": [0, 80]}}, None, "data offsets"),
+    ({"a": {"dtype": "F32", "shape": [4], "data_offsets": [0, 8]}}, None, "data offsets"),
+    ({"a": {"dtype": "F32", "shape": [4], "data_offsets": [0, 16.5]}}, None, "integer"),
+    ({"a": {"dtype": "F32", "shape": [4], "data_offsets": [0, 1e30]}}, None, "integer"),
+    ({"a": {"dtype": "F32", "shape": [-4], "data_offsets": [0, 16]}}, None, "shape"),
+    ({"a": {"dtype": "F32", "shape": [4], "data_offsets": [0]}}, None, "data_offsets"),
+    ({"a": {"dtype": "Q4", "shape": [4], "data_offsets": [0, 16]}}, None, "dtype"),
+    ({}, (1 << 64) - 1, "header length"),
+    ({}, 1 << 20, "header length"),
+])
+def test_malformed_weights_header_rejected_before_any_gpu_call(tmp_path, header, hlen, match):
+    """Every tensor entry of model.safetensors must describe a byte range inside the data
+    section that holds exactly its shape; the whole header is checked when the file is
+    opened, before any device call."""
+    d = _config_dir(tmp_path)
+    _weights_file(tmp_path, {"__metadata__": {"format": "pt"}, **header}, hlen=hlen)
+    with pytest.raises(E.InvalidInputError, match=match):
+        E.HipTtsEngine(d)

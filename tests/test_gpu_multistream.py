@@ -12,7 +12,7 @@ import pytest
 from q3t import engine as E
 from q3t.workloads import MULTI_WORKLOADS
 
-from parity import LOGIT_TOL, check_codes, fixture_exists, load_fixture
+from parity import LOGIT_TOL, check_codes, load_fixture
 
 pytestmark = pytest.mark.gpu
 
@@ -76,8 +76,7 @@ def test_tiny_multistream_matches_oracle(models):
     r = run_batch(models, name, trace=True)
     for j in range(w.streams):
         sf = stream_fixture(fx, j)
-        greedy = not w.options_kwargs()[j]["do_sample"]
-        same = check_codes(r["codes"][j], r["eos"][j], sf, allow_ties=greedy)
+        same = check_codes(r["codes"][j], r["eos"][j], sf)
         rows = min(len(sf["talker_logits"]), same + 1)
         err = float(np.abs(r["logits"][j][:rows] - sf["talker_logits"][:rows].astype(np.float32)).max())
         print(f"stream {j}: {same} frames identical, talker logit err {err:.2e}")
@@ -162,25 +161,29 @@ def test_streams_start_reports_busy_and_capacity(models):
             eng.start_streams(inputs[:1], [big], lk)
 
 
-@pytest.mark.skipif(not fixture_exists("cfg5_0.6b_multistream"), reason="config-5 fixture not generated")
-def test_cfg5_sixteen_streams_match_oracle(models):
+@pytest.mark.parametrize("trace", [False, True])
+def test_cfg5_sixteen_streams_match_oracle(models, trace):
+    """every stream's codes equal its float64 single-stream rollout over its
+    whole length.  Untraced is the path bench.py times: an all-greedy batch hands each
+    CodePredictor group's token to the next group through the LM head's per-row argmax keys
+    and the layer-0 q/k/v table rows.  Traced, the batch takes the selection kernels and
+    records the Talker logits, which are held to 2e-2."""
     name = "cfg5_0.6b_multistream"
     fx = load_fixture(name)
     w = MULTI_WORKLOADS[name]
     model, _ = models.get(w.spec, w.weight_seed)
     assert model.checksum() == fx["meta"]["checksum"]
-    r = run_batch(models, name, trace=True)
-    identical = 0
+    r = run_batch(models, name, trace=trace)
     for j in range(w.streams):
         sf = stream_fixture(fx, j)
         same = check_codes(r["codes"][j], r["eos"][j], sf)
-        identical += same == len(sf["codes"])
-        rows = min(len(sf["talker_logits"]), same + 1)
-        err = float(np.abs(r["logits"][j][:rows] - sf["talker_logits"][:rows].astype(np.float32)).max())
-        print(f"stream {j}: P={fx['meta']['prefill_steps'][j]} {same}/{len(sf['codes'])} frames identical, "
-              f"talker logit err {err:.2e}")
-        assert err <= LOGIT_TOL
-    print(f"{identical}/{w.streams} streams bit-identical over every frame")
+        msg = f"stream {j}: P={fx['meta']['prefill_steps'][j]} {same}/{len(sf['codes'])} frames identical"
+        if trace:
+            rows = min(len(sf["talker_logits"]), same + 1)
+            err = float(np.abs(r["logits"][j][:rows] - sf["talker_logits"][:rows].astype(np.float32)).max())
+            msg += f", talker logit err {err:.2e}"
+            assert err <= LOGIT_TOL
+        print(msg)
 
 
 def test_batched_stream_ends_by_eos_while_others_continue(models, tmp_path):

@@ -12,7 +12,8 @@ from q3t import engine as E
 from q3t import synth
 from q3t.workloads import WORKLOADS
 
-from parity import LOGIT_TOL, check_codes, check_talker_logits, fixture_exists, load_fixture
+from parity import (LOGIT_TOL, check_codes, check_codes_near_tie, check_cp_logits, check_talker_logits,
+                    load_fixture)
 
 pytestmark = pytest.mark.gpu
 
@@ -51,11 +52,10 @@ def test_small_workloads_match_fixture(models, name):
     model, _ = models.get(fx["meta"]["spec"], fx["meta"]["weight_seed"])
     assert model.checksum() == fx["meta"]["checksum"]
     r = run(models, name)
-    same = check_codes(r["codes"], r["eos"], fx, allow_ties=not WORKLOADS[name].do_sample)
+    same = check_codes(r["codes"], r["eos"], fx)
     err = check_talker_logits(r["talker_logits"], fx, same)
-    cp_err = float(np.abs(r["cp_logits"][:len(fx["cp_logits"])] - fx["cp_logits"].astype(np.float32)).max())
+    cp_err = check_cp_logits(r["cp_logits"], fx)
     print(f"{name}: {same} frames identical, talker logit err {err:.2e}, cp logit err {cp_err:.2e}")
-    assert cp_err <= LOGIT_TOL
 
 
 def test_chunking_and_generate_codes_agree(models):
@@ -148,7 +148,7 @@ def test_sampled_talker_with_greedy_subtalker_matches_oracle(models):
                                     repetition_penalty=1.05, seed=11)
     r = run(models, "tiny_greedy", options=opts)
     fx = _as_fixture(_oracle_rollout(model, inputs, opts, w.max_cache_steps))
-    same = check_codes(r["codes"], r["eos"], fx, allow_ties=False)
+    same = check_codes(r["codes"], r["eos"], fx)
     check_talker_logits(r["talker_logits"], fx, same)
     print(f"sampled Talker + greedy CodePredictor: {same} frames identical")
 
@@ -166,7 +166,7 @@ def test_one_query_head_per_kv_head_matches_oracle(models, sampled):
     opts = E.GenerateOptions.greedy(12, **kw)
     r = run(models, "tiny_greedy", options=opts, inputs=inputs, model_dir=d, cap=64)
     fx = _as_fixture(_oracle_rollout(model, inputs, opts, 64))
-    same = check_codes(r["codes"], r["eos"], fx, allow_ties=not sampled)
+    same = check_codes(r["codes"], r["eos"], fx)
     err = check_talker_logits(r["talker_logits"], fx, same)
     print(f"tiny-g1 sampled={sampled}: {same} frames identical, talker logit err {err:.2e}")
 
@@ -179,7 +179,7 @@ def test_bf16_kv_cache_matches_bf16_oracle(models):
                          kv_bf16=True)
     r = run(models, "tiny_greedy", kv_bf16=True)
     fx = _as_fixture(tr)
-    same = check_codes(r["codes"], r["eos"], fx)
+    same = check_codes_near_tie(r["codes"], r["eos"], fx)
     check_talker_logits(r["talker_logits"], fx, same)
 
 
@@ -286,16 +286,20 @@ def test_two_stream_slots_are_independent(models):
     np.testing.assert_array_equal(np.concatenate(out_b), ref)
 
 
-@pytest.mark.parametrize("name", ["cfg2_0.6b_greedy", "cfg3_0.6b_sampled", "cfg4_1.7b_greedy"])
+@pytest.mark.parametrize("name", ["cfg1_cpu_0.6b", "cfg2_0.6b_greedy", "cfg3_0.6b_sampled", "cfg4_1.7b_greedy"])
 def test_baseline_workloads_match_fixture(models, name):
-    if not fixture_exists(name):
-        pytest.skip(f"fixture {name} not generated")
+    """BASELINE configs 1-4 against their float64 fixtures: every frame's 16 codes, the frame
+    count and the EOS flag identical; Talker logits of every row and the first frames'
+    CodePredictor logits within 2e-2.  Config 1 is the reference's CPU case (non-streaming,
+    P = 41, 40 frames), run here on the GPU path."""
     fx = load_fixture(name)
     model, _ = models.get(fx["meta"]["spec"], fx["meta"]["weight_seed"])
     assert model.checksum() == fx["meta"]["checksum"]
     r = run(models, name)
-    same = check_codes(r["codes"], r["eos"], fx, allow_ties=not WORKLOADS[name].do_sample)
+    same = check_codes(r["codes"], r["eos"], fx)
     err = check_talker_logits(r["talker_logits"], fx, same)
-    print(f"{name}: {same}/{len(fx['codes'])} frames identical, talker logit max err {err:.2e}")
+    cp_err = check_cp_logits(r["cp_logits"], fx)
+    print(f"{name}: {same}/{len(fx['codes'])} frames identical, talker logit max err {err:.2e}, "
+          f"CodePredictor logit max err {cp_err:.2e}")
     if name.startswith("cfg4"):
         models.drop(fx["meta"]["spec"], fx["meta"]["weight_seed"])
