@@ -155,6 +155,18 @@ int q3t_prepare_text(q3t_engine *engine, const int32_t *content_ids, int32_t n_i
                      int32_t language, int32_t text_lookahead_tokens, float *prefill, int32_t *prefill_steps,
                      float *trailing, int32_t *trailing_steps, float *tts_pad);
 
+/* q3t_prepare_text without any device allocation.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, rows and errors as q3t_prepare_text; its workspace and staging
+ * rows live in a statically sized per-GPU array of 16 MiB (the GEMMs' K-split partials stay in
+ * the engine's own workspace, allocated at q3t_engine_create), which bounds the prompt: about
+ * 650 content ids at Talker hidden 1024 and 500 at 2048 (text_hidden 2048), Q3T_ERR_INVALID
+ * beyond.  Every call on one GPU shares that array, from any engine: calls that overlap on one
+ * GPU (another thread) race and must be serialised by the caller. */
+int q3t_prepare_text_noalloc(q3t_engine *engine, const int32_t *content_ids, int32_t n_ids, int32_t speaker,
+                             int32_t language, int32_t text_lookahead_tokens, float *prefill,
+                             int32_t *prefill_steps, float *trailing, int32_t *trailing_steps, float *tts_pad);
+
 /* HipTtsEngine::start_stream (generation.rs:421-440) from content token ids: the rows
  * q3t_prepare_text describes are built on the device straight into the stream's slot (no
  * host round trip), then as q3t_stream_start.  The speaker and language come from opts. */

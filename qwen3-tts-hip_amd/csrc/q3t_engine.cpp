@@ -257,6 +257,8 @@ struct Engine {
   // K-split partial sums of prompt-prefill and text-projection GEMMs over few rows
   static constexpr int64_t kSplitFloats = (int64_t)4 << 20;
   float *split_ws = nullptr;
+  // result of resolving the device's no-allocation scratch at creation
+  hipError_t scratch_status = hipErrorNotInitialized;
   // Prompt preparation on the device (text.rs:516-603), when the checkpoint holds
   // talker.model.text_embedding.weight: the table [text_vocab][text_hidden] and the text
   // projection fc1 [tp_inter][text_hidden] + bias, fc2 [H][tp_inter] + bias.
@@ -1233,6 +1235,8 @@ int q3t_engine_create(const q3t_engine_options *opts, q3t_engine **out) {
 
     SafeTensors st(dir + "/model.safetensors");
     HIPC(hipSetDevice(e->device));
+    // the no-allocation scratch of this device (kept by the library until the process ends)
+    e->scratch_status = noalloc_scratch_setup(e->device);
     int64_t &tally = e->device_bytes;
     load_stack(st, "talker.model", td, e->cap, e->talker, tally);
     load_stack(st, "talker.code_predictor.model", cd, e->groups, e->cp, tally);
@@ -1520,52 +1524,78 @@ TextPlan plan_trailing_rows(const Engine &e, const int32_t *ids, int n, int firs
   return p;
 }
 
-// Runs a TextPlan on stream s: text-embedding gather -> fc1 (+ bias) -> SiLU -> fc2 (+ bias)
-// -> plus codec rows, into prefill / trailing / pad (device pointers).  Synchronous.
-void prepare_text_device(Engine &e, const TextPlan &p, float *prefill, float *trailing, float *pad, hipStream_t s) {
+// Device workspace of one TextPlan run: ids / codec ids / destinations (3M int32), the
+// gathered text-embedding rows X [M, text_hidden], the fc1 activations [M, tp_inter], the fc2
+// output Y [M, H] and, for voice clone, the x-vector [H]; each part 256-byte aligned.
+struct TextWorkspace {
+  int32_t *ids = nullptr;
+  float *X = nullptr, *Hd = nullptr, *Y = nullptr, *xvec = nullptr;
+};
+
+inline size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+size_t text_workspace_bytes(const Engine &e, const TextPlan &p) {
+  const size_t M = p.ids.size();
+  return align256(M * 4 * 3) + align256(M * e.text_hidden * 4) + align256(M * e.tp_inter * 4) +
+         align256(M * e.talker_hidden * 4) + align256(p.xvec.size() * 4);
+}
+
+TextWorkspace carve_text_workspace(const Engine &e, const TextPlan &p, char *base) {
+  const size_t M = p.ids.size();
+  TextWorkspace w;
+  w.ids = (int32_t *)base;
+  base += align256(M * 4 * 3);
+  w.X = (float *)base;
+  base += align256(M * e.text_hidden * 4);
+  w.Hd = (float *)base;
+  base += align256(M * e.tp_inter * 4);
+  w.Y = (float *)base;
+  base += align256(M * e.talker_hidden * 4);
+  if (!p.xvec.empty()) w.xvec = (float *)base;
+  return w;
+}
+
+// Runs a TextPlan on stream s in the workspace w: text-embedding gather -> fc1 (+ bias) -> SiLU
+// -> fc2 (+ bias) -> plus codec rows, into prefill / trailing / pad (device pointers).  Every
+// workspace part is written before it is read (nothing needs to start at zero).  Synchronous.
+void run_text_plan(Engine &e, const TextPlan &p, const TextWorkspace &w, float *prefill, float *trailing, float *pad,
+                   hipStream_t s) {
   const int M = (int)p.ids.size(), H = e.talker_hidden;
+  int32_t *ids = w.ids, *codec = w.ids + M, *dst = w.ids + 2 * M;
+  if (!p.xvec.empty())
+    HIPC(hipMemcpyAsync(w.xvec, p.xvec.data(), p.xvec.size() * 4, hipMemcpyHostToDevice, s));
+  std::vector<int32_t> host(p.ids);
+  host.insert(host.end(), p.codec.begin(), p.codec.end());
+  host.insert(host.end(), p.dst.begin(), p.dst.end());
+  HIPC(hipMemcpyAsync(ids, host.data(), host.size() * 4, hipMemcpyHostToDevice, s));
+  hip_check(launch_text_gather(e.text_emb, e.text_hidden, ids, M, w.X, s), "launch_text_gather");
+  GemmArgs g{};
+  g.X = w.X; g.ldx = e.text_hidden; g.W = e.tp_fc1; g.bias = e.tp_b1; g.Y = w.Hd; g.ldy = e.tp_inter;
+  g.M = M; g.N = e.tp_inter; g.K = e.text_hidden;
+  g.split_ws = e.split_ws; g.split_cap = Engine::kSplitFloats;
+  hip_check(launch_gemm(EPI_BIAS, g, s), "launch_gemm(text fc1)");
+  hip_check(launch_silu(w.Hd, (size_t)M * e.tp_inter, s), "launch_silu");
+  g = GemmArgs{};
+  g.X = w.Hd; g.ldx = e.tp_inter; g.W = e.tp_fc2; g.bias = e.tp_b2; g.Y = w.Y; g.ldy = H;
+  g.M = M; g.N = H; g.K = e.tp_inter;
+  g.split_ws = e.split_ws; g.split_cap = Engine::kSplitFloats;
+  hip_check(launch_gemm(EPI_BIAS, g, s), "launch_gemm(text fc2)");
+  hip_check(launch_text_assemble(w.Y, H, M, codec, e.codec_emb, w.xvec, dst, prefill, trailing, pad, s),
+            "launch_text_assemble");
+  HIPC(hipStreamSynchronize(s));
+}
+
+// run_text_plan in a workspace allocated for the call.
+void prepare_text_device(Engine &e, const TextPlan &p, float *prefill, float *trailing, float *pad, hipStream_t s) {
   int64_t bytes = 0;
-  std::vector<void *> owned;
-  auto take = [&](size_t n) {
-    void *q = dev_alloc<char>(n, bytes);
-    owned.push_back(q);
-    return q;
-  };
+  char *base = dev_alloc<char>(text_workspace_bytes(e, p), bytes);
   try {
-    int32_t *ids = (int32_t *)take((size_t)M * 4 * 3);
-    int32_t *codec = ids + M, *dst = ids + 2 * M;
-    float *X = (float *)take((size_t)M * e.text_hidden * 4);
-    float *Hd = (float *)take((size_t)M * e.tp_inter * 4);
-    float *Y = (float *)take((size_t)M * H * 4);
-    float *xvec = nullptr;
-    if (!p.xvec.empty()) {
-      xvec = (float *)take(p.xvec.size() * 4);
-      HIPC(hipMemcpyAsync(xvec, p.xvec.data(), p.xvec.size() * 4, hipMemcpyHostToDevice, s));
-    }
-    std::vector<int32_t> host(p.ids);
-    host.insert(host.end(), p.codec.begin(), p.codec.end());
-    host.insert(host.end(), p.dst.begin(), p.dst.end());
-    HIPC(hipMemcpyAsync(ids, host.data(), host.size() * 4, hipMemcpyHostToDevice, s));
-    hip_check(launch_text_gather(e.text_emb, e.text_hidden, ids, M, X, s), "launch_text_gather");
-    GemmArgs g{};
-    g.X = X; g.ldx = e.text_hidden; g.W = e.tp_fc1; g.bias = e.tp_b1; g.Y = Hd; g.ldy = e.tp_inter;
-    g.M = M; g.N = e.tp_inter; g.K = e.text_hidden;
-    g.split_ws = e.split_ws; g.split_cap = Engine::kSplitFloats;
-    hip_check(launch_gemm(EPI_BIAS, g, s), "launch_gemm(text fc1)");
-    hip_check(launch_silu(Hd, (size_t)M * e.tp_inter, s), "launch_silu");
-    g = GemmArgs{};
-    g.X = Hd; g.ldx = e.tp_inter; g.W = e.tp_fc2; g.bias = e.tp_b2; g.Y = Y; g.ldy = H;
-    g.M = M; g.N = H; g.K = e.tp_inter;
-    g.split_ws = e.split_ws; g.split_cap = Engine::kSplitFloats;
-    hip_check(launch_gemm(EPI_BIAS, g, s), "launch_gemm(text fc2)");
-    hip_check(launch_text_assemble(Y, H, M, codec, e.codec_emb, xvec, dst, prefill, trailing, pad, s),
-              "launch_text_assemble");
-    HIPC(hipStreamSynchronize(s));
+    run_text_plan(e, p, carve_text_workspace(e, p, base), prefill, trailing, pad, s);
   } catch (...) {
-    for (void *q : owned) (void)hipFree(q);
+    (void)hipFree(base);
     throw;
   }
-  for (void *q : owned) (void)hipFree(q);
+  (void)hipFree(base);
 }
 
 q3t_stream *new_stream(Engine &e, int slot, int max_frames) {
@@ -1720,6 +1750,36 @@ int q3t_prepare_text(q3t_engine *e, const int32_t *content_ids, int32_t n_ids, i
       fail(Q3T_ERR_INVALID, "null argument");
     const TextPlan p = plan_text(*e, content_ids, n_ids, speaker, language, text_lookahead_tokens, n_ids + 1);
     prepare_text_to_host(e, p, prefill, prefill_steps, trailing, trailing_steps, tts_pad);
+  });
+}
+
+int q3t_prepare_text_noalloc(q3t_engine *e, const int32_t *content_ids, int32_t n_ids, int32_t speaker,
+                             int32_t language, int32_t text_lookahead_tokens, float *prefill, int32_t *prefill_steps,
+                             float *trailing, int32_t *trailing_steps, float *tts_pad) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!e || !prefill || !prefill_steps || !trailing || !trailing_steps || !tts_pad)
+      fail(Q3T_ERR_INVALID, "null argument");
+    const TextPlan p = plan_text(*e, content_ids, n_ids, speaker, language, text_lookahead_tokens, n_ids + 1);
+    // scratch layout: the plan's workspace, then the output rows [prefill | trailing | pad]
+    const size_t H = (size_t)e->talker_hidden, rows = (size_t)p.prefill_steps + p.trailing_steps + 1;
+    const size_t ws = text_workspace_bytes(*e, p), need = ws + rows * H * 4;
+    if (need > kNoAllocScratchBytes)
+      fail(Q3T_ERR_INVALID,
+           "%d content ids need %zu bytes of device scratch; q3t_prepare_text_noalloc holds at most %zu "
+           "(use q3t_prepare_text for longer prompts)",
+           n_ids, need, kNoAllocScratchBytes);
+    if (e->scratch_status != hipSuccess) hip_check(e->scratch_status, "hipGetSymbolAddress(scratch)");
+    HIPC(hipSetDevice(e->device));
+    char *base = (char *)noalloc_scratch(e->device);
+    if (!base) fail(Q3T_ERR_HIP, "no device scratch on device %d", e->device);
+    float *d = (float *)(base + ws), *dt = d + (size_t)p.prefill_steps * H, *dp = dt + (size_t)p.trailing_steps * H;
+    run_text_plan(*e, p, carve_text_workspace(*e, p, base), d, dt, dp, e->pools.stream);
+    HIPC(hipMemcpy(prefill, d, (size_t)p.prefill_steps * H * 4, hipMemcpyDeviceToHost));
+    HIPC(hipMemcpy(trailing, dt, (size_t)p.trailing_steps * H * 4, hipMemcpyDeviceToHost));
+    HIPC(hipMemcpy(tts_pad, dp, H * 4, hipMemcpyDeviceToHost));
+    *prefill_steps = p.prefill_steps;
+    *trailing_steps = p.trailing_steps;
   });
 }
 

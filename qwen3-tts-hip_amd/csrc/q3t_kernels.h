@@ -99,4 +99,13 @@ hipError_t launch_sample_draws(const float *logits, int V, const SamplingParams 
 // Largest vocabulary the select kernels hold in LDS.
 constexpr int kMaxVocab = 4096;
 
+// Device scratch of the entry points that allocate nothing (q3t_prepare_text_noalloc): one
+// statically sized array per GPU, shared by every call on that GPU (calls that overlap on one
+// GPU race).  noalloc_scratch_setup resolves the array's address on the current device (once
+// per device; call it with that device current); noalloc_scratch returns it (nullptr before
+// a successful setup).
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+hipError_t noalloc_scratch_setup(int device);
+void *noalloc_scratch(int device);
+
 }  // namespace q3t

@@ -9,6 +9,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include <hip/hip_ext.h>
 
@@ -2680,6 +2681,39 @@ hipError_t launch_sample_draws(const float *logits, int V, const SamplingParams 
   hipLaunchKernelGGL(k_sample_draws, dim3(n), dim3(1024), 0, s, logits, V, sp, (uint32_t)(seed & 0xffffffffu),
                      (uint32_t)(seed >> 32), kind, out);
   return hipGetLastError();
+}
+
+// The no-allocation scratch.  Each GPU holds its own copy of the array, at its own address,
+// until the process ends.  In host code `scratch` names a host-side stand-in, never a device
+// address: host code uses only the pointer hipGetSymbolAddress returns for the device.
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+hipError_t noalloc_scratch_setup(int device) {
+  if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device]) return hipSuccess;
+  int current = -1;
+  hipError_t err = hipGetDevice(&current);
+  if (err != hipSuccess) return err;
+  if (current != device) return hipErrorInvalidDevice;
+  void *ptr = nullptr;
+  err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (err != hipSuccess) return err;
+  if (!ptr) return hipErrorInvalidSymbol;
+  g_scratch_ptr[device] = ptr;
+  return hipSuccess;
+}
+
+void *noalloc_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return g_scratch_ptr[device];
 }
 
 }  // namespace q3t

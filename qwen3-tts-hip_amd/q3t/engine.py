@@ -185,6 +185,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                                                  P(_ChunkInfo)]),
         "q3t_prepare_text": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32,
                                             ctypes.c_int32, f32p, i32p, f32p, i32p, f32p]),
+        "q3t_prepare_text_noalloc": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32, ctypes.c_int32,
+                                                    ctypes.c_int32, ctypes.c_int32, f32p, i32p, f32p, i32p, f32p]),
         "q3t_stream_start_text": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32, ctypes.c_int32,
                                                  P(_GenerateOptions), P(ctypes.c_void_p)]),
         "q3t_prepare_text_voice_clone": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32, f32p, ctypes.c_int32,
@@ -647,9 +649,11 @@ class HipTtsEngine:
         return self.info.get("text_vocab", 0) > 0
 
     def prepare_text(self, content_ids: Sequence[int], speaker: str = "ryan", language: str = "english",
-                     text_lookahead_tokens: int = 1 << 30) -> PreparedInputs:
+                     text_lookahead_tokens: int = 1 << 30, no_alloc: bool = False) -> PreparedInputs:
         """``TtsTextPrep::prepare_custom_voice_with_lookahead`` (text.rs:340-382) on the device
-        (``q3t_prepare_text``): content ids -> prefill rows, trailing text rows, tts_pad row."""
+        (``q3t_prepare_text``): content ids -> prefill rows, trailing text rows, tts_pad row.
+        ``no_alloc`` runs ``q3t_prepare_text_noalloc`` instead: the same rows with no device
+        allocation (a bounded prompt length; calls on one GPU must not overlap)."""
         ids = np.ascontiguousarray(np.asarray(content_ids, dtype=np.int64).astype(np.int32))
         n, H = int(ids.size), self.info["talker_hidden"]
         opts = GenerateOptions(speaker=speaker, language=language)._c()
@@ -658,8 +662,9 @@ class HipTtsEngine:
         pad = np.zeros(H, np.float32)
         P, T = ctypes.c_int32(), ctypes.c_int32()
         lookahead = min(int(text_lookahead_tokens), 0x7FFFFFFF)
-        _check(_lib.q3t_prepare_text(self._h, _iptr(ids), n, opts.speaker, opts.language, lookahead, _fptr(pre),
-                                     ctypes.byref(P), _fptr(trail), ctypes.byref(T), _fptr(pad)))
+        fn = _lib.q3t_prepare_text_noalloc if no_alloc else _lib.q3t_prepare_text
+        _check(fn(self._h, _iptr(ids), n, opts.speaker, opts.language, lookahead, _fptr(pre),
+                  ctypes.byref(P), _fptr(trail), ctypes.byref(T), _fptr(pad)))
         return PreparedInputs(content_ids=ids.astype(np.int64), prefill=pre[:P.value].copy(),
                               trailing_text=trail[:T.value].copy(), tts_pad_embed=pad)
 
