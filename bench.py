@@ -12,7 +12,10 @@ Prints one JSON line.  Besides the contract fields it carries:
   rtf, frame_ms                  per-frame latency view of the same run
   frame_algorithmic_GBps         bytes one frame must move (weights + KV) / frame time
   roofline                       the dominant kernel, timed live with HIP events
-  multistream                    BASELINE config 5 (16 streams together) on the same model
+  per_step                       Talker-step and CodePredictor-pass rooflines (phases timed as graphs)
+  multistream                    BASELINE config 5 (16 streams together) on the same model, with
+                                 the batched frame's roofline
+  multistream_kv_bf16            the same on the bf16 KV cache
   sampled                        BASELINE config 3 (sampling on both heads) on the same model
   cfg4                           BASELINE config 4 (1.7B, 480 frames, KV 512), one generation
   first_audio                    time from start_stream to the first audio chunk
@@ -52,6 +55,57 @@ def frame_bytes(spec, active_steps_mean: float, kv_elem: int) -> float:
     kv_row_c = c.layers * 2 * c.kv_heads * c.head_dim * kv_elem
     kv = kv_row_t * active_steps_mean + kv_row_c * sum(range(1, spec.num_code_groups + 1))
     return talker + groups * cp_pass + kv
+
+
+def step_bytes(spec, kv_elem: int):
+    """Algorithmic bytes of one Talker step (stack + codec head + final norm, bf16) and of one
+    CodePredictor pass (stack + one LM head + final norm (+ projection)), without KV, and the
+    KV bytes of one cached position of each stack (K and V, all layers)."""
+    t, c = spec.talker, spec.code_predictor
+
+    def stack_params(s):
+        q, kv = s.q_heads * s.head_dim, s.kv_heads * s.head_dim
+        return s.layers * ((q + 2 * kv) * s.hidden + s.hidden * q + 3 * s.intermediate * s.hidden)
+
+    talker = 2 * (stack_params(t) + t.vocab * t.hidden + t.hidden)
+    proj = c.hidden * t.hidden if spec.has_projection else 0
+    cp_pass = 2 * (stack_params(c) + c.vocab * c.hidden + c.hidden + proj)
+    kv_t = t.layers * 2 * t.kv_heads * t.head_dim * kv_elem
+    kv_c = c.layers * 2 * c.kv_heads * c.head_dim * kv_elem
+    return talker, cp_pass, kv_t, kv_c
+
+
+def per_step(st, spec, prefill_steps: int, chunk: int, kv_elem: int) -> dict:
+    """Runs the stream `st` to its end with both phases of every frame timed on the GPU
+    (q3t_debug_phase_times: the CodePredictor and the Talker step each replayed as its own
+    graph) and returns the per-step rooflines: Talker step = bytes / time over the frames that
+    run a Talker step (all but the last), CodePredictor pass = the frame's 15 passes / 15."""
+    import numpy as np
+    cp, tk = [], []
+    while True:
+        c, a, b = st.next_codes_chunk_timed(chunk)
+        cp += list(a)
+        tk += list(b)
+        if c is None:
+            break
+    F = len(cp)
+    talker_w, cp_w, kv_t, kv_c = step_bytes(spec, kv_elem)
+    groups = spec.num_code_groups - 1
+    # frame f: the Talker attention at position P + f reads P + f + 1 rows and writes one; the
+    # CodePredictor's pass at position p (1 .. groups) reads p + 1 rows (the prefix pass 2)
+    t_bytes = [talker_w + kv_t * (prefill_steps + f + 2) for f in range(F - 1)]
+    c_bytes = groups * cp_w + kv_c * (sum(range(2, groups + 2)) + 2)
+    t_us = np.asarray(tk[:F - 1], np.float64)
+    c_us = np.asarray(cp, np.float64)
+    t_gbps = sum(t_bytes) / (t_us.sum() * 1e-6) / 1e9
+    c_gbps = F * c_bytes / (c_us.sum() * 1e-6) / 1e9
+    return {"frames": F, "timing": "each phase replayed as its own graph, hipEvents between them",
+            "talker_step_us": round(float(t_us.mean()), 3), "talker_step_us_median": round(float(np.median(t_us)), 3),
+            "talker_step_bytes_mean": int(np.mean(t_bytes)), "talker_step_GBps": round(t_gbps, 1),
+            "talker_step_frac": round(t_gbps / HBM_PEAK_GBPS, 4),
+            "cp_pass_us": round(float(c_us.mean()) / groups, 3), "cp_pass_bytes": int(c_bytes / groups),
+            "cp_pass_GBps": round(c_gbps, 1), "cp_pass_frac": round(c_gbps / HBM_PEAK_GBPS, 4),
+            "frame_us_sum_of_phases": round(float(c_us.mean() + t_us.mean()), 3)}
 
 
 def measured_traffic(workload: str, kernel: str):
@@ -115,10 +169,12 @@ def cpu_baseline(runs: int = 3) -> dict:
 
 
 def multistream(eng_cls, model_dir: str, name: str, steps: int, warmup: int, use_graph: bool,
-                frames_cap: int = 0) -> dict:
+                frames_cap: int = 0, kv_bf16: bool = False) -> dict:
     """BASELINE config 5 on the same model: every stream started together (one prefill over
     all prompts), then chunks pulled for all live streams at once until each has ended.
-    A step is one such generation; value = frames of all streams / seconds."""
+    A step is one such generation; value = frames of all streams / seconds.  `roofline`: the
+    algorithmic bytes of the batched frames (every weight once per batched frame, plus each
+    live stream's KV rows) over the step time without the prefill."""
     from q3t import engine as E
     from q3t import synth
     from q3t.workloads import MULTI_WORKLOADS
@@ -132,7 +188,7 @@ def multistream(eng_cls, model_dir: str, name: str, steps: int, warmup: int, use
         opts = [E.GenerateOptions(**{**kw, "max_frames": min(kw["max_frames"], frames_cap)})
                 for kw in w.options_kwargs()]
     eng = eng_cls(model_dir, E.EngineOptions(max_cache_steps=w.max_cache_steps, max_streams=w.streams,
-                                             use_graph=use_graph))
+                                             use_graph=use_graph, kv_bf16=kv_bf16))
     lk = E.StreamOptions(text_lookahead_tokens=1 << 30)
 
     def one():
@@ -161,11 +217,34 @@ def multistream(eng_cls, model_dir: str, name: str, steps: int, warmup: int, use
     el = time.perf_counter() - t0
     eng.close()
     lengths, budgets, _ = w.plan()
+    if frames_cap > 0:
+        budgets = [min(f, frames_cap) for f in budgets]
+    spec = synth.SPECS[w.spec]
+    talker_w, cp_w, kv_t, kv_c = step_bytes(spec, 2 if kv_bf16 else 4)
+    groups = spec.num_code_groups - 1
+    weights = talker_w + groups * cp_w
+    cp_kv = kv_c * (sum(range(2, groups + 2)) + 2)
+    # batched frame f: every stream with more than f frames is live (no EOS in this greedy
+    # workload); a live stream at prefill P reads P + f + 2 Talker KV rows (P + f + 1 read, 1
+    # written) and its CodePredictor rows
+    n_batched = max(budgets)
+    kv = sum(sum(kv_t * (9 + n + f + 2) for f in range(fr - 1)) + fr * cp_kv for n, fr in zip(lengths, budgets))
+    alg_bytes = n_batched * weights + kv
+    decode_s = (el - prefill_s) / steps
+    gbps = alg_bytes / decode_s / 1e9
     return {"workload": name, "streams": w.streams, "value": round(frames / el, 2), "unit": "frames/s (all streams)",
             "steps": steps, "warmup": warmup, "ms_per_step": round(1000 * el / steps, 3),
             "frames_per_step": frames // steps, "prefill_rows": sum(9 + n for n in lengths),
             "prefill_ms": round(1000 * prefill_s / steps, 3), "kv_capacity": w.max_cache_steps,
-            "rtf_per_stream": round(el / steps * w.streams / (frames / steps) / FRAME_SECONDS, 5)}
+            "kv_cache": "bf16" if kv_bf16 else "fp32",
+            "rtf_per_stream": round(el / steps * w.streams / (frames / steps) / FRAME_SECONDS, 5),
+            "decode_frames_per_s": round(frames / steps / decode_s, 2),
+            "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": round(gbps / HBM_PEAK_GBPS, 4), "batched_frames": n_batched,
+                         "algorithmic_bytes_per_step": int(alg_bytes),
+                         "batched_frame_ms": round(1000 * decode_s / n_batched, 4),
+                         "note": "every weight once per batched frame + each live stream's KV rows, over "
+                                 "the step time without the prefill"}}
 
 
 def big_model_line(E, synth, w, use_graph: bool) -> dict:
@@ -195,6 +274,8 @@ def big_model_line(E, synth, w, use_graph: bool) -> dict:
         n = one()
         eng.synchronize()
         el = time.perf_counter() - t0
+        with eng.start_stream(inputs, opts) as st:
+            steps = per_step(st, spec, inputs.prefill_steps, w.chunk_frames, 4)
         eng.close()
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
@@ -202,7 +283,7 @@ def big_model_line(E, synth, w, use_graph: bool) -> dict:
     return {"workload": w.name, "frames": n, "value": round(n / el, 2), "unit": "frames/s",
             "rtf": round(el / (n * FRAME_SECONDS), 5), "frame_ms": round(1000 * el / n, 4),
             "frame_algorithmic_GBps": round(fb / (el / n) / 1e9, 1), "prefill_steps": inputs.prefill_steps,
-            "kv_capacity": w.max_cache_steps}
+            "kv_capacity": w.max_cache_steps, "per_step": steps}
 
 
 def codec_decode_only(E, synth, frames: int, steps: int) -> int:
@@ -249,6 +330,11 @@ def main() -> int:
                     help="skip the device prompt-preparation timing (and the text-embedding table it needs)")
     ap.add_argument("--no-cfg4", action="store_true", help="skip the 1.7B (config 4) generation")
     ap.add_argument("--no-sampled", action="store_true", help="skip the sampled (config 3) generation")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the dominant kernel's eager per-dispatch timing (no graphs: the command rocprofv3 "
+                         "traces for profiles/) and exit")
+    ap.add_argument("--no-multistream-bf16", action="store_true",
+                    help="skip the config-5 run on the bf16 KV cache")
     ap.add_argument("--kernel-classes", action="store_true",
                     help="graph-time every kernel class of q3t_bench_kernel on the workload's model and exit")
     args = ap.parse_args()
@@ -292,6 +378,19 @@ def main() -> int:
             tp.prepare(w.prompt(), text_lookahead_tokens=look)
         host_prep = (time.perf_counter() - t0) / 3
     del model
+    if args.roofline_only:
+        eng = E.HipTtsEngine(tmp, E.EngineOptions(max_cache_steps=w.max_cache_steps))
+        eng.bench_kernel_timed(2, 103)
+        us, b = eng.bench_kernel_timed(2, 1030)
+        eng.close()
+        import shutil
+        shutil.rmtree(tmp, ignore_errors=True)
+        gbps = b / (us * 1e-6) / 1e9
+        print(json.dumps({"kernel": E.HipTtsEngine.KERNELS[2], "avg_launch_us": round(us, 3),
+                          "algorithmic_bytes_per_launch": int(b), "achieved": round(gbps, 1),
+                          "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                          "timing": "eager launches, per-dispatch start/stop events (1030 + 103 warm + 1133 warm)"}))
+        return 0
     if args.kernel_classes:
         eng = E.HipTtsEngine(tmp, E.EngineOptions(max_cache_steps=w.max_cache_steps))
         for k, name in E.HipTtsEngine.KERNELS.items():
@@ -345,6 +444,8 @@ def main() -> int:
     frame_s = elapsed / frames
     roofline = eng.dominant_kernel_roofline(HBM_PEAK_GBPS)
     roofline["traffic"] = measured_traffic(w.name, roofline["kernel"])
+    with eng.start_stream(inputs, opts) as st_steps:
+        steps_line = per_step(st_steps, spec, P, w.chunk_frames, 2 if args.kv_bf16 else 4)
     text_prep = None
     if with_text:
         # Prompt preparation of the same prompt on the device (q3t_prepare_text, host copies
@@ -418,9 +519,12 @@ def main() -> int:
     cfg4 = None
     if not args.no_cfg4 and w.name == "cfg2_0.6b_greedy" and args.frames == 0:
         cfg4 = big_model_line(E, synth, WORKLOADS["cfg4_1.7b_greedy"], not args.eager)
-    multi = None
+    multi = multi_bf16 = None
     if args.multistream and w.spec == "0.6b" and w.weight_seed == 0:
         multi = multistream(E.HipTtsEngine, tmp, args.multistream, max(1, min(args.steps, 2)), 1, not args.eager)
+        if not args.no_multistream_bf16:
+            multi_bf16 = multistream(E.HipTtsEngine, tmp, args.multistream, max(1, min(args.steps, 2)), 1,
+                                     not args.eager, kv_bf16=True)
     import shutil
     shutil.rmtree(tmp, ignore_errors=True)
 
@@ -446,9 +550,12 @@ def main() -> int:
         "frame_algorithmic_GBps": round(fb / frame_s / 1e9, 1),
         "frame_algorithmic_bytes": int(fb),
         "roofline": roofline,
+        "per_step": steps_line,
     }
     if multi is not None:
         out["multistream"] = multi
+    if multi_bf16 is not None:
+        out["multistream_kv_bf16"] = multi_bf16
     if text_prep is not None:
         out["text_prep"] = text_prep
     if codec is not None:

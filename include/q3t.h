@@ -320,6 +320,23 @@ int q3t_engine_synchronize(q3t_engine *engine);
 int q3t_bench_kernel(q3t_engine *engine, int32_t kernel, int32_t iters, double *avg_us,
                      double *bytes_per_launch);
 
+/* q3t_bench_kernel with every launch issued eagerly and bracketed by its own dispatch's
+ * start / stop timestamps (hipExtLaunchKernelGGL events): *avg_us is the kernel's duration
+ * without the dependent-launch gap, the per-dispatch duration a kernel trace reports for the
+ * same launches.  Kernel class 6 is not available here.  Bench hook, no counterpart in the
+ * reference. */
+int q3t_bench_kernel_timed(q3t_engine *engine, int32_t kernel, int32_t iters, double *avg_us,
+                           double *bytes_per_launch);
+
+/* q3t_stream_next_codes with the GPU time of each frame's two phases: the CodePredictor's 15
+ * groups (cp_us[i]) and the Talker step with its token selection (talker_us[i]), each phase
+ * replayed as its own graph (eager launches without use_graph) with events between them and
+ * a synchronisation after every frame.  *timed = the frames timed (<= max_chunk_frames).  Bench
+ * hook for per-step rooflines (the reference's GenerationProfile splits the same phases,
+ * generation.rs:104-131). */
+int q3t_debug_phase_times(q3t_stream *stream, int32_t max_chunk_frames, int32_t *codes, q3t_chunk_info *info,
+                          float *cp_us, float *talker_us, int32_t *timed);
+
 /* The fused token sampler on its own: n draws from one logit row [V] (host array), draw i
  * using Philox4x32-10 counter (i, kind, 0, 0) and key seed.  This is the code path of the
  * frame loop's select kernels, exposed the way the reference exposes its sample_topk_f32

@@ -179,6 +179,10 @@ struct Slot {
   hipGraphExec_t graph = nullptr;
   bool graph_traced = false;
   bool graph_cp_greedy = false;
+  // The frame as two graphs, the CodePredictor and the Talker step (q3t_debug_phase_times),
+  // keyed like `graph`.
+  hipGraphExec_t phase_graph[2] = {nullptr, nullptr};
+  bool phase_traced = false, phase_cp_greedy = false;
   SlotState *h_state = nullptr;  // pinned host mirror
   // Greedy CodePredictor (the stream's subtalker does not sample): each LM head hands its
   // argmax to the next group's first GEMV through cp_keys ([groups - 1][kHandoffKeys] order
@@ -933,6 +937,8 @@ void alloc_pools(Engine &e, int n) {
 void free_pools(Engine &e) {
   for (Slot &sl : e.slots) {
     if (sl.graph) (void)hipGraphExecDestroy(sl.graph);
+    for (hipGraphExec_t g : sl.phase_graph)
+      if (g) (void)hipGraphExecDestroy(g);
     if (sl.stream) (void)hipStreamDestroy(sl.stream);
   }
   e.slots.clear();
@@ -1999,6 +2005,35 @@ int frames_to_run(q3t_stream *sp, int max_chunk, int32_t *codes, q3t_chunk_info 
   return n;
 }
 
+// The CodePredictor (phase 0) and the Talker step (phase 1) of a frame, each captured as a
+// graph of the slot (as run_frames captures the whole frame).
+void ensure_phase_graphs(Engine &e, Slot &s) {
+  if (s.phase_graph[0] && s.phase_traced == (bool)e.trace && s.phase_cp_greedy == s.cp_greedy) return;
+  for (hipGraphExec_t &g : s.phase_graph)
+    if (g) {
+      HIPC(hipGraphExecDestroy(g));
+      g = nullptr;
+    }
+  for (int ph = 0; ph < 2; ++ph) {
+    hipGraph_t g = nullptr;
+    HIPC(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal));
+    try {
+      if (ph == 0) e.enqueue_code_predictor(s, s.stream);
+      else e.enqueue_talker_decode(s, s.stream);
+    } catch (...) {
+      (void)hipStreamEndCapture(s.stream, &g);
+      if (g) (void)hipGraphDestroy(g);
+      throw;
+    }
+    HIPC(hipStreamEndCapture(s.stream, &g));
+    const hipError_t err = hipGraphInstantiate(&s.phase_graph[ph], g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    hip_check(err, "hipGraphInstantiate");
+  }
+  s.phase_traced = (bool)e.trace;
+  s.phase_cp_greedy = s.cp_greedy;
+}
+
 // After up to n frames ran: the new codes to the caller, the host's view of the stream.
 void collect_frames(q3t_stream *sp, int n, int32_t *codes, q3t_chunk_info *info) {
   Engine &e = *sp->engine;
@@ -2059,6 +2094,38 @@ int q3t_stream_next_codes_profiled(q3t_stream *sp, int32_t max_chunk, int32_t *c
       prof->talker_decode_seconds += ev.seconds(1, 2);
       ++ran;
     }
+    collect_frames(sp, n, codes, info);
+  });
+}
+
+int q3t_debug_phase_times(q3t_stream *sp, int32_t max_chunk, int32_t *codes, q3t_chunk_info *info, float *cp_us,
+                          float *talker_us, int32_t *timed) {
+  return guarded([&] {
+    using namespace q3t;
+    if (!cp_us || !talker_us || !timed) fail(Q3T_ERR_INVALID, "null argument");
+    *timed = 0;
+    const int n = frames_to_run(sp, max_chunk, codes, info);
+    if (n == 0) return;
+    Engine &e = *sp->engine;
+    Slot &s = e.slots[sp->slot];
+    HIPC(hipSetDevice(e.device));
+    if (e.use_graph) ensure_phase_graphs(e, s);
+    Events ev(3);
+    int ran = 0;
+    while (ran < n && !s.h_state->done) {
+      HIPC(hipEventRecord(ev.ev[0], s.stream));
+      if (e.use_graph) HIPC(hipGraphLaunch(s.phase_graph[0], s.stream));
+      else e.enqueue_code_predictor(s, s.stream);
+      HIPC(hipEventRecord(ev.ev[1], s.stream));
+      if (e.use_graph) HIPC(hipGraphLaunch(s.phase_graph[1], s.stream));
+      else e.enqueue_talker_decode(s, s.stream);
+      HIPC(hipEventRecord(ev.ev[2], s.stream));
+      sync_state(s);
+      cp_us[ran] = (float)(1e6 * ev.seconds(0, 1));
+      talker_us[ran] = (float)(1e6 * ev.seconds(1, 2));
+      ++ran;
+    }
+    *timed = ran;
     collect_frames(sp, n, codes, info);
   });
 }
@@ -2255,8 +2322,9 @@ int q3t_debug_code_predictor(q3t_engine *e, const float *talker_hidden, const fl
   });
 }
 
-int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_us, double *bytes) {
-  return guarded([&] {
+namespace {
+int bench_kernel_impl(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_us, double *bytes, bool timed) {
+  return q3t::guarded([&] {
     using namespace q3t;
     if (!e || !avg_us || !bytes) fail(Q3T_ERR_INVALID, "null argument");
     if (iters <= 0 || iters > 8192) fail(Q3T_ERR_INVALID, "iters must be in 1..8192");
@@ -2294,7 +2362,9 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
       pr.codec_eos = e->codec_eos;
       HIPC(hipMemcpy(s.prm, &pr, sizeof pr, hipMemcpyHostToDevice));
     }
+    if (timed && kernel == 6) fail(Q3T_ERR_INVALID, "kernel class 6 has no timed launch");
     double total_bytes = 0.0;
+    const LaunchTiming *lt = nullptr;  // set per launch in the timed mode
     auto enqueue = [&](int i, bool count) {
       const L &l = seq[(size_t)i % seq.size()];
       const Dims &d = l.w->d;
@@ -2305,7 +2375,7 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
       switch (kernel) {
         case 0:  // QKV projection with the input RMSNorm prologue
           e->gemv(EPI_STORE, true, W.qkv, xin, W.g_in, d.eps, nullptr, nullptr, s.qkv, d.qkv_rows(), d.hidden,
-                  SKIP_NEVER, s.st, s.stream, nt);
+                  SKIP_NEVER, s.st, s.stream, nt, lt);
           b = 2.0 * d.qkv_rows() * d.hidden + 4.0 * (d.hidden * 2 + d.qkv_rows());
           break;
         case 1: {  // O projection + residual (Talker layers merge attention partials first; split
@@ -2322,7 +2392,7 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
             og.attn_pos_const = l.w->cap / 2;
             og.attn_q_heads = d.q_heads;
             og.attn_kv_heads = d.kv_heads;
-            hip_check(launch_oproj_heads(og, s.stream), "launch_oproj_heads");
+            hip_check(launch_oproj_heads(og, s.stream, lt), "launch_oproj_heads");
             b = 2.0 * d.hidden * d.q_out() + 4.0 * (d.kv_heads * d.hidden) +
                 4.0 * d.q_heads * (d.head_dim + 2) * std::min(attn_chunks(l.w->cap), (l.w->cap / 2) / attn_chunk_len(l.w->cap) + 1);
             break;
@@ -2337,7 +2407,7 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
             og.attn_q_heads = d.q_heads;
             og.attn_kv_heads = d.kv_heads;
           }
-          hip_check(launch_gemv(EPI_RESIDUAL, false, nt, og, s.stream), "launch_gemv");
+          hip_check(launch_gemv(EPI_RESIDUAL, false, nt, og, s.stream, lt), "launch_gemv");
           b = 2.0 * d.hidden * d.q_out() + 4.0 * (d.q_out() + 2 * d.hidden);
           break;
         }
@@ -2352,12 +2422,12 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
             gu.x_store = s.x_mid;
             b += 4.0 * (d.kv_heads + 1) * d.hidden;
           }
-          hip_check(launch_gemv(EPI_SWIGLU, true, nt, gu, s.stream), "launch_gemv");
+          hip_check(launch_gemv(EPI_SWIGLU, true, nt, gu, s.stream, lt), "launch_gemv");
           break;
         }
         case 3:  // down projection + residual
           e->gemv(EPI_RESIDUAL, false, W.down, s.act, nullptr, 0.f, s.attn, nullptr, s.attn, d.hidden,
-                  d.intermediate, SKIP_NEVER, s.st, s.stream, nt);
+                  d.intermediate, SKIP_NEVER, s.st, s.stream, nt, lt);
           b = 2.0 * d.hidden * d.intermediate + 4.0 * (d.intermediate + 2 * d.hidden);
           break;
         case 4: {  // Talker attention over a full cache (L = max_cache_steps)
@@ -2367,7 +2437,7 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
                       s.attn, d.q_heads, d.kv_heads, l.w->cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
                       POS_CONST, l.w->cap - 1, SKIP_NEVER, e->kv_bf16, s.st, s.attn_part, s.attn_part_chunks,
                       attn_chunk_len(l.w->cap), attn_chunks(l.w->cap) > 1 ? 1 : 0};
-          hip_check(launch_attn_decode(aa, d.head_dim, s.stream), "launch_attn_decode");
+          hip_check(launch_attn_decode(aa, d.head_dim, s.stream, lt), "launch_attn_decode");
           b = 2.0 * esz * d.kv_heads * d.head_dim * l.w->cap + 4.0 * (d.qkv_rows() + d.q_out());
           break;
         }
@@ -2379,7 +2449,7 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
                       s.attn, d.q_heads, d.kv_heads, l.w->cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
                       POS_CONST, pos, SKIP_NEVER, e->kv_bf16, s.st, s.attn_part, s.attn_part_chunks,
                       attn_chunk_len(l.w->cap), 0};
-          hip_check(launch_attn_decode(aa, d.head_dim, s.stream), "launch_attn_decode");
+          hip_check(launch_attn_decode(aa, d.head_dim, s.stream, lt), "launch_attn_decode");
           b = 2.0 * esz * d.kv_heads * d.head_dim * (pos + 1) + 4.0 * (d.qkv_rows() + d.q_out());
           break;
         }
@@ -2399,7 +2469,7 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
                       s.attn, d.q_heads, d.kv_heads, l.w->cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
                       POS_CONST, l.w->cap / 2, SKIP_NEVER, e->kv_bf16, s.st, s.attn_part, s.attn_part_chunks,
                       attn_chunk_len(l.w->cap), attn_chunks(l.w->cap) > 1 ? 1 : 0};
-          hip_check(launch_attn_decode(aa, d.head_dim, s.stream), "launch_attn_decode");
+          hip_check(launch_attn_decode(aa, d.head_dim, s.stream, lt), "launch_attn_decode");
           b = 2.0 * esz * d.kv_heads * d.head_dim * (l.w->cap / 2 + 1) + 4.0 * (d.qkv_rows() + d.q_out());
           break;
         }
@@ -2413,7 +2483,7 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
           aa.wo = W.o;
           aa.wo_rows = d.hidden;
           aa.opart = s.opart;
-          hip_check(launch_attn_oproj(aa, d.head_dim, s.stream), "launch_attn_oproj");
+          hip_check(launch_attn_oproj(aa, d.head_dim, s.stream, lt), "launch_attn_oproj");
           b = 2.0 * esz * d.kv_heads * d.head_dim * (pos + 1) + 4.0 * d.qkv_rows() + 2.0 * d.hidden * d.q_out() +
               4.0 * d.kv_heads * d.hidden;
           break;
@@ -2421,7 +2491,7 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
         case 8: {  // CodePredictor LM head (final norm prologue)
           const int g = i % (e->groups - 1);
           e->gemv(EPI_STORE, true, e->lm_heads + (size_t)g * cd.vocab * cd.hidden, s.x_c, e->c_norm, cd.eps,
-                  nullptr, nullptr, s.logits_c, cd.vocab, cd.hidden, SKIP_NEVER, s.st, s.stream);
+                  nullptr, nullptr, s.logits_c, cd.vocab, cd.hidden, SKIP_NEVER, s.st, s.stream, false, lt);
           b = 2.0 * cd.vocab * cd.hidden + 4.0 * (2 * cd.hidden + cd.vocab);
           break;
         }
@@ -2439,6 +2509,26 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
       if (ev0) (void)hipEventDestroy(ev0);
       if (ev1) (void)hipEventDestroy(ev1);
     };
+    if (timed) {
+      // Eager launches, each bracketed by its own dispatch's start / stop timestamps
+      // (hipExtLaunchKernelGGL events): the kernel's duration without the launch gap, the
+      // quantity a kernel trace reports per dispatch.  One warm pass first.
+      Events evs(2 * iters);
+      for (int i = 0; i < iters; ++i) enqueue(i, false);
+      HIPC(hipStreamSynchronize(s.stream));
+      for (int i = 0; i < iters; ++i) {
+        const LaunchTiming t{evs.ev[2 * i], evs.ev[2 * i + 1]};
+        lt = &t;
+        enqueue(i, true);
+        lt = nullptr;
+      }
+      HIPC(hipStreamSynchronize(s.stream));
+      double us = 0.0;
+      for (int i = 0; i < iters; ++i) us += 1e6 * evs.seconds(2 * i, 2 * i + 1);
+      *avg_us = us / iters;
+      *bytes = total_bytes / iters;
+      return;
+    }
     try {
       HIPC(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal));
       try {
@@ -2466,6 +2556,15 @@ int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_u
     }
     cleanup();
   });
+}
+}  // namespace
+
+int q3t_bench_kernel(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_us, double *bytes) {
+  return bench_kernel_impl(e, kernel, iters, avg_us, bytes, false);
+}
+
+int q3t_bench_kernel_timed(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_us, double *bytes) {
+  return bench_kernel_impl(e, kernel, iters, avg_us, bytes, true);
 }
 
 int q3t_debug_gemm(q3t_engine *e, int32_t epi, const float *X, int32_t M, int32_t K, const uint16_t *W, int32_t N,

@@ -180,6 +180,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                                                      f32p, P(_GenerateOptions), P(ctypes.c_void_p), P(_Profile)]),
         "q3t_stream_next_codes_profiled": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, i32p, P(_ChunkInfo),
                                                           P(_Profile)]),
+        "q3t_debug_phase_times": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, i32p, P(_ChunkInfo), f32p, f32p,
+                                                 i32p]),
         "q3t_decode_codes": (ctypes.c_int, [ctypes.c_void_p, i32p, ctypes.c_int32, f32p]),
         "q3t_stream_next_audio": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32, i32p, f32p, i32p,
                                                  P(_ChunkInfo)]),
@@ -212,6 +214,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
                                             ctypes.c_int32, i32p]),
         "q3t_engine_synchronize": (ctypes.c_int, [ctypes.c_void_p]),
         "q3t_bench_kernel": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
+                                            P(ctypes.c_double), P(ctypes.c_double)]),
+        "q3t_bench_kernel_timed": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, ctypes.c_int32,
                                             P(ctypes.c_double), P(ctypes.c_double)]),
         "q3t_debug_gemm": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, f32p, ctypes.c_int32, ctypes.c_int32,
                                           P(ctypes.c_uint16), ctypes.c_int32, f32p, ctypes.c_float, f32p, f32p,
@@ -470,14 +474,31 @@ class HipTtsEngine:
         _check(_lib.q3t_bench_kernel(self._h, int(kernel), int(iters), ctypes.byref(us), ctypes.byref(b)))
         return us.value, b.value
 
+    def bench_kernel_timed(self, kernel: int, iters: int = 1030):
+        """(average kernel duration in microseconds without the launch gap, algorithmic bytes per
+        launch) of one kernel class, eager launches timed by their own dispatch events."""
+        us, b = ctypes.c_double(), ctypes.c_double()
+        _check(_lib.q3t_bench_kernel_timed(self._h, int(kernel), int(iters), ctypes.byref(us), ctypes.byref(b)))
+        return us.value, b.value
+
     def dominant_kernel_roofline(self, peak_gbps: float, kernel: int = 2, iters: int = 1030) -> dict:
-        """Roofline entry for the kernel class that dominates a frame's time (the gate/up GEMV)."""
-        self.bench_kernel(kernel, 103)   # warm
-        us, b = self.bench_kernel(kernel, iters)
+        """Roofline entry for the kernel class that dominates a frame's time (the gate/up GEMV).
+
+        ``achieved`` divides the algorithmic bytes of a launch by the kernel's own duration: the
+        1030 launches of one frame order are issued eagerly, each timed by its dispatch's start
+        and stop events (the per-dispatch duration rocprofv3's kernel trace reports for the same
+        command).  ``graph_us_per_launch`` is the same sequence replayed as one graph, timed as a
+        whole (the dependent-launch gap included): the cost a frame sees."""
+        self.bench_kernel_timed(kernel, 103)   # warm
+        us, b = self.bench_kernel_timed(kernel, iters)
+        self.bench_kernel(kernel, 103)
+        gus, _ = self.bench_kernel(kernel, iters)
         achieved = b / (us * 1e-6) / 1e9
         return {"kernel": self.KERNELS[kernel], "bound": "hbm", "achieved": round(achieved, 1),
                 "peak": peak_gbps, "unit": "GB/s", "frac": round(achieved / peak_gbps, 4), "traffic": None,
-                "avg_launch_us": round(us, 3), "algorithmic_bytes_per_launch": int(b), "launches_timed": iters}
+                "avg_launch_us": round(us, 3), "timing": "eager launches, per-dispatch start/stop events",
+                "graph_us_per_launch": round(gus, 3), "graph_frac_gap_included": round(b / (gus * 1e-6) / 1e9 / peak_gbps, 4),
+                "algorithmic_bytes_per_launch": int(b), "launches_timed": iters}
 
     def debug_gemm(self, epi: int, X: np.ndarray, W_bits: np.ndarray, N: int, gamma=None, eps: float = 1e-6,
                    res=None, bias=None) -> np.ndarray:
@@ -852,6 +873,20 @@ class HipTtsStream:
         info = _ChunkInfo()
         _check(_lib.q3t_stream_next_codes(self._h, max_chunk_frames, _iptr(buf), ctypes.byref(info)))
         return self._accept(buf, info)
+
+    def next_codes_chunk_timed(self, max_chunk_frames: int):
+        """``next_codes_chunk`` with each frame's phases timed on the GPU (``q3t_debug_phase_times``):
+        (chunk or None, CodePredictor microseconds per frame, Talker-step microseconds per frame)."""
+        if max_chunk_frames <= 0:
+            raise InvalidInputError(Q3T_ERR_INVALID, "max_chunk_frames must be non-zero")
+        buf = np.zeros((max_chunk_frames, self.engine.code_groups), dtype=np.int32)
+        cp = np.zeros(max_chunk_frames, np.float32)
+        tk = np.zeros(max_chunk_frames, np.float32)
+        info = _ChunkInfo()
+        n = ctypes.c_int32()
+        _check(_lib.q3t_debug_phase_times(self._h, max_chunk_frames, _iptr(buf), ctypes.byref(info), _fptr(cp),
+                                          _fptr(tk), ctypes.byref(n)))
+        return self._accept(buf, info), cp[:n.value].copy(), tk[:n.value].copy()
 
     def next_audio_chunk(self, max_chunk_frames: int) -> Optional[GeneratedAudioChunk]:
         """``next_audio_chunk`` (generation.rs:965-989): the next codes chunk, decoded with up

@@ -100,6 +100,34 @@ def test_generate_codes_profiled(models, name):
           f"talker {1e3 * prof.talker_decode_seconds:.2f} ms, prefill {1e3 * prof.prefill_seconds:.3f} ms")
 
 
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_phase_timed_frames_equal_plain_frames(models, use_graph):
+    """q3t_debug_phase_times (the CodePredictor and the Talker step replayed as two graphs, or
+    launched eagerly, with events between them) produces the same codes as next_codes_chunk and
+    a positive time for every phase of every frame; the timed kernel hook runs too."""
+    w = WORKLOADS["tiny_greedy"]
+    model, d = models.get(w.spec)
+    opts = E.GenerateOptions(**w.options_kwargs())
+    print(f"[gpu] phase times graph={use_graph}", flush=True)
+    with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=w.max_cache_steps, use_graph=use_graph)) as eng:
+        ref = eng.generate_codes(w.inputs(model), opts).codes
+        got, cps, tks = [], [], []
+        with eng.start_stream(w.inputs(model), opts) as st:
+            while True:
+                c, cp, tk = st.next_codes_chunk_timed(5)
+                cps += list(cp)
+                tks += list(tk)
+                if c is None:
+                    break
+                got.append(c.codes)
+                assert len(cp) == c.frames
+        us, b = eng.bench_kernel_timed(2, 40)
+    np.testing.assert_array_equal(np.concatenate(got), ref)
+    assert len(cps) == len(ref) and min(cps) > 0 and min(tks) > 0
+    assert us > 0 and b > 0
+    print(f"CodePredictor {np.mean(cps):.1f} us, Talker step {np.mean(tks):.1f} us per frame; gate/up {us:.2f} us")
+
+
 def test_graph_replay_is_bitwise_equal_to_eager(models):
     a = run(models, "tiny_sampled", use_graph=True)
     b = run(models, "tiny_sampled", use_graph=False)
