@@ -64,6 +64,11 @@ typedef struct {
   float subtalker_top_p;
   float subtalker_temperature;
   uint64_t seed;
+  /* No counterpart in GenerateOptions: how repetition_penalty counts the history.  0 (default):
+   * once per distinct earlier semantic token, as HF's processor in the Python reference does.
+   * 1: once per occurrence, compounding, as the crate's GPU kernel apply_repetition_penalty_f32
+   * does over the full semantic_history (src/gpu/kernels.rs:408-426, generation.rs:717-727). */
+  int32_t repetition_penalty_per_occurrence;
 } q3t_generate_options;
 
 /* Shapes read from config.json (src/model/config.rs:8-43). */

@@ -196,6 +196,7 @@ class GenerateOptions:
     subtalker_top_p: float = 1.0
     subtalker_temperature: float = 0.9
     seed: int = 0
+    repetition_penalty_per_occurrence: bool = False   # see sampling.apply_repetition_penalty
 
     @classmethod
     def greedy(cls, max_frames: int = 240) -> "GenerateOptions":
@@ -274,11 +275,11 @@ class Oracle:
         self.hidden = rmsnorm(pre_norm, self.t_norm, self.t_dims.eps)
         return self.codec_head @ self.hidden
 
-    def talker_select(self, logits, history, penalty, cfg: SamplingConfig, u):
+    def talker_select(self, logits, history, penalty, cfg: SamplingConfig, u, per_occurrence: bool = False):
         """compute_logits_and_token_with_options (talker.rs:431-496)."""
         l = logits
         if history is not None and len(history):
-            l = apply_repetition_penalty(l, history, penalty)
+            l = apply_repetition_penalty(l, history, penalty, per_occurrence)
         l = suppress(l, self.codec_eos)
         return select(l, cfg, u), top2_margin(l)
 
@@ -391,7 +392,8 @@ class Oracle:
                 use_hist = opts.repetition_penalty != 1.0 or tcfg.do_sample
                 u = philox.sampler_uniform(opts.seed, frame + 1, 0) if tcfg.do_sample else None
                 semantic, margin = self.talker_select(logits, history if use_hist else None,
-                                                      opts.repetition_penalty, tcfg, u)
+                                                      opts.repetition_penalty, tcfg, u,
+                                                      opts.repetition_penalty_per_occurrence)
                 if forced_codes is not None and frame + 1 < len(forced_codes):
                     semantic = int(forced_codes[frame + 1][0])
                 t_logits.append(logits)

@@ -48,12 +48,18 @@ class SamplingConfig:
 GREEDY = SamplingConfig()
 
 
-def apply_repetition_penalty(logits: np.ndarray, history: Sequence[int], penalty: float) -> np.ndarray:
+def apply_repetition_penalty(logits: np.ndarray, history: Sequence[int], penalty: float,
+                             per_occurrence: bool = False) -> np.ndarray:
+    """``l < 0 ? l * p : l / p`` on each penalised token.  Default: once per distinct token of
+    the history (HF's processor, which the Python reference runs).  ``per_occurrence``: once per
+    history entry, in order, compounding, as apply_repetition_penalty_f32 does over the crate's
+    full semantic_history (src/gpu/kernels.rs:408-426; generation.rs:717-727)."""
     out = np.array(logits, copy=True)
     if penalty == 1.0 or len(history) == 0:
         return out
     v = out.shape[-1]
-    for t in sorted(set(int(h) for h in history)):
+    tokens = [int(h) for h in history] if per_occurrence else sorted(set(int(h) for h in history))
+    for t in tokens:
         if 0 <= t < v:
             out[t] = out[t] * penalty if out[t] < 0 else out[t] / penalty
     return out

@@ -35,7 +35,8 @@ struct SlotParams {
   uint32_t seed_lo, seed_hi;
   int32_t trace;        // record raw logits
   int32_t codec_eos;
-  int32_t pad0, pad1;
+  int32_t penalty_per_occurrence;  // repetition penalty compounds per history occurrence
+  int32_t pad1;
 };
 
 enum SkipMode : int32_t {

@@ -824,6 +824,8 @@ void validate_options(const q3t_generate_options *o) {
   if (!o) fail(Q3T_ERR_INVALID, "options must not be null");
   if (o->max_frames <= 0) fail(Q3T_ERR_INVALID, "max_frames must be non-zero");
   if (!(o->repetition_penalty > 0.0f)) fail(Q3T_ERR_INVALID, "repetition_penalty must be positive");
+  if (o->repetition_penalty_per_occurrence != 0 && o->repetition_penalty_per_occurrence != 1)
+    fail(Q3T_ERR_INVALID, "repetition_penalty_per_occurrence must be 0 or 1");
   validate_sampling(o->do_sample, o->top_k, o->top_p, o->temperature, "talker");
   validate_sampling(o->subtalker_dosample, o->subtalker_top_k, o->subtalker_top_p, o->subtalker_temperature,
                     "subtalker");
@@ -1189,6 +1191,7 @@ void q3t_generate_options_default(q3t_generate_options *o) {
   o->subtalker_top_p = 1.0f;
   o->subtalker_temperature = 0.9f;
   o->seed = 0;
+  o->repetition_penalty_per_occurrence = 0;
 }
 
 const char *q3t_last_error(void) { return q3t::g_last_error.c_str(); }
@@ -1426,6 +1429,7 @@ void stage_state(Engine &e, int slot, int prefill_steps, int trailing_rows, cons
                          o->subtalker_temperature};
   pr.repetition_penalty = o->repetition_penalty;
   pr.use_history = (o->repetition_penalty != 1.0f || o->do_sample) ? 1 : 0;
+  pr.penalty_per_occurrence = o->repetition_penalty_per_occurrence;
   pr.seed_lo = (uint32_t)(o->seed & 0xffffffffu);
   pr.seed_hi = (uint32_t)(o->seed >> 32);
   pr.trace = e.trace;

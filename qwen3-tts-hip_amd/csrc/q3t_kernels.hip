@@ -1974,7 +1974,7 @@ __global__ __launch_bounds__(1024) void k_select_talker(SelectTalkerArgs a) {
   a.codes += row * a.codes_row;
   if (a.trace) a.trace += row * a.trace_row;
   __shared__ SelectShared sh;
-  __shared__ unsigned char seen[kMaxVocab];
+  __shared__ uint32_t seen[kMaxVocab];  // history occurrences of each token
   __shared__ float red[16];
   const int tid = threadIdx.x;
   const SlotParams prm = *a.prm;
@@ -1986,15 +1986,21 @@ __global__ __launch_bounds__(1024) void k_select_talker(SelectTalkerArgs a) {
     __syncthreads();
     for (int f = tid; f <= frame; f += 1024) {
       const int t = a.codes[(size_t)f * a.groups];
-      if (t >= 0 && t < a.V) seen[t] = 1;
+      if (t >= 0 && t < a.V) {
+        if (prm.penalty_per_occurrence) atomicAdd(&seen[t], 1u);
+        else seen[t] = 1;
+      }
     }
     __syncthreads();
   }
+  // Once per distinct token (HF), or once per occurrence in sequence (the crate's GPU kernel,
+  // kernels.rs:408-426): the same fp32 operation repeated, so both orders give one result.
   const float pen = prm.repetition_penalty;
   for (int i = tid; i < a.V; i += 1024) {
     float l = a.logits[i];
     if (a.trace) a.trace[(size_t)step * a.V + i] = l;
-    if (hist && seen[i]) l = (l < 0.0f) ? l * pen : l / pen;
+    const uint32_t times = hist ? seen[i] : 0u;
+    for (uint32_t r = 0; r < times; ++r) l = (l < 0.0f) ? l * pen : l / pen;
     if (i >= a.V - 1024 && i != prm.codec_eos) l = -INFINITY;
     sh.lg[i] = l;
   }

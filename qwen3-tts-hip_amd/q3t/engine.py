@@ -122,7 +122,8 @@ class _GenerateOptions(ctypes.Structure):
                 ("top_p", ctypes.c_float), ("temperature", ctypes.c_float),
                 ("repetition_penalty", ctypes.c_float), ("subtalker_dosample", ctypes.c_int32),
                 ("subtalker_top_k", ctypes.c_int32), ("subtalker_top_p", ctypes.c_float),
-                ("subtalker_temperature", ctypes.c_float), ("seed", ctypes.c_uint64)]
+                ("subtalker_temperature", ctypes.c_float), ("seed", ctypes.c_uint64),
+                ("repetition_penalty_per_occurrence", ctypes.c_int32)]
 
 
 class _EngineInfo(ctypes.Structure):
@@ -278,6 +279,10 @@ class GenerateOptions:
     subtalker_top_p: float = 1.0
     subtalker_temperature: float = 0.9
     seed: int = 0
+    # Not in the crate's GenerateOptions: False counts each distinct earlier semantic token
+    # once (HF, the Python reference); True compounds per occurrence, as the crate's GPU kernel
+    # does (src/gpu/kernels.rs:408-426).
+    repetition_penalty_per_occurrence: bool = False
 
     @classmethod
     def greedy(cls, max_frames: int = 240, **kw) -> "GenerateOptions":
@@ -303,6 +308,7 @@ class GenerateOptions:
         o.subtalker_top_p = float(self.subtalker_top_p)
         o.subtalker_temperature = float(self.subtalker_temperature)
         o.seed = int(self.seed) & 0xFFFFFFFFFFFFFFFF
+        o.repetition_penalty_per_occurrence = int(bool(self.repetition_penalty_per_occurrence))
         return o
 
     def validate(self) -> None:

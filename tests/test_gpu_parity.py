@@ -154,11 +154,14 @@ def _as_fixture(tr):
                 cp_margins=tr.cp_margins, meta=dict(ended_by_eos=tr.ended_by_eos))
 
 
-def test_greedy_repetition_penalty_matches_oracle(models):
+@pytest.mark.parametrize("per_occurrence", [False, True])
+def test_greedy_repetition_penalty_matches_oracle(models, per_occurrence):
+    """Repetition penalty 1.3 on a greedy Talker, counted once per distinct token (HF) or once
+    per occurrence (the crate's GPU kernel, kernels.rs:408-426)."""
     w = WORKLOADS["tiny_greedy"]
     model, _ = models.get(w.spec)
     inputs = w.inputs(model)
-    opts = E.GenerateOptions.greedy(16, repetition_penalty=1.3)
+    opts = E.GenerateOptions.greedy(16, repetition_penalty=1.3, repetition_penalty_per_occurrence=per_occurrence)
     r = run(models, "tiny_greedy", options=opts)
     fx = _as_fixture(_oracle_rollout(model, inputs, opts, w.max_cache_steps))
     same = check_codes(r["codes"], r["eos"], fx)

@@ -40,6 +40,7 @@ def test_option_defaults_match_the_reference():
             o.temperature, o.repetition_penalty, o.subtalker_dosample, o.subtalker_top_k, o.subtalker_top_p,
             o.subtalker_temperature, o.seed) == ("ryan", "english", 240, True, True, 50, 1.0, 0.9, 1.05, True, 50,
                                                  1.0, 0.9, 0)
+    assert o.repetition_penalty_per_occurrence is False and o._c().repetition_penalty_per_occurrence == 0
     s = E.StreamOptions()
     assert (s.text_lookahead_tokens, s.left_context_frames) == (8, 25)
     assert (E.DEFAULT_MAX_CACHE_STEPS, E.DEFAULT_PREFILL_HEADROOM, E.SAMPLE_RATE) == (512, 256, 24000)

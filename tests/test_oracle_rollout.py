@@ -99,9 +99,9 @@ def test_repetition_history_is_all_emitted_semantics():
     seen = []
 
     class Spy(ScriptedOracle):
-        def talker_select(self, logits, history, penalty, cfg, u):
+        def talker_select(self, logits, history, penalty, cfg, u, per_occurrence=False):
             seen.append(None if history is None else list(history))
-            return super().talker_select(logits, history, penalty, cfg, u)
+            return super().talker_select(logits, history, penalty, cfg, u, per_occurrence)
 
     o = Spy([3, 4, 3, 5])
     opts = GenerateOptions(max_frames=4, do_sample=False, repetition_penalty=1.2, subtalker_dosample=False)

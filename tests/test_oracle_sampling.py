@@ -34,6 +34,23 @@ def test_repetition_penalty_once_per_distinct_token():
     np.testing.assert_array_equal(S.apply_repetition_penalty(l, [], 2.0), l)
 
 
+def test_repetition_penalty_per_occurrence_compounds():
+    """The crate's GPU kernel applies the penalty once per history entry (kernels.rs:408-426):
+    a token seen three times is divided (positive) or multiplied (negative) three times."""
+    l = np.array([8.0, -2.0, 1.0, 0.5, 3.0])
+    hist = [0, 1, 0, 0, 4, 9, -1]          # out-of-range ids are skipped, as in the kernel
+    out = S.apply_repetition_penalty(l, hist, 2.0, per_occurrence=True)
+    np.testing.assert_array_equal(out, [1.0, -4.0, 1.0, 0.5, 1.5])
+    once = S.apply_repetition_penalty(l, hist, 2.0)
+    np.testing.assert_array_equal(once, [4.0, -4.0, 1.0, 0.5, 1.5])
+    # a history without repeats gives the same result under both rules
+    np.testing.assert_array_equal(S.apply_repetition_penalty(l, [0, 1, 4], 1.3, per_occurrence=True),
+                                  S.apply_repetition_penalty(l, [0, 1, 4], 1.3))
+    # the order of the history does not matter (each token's logit sees only its own entries)
+    np.testing.assert_array_equal(S.apply_repetition_penalty(l, [0, 0, 1, 0, 4], 1.7, per_occurrence=True),
+                                  S.apply_repetition_penalty(l, [4, 0, 1, 0, 0], 1.7, per_occurrence=True))
+
+
 def _brute_distribution(logits, k, p, T):
     """Enumerate the kept set from the definitions, independently of kept_distribution."""
     idx = sorted(range(len(logits)), key=lambda i: (-logits[i], i))
