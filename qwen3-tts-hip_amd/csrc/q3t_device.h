@@ -195,8 +195,9 @@ struct GemmArgs {
   int32_t xseg_len, xseg_stride;
   float eps;               // skinny GEMM with a fused RMSNorm
   const int32_t *row_on;   // skinny GEMM: row m is stored only where row_on[m] (null: all rows)
-  // skinny GEMM layouts: X / Y / res in T16 (ld ignored) instead of row-major, and W packed
-  // as [N/16][K/32][64 lanes][8] (each k step of a 16-column tile is 1 KiB contiguous).
+  // skinny GEMM layouts: X / Y / res in T16 (ld ignored) instead of row-major.  Its W must be
+  // packed (w_packed = 1) as [N/16][K/32][64 lanes][8] (each k step of a 16-column tile is
+  // 1 KiB contiguous).
   int32_t x_t16, y_t16, r_t16, w_packed;
   // skinny GEMM, EPI_STORE: instead of Y, each workgroup (16 columns) stores every row's
   // largest order key (value, lowest column) at keys_out[m * keys_row + blockIdx.x].

@@ -2605,6 +2605,16 @@ int q3t_debug_gemm(q3t_engine *e, int32_t epi, const float *X, int32_t M, int32_
       if (gemm_skinny_supports(M, K, gamma != nullptr)) {  // the batched-decode kernel (fused RMSNorm)
         if (gamma) g.gamma = (const float *)up(gamma, (size_t)K * 4);
         g.eps = eps;
+        // Packed weights in whole 16-column tiles: the last tile's missing rows are zeros.
+        if (N % 16 && epi == EPI_SWIGLU) fail(Q3T_ERR_INVALID, "the batched-decode SwiGLU GEMM needs N %% 16 == 0");
+        const size_t prows = (wrows + 15) / 16 * 16;
+        uint16_t *padded = (uint16_t *)up(nullptr, prows * K * 2);
+        HIPC(hipMemset(padded, 0, prows * K * 2));
+        HIPC(hipMemcpy(padded, g.W, wrows * K * 2, hipMemcpyDeviceToDevice));
+        uint16_t *packed = (uint16_t *)up(nullptr, prows * K * 2);
+        hip_check(launch_pack_weights(padded, packed, (int)prows, K, nullptr), "launch_pack_weights");
+        g.W = packed;
+        g.w_packed = 1;
         hip_check(launch_gemm_skinny(epi, gamma != nullptr, g, nullptr), "launch_gemm_skinny");
       } else {
         if (gamma) {

@@ -1251,10 +1251,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
     }
 }
 
-__device__ const int32_t kAllRowsOn[16] = {1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1};
-
-// KEYS (EPI_STORE): store per-row argmax keys (GemmArgs::keys_out) instead of Y.
-template <int EPI, bool NORM, int KS, bool KEYS = false>  // KS = 32-wide k steps per wave = K / (16 * 32)
+// KEYS (EPI_STORE): store per-row argmax keys (GemmArgs::keys_out) instead of Y.  XT16: X is
+// a T16 block (else row-major with leading dimension ldx).  W is always in k_pack_w's layout,
+// in whole 16-column tiles (the last one padded).
+// Both operand layouts are compile-time so that the load phase has no branch: a branch there
+// makes the first MFMA wait for every load of the pass (vmcnt(0)) instead of its own step's.
+template <int EPI, bool NORM, int KS, bool KEYS = false, bool XT16 = true>  // KS = K / (16 * 32)
 __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
   static_assert(!KEYS || EPI == EPI_STORE, "keys replace the plain store");
   constexpr int T = (EPI == EPI_SWIGLU) ? 2 : 1;
@@ -1275,7 +1277,9 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
   const int ol = ot >> 2, oe = ot & 3;
   const int om = 4 * (ol >> 4) + oe, on = n0 + (ol & 15);
   const int cm = min(om, a.M - 1), cn = min(on, a.N - 1);
-  const int oflag = (a.row_on ? a.row_on : kAllRowsOn)[cm];  // no branch: the wait stays at the use
+  // A global load (never a flat one: a pending flat load makes every later wait a vmcnt(0)).
+  int oflag = 1;
+  if (a.row_on) oflag = a.row_on[cm];
   float oadd = 0.f;
   if constexpr (EPI == EPI_RESIDUAL) oadd = a.res[a.r_t16 ? t16_index(cm, cn) : (size_t)cm * a.ldr + cn];
   if constexpr (EPI == EPI_BIAS) oadd = a.bias[cn];
@@ -1298,7 +1302,7 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
       const int k0 = kbase + (p0 + st) * 32;
       const int k = k0 + 8 * kb;
       const float4 *px = reinterpret_cast<const float4 *>(
-          a.x_t16 ? a.X + ((size_t)(k0 >> 5) * 64 + lane) * 8 : a.X + (size_t)arow * a.ldx + k);
+          XT16 ? a.X + ((size_t)(k0 >> 5) * 64 + lane) * 8 : a.X + (size_t)arow * a.ldx + k);
       const float4 x0 = px[0], x1 = px[1];
       xa[st][0] = x0.x; xa[st][1] = x0.y; xa[st][2] = x0.z; xa[st][3] = x0.w;
       xa[st][4] = x1.x; xa[st][5] = x1.y; xa[st][6] = x1.z; xa[st][7] = x1.w;
@@ -1309,14 +1313,9 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
         ga[st][4] = g1.x; ga[st][5] = g1.y; ga[st][6] = g1.z; ga[st][7] = g1.w;
       }
 #pragma unroll
-      for (int t = 0; t < T; ++t) {
-        if (a.w_packed) {  // tile blockIdx.x (+ N / 16 for the up rows), k step k0 / 32
-          const size_t tile = blockIdx.x + (size_t)t * (a.N >> 4);
-          wb[st][t] = *reinterpret_cast<const uint4 *>(a.W + ((tile * (a.K >> 5) + (k0 >> 5)) * 64 + lane) * 8);
-        } else {
-          const int col = min(n0 + li, a.N - 1) + t * a.N;
-          wb[st][t] = *reinterpret_cast<const uint4 *>(a.W + (size_t)col * a.K + k);
-        }
+      for (int t = 0; t < T; ++t) {  // tile blockIdx.x (+ N / 16 for the up rows), k step k0 / 32
+        const size_t tile = blockIdx.x + (size_t)t * (a.N >> 4);
+        wb[st][t] = *reinterpret_cast<const uint4 *>(a.W + ((tile * (a.K >> 5) + (k0 >> 5)) * 64 + lane) * 8);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -2489,33 +2488,39 @@ static hipError_t gemm_epi(const GemmArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int EPI, bool NORM>
+template <int EPI, bool NORM, bool XT16>
 static hipError_t skinny_ks(const GemmArgs &a, hipStream_t s) {
   const dim3 grid((a.N + 15) / 16), block(1024);
   switch (a.K / 512) {
-    case 1: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 1>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 2>), grid, block, 0, s, a); break;
-    case 3: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 3>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 4>), grid, block, 0, s, a); break;
+    case 1: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 1, false, XT16>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 2, false, XT16>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 3, false, XT16>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 4, false, XT16>), grid, block, 0, s, a); break;
     case 6:
       if constexpr (NORM) return hipErrorInvalidValue;
-      else hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 6>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 6, false, XT16>), grid, block, 0, s, a);
       break;
     case 8:
       if constexpr (NORM) return hipErrorInvalidValue;
-      else hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 8>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 8, false, XT16>), grid, block, 0, s, a);
       break;
     case 12:
       if constexpr (NORM) return hipErrorInvalidValue;
-      else hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 12>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 12, false, XT16>), grid, block, 0, s, a);
       break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
-// The greedy hand-off producer (LM heads over stream rows): per-row argmax keys, no Y.
+template <int EPI, bool NORM>
+static hipError_t skinny_ks(const GemmArgs &a, hipStream_t s) {
+  return a.x_t16 ? skinny_ks<EPI, NORM, true>(a, s) : skinny_ks<EPI, NORM, false>(a, s);
+}
+
+// The greedy hand-off producer (LM heads over stream rows, T16 input): per-row argmax keys, no Y.
 static hipError_t skinny_keys(const GemmArgs &a, hipStream_t s) {
+  if (!a.x_t16) return hipErrorInvalidValue;
   const dim3 grid((a.N + 15) / 16), block(1024);
   switch (a.K / 512) {
     case 1: hipLaunchKernelGGL((k_gemm_skinny<EPI_STORE, true, 1, true>), grid, block, 0, s, a); break;
@@ -2533,8 +2538,11 @@ bool gemm_skinny_supports(int M, int K, bool norm) {
 hipError_t launch_gemm_skinny(int epi, bool norm, const GemmArgs &a, hipStream_t s) {
   if (!gemm_skinny_supports(a.M, a.K, norm) || a.N <= 0 || a.ldx % 4 || (norm && (!a.gamma || a.row_scale)))
     return hipErrorInvalidValue;
-  // T16 output / residual needs N % 32 (whole k steps); packed weights need whole 16-column tiles.
-  if (((a.y_t16 || a.r_t16) && a.N % 32) || (a.w_packed && a.N % 16)) return hipErrorInvalidValue;
+  // T16 output / residual needs N % 32 (whole k steps).  The weights must be packed
+  // (launch_pack_weights) in whole 16-column tiles, the last one padded; SwiGLU's up tiles
+  // start at tile N / 16, so it needs N % 16 == 0.
+  if (((a.y_t16 || a.r_t16) && a.N % 32) || !a.w_packed || (epi == EPI_SWIGLU && a.N % 16))
+    return hipErrorInvalidValue;
   if (a.keys_out) {
     if (epi != EPI_STORE || !norm || a.keys_row < (a.N + 15) / 16) return hipErrorInvalidValue;
     return skinny_keys(a, s);
