@@ -357,7 +357,8 @@ int q3t_sampler_draw(q3t_engine *engine, const float *logits, int32_t vocab, int
  * W = [gate rows; up rows] ([2N][K]), 3 + bias[N]).  gamma != NULL applies RMSNorm(eps) with
  * gain gamma[K] to each row of X first.  W is bf16 bits; X, Y, res, bias fp32 host arrays.
  * M <= 16 with K = 512 * {1,2,3,4,6,8,12} runs the batched-decode (skinny) kernel, other
- * shapes the prefill kernel. */
+ * shapes the prefill kernel.  epi 4 is epi 1 in the batched frame's K-split form (M <= 16,
+ * K = 1024 * {1,2,3,4,6}, N % 32 == 0, no gamma): two K halves summed by fp32 atomic adds. */
 int q3t_debug_gemm(q3t_engine *engine, int32_t epi, const float *X, int32_t M, int32_t K,
                    const uint16_t *W, int32_t N, const float *gamma, float eps, const float *res,
                    const float *bias, float *Y);

@@ -208,6 +208,13 @@ struct GemmArgs {
   // kernel adds the splits in order and applies the epilogue.  Null: never split.
   float *split_ws;
   int64_t split_cap;
+  // skinny GEMM, EPI_RESIDUAL, T16 Y: K split in two halves over grid y.  Each half adds its
+  // sums to Y with an fp32 atomic add, so Y must hold zeros; two adds onto zero commute, so
+  // the result does not depend on their order.  The first half also adds the residual, and
+  // then stores zero to res_zero (T16, may be res itself) at the same element: the buffer
+  // the next split GEMM of the chain accumulates into.
+  int32_t split2;
+  float *res_zero;
 };
 
 // Prompt prefill attention over rows at positions pos0 .. pos0 + P - 1.

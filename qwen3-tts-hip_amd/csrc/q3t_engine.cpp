@@ -280,6 +280,10 @@ struct Engine {
   // Batched-frame activations in T16 (16 stream rows): residual streams, attention output,
   // MLP activation, projected CodePredictor inputs.
   float *bx_t = nullptr, *bx_c = nullptr, *battn = nullptr, *bact = nullptr, *bcp_in = nullptr;
+  // The mid-layer residual (after attention) of the K-split O / down GEMMs: all zeros
+  // except between a layer's O GEMM, which accumulates into it, and its down GEMM, which
+  // reads it as the residual and zeroes it again.
+  float *bmid = nullptr;
   std::vector<Slot> slots;
   Pools pools;
   bool rows_ok = false;  // the batched frame's fused-norm GEMMs support both hidden sizes
@@ -649,6 +653,11 @@ struct Engine {
   };
   static Act t16(const float *p) { return Act{p, -1}; }
 
+  // The batched frame's O and down GEMMs split K in two (rgemm_split2) when both can.
+  bool split2_ok(const Dims &d) const {
+    return bmid && gemm_skinny_split2_supports(d.q_out()) && gemm_skinny_split2_supports(d.intermediate);
+  }
+
   // Skinny matrix-core GEMM over the stream rows, packed weights Wp.
   void rgemm(int epi, bool norm, const uint16_t *Wp, Act X, const float *gamma, float eps, Act res,
              const float *bias, Act Y, int N, int K, int rows, hipStream_t s, uint64_t *keys_out = nullptr,
@@ -678,6 +687,7 @@ struct Engine {
     const int nch = (w.cap + chunk - 1) / chunk;
     const int partial = nch > 1 ? 1 : 0;
     const Act none{nullptr, 0};
+    const bool split = split2_ok(d);
     for (int l = 0; l < d.layers; ++l) {
       const LayerW &L = w.layers[l];
       const Act src = l == 0 ? in : t16(x);
@@ -707,11 +717,34 @@ struct Engine {
                         p.row_on,    1};
         hip_check(launch_attn_merge(m, rows, s), "launch_attn_merge");
       }
+      if (split) {
+        // O: bmid (zeros) += src + W_o . attn in two K halves, the first half also zeroing x
+        // (which the down GEMM then accumulates into); down: x += bmid + W_d . act, zeroing bmid.
+        rgemm_split2(L.o_p, t16(battn), src, x, bmid, H, d.q_out(), rows, s);
+        rgemm(EPI_SWIGLU, true, L.gu_p, t16(bmid), L.g_post, d.eps, none, nullptr, t16(bact), d.intermediate, H,
+              rows, s);
+        rgemm_split2(L.down_p, t16(bact), t16(bmid), bmid, x, H, d.intermediate, rows, s);
+        continue;
+      }
       rgemm(EPI_RESIDUAL, false, L.o_p, t16(battn), nullptr, 0.f, src, nullptr, t16(x), H, d.q_out(), rows, s);
       rgemm(EPI_SWIGLU, true, L.gu_p, t16(x), L.g_post, d.eps, none, nullptr, t16(bact), d.intermediate, H, rows, s);
       rgemm(EPI_RESIDUAL, false, L.down_p, t16(bact), nullptr, 0.f, t16(x), nullptr, t16(x), H, d.intermediate,
             rows, s);
     }
+  }
+
+  // Y (T16, zeros) += res + X . Wp^T over two K halves (GemmArgs::split2); the first half
+  // stores zero to res_zero (T16) at each element it adds.
+  void rgemm_split2(const uint16_t *Wp, Act X, Act res, float *res_zero, float *Y, int N, int K, int rows,
+                    hipStream_t s) {
+    GemmArgs g{};
+    g.X = X.p; g.ldx = K; g.x_t16 = 1;
+    g.W = Wp; g.w_packed = 1;
+    g.res = res.p; g.ldr = res.ld < 0 ? N : res.ld; g.r_t16 = res.ld < 0;
+    g.Y = Y; g.ldy = N; g.y_t16 = 1;
+    g.M = rows; g.N = N; g.K = K; g.row_on = pools.row_on;
+    g.split2 = 1; g.res_zero = res_zero;
+    hip_check(launch_gemm_skinny(EPI_RESIDUAL, false, g, s), "launch_gemm_skinny(split2)");
   }
 
   void select_talker_rows(int rows, int after_frame, Act x, hipStream_t s) {
@@ -1051,6 +1084,7 @@ void alloc_rows(Engine &e) {
   e.battn = zeroed((size_t)16 * std::max(td.q_out(), cd.q_out()));
   e.bact = zeroed((size_t)16 * std::max(td.intermediate, cd.intermediate));
   e.bcp_in = zeroed((size_t)3 * 16 * Hc);
+  e.bmid = zeroed((size_t)16 * std::max(Ht, Hc));
 }
 
 // Logit trace buffers for every slot, allocated the first time a traced stream starts.
@@ -1338,7 +1372,7 @@ int q3t_engine_destroy(q3t_engine *e) {
                     e->cp.mats_p,   e->codec_head_p, e->lm_heads_p,  e->proj_w_p,    e->bx_t,
                     e->bx_c,        e->battn,        e->bact,        e->bcp_in,      e->cp_qkv_table,
                     e->cp_in_table, e->text_emb,     e->tp_fc1,      e->tp_fc2,      e->tp_b1,
-                    e->tp_b2,       e->split_ws};
+                    e->tp_b2,       e->split_ws,    e->bmid};
     for (void *p : ptrs)
       if (p) (void)hipFree(p);
     delete e;
@@ -2577,6 +2611,13 @@ int q3t_debug_gemm(q3t_engine *e, int32_t epi, const float *X, int32_t M, int32_
     using namespace q3t;
     if (!e || !X || !W || !Y) fail(Q3T_ERR_INVALID, "null argument");
     if (M <= 0 || N <= 0 || K <= 0 || K % 32) fail(Q3T_ERR_INVALID, "need M, N > 0 and K a positive multiple of 32");
+    // 4: the residual product in the batched frame's K-split form (GemmArgs::split2).
+    const bool split2 = epi == 4;
+    if (split2) {
+      if (M > 16 || gamma || !gemm_skinny_split2_supports(K) || N % 32)
+        fail(Q3T_ERR_INVALID, "the split GEMM needs M <= 16, K = 1024 * {1,2,3,4,6}, N %% 32 == 0, no RMSNorm");
+      epi = EPI_RESIDUAL;
+    }
     if (epi < EPI_STORE || epi > EPI_BIAS) fail(Q3T_ERR_INVALID, "unknown epilogue %d", epi);
     if ((epi == EPI_RESIDUAL && !res) || (epi == EPI_BIAS && !bias)) fail(Q3T_ERR_INVALID, "missing operand");
     HIPC(hipSetDevice(e->device));
@@ -2602,6 +2643,33 @@ int q3t_debug_gemm(q3t_engine *e, int32_t epi, const float *X, int32_t M, int32_
       g.ldr = N;
       if (res) g.res = (const float *)up(res, (size_t)M * N * 4);
       if (bias) g.bias = (const float *)up(bias, (size_t)N * 4);
+      if (split2) {
+        // T16 operands (16 rows, the rows past M zero); Y starts at zero; res_zero starts at
+        // ones and must come back zero in the M x N elements the product stored.
+        std::vector<float> xt((size_t)16 * K, 0.f), yt((size_t)16 * N, 0.f), zt((size_t)16 * N, 1.f);
+        for (int m = 0; m < M; ++m)
+          for (int k = 0; k < K; ++k) xt[t16_index(m, k)] = X[(size_t)m * K + k];
+        g.X = (const float *)up(xt.data(), xt.size() * 4);
+        g.x_t16 = 1;
+        g.Y = (float *)up(yt.data(), yt.size() * 4);
+        g.y_t16 = 1;
+        g.res_zero = (float *)up(zt.data(), zt.size() * 4);
+        g.split2 = 1;
+        uint16_t *packed = (uint16_t *)up(nullptr, (size_t)N * K * 2);
+        hip_check(launch_pack_weights(g.W, packed, N, K, nullptr), "launch_pack_weights");
+        g.W = packed;
+        g.w_packed = 1;
+        hip_check(launch_gemm_skinny(EPI_RESIDUAL, false, g, nullptr), "launch_gemm_skinny(split2)");
+        HIPC(hipMemcpy(yt.data(), g.Y, yt.size() * 4, hipMemcpyDeviceToHost));
+        HIPC(hipMemcpy(zt.data(), g.res_zero, zt.size() * 4, hipMemcpyDeviceToHost));
+        for (int m = 0; m < M; ++m)
+          for (int n = 0; n < N; ++n) {
+            Y[(size_t)m * N + n] = yt[t16_index(m, n)];
+            if (zt[t16_index(m, n)] != 0.f) fail(Q3T_ERR_HIP, "split GEMM left res_zero[%d][%d] unzeroed", m, n);
+          }
+        for (void *p : owned) (void)hipFree(p);
+        return;
+      }
       if (gemm_skinny_supports(M, K, gamma != nullptr)) {  // the batched-decode kernel (fused RMSNorm)
         if (gamma) g.gamma = (const float *)up(gamma, (size_t)K * 4);
         g.eps = eps;

@@ -60,6 +60,8 @@ hipError_t launch_gemm(int epi, const GemmArgs &a, hipStream_t stream);
 // gain gamma (row_scale must be null).  Requires K = 512 * c, c in {1, 2, 3, 4, 6, 8, 12}
 // (K <= 2048 with norm).
 bool gemm_skinny_supports(int M, int K, bool norm);
+// GemmArgs::split2 (EPI_RESIDUAL, T16 X and Y): K = 1024 * c, c in {1, 2, 3, 4, 6}.
+bool gemm_skinny_split2_supports(int K);
 hipError_t launch_gemm_skinny(int epi, bool norm, const GemmArgs &a, hipStream_t stream);
 // dst = src [rows][K] bf16 in the skinny GEMM's packed layout (GemmArgs::w_packed).
 // Requires rows % 16 == 0 and K % 32 == 0.

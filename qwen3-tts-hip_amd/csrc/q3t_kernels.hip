@@ -1256,16 +1256,19 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
 // in whole 16-column tiles (the last one padded).
 // Both operand layouts are compile-time so that the load phase has no branch: a branch there
 // makes the first MFMA wait for every load of the pass (vmcnt(0)) instead of its own step's.
-template <int EPI, bool NORM, int KS, bool KEYS = false, bool XT16 = true>  // KS = K / (16 * 32)
+// SPLIT (GemmArgs::split2): grid y = 2 halves of K, KS = K / (2 * 16 * 32); the halves meet
+// in fp32 atomic adds on a zeroed T16 Y.
+template <int EPI, bool NORM, int KS, bool KEYS = false, bool XT16 = true, bool SPLIT = false>  // KS = K / (16 * 32)
 __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
   static_assert(!KEYS || EPI == EPI_STORE, "keys replace the plain store");
+  static_assert(!SPLIT || (EPI == EPI_RESIDUAL && !NORM && XT16), "the split GEMM is the T16 residual form");
   constexpr int T = (EPI == EPI_SWIGLU) ? 2 : 1;
   constexpr int KW = KS * 32;  // k range per wave
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;  // 0..15
   const int li = lane & 15, kb = lane >> 4;
   const int n0 = blockIdx.x * 16;
-  const int kbase = wave * KW;
+  const int kbase = (SPLIT ? blockIdx.y * (a.K >> 1) : 0) + wave * KW;
   const int arow = min(li, a.M - 1);
   __shared__ f32x4_t part[16][T][64];
   __shared__ float ssq[16][16];
@@ -1385,6 +1388,15 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
   }
   if (om >= a.M || on >= a.N || !oflag) return;
   float y = v[0];
+  if constexpr (SPLIT) {
+    const size_t oi = t16_index(om, on);
+    if (blockIdx.y == 0) {
+      y = oadd + y;
+      a.res_zero[oi] = 0.f;  // after this thread's own residual read (res_zero may be res)
+    }
+    unsafeAtomicAdd(a.Y + oi, y);
+    return;
+  }
   if constexpr (EPI == EPI_SWIGLU) {
     y = y / (1.0f + expf(-y)) * v[T - 1];
   } else if constexpr (EPI == EPI_RESIDUAL || EPI == EPI_BIAS) {
@@ -2518,6 +2530,22 @@ static hipError_t skinny_ks(const GemmArgs &a, hipStream_t s) {
   return a.x_t16 ? skinny_ks<EPI, NORM, true>(a, s) : skinny_ks<EPI, NORM, false>(a, s);
 }
 
+// The K-split residual GEMM (GemmArgs::split2): 2 x N / 16 workgroups, each half of K.
+static hipError_t skinny_split2(const GemmArgs &a, hipStream_t s) {
+  const dim3 grid((a.N + 15) / 16, 2), block(1024);
+  switch (a.K / 1024) {
+    case 1: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 1, false, true, true>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 2, false, true, true>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 3, false, true, true>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 4, false, true, true>), grid, block, 0, s, a); break;
+    case 6: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 6, false, true, true>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+bool gemm_skinny_split2_supports(int K) { return K % 1024 == 0 && (K / 1024 <= 4 || K / 1024 == 6); }
+
 // The greedy hand-off producer (LM heads over stream rows, T16 input): per-row argmax keys, no Y.
 static hipError_t skinny_keys(const GemmArgs &a, hipStream_t s) {
   if (!a.x_t16) return hipErrorInvalidValue;
@@ -2546,6 +2574,11 @@ hipError_t launch_gemm_skinny(int epi, bool norm, const GemmArgs &a, hipStream_t
   if (a.keys_out) {
     if (epi != EPI_STORE || !norm || a.keys_row < (a.N + 15) / 16) return hipErrorInvalidValue;
     return skinny_keys(a, s);
+  }
+  if (a.split2) {
+    if (epi != EPI_RESIDUAL || norm || !a.x_t16 || !a.y_t16 || !a.res_zero || !gemm_skinny_split2_supports(a.K))
+      return hipErrorInvalidValue;
+    return skinny_split2(a, s);
   }
   switch (epi) {
     case EPI_STORE: return norm ? skinny_ks<EPI_STORE, true>(a, s) : skinny_ks<EPI_STORE, false>(a, s);

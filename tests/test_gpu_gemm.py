@@ -83,9 +83,32 @@ def test_epilogues_skinny_and_tiled(eng, M):
     _close(eng.debug_gemm(2, X, Wb, N, gamma=g), gate / (1 + np.exp(-gate)) * up)
 
 
+@pytest.mark.parametrize("M,N,K", [(16, 1024, 2048), (16, 1024, 3072), (5, 256, 1024), (11, 64, 6144),
+                                   (1, 2048, 4096)])
+def test_residual_k_split(eng, M, N, K):
+    """The batched frame's O / down form: K in two halves whose sums meet in fp32 atomic adds
+    on a zeroed T16 output, the first half adding the residual and zeroing the next GEMM's
+    accumulator (the hook fails if any of its M x N elements is left nonzero).  Two adds onto
+    zero commute, so repeated calls agree bit for bit."""
+    print(f"[gpu] gemm residual K split M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M * 13 + K)
+    X = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    Wb = _weights(N, K, N * 3 + K)
+    W = synth.bf16_bits_to_f32(Wb).astype(np.float64)
+    res = rng.standard_normal((M, N)).astype(np.float32)
+    got = eng.debug_gemm(4, X, Wb, N, res=res)
+    _close(got, res + X.astype(np.float64) @ W.T)
+    assert np.array_equal(got.view(np.uint32), eng.debug_gemm(4, X, Wb, N, res=res).view(np.uint32))
+    # the same product through the single-pass kernel, to fp32 summation order
+    np.testing.assert_allclose(got, eng.debug_gemm(1, X, Wb, N, res=res), rtol=0, atol=2e-6 * np.abs(got).max())
+
+
 def test_rejects_bad_shapes(eng):
     with pytest.raises(E.InvalidInputError):
         eng.debug_gemm(0, np.zeros((4, 48), np.float32), np.zeros((8, 48), np.uint16), 8)
+    with pytest.raises(E.InvalidInputError):  # the K split needs K = 1024 * c
+        eng.debug_gemm(4, np.zeros((4, 512), np.float32), np.zeros((32, 512), np.uint16), 32,
+                       res=np.zeros((4, 32), np.float32))
 
 
 @pytest.mark.parametrize("M,K", [(128, 1024), (300, 2048), (521, 1024)])
