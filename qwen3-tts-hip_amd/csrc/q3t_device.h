@@ -215,6 +215,12 @@ struct GemmArgs {
   // the next split GEMM of the chain accumulates into.
   int32_t split2;
   float *res_zero;
+  // skinny GEMM: mb = 2 runs two 16-row blocks (two positions of the same stream rows, row m
+  // of either block masked by row_on[m]) against one pass over W.  Block 1 of a T16 operand
+  // starts 16 * K (X) or 16 * N (Y, res, res_zero) elements after block 0; of a row-major one,
+  // x_blk / r_blk / y_blk elements after.
+  int32_t mb;
+  int64_t x_blk, r_blk, y_blk;
 };
 
 // Prompt prefill attention over rows at positions pos0 .. pos0 + P - 1.
@@ -233,6 +239,13 @@ struct PrefillAttnArgs {
   int32_t wo_rows;
   float *opart;
   int64_t opart_row;
+  // launch_prefix_attention_rows (stream rows, grid z = row r, no fused projection): row r
+  // reads position p's projections at qkv + r * ldq + p * ld_pos, its caches at kcache /
+  // vcache + r * kv_row elements and its state at st + r (nothing is done for an ended or
+  // masked row), and writes T16 blocks: position p at out + p * 16 * ldo (ldo = q_heads * d).
+  int64_t ld_pos, kv_row;
+  const SlotState *st;
+  const int32_t *row_on;
 };
 
 struct SelectTalkerArgs {

@@ -284,6 +284,8 @@ struct Engine {
   // except between a layer's O GEMM, which accumulates into it, and its down GEMM, which
   // reads it as the residual and zeroes it again.
   float *bmid = nullptr;
+  // The two-block prefix pass's q/k/v rows: [2 positions][16 rows][qkv_rows] (row-major).
+  float *bqkv2 = nullptr;
   std::vector<Slot> slots;
   Pools pools;
   bool rows_ok = false;  // the batched frame's fused-norm GEMMs support both hidden sizes
@@ -735,16 +737,64 @@ struct Engine {
 
   // Y (T16, zeros) += res + X . Wp^T over two K halves (GemmArgs::split2); the first half
   // stores zero to res_zero (T16) at each element it adds.
+  // mb = 2: two row blocks (the prefix pass); a row-major res has its block 1 res_blk
+  // elements after block 0.
   void rgemm_split2(const uint16_t *Wp, Act X, Act res, float *res_zero, float *Y, int N, int K, int rows,
-                    hipStream_t s) {
+                    hipStream_t s, int mb = 1, int64_t res_blk = 0) {
     GemmArgs g{};
     g.X = X.p; g.ldx = K; g.x_t16 = 1;
     g.W = Wp; g.w_packed = 1;
-    g.res = res.p; g.ldr = res.ld < 0 ? N : res.ld; g.r_t16 = res.ld < 0;
+    g.res = res.p; g.ldr = res.ld < 0 ? N : res.ld; g.r_t16 = res.ld < 0; g.r_blk = res_blk;
     g.Y = Y; g.ldy = N; g.y_t16 = 1;
     g.M = rows; g.N = N; g.K = K; g.row_on = pools.row_on;
-    g.split2 = 1; g.res_zero = res_zero;
+    g.split2 = 1; g.res_zero = res_zero; g.mb = mb;
     hip_check(launch_gemm_skinny(EPI_RESIDUAL, false, g, s), "launch_gemm_skinny(split2)");
+  }
+
+  // The CodePredictor's two prefix positions of every stream row in one pass per layer: the
+  // skinny GEMMs run two 16-row blocks (block p = position p) against one read of each weight,
+  // and one prefix-attention launch stores both positions' K/V rows and attends causally.
+  // Position p's input is block p of `in` (T16, or row-major with block p in_blk elements
+  // after block 0); block p of bx_c receives its output.  Needs prefix2_ok().
+  void rows_prefix_pass(Act in, int64_t in_blk, int rows, hipStream_t s) {
+    const StackW &w = cp;
+    const Dims &d = w.d;
+    Pools &p = pools;
+    const int H = d.hidden, Q = d.qkv_rows(), O = d.q_out(), I = d.intermediate;
+    const size_t cache_layer = (size_t)d.kv_heads * w.cap * d.head_dim * (kv_bf16 ? 2 : 4);
+    for (int l = 0; l < d.layers; ++l) {
+      const LayerW &L = w.layers[l];
+      const Act src = l == 0 ? in : t16(bx_c);
+      const int64_t src_blk = l == 0 ? in_blk : 0;
+      GemmArgs g{};
+      g.X = src.p; g.ldx = src.ld < 0 ? H : src.ld; g.x_t16 = src.ld < 0; g.x_blk = src_blk;
+      g.gamma = L.g_in; g.eps = d.eps; g.W = L.qkv_p; g.w_packed = 1;
+      g.Y = bqkv2; g.ldy = Q; g.y_blk = (int64_t)16 * Q;
+      g.M = rows; g.N = Q; g.K = H; g.row_on = p.row_on; g.mb = 2;
+      hip_check(launch_gemm_skinny(EPI_STORE, true, g, s), "launch_gemm_skinny(prefix qkv)");
+      PrefillAttnArgs pa{bqkv2, L.gq, L.gk, w.rope, p.c_k + l * cache_layer, p.c_v + l * cache_layer, battn, 2, 0,
+                         Q, O, d.q_heads, d.kv_heads, w.cap, d.eps, 1.0f / std::sqrt((float)d.head_dim), kv_bf16};
+      pa.ld_pos = (int64_t)16 * Q;
+      pa.kv_row = (int64_t)p.c_kv_row;
+      pa.st = p.st;
+      pa.row_on = p.row_on;
+      hip_check(launch_prefix_attention_rows(pa, rows, s), "launch_prefix_attention_rows");
+      rgemm_split2(L.o_p, t16(battn), src, bx_c, bmid, H, O, rows, s, 2, src_blk);
+      g = GemmArgs{};
+      g.X = bmid; g.ldx = H; g.x_t16 = 1;
+      g.gamma = L.g_post; g.eps = d.eps; g.W = L.gu_p; g.w_packed = 1;
+      g.Y = bact; g.ldy = I; g.y_t16 = 1;
+      g.M = rows; g.N = I; g.K = H; g.row_on = p.row_on; g.mb = 2;
+      hip_check(launch_gemm_skinny(EPI_SWIGLU, true, g, s), "launch_gemm_skinny(prefix gate/up)");
+      rgemm_split2(L.down_p, t16(bact), t16(bmid), bmid, bx_c, H, I, rows, s, 2);
+    }
+  }
+
+  // The two-block prefix pass applies: the split O / down GEMMs, and K = H within the
+  // two-block RMSNorm GEMMs' sizes.
+  bool prefix2_ok() const {
+    auto k_ok = [](int k) { return k == 512 || k == 1024 || k == 2048; };
+    return bqkv2 && split2_ok(cd) && k_ok(cd.hidden) && (!has_proj || k_ok(talker_hidden));
   }
 
   void select_talker_rows(int rows, int after_frame, Act x, hipStream_t s) {
@@ -774,14 +824,31 @@ struct Engine {
     const Act none{nullptr, 0};
     const size_t hc16 = (size_t)16 * Hc;
     Act in0{p.cp_prefix, 2 * Ht}, in1{p.cp_prefix + Ht, 2 * Ht};
-    if (has_proj) {
-      rgemm(EPI_BIAS, false, proj_w_p, in0, nullptr, 0.f, none, proj_b, t16(bcp_in), Hc, Ht, rows, s);
-      rgemm(EPI_BIAS, false, proj_w_p, in1, nullptr, 0.f, none, proj_b, t16(bcp_in + hc16), Hc, Ht, rows, s);
-      in0 = t16(bcp_in);
-      in1 = t16(bcp_in + hc16);
+    // group 0's LM head reads the prefix's position-1 output: block 1 of bx_c after the
+    // two-block pass, else bx_c after the second one-position pass
+    const float *x_pre = bx_c;
+    if (prefix2_ok()) {
+      Act in = in0;
+      if (has_proj) {
+        GemmArgs g{};
+        g.X = p.cp_prefix; g.ldx = 2 * Ht; g.x_blk = Ht; g.W = proj_w_p; g.w_packed = 1; g.bias = proj_b;
+        g.Y = bcp_in; g.ldy = Hc; g.y_t16 = 1;
+        g.M = rows; g.N = Hc; g.K = Ht; g.row_on = p.row_on; g.mb = 2;
+        hip_check(launch_gemm_skinny(EPI_BIAS, false, g, s), "launch_gemm_skinny(prefix projection)");
+        in = t16(bcp_in);
+      }
+      rows_prefix_pass(in, has_proj ? 0 : Ht, rows, s);
+      x_pre = bx_c + hc16;
+    } else {
+      if (has_proj) {
+        rgemm(EPI_BIAS, false, proj_w_p, in0, nullptr, 0.f, none, proj_b, t16(bcp_in), Hc, Ht, rows, s);
+        rgemm(EPI_BIAS, false, proj_w_p, in1, nullptr, 0.f, none, proj_b, t16(bcp_in + hc16), Hc, Ht, rows, s);
+        in0 = t16(bcp_in);
+        in1 = t16(bcp_in + hc16);
+      }
+      rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in0, bx_c, rows, POS_CONST, 0, SKIP_DONE, s);
+      rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in1, bx_c, rows, POS_CONST, 1, SKIP_DONE, s);
     }
-    rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in0, bx_c, rows, POS_CONST, 0, SKIP_DONE, s);
-    rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in1, bx_c, rows, POS_CONST, 1, SKIP_DONE, s);
     for (int g = 0; g < nac; ++g) {
       if (g > 0 && fused) {
         TokenHandoff t{};
@@ -809,12 +876,13 @@ struct Engine {
         }
         rows_stack_step(cp, p.c_k, p.c_v, p.c_kv_row, in, bx_c, rows, POS_CONST, g + 1, SKIP_DONE, s);
       }
+      const float *xg = g == 0 ? x_pre : bx_c;
       if (fused && g < nac - 1) {
-        rgemm(EPI_STORE, true, lm_heads_p + (size_t)g * Vc * Hc, t16(bx_c), c_norm, cd.eps, none, nullptr,
+        rgemm(EPI_STORE, true, lm_heads_p + (size_t)g * Vc * Hc, t16(xg), c_norm, cd.eps, none, nullptr,
               Act{p.logits_c, Vc}, Vc, Hc, rows, s, p.cp_keys + (size_t)g * kHandoffKeys, keys_row);
         continue;
       }
-      rgemm(EPI_STORE, true, lm_heads_p + (size_t)g * Vc * Hc, t16(bx_c), c_norm, cd.eps, none, nullptr,
+      rgemm(EPI_STORE, true, lm_heads_p + (size_t)g * Vc * Hc, t16(xg), c_norm, cd.eps, none, nullptr,
             Act{p.logits_c, Vc}, Vc, Hc, rows, s);
       SelectCpArgs a{p.logits_c, cp_emb + (size_t)g * Vc * Ht, p.cur, p.emb_sum, p.codes,
                      trace ? p.trace_c : nullptr, p.t_in, codec_emb, p.trailing, p.st, p.prm, Vc, Ht, groups, g};
@@ -1079,12 +1147,14 @@ void alloc_rows(Engine &e) {
     HIPC(hipMemset(q, 0, n * 4));
     return q;
   };
+  // The CodePredictor's buffers hold two 16-row blocks (its prefix pass runs both positions).
   e.bx_t = zeroed((size_t)16 * Ht);
-  e.bx_c = zeroed((size_t)16 * Hc);
-  e.battn = zeroed((size_t)16 * std::max(td.q_out(), cd.q_out()));
-  e.bact = zeroed((size_t)16 * std::max(td.intermediate, cd.intermediate));
+  e.bx_c = zeroed((size_t)32 * Hc);
+  e.battn = zeroed((size_t)16 * std::max(td.q_out(), 2 * cd.q_out()));
+  e.bact = zeroed((size_t)16 * std::max(td.intermediate, 2 * cd.intermediate));
   e.bcp_in = zeroed((size_t)3 * 16 * Hc);
-  e.bmid = zeroed((size_t)16 * std::max(Ht, Hc));
+  e.bmid = zeroed((size_t)16 * std::max(Ht, 2 * Hc));
+  e.bqkv2 = zeroed((size_t)32 * cd.qkv_rows());
 }
 
 // Logit trace buffers for every slot, allocated the first time a traced stream starts.
@@ -1372,7 +1442,7 @@ int q3t_engine_destroy(q3t_engine *e) {
                     e->cp.mats_p,   e->codec_head_p, e->lm_heads_p,  e->proj_w_p,    e->bx_t,
                     e->bx_c,        e->battn,        e->bact,        e->bcp_in,      e->cp_qkv_table,
                     e->cp_in_table, e->text_emb,     e->tp_fc1,      e->tp_fc2,      e->tp_b1,
-                    e->tp_b2,       e->split_ws,    e->bmid};
+                    e->tp_b2,       e->split_ws,    e->bmid,        e->bqkv2};
     for (void *p : ptrs)
       if (p) (void)hipFree(p);
     delete e;

@@ -90,6 +90,9 @@ hipError_t launch_prefill_attention(const PrefillAttnArgs &a, hipStream_t stream
 // With a.wo set, the output projection is fused in as in launch_attn_oproj: row p's per-KV-head
 // shares go to a.opart + p * a.opart_row (a.out unused).
 hipError_t launch_prefix_attention(const PrefillAttnArgs &a, hipStream_t stream);
+// The same prefix for stream rows 0 .. rows - 1 (PrefillAttnArgs::ld_pos, kv_row, st, row_on),
+// output in T16 blocks, one per position; no fused projection.
+hipError_t launch_prefix_attention_rows(const PrefillAttnArgs &a, int rows, hipStream_t stream);
 
 // Token selection, one workgroup per stream row (rows > 1 needs row_on and the row strides).
 hipError_t launch_select_talker(const SelectTalkerArgs &a, hipStream_t stream, int rows = 1);

@@ -1258,10 +1258,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
 // makes the first MFMA wait for every load of the pass (vmcnt(0)) instead of its own step's.
 // SPLIT (GemmArgs::split2): grid y = 2 halves of K, KS = K / (2 * 16 * 32); the halves meet
 // in fp32 atomic adds on a zeroed T16 Y.
-template <int EPI, bool NORM, int KS, bool KEYS = false, bool XT16 = true, bool SPLIT = false>  // KS = K / (16 * 32)
+// MB = 2 (GemmArgs::mb): two 16-row blocks against one pass over W, the two positions of the
+// same stream rows (row m of block b is stream row m, masked by row_on[m]).  T16 operands of
+// block b start 16 * K (X) or 16 * N (Y, res, res_zero) elements after block 0; row-major ones
+// x_blk / r_blk / y_blk elements after.
+template <int EPI, bool NORM, int KS, bool KEYS = false, bool XT16 = true, bool SPLIT = false, int MB = 1>
 __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
   static_assert(!KEYS || EPI == EPI_STORE, "keys replace the plain store");
   static_assert(!SPLIT || (EPI == EPI_RESIDUAL && !NORM && XT16), "the split GEMM is the T16 residual form");
+  static_assert(MB == 1 || (MB == 2 && !KEYS), "two row blocks: no key store");
   constexpr int T = (EPI == EPI_SWIGLU) ? 2 : 1;
   constexpr int KW = KS * 32;  // k range per wave
   const int lane = threadIdx.x & 63;
@@ -1270,21 +1275,23 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
   const int n0 = blockIdx.x * 16;
   const int kbase = (SPLIT ? blockIdx.y * (a.K >> 1) : 0) + wave * KW;
   const int arow = min(li, a.M - 1);
-  __shared__ f32x4_t part[16][T][64];
-  __shared__ float ssq[16][16];
-  __shared__ float inv_rms[16];
+  __shared__ f32x4_t part[16][MB * T][64];
+  __shared__ float ssq[16][MB * 16];
 
-  // Output (om, on) of this thread's epilogue (threads 0..255, one output each).  Its
-  // residual / bias / row mask are loaded first so that the epilogue waits on nothing.
+  // Output (ob, om, on) of this thread's epilogue (threads 0 .. 256 MB - 1, one output each:
+  // block ob, row om, column on).  Its residual / bias / row mask are loaded first so that the
+  // epilogue waits on nothing.
   const int ot = threadIdx.x;
-  const int ol = ot >> 2, oe = ot & 3;
+  const int ob = min(ot >> 8, MB - 1);
+  const int ol = (ot & 255) >> 2, oe = ot & 3;
   const int om = 4 * (ol >> 4) + oe, on = n0 + (ol & 15);
   const int cm = min(om, a.M - 1), cn = min(on, a.N - 1);
   // A global load (never a flat one: a pending flat load makes every later wait a vmcnt(0)).
   int oflag = 1;
   if (a.row_on) oflag = a.row_on[cm];
   float oadd = 0.f;
-  if constexpr (EPI == EPI_RESIDUAL) oadd = a.res[a.r_t16 ? t16_index(cm, cn) : (size_t)cm * a.ldr + cn];
+  if constexpr (EPI == EPI_RESIDUAL)
+    oadd = a.res[a.r_t16 ? (size_t)ob * 16 * a.N + t16_index(cm, cn) : (size_t)cm * a.ldr + (size_t)ob * a.r_blk + cn];
   if constexpr (EPI == EPI_BIAS) oadd = a.bias[cn];
 
   // k steps in passes of KP (all loads of a pass in flight together): registers for
@@ -1292,23 +1299,29 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
   constexpr int KP = KS <= 6 ? KS : (KS % 6 == 0 ? 6 : 4);
   static_assert(KS % KP == 0, "pass length");
   static_assert(!NORM || KS <= 4, "the fused RMSNorm keeps the whole row slice in registers");
-  f32x4_t acc[T];
+  f32x4_t acc[MB][T];
 #pragma unroll
-  for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int b = 0; b < MB; ++b)
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[b][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int p0 = 0; p0 < KS; p0 += KP) {
-    float xa[KP][8];
+    float xa[MB][KP][8];
     float ga[NORM ? KP : 1][8];
     uint4 wb[KP][T];
 #pragma unroll
     for (int st = 0; st < KP; ++st) {
       const int k0 = kbase + (p0 + st) * 32;
       const int k = k0 + 8 * kb;
-      const float4 *px = reinterpret_cast<const float4 *>(
-          XT16 ? a.X + ((size_t)(k0 >> 5) * 64 + lane) * 8 : a.X + (size_t)arow * a.ldx + k);
-      const float4 x0 = px[0], x1 = px[1];
-      xa[st][0] = x0.x; xa[st][1] = x0.y; xa[st][2] = x0.z; xa[st][3] = x0.w;
-      xa[st][4] = x1.x; xa[st][5] = x1.y; xa[st][6] = x1.z; xa[st][7] = x1.w;
+#pragma unroll
+      for (int b = 0; b < MB; ++b) {
+        const float4 *px = reinterpret_cast<const float4 *>(
+            XT16 ? a.X + (size_t)b * 16 * a.K + ((size_t)(k0 >> 5) * 64 + lane) * 8
+                 : a.X + (size_t)arow * a.ldx + (size_t)b * a.x_blk + k);
+        const float4 x0 = px[0], x1 = px[1];
+        xa[b][st][0] = x0.x; xa[b][st][1] = x0.y; xa[b][st][2] = x0.z; xa[b][st][3] = x0.w;
+        xa[b][st][4] = x1.x; xa[b][st][5] = x1.y; xa[b][st][6] = x1.z; xa[b][st][7] = x1.w;
+      }
       if constexpr (NORM) {
         const float4 *pg = reinterpret_cast<const float4 *>(a.gamma + k);
         const float4 g0 = pg[0], g1 = pg[1];
@@ -1324,53 +1337,63 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
     __builtin_amdgcn_sched_barrier(0);
 
     if constexpr (NORM) {  // single pass: this wave holds its whole k range of every row
-      float ss = 0.f;
 #pragma unroll
-      for (int st = 0; st < KP; ++st)
+      for (int b = 0; b < MB; ++b) {
+        float ss = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ss = fmaf(xa[st][e], xa[st][e], ss);
-      ss += __shfl_xor(ss, 16, 64);  // the four lanes of a row (kb = 0..3)
-      ss += __shfl_xor(ss, 32, 64);
-      if (kb == 0) ssq[wave][li] = ss;
-      __syncthreads();
-      if (threadIdx.x < 16) {
-        float tot = 0.f;
-        for (int w = 0; w < 16; ++w) tot += ssq[w][threadIdx.x];
-        inv_rms[threadIdx.x] = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+        for (int st = 0; st < KP; ++st)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss = fmaf(xa[b][st][e], xa[b][st][e], ss);
+        ss += __shfl_xor(ss, 16, 64);  // the four lanes of a row (kb = 0..3)
+        ss += __shfl_xor(ss, 32, 64);
+        if (kb == 0) ssq[wave][b * 16 + li] = ss;
       }
       __syncthreads();
-      const float r = inv_rms[li];
+      // every lane sums its row's 16 wave shares itself (the same order for all): one
+      // barrier instead of a second one behind 16 threads
 #pragma unroll
-      for (int st = 0; st < KP; ++st)
+      for (int b = 0; b < MB; ++b) {
+        float tot = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xa[st][e] = (xa[st][e] * r) * ga[st][e];
+        for (int w = 0; w < 16; ++w) tot += ssq[w][b * 16 + li];
+        const float r = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+#pragma unroll
+        for (int st = 0; st < KP; ++st)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) xa[b][st][e] = (xa[b][st][e] * r) * ga[st][e];
+      }
     }
 
 #pragma unroll
     for (int st = 0; st < KP; ++st) {
-      bf16x8_t hi, mid, lo;
-      split_bf16x8(xa[st], hi, mid, lo);
 #pragma unroll
-      for (int t = 0; t < T; ++t) {
-        const bf16x8_t b = __builtin_bit_cast(bf16x8_t, wb[st][t]);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, b, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b, acc[t], 0, 0, 0);
+      for (int b = 0; b < MB; ++b) {
+        bf16x8_t hi, mid, lo;
+        split_bf16x8(xa[b][st], hi, mid, lo);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const bf16x8_t w = __builtin_bit_cast(bf16x8_t, wb[st][t]);
+          acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, w, acc[b][t], 0, 0, 0);
+          acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(mid, w, acc[b][t], 0, 0, 0);
+          acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, w, acc[b][t], 0, 0, 0);
+        }
       }
     }
   }
 #pragma unroll
-  for (int t = 0; t < T; ++t) part[wave][t][lane] = acc[t];
+  for (int b = 0; b < MB; ++b)
+#pragma unroll
+    for (int t = 0; t < T; ++t) part[wave][b * T + t][lane] = acc[b][t];
   __syncthreads();
-  if (ot >= 256) return;
+  if (ot >= 256 * MB) return;
   // Sum of the 16 waves' k ranges in wave order (C[i][j] sits in lane j + 16 (i / 4),
   // element i % 4: this thread's (om, on) is lane ol, element oe).
   float v[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) {
-    float sacc = part[0][t][ol][oe];
+    float sacc = part[0][ob * T + t][ol][oe];
 #pragma unroll
-    for (int w = 1; w < 16; ++w) sacc += part[w][t][ol][oe];
+    for (int w = 1; w < 16; ++w) sacc += part[w][ob * T + t][ol][oe];
     v[t] = sacc;
   }
   if constexpr (KEYS) {
@@ -1389,7 +1412,7 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
   if (om >= a.M || on >= a.N || !oflag) return;
   float y = v[0];
   if constexpr (SPLIT) {
-    const size_t oi = t16_index(om, on);
+    const size_t oi = (size_t)ob * 16 * a.N + t16_index(om, on);
     if (blockIdx.y == 0) {
       y = oadd + y;
       a.res_zero[oi] = 0.f;  // after this thread's own residual read (res_zero may be res)
@@ -1402,7 +1425,7 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
   } else if constexpr (EPI == EPI_RESIDUAL || EPI == EPI_BIAS) {
     y = (EPI == EPI_RESIDUAL) ? oadd + y : y + oadd;
   }
-  a.Y[a.y_t16 ? t16_index(om, on) : (size_t)om * a.ldy + on] = y;
+  a.Y[a.y_t16 ? (size_t)ob * 16 * a.N + t16_index(om, on) : (size_t)om * a.ldy + (size_t)ob * a.y_blk + on] = y;
 }
 
 // inv_rms[m] = 1 / sqrt(mean(X[m]^2) + eps), one wave per row.
@@ -1466,12 +1489,22 @@ __global__ __launch_bounds__(256) void k_prefill_qkv(PrefillAttnArgs a) {
 // OPROJ: the output projection fused in as in k_attn_split (grid (kv_heads, wo_rows / 32));
 // row p's per-head shares go to opart + p * opart_row + h * wo_rows.  Only row block 0 stores
 // the K/V rows.
-template <int G, typename KVT, int P, bool OPROJ = false>
+// ROWS: stream rows (PrefillAttnArgs::ld_pos ..), grid (kv_heads, 1, rows); the output goes to
+// T16 blocks, one per position.
+template <int G, typename KVT, int P, bool OPROJ = false, bool ROWS = false>
 __global__ __launch_bounds__(256) void k_attn_prefix(PrefillAttnArgs a) {
+  static_assert(!(OPROJ && ROWS), "stream rows take the unfused form");
   constexpr int D = 128, NV = P * (G + 2), VPW = (NV + 3) / 4;
   const int h = blockIdx.x;
   const int rb = OPROJ ? blockIdx.y : 0;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int row = ROWS ? blockIdx.z : 0;
+  if constexpr (ROWS) {
+    a.qkv += (size_t)row * a.ldq;
+    a.kcache = reinterpret_cast<KVT *>(a.kcache) + row * a.kv_row;
+    a.vcache = reinterpret_cast<KVT *>(a.vcache) + row * a.kv_row;
+  }
+  const int64_t ld_pos = ROWS ? a.ld_pos : a.ldq;
   __shared__ float qs[P][G][D], ks[P][D], vs[P][D];
   __shared__ float sc[P][G][P];
   __shared__ float ao[OPROJ ? P : 1][G * D];
@@ -1494,13 +1527,17 @@ __global__ __launch_bounds__(256) void k_attn_prefix(PrefillAttnArgs a) {
     const int p = vi / (G + 2), kind = vi % (G + 2);
     const int off = kind < G ? (h * G + kind) * D
                              : (kind == G ? a.q_heads * D + h * D : (a.q_heads + a.kv_heads) * D + h * D);
-    const float *src = a.qkv + (size_t)p * a.ldq + off;
+    const float *src = a.qkv + (size_t)p * ld_pos + off;
     x0[i] = src[lane];
     x1[i] = src[lane + 64];
     const float *gain = kind < G ? a.gq : a.gk;  // unused for v
     g0[i] = gain[lane];
     g1[i] = gain[lane + 64];
     cs[i] = a.rope[(size_t)p * (D / 2) + lane];
+  }
+  if constexpr (ROWS) {  // workgroup-uniform, after the loads (valid for any state)
+    if (a.row_on && !a.row_on[row]) return;
+    if (skip_work(a.st + row, SKIP_DONE)) return;
   }
 #pragma unroll
   for (int i = 0; i < VPW; ++i) {
@@ -1558,6 +1595,8 @@ __global__ __launch_bounds__(256) void k_attn_prefix(PrefillAttnArgs a) {
     }
     if constexpr (OPROJ)
       ao[p][g * D + d] = acc / l;
+    else if constexpr (ROWS)
+      a.out[(size_t)p * 16 * a.ldo + t16_index(row, (h * G + g) * D + d)] = acc / l;
     else
       a.out[(size_t)p * a.ldo + (h * G + g) * D + d] = acc / l;
   }
@@ -2531,17 +2570,41 @@ static hipError_t skinny_ks(const GemmArgs &a, hipStream_t s) {
 }
 
 // The K-split residual GEMM (GemmArgs::split2): 2 x N / 16 workgroups, each half of K.
+template <int MB>
 static hipError_t skinny_split2(const GemmArgs &a, hipStream_t s) {
   const dim3 grid((a.N + 15) / 16, 2), block(1024);
   switch (a.K / 1024) {
-    case 1: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 1, false, true, true>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 2, false, true, true>), grid, block, 0, s, a); break;
-    case 3: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 3, false, true, true>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 4, false, true, true>), grid, block, 0, s, a); break;
-    case 6: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 6, false, true, true>), grid, block, 0, s, a); break;
+    case 1: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 1, false, true, true, MB>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 2, false, true, true, MB>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 3, false, true, true, MB>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 4, false, true, true, MB>), grid, block, 0, s, a); break;
+    case 6: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 6, false, true, true, MB>), grid, block, 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+// Two row blocks (GemmArgs::mb = 2), the forms the CodePredictor's two-position prefix pass
+// runs: QKV (RMSNorm, T16 or row-major input), gate/up (RMSNorm, SwiGLU), the projection
+// (bias, row-major input); K = 512 * {1, 2, 4}.
+template <int EPI, bool NORM, bool XT16>
+static hipError_t skinny_mb2_ks(const GemmArgs &a, hipStream_t s) {
+  const dim3 grid((a.N + 15) / 16), block(1024);
+  switch (a.K / 512) {
+    case 1: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 1, false, XT16, false, 2>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 2, false, XT16, false, 2>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 4, false, XT16, false, 2>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+static hipError_t skinny_mb2(int epi, bool norm, const GemmArgs &a, hipStream_t s) {
+  if (epi == EPI_STORE && norm) return a.x_t16 ? skinny_mb2_ks<EPI_STORE, true, true>(a, s)
+                                                : skinny_mb2_ks<EPI_STORE, true, false>(a, s);
+  if (epi == EPI_SWIGLU && norm && a.x_t16) return skinny_mb2_ks<EPI_SWIGLU, true, true>(a, s);
+  if (epi == EPI_BIAS && !norm && !a.x_t16) return skinny_mb2_ks<EPI_BIAS, false, false>(a, s);
+  return hipErrorInvalidValue;
 }
 
 bool gemm_skinny_split2_supports(int K) { return K % 1024 == 0 && (K / 1024 <= 4 || K / 1024 == 6); }
@@ -2572,14 +2635,16 @@ hipError_t launch_gemm_skinny(int epi, bool norm, const GemmArgs &a, hipStream_t
   if (((a.y_t16 || a.r_t16) && a.N % 32) || !a.w_packed || (epi == EPI_SWIGLU && a.N % 16))
     return hipErrorInvalidValue;
   if (a.keys_out) {
-    if (epi != EPI_STORE || !norm || a.keys_row < (a.N + 15) / 16) return hipErrorInvalidValue;
+    if (epi != EPI_STORE || !norm || a.keys_row < (a.N + 15) / 16 || a.mb == 2) return hipErrorInvalidValue;
     return skinny_keys(a, s);
   }
+  if (a.mb != 0 && a.mb != 1 && a.mb != 2) return hipErrorInvalidValue;
   if (a.split2) {
     if (epi != EPI_RESIDUAL || norm || !a.x_t16 || !a.y_t16 || !a.res_zero || !gemm_skinny_split2_supports(a.K))
       return hipErrorInvalidValue;
-    return skinny_split2(a, s);
+    return a.mb == 2 ? skinny_split2<2>(a, s) : skinny_split2<1>(a, s);
   }
+  if (a.mb == 2) return skinny_mb2(epi, norm, a, s);
   switch (epi) {
     case EPI_STORE: return norm ? skinny_ks<EPI_STORE, true>(a, s) : skinny_ks<EPI_STORE, false>(a, s);
     case EPI_RESIDUAL: return norm ? hipErrorInvalidValue : skinny_ks<EPI_RESIDUAL, false>(a, s);
@@ -2669,6 +2734,23 @@ hipError_t launch_prefix_attention(const PrefillAttnArgs &a, hipStream_t s) {
   } else {
     if (G == 1) hipLaunchKernelGGL((k_attn_prefix<1, float, 2>), grid, block, 0, s, a);
     else hipLaunchKernelGGL((k_attn_prefix<2, float, 2>), grid, block, 0, s, a);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_prefix_attention_rows(const PrefillAttnArgs &a, int rows, hipStream_t s) {
+  if (a.P != 2 || a.pos0 != 0 || a.kv_heads <= 0 || a.q_heads % a.kv_heads || a.cap < 2 || a.wo || rows < 1 ||
+      rows > kMaxRows || !a.st || a.ldo != a.q_heads * 128 || a.ldo % 32 || (rows > 1 && a.kv_row <= 0))
+    return hipErrorInvalidValue;
+  const int G = a.q_heads / a.kv_heads;
+  if (G != 1 && G != 2) return hipErrorInvalidValue;
+  const dim3 grid(a.kv_heads, 1, rows), block(256);
+  if (a.kv_bf16) {
+    if (G == 1) hipLaunchKernelGGL((k_attn_prefix<1, uint16_t, 2, false, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_attn_prefix<2, uint16_t, 2, false, true>), grid, block, 0, s, a);
+  } else {
+    if (G == 1) hipLaunchKernelGGL((k_attn_prefix<1, float, 2, false, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_attn_prefix<2, float, 2, false, true>), grid, block, 0, s, a);
   }
   return hipGetLastError();
 }

@@ -135,4 +135,7 @@ MULTI_WORKLOADS: Dict[str, MultiWorkload] = {w.name: w for w in [
     MultiWorkload("tiny_multistream_greedy", "tiny", 5, (4, 40), (8, 24), 7, chunk_frames=5),
     # the Talker -> CodePredictor projection (1.7B layout) on the batched path
     MultiWorkload("tinyproj_multistream", "tiny-proj", 3, (4, 24), (6, 14), 6, chunk_frames=4, sampled_every=2),
+    # a CodePredictor wide enough for the split O / down GEMMs and the two-position prefix
+    # pass (hidden 1024), behind a 512 -> 1024 projection, one query head per KV head
+    MultiWorkload("tinyg1_multistream", "tiny-g1", 4, (4, 24), (6, 14), 8, chunk_frames=4, sampled_every=3),
 ]}

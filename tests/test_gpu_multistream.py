@@ -83,7 +83,8 @@ def test_tiny_multistream_matches_oracle(models):
         assert err <= LOGIT_TOL
 
 
-@pytest.mark.parametrize("name", ["tiny_multistream", "tinyproj_multistream", "tiny_multistream_greedy"])
+@pytest.mark.parametrize("name", ["tiny_multistream", "tinyproj_multistream", "tiny_multistream_greedy",
+                                  "tinyg1_multistream"])
 def test_multistream_equals_single_stream_path(models, name):
     r = run_batch(models, name)
     for j in range(MULTI_WORKLOADS[name].streams):
@@ -91,7 +92,7 @@ def test_multistream_equals_single_stream_path(models, name):
         np.testing.assert_array_equal(r["codes"][j], g.codes, err_msg=f"stream {j}")
 
 
-@pytest.mark.parametrize("name", ["tiny_multistream", "tiny_multistream_greedy"])
+@pytest.mark.parametrize("name", ["tiny_multistream", "tiny_multistream_greedy", "tinyg1_multistream"])
 def test_multistream_graph_replay_equals_eager(models, name):
     a = run_batch(models, name, use_graph=True)
     b = run_batch(models, name, use_graph=False)
