@@ -767,12 +767,18 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
       ao[o] = v_o / stat[g_o][1];
     }
     __syncthreads();
+    // every row's sum first, then the stores: with no store (and its lane mask) between
+    // them, the NWO independent dot / DPP chains share one basic block and interleave
+    float sum[NWO];
 #pragma unroll
     for (int i = 0; i < NWO; ++i) {
-      const int r = rb * kOprojRows + wave * (kOprojRows / 4) + i * RPL + lane / LPR;
-      float sum = row16_sum(dot8(wo[i], ao + (lane % LPR) * 8));
-      if constexpr (LPR == 32) sum += dpp_f<0x142, 0xa>(sum, 0.f);
-      if (lane % LPR == LPR - 1) a.opart[(size_t)h * a.wo_rows + r] = sum;
+      sum[i] = row16_sum(dot8(wo[i], ao + (lane % LPR) * 8));
+      if constexpr (LPR == 32) sum[i] += dpp_f<0x142, 0xa>(sum[i], 0.f);
+    }
+    if (lane % LPR == LPR - 1) {
+#pragma unroll
+      for (int i = 0; i < NWO; ++i)
+        a.opart[(size_t)h * a.wo_rows + rb * kOprojRows + wave * (kOprojRows / 4) + i * RPL + lane / LPR] = sum[i];
     }
     return;
   }
@@ -860,12 +866,17 @@ __global__ __launch_bounds__(256) void k_oproj_heads(GemvArgs a) {
     ao[t] = num / den;
   }
   __syncthreads();
+  // the rows' sums first, then the stores (one basic block: the chains interleave)
+  float sum[NWO];
 #pragma unroll
   for (int i = 0; i < NWO; ++i) {
-    const int r = rb * kOprojRows + wave * (kOprojRows / 4) + i * RPL + lane / LPR;
-    float sum = row16_sum(dot8(wo[i], ao + (lane % LPR) * 8));
-    if constexpr (LPR == 32) sum += dpp_f<0x142, 0xa>(sum, 0.f);
-    if (lane % LPR == LPR - 1) a.out[(size_t)h * a.N + r] = sum;
+    sum[i] = row16_sum(dot8(wo[i], ao + (lane % LPR) * 8));
+    if constexpr (LPR == 32) sum[i] += dpp_f<0x142, 0xa>(sum[i], 0.f);
+  }
+  if (lane % LPR == LPR - 1) {
+#pragma unroll
+    for (int i = 0; i < NWO; ++i)
+      a.out[(size_t)h * a.N + rb * kOprojRows + wave * (kOprojRows / 4) + i * RPL + lane / LPR] = sum[i];
   }
 }
 
@@ -1602,14 +1613,21 @@ __global__ __launch_bounds__(256) void k_attn_prefix(PrefillAttnArgs a) {
   }
   if constexpr (OPROJ) {
     __syncthreads();
+    // every (row, position) sum first, then the stores (one basic block: the chains interleave)
+    float sum[NWO][P];
 #pragma unroll
-    for (int i = 0; i < NWO; ++i) {
-      const int r = rb * kOprojRows + wave * (kOprojRows / 4) + i * RPL + lane / LPR;
+    for (int i = 0; i < NWO; ++i)
 #pragma unroll
       for (int p = 0; p < P; ++p) {
-        float sum = row16_sum(dot8(wo[i], ao[p] + (lane % LPR) * 8));
-        if constexpr (LPR == 32) sum += dpp_f<0x142, 0xa>(sum, 0.f);
-        if (lane % LPR == LPR - 1) a.opart[p * a.opart_row + (size_t)h * a.wo_rows + r] = sum;
+        sum[i][p] = row16_sum(dot8(wo[i], ao[p] + (lane % LPR) * 8));
+        if constexpr (LPR == 32) sum[i][p] += dpp_f<0x142, 0xa>(sum[i][p], 0.f);
+      }
+    if (lane % LPR == LPR - 1) {
+#pragma unroll
+      for (int i = 0; i < NWO; ++i) {
+        const int r = rb * kOprojRows + wave * (kOprojRows / 4) + i * RPL + lane / LPR;
+#pragma unroll
+        for (int p = 0; p < P; ++p) a.opart[p * a.opart_row + (size_t)h * a.wo_rows + r] = sum[i][p];
       }
     }
   }
