@@ -1832,11 +1832,133 @@ __device__ __forceinline__ float wave_incl_scan(float v) {
   return v;
 }
 
+// ---- top-k sampling for 1 <= top_k <= 64 and V <= 2048 (the CodePredictor's heads) ----
+// Candidate key: (value's order bits << 32) | (2^32 - 1 - index) for a finite value (-0 as
+// +0), 0 otherwise, so that larger keys rank first by (value desc, index asc), the order
+// block_sample ranks candidates in.
+__device__ __forceinline__ uint64_t sample_key(float v, int idx) {
+  if (!isfinite(v)) return 0;
+  uint32_t u = __float_as_uint(v);
+  if (u == 0x80000000u) u = 0;
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)u << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
+}
+__device__ __forceinline__ float sample_key_value(uint64_t key) {
+  const uint32_t u = (uint32_t)(key >> 32);
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+// Compare-exchange across lanes l and l ^ j: keep the larger key where keep_max.
+__device__ __forceinline__ uint64_t wave_cx_u64(uint64_t v, int j, bool keep_max) {
+  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, j, 64);
+  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), j, 64);
+  const uint64_t o = ((uint64_t)hi << 32) | lo;
+  return keep_max ? (v > o ? v : o) : (v < o ? v : o);
+}
+// Bitonic sort of the wave's E * 64 keys (key[e] of lane l at position e * 64 + l), descending.
+template <int E>
+__device__ void wave_sort_desc(uint64_t (&key)[E]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 2; k <= 64 * E; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j >= 1; j >>= 1) {
+      if (j >= 64) {  // partners in the same lane
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int je = j >> 6;
+          if (e & je) continue;
+          const bool desc = ((e * 64 + lane) & k) == 0;
+          const uint64_t x = key[e], y = key[e | je];
+          key[e] = (x > y) == desc ? x : y;
+          key[e | je] = (x > y) == desc ? y : x;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const bool desc = ((e * 64 + lane) & k) == 0;
+          key[e] = wave_cx_u64(key[e], j, ((lane & j) == 0) == desc);
+        }
+      }
+    }
+  }
+}
+// The 64 largest of two descending 64-key lists a (lane i: a[i]) and b (lane i: b[63 - i]),
+// descending: max(a[i], b[63 - i]) is a bitonic sequence holding them, then a bitonic merge.
+__device__ __forceinline__ uint64_t wave_merge_top64(uint64_t a, uint64_t b_rev) {
+  const int lane = threadIdx.x & 63;
+  uint64_t v = a > b_rev ? a : b_rev;
+#pragma unroll
+  for (int j = 32; j >= 1; j >>= 1) v = wave_cx_u64(v, j, (lane & j) == 0);
+  return v;
+}
+
+// block_sample for 1 <= top_k <= 64, V <= 2048 (1024 threads): each wave sorts its 128 keys,
+// a four-level merge tree keeps the 64 largest, and wave 0 draws from the first k as
+// block_sample does (the same weights, the same prefix sums in the same order, the same
+// top-p cut and inverse CDF), so it returns the same token for the same u.
+__device__ int block_sample_top64(SelectShared &sh, int V, const SamplingParams &sp, float u) {
+  constexpr int E = 2;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint64_t key[E];
+  int nf = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = (wave * E + e) * 64 + lane;
+    key[e] = i < V ? sample_key(sh.lg[i], i) : 0;
+    nf += key[e] != 0;
+  }
+  wave_sort_desc<E>(key);
+  uint64_t *buf = reinterpret_cast<uint64_t *>(sh.cv);  // [2][16][64] ping-pong lists
+  buf[wave * 64 + lane] = key[0];
+  nf = (int)wave_incl_scan((uint32_t)nf);
+  if (lane == 63) sh.wi[wave] = nf;
+  __syncthreads();
+  int src = 0;
+  uint64_t top = 0;
+#pragma unroll
+  for (int lists = 8; lists >= 1; lists >>= 1) {
+    if (wave < lists) {
+      const uint64_t *A = buf + (src * 16 + 2 * wave) * 64;
+      top = wave_merge_top64(A[lane], A[64 + 63 - lane]);
+      if (lists > 1) buf[((src ^ 1) * 16 + wave) * 64 + lane] = top;
+    }
+    if (lists > 1) __syncthreads();
+    src ^= 1;
+  }
+  if (wave == 0) {
+    int n_finite = 0;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) n_finite += sh.wi[w];
+    int tok = 0;
+    if (n_finite > 0) {
+      const int k_eff = min(sp.top_k, n_finite);
+      const float v = sample_key_value(top);
+      const float vmax = __shfl(v, 0, 64);
+      const float p = lane < k_eff ? expf((v - vmax) / sp.temperature) : 0.f;
+      const float c = wave_incl_scan(p);
+      const float total = __shfl(c, k_eff - 1, 64);
+      int kept = k_eff;
+      if (sp.top_p < 1.0f) {
+        const uint64_t hit = __ballot(lane < k_eff && c >= sp.top_p * total);
+        if (hit) kept = min(kept, (int)__ffsll((unsigned long long)hit));
+      }
+      const float target = u * __shfl(c, kept - 1, 64);
+      const uint64_t hit = __ballot(lane < kept && target <= c);
+      const int pick = hit ? __ffsll((unsigned long long)hit) - 1 : kept - 1;
+      tok = (int)(0xffffffffu - (uint32_t)__shfl((int)(uint32_t)top, pick, 64));
+    }
+    if (lane == 0) sh.misc[0] = tok;
+  }
+  __syncthreads();
+  return sh.misc[0];
+}
+
 // Top-k / temperature / top-p sampling over the finite entries of lg[0..V).
 // k-th largest found by an 8-bit radix select on order keys; the candidates are ranked by
 // (value desc, index asc); inverse CDF over the kept prefix with target = u * sum(p).  The
 // bin scans and the CDF are wave-parallel prefix sums.
 __device__ int block_sample(SelectShared &sh, int V, const SamplingParams &sp, float u) {
+  if (V <= 2048 && sp.top_k >= 1 && sp.top_k <= 64) return block_sample_top64(sh, V, sp, u);
   const int tid = threadIdx.x, wave = tid >> 6;
   if (tid == 0) sh.misc[2] = 0;  // candidate count
   int local = 0;

@@ -78,3 +78,30 @@ def test_masked_logits_never_drawn(eng):
     logits[2048:] = -np.inf
     draws = eng.sampler_draw(logits, 2000, True, 0, 1.0, 2.0, seed=1)
     assert draws.max() < 2048
+
+
+@pytest.mark.parametrize("V,top_k,top_p,T,mode", [
+    (2048, 50, 1.0, 0.9, "gauss"),   # config 3 CodePredictor settings
+    (2048, 64, 0.8, 0.7, "ties"),    # ties, -inf, signed zeros, -FLT_MAX
+    (2048, 1, 1.0, 1.0, "ties"),
+    (1000, 50, 0.9, 0.9, "sparse"),  # fewer finite logits than top_k
+])
+def test_top64_path_equals_radix_path(eng, V, top_k, top_p, T, mode):
+    """Top-k of at most 64 over at most 2048 logits takes the sort-and-merge sampler; the same
+    logits padded with -inf to 2049 entries take the radix-select sampler.  The candidates,
+    their order and the inverse CDF are the same, so every draw must agree."""
+    rng = np.random.default_rng(V + top_k)
+    logits = (rng.standard_normal(V) * 3).astype(np.float32)
+    if mode == "ties":
+        r = rng.integers(0, 16, V)
+        logits[r == 0] = -np.inf
+        logits[r == 1] = 1.5
+        logits[r == 2] = np.where(rng.integers(0, 2, (r == 2).sum()) == 1, 0.0, -0.0)
+        logits[r == 3] = -np.finfo(np.float32).max
+    elif mode == "sparse":
+        logits[np.arange(V) % 37 != 0] = -np.inf
+    padded = np.concatenate([logits, np.full(2049 - V, -np.inf, np.float32)])
+    print(f"[gpu] sampler paths V={V} k={top_k} p={top_p} T={T} {mode}", flush=True)
+    fast = eng.sampler_draw(logits, 4096, True, top_k, top_p, T, seed=77, kind=2)
+    radix = eng.sampler_draw(padded, 4096, True, top_k, top_p, T, seed=77, kind=2)
+    np.testing.assert_array_equal(fast, radix)
