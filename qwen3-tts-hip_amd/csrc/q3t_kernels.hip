@@ -576,7 +576,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   const KVT *vbase = vcache + (size_t)h * a.cap * D;
 
   __shared__ float qs[G * D];
-  __shared__ float ks[D], vs[D];
+  __shared__ __align__(16) float ks[D], vs[D];
   __shared__ float sc[G][CH];
   __shared__ float red[4][G][D];
   __shared__ float stat[G][2];
@@ -690,14 +690,22 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   }
   __syncthreads();
 
-  // 2a: scores of this chunk.
+  // 2a: scores of this chunk.  The stored row's slice is read from LDS unconditionally, once:
+  // read under the row test, it became a branch and a masked scalar LDS read per element.
+  float kown[8];
+  {
+    const float4 a0 = *reinterpret_cast<const float4 *>(&ks[sub * 8]);
+    const float4 a1 = *reinterpret_cast<const float4 *>(&ks[sub * 8 + 4]);
+    kown[0] = a0.x; kown[1] = a0.y; kown[2] = a0.z; kown[3] = a0.w;
+    kown[4] = a1.x; kown[5] = a1.y; kown[6] = a1.z; kown[7] = a1.w;
+  }
 #pragma unroll
   for (int i = 0; i < CH / 16; ++i) {
     const int t = t0 + wave * 4 + grp + 16 * i;
     if (t0 + wave * 4 + 16 * i >= t1) break;  // wave-uniform
     float kv[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) kv[j] = (t < tpast) ? kpre[i][j] : ((t == pos) ? ks[sub * 8 + j] : 0.f);
+    for (int j = 0; j < 8; ++j) kv[j] = (t < tpast) ? kpre[i][j] : ((t == pos) ? kown[j] : 0.f);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float sacc = 0.f;
