@@ -90,6 +90,46 @@ __device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
 
 __device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
+// The value of lane (lane ^ J) on the VALU instead of an LDS permute (ds_bpermute): quad
+// permutes for J = 1, 2; row shifts by J, one chosen per lane, for J = 4, 8 (the partner is
+// always inside the row of 16); gfx950's row swaps for J = 16 (v_permlane16_swap: lane l gets
+// lanes l & ~16 and l | 16) and J = 32 (v_permlane32_swap: lanes l & ~32 and l | 32).
+template <int J>
+__device__ __forceinline__ uint32_t lane_xor_u32(uint32_t x) {
+  const uint32_t lane = threadIdx.x & 63;
+  if constexpr (J == 1) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xf, 0xf, false);
+  } else if constexpr (J == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xf, 0xf, false);
+  } else if constexpr (J == 4 || J == 8) {
+    const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x100 + J, 0xf, 0xf, false);  // lane + J
+    const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x110 + J, 0xf, 0xf, false);  // lane - J
+    return (lane & J) ? dn : up;
+  } else if constexpr (J == 16) {
+    const auto q = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (lane & 16) ? q[0] : q[1];
+  } else {
+    static_assert(J == 32, "lane distance");
+    const auto q = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (lane & 32) ? q[0] : q[1];
+  }
+}
+
+template <int J>
+__device__ __forceinline__ uint64_t lane_xor_u64(uint64_t x) {
+  return ((uint64_t)lane_xor_u32<J>((uint32_t)(x >> 32)) << 32) | lane_xor_u32<J>((uint32_t)x);
+}
+
+// x + (x of lane ^ 16) and x + (x of lane ^ 32): the same sum in both lanes of each pair.
+__device__ __forceinline__ float pair16_sum(float x) {
+  const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+__device__ __forceinline__ float pair32_sum(float x) {
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 // Largest key of the wave, in every lane (same permutation sequence as wave_max).
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   v = umax64(v, dpp_u64<0xB1>(v));
@@ -1363,8 +1403,8 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
         for (int st = 0; st < KP; ++st)
 #pragma unroll
           for (int e = 0; e < 8; ++e) ss = fmaf(xa[b][st][e], xa[b][st][e], ss);
-        ss += __shfl_xor(ss, 16, 64);  // the four lanes of a row (kb = 0..3)
-        ss += __shfl_xor(ss, 32, 64);
+        ss = pair16_sum(ss);  // the four lanes of a row (kb = 0..3)
+        ss = pair32_sum(ss);
         if (kb == 0) ssq[wave][b * 16 + li] = ss;
       }
       __syncthreads();
@@ -1419,12 +1459,10 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
     // The 16 columns of row om sit in lanes oe + 4c (c = 0..15) of one wave: their largest
     // key, in every one of those lanes, then stored by lane oe.
     uint64_t key = (om < a.M && on < a.N) ? order_key(v[0], on) : 0;
-#pragma unroll
-    for (int m = 4; m < 64; m <<= 1) {
-      const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)key, m, 64);
-      const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(key >> 32), m, 64);
-      key = umax64(key, ((uint64_t)hi << 32) | lo);
-    }
+    key = umax64(key, lane_xor_u64<4>(key));
+    key = umax64(key, lane_xor_u64<8>(key));
+    key = umax64(key, lane_xor_u64<16>(key));
+    key = umax64(key, lane_xor_u64<32>(key));
     if ((ol & 15) == 0 && om < a.M && oflag) a.keys_out[om * a.keys_row + blockIdx.x] = key;
     return;
   }
@@ -1855,12 +1893,21 @@ __device__ __forceinline__ float sample_key_value(uint64_t key) {
   const uint32_t u = (uint32_t)(key >> 32);
   return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
 }
-// Compare-exchange across lanes l and l ^ j: keep the larger key where keep_max.
-__device__ __forceinline__ uint64_t wave_cx_u64(uint64_t v, int j, bool keep_max) {
-  const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)v, j, 64);
-  const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(v >> 32), j, 64);
-  const uint64_t o = ((uint64_t)hi << 32) | lo;
+// Compare-exchange across lanes l and l ^ J: keep the larger key where keep_max.
+template <int J>
+__device__ __forceinline__ uint64_t wave_cx_u64(uint64_t v, bool keep_max) {
+  const uint64_t o = lane_xor_u64<J>(v);
   return keep_max ? (v > o ? v : o) : (v < o ? v : o);
+}
+__device__ __forceinline__ uint64_t wave_cx_u64(uint64_t v, int j, bool keep_max) {
+  switch (j) {
+    case 1: return wave_cx_u64<1>(v, keep_max);
+    case 2: return wave_cx_u64<2>(v, keep_max);
+    case 4: return wave_cx_u64<4>(v, keep_max);
+    case 8: return wave_cx_u64<8>(v, keep_max);
+    case 16: return wave_cx_u64<16>(v, keep_max);
+    default: return wave_cx_u64<32>(v, keep_max);
+  }
 }
 // Bitonic sort of the wave's E * 64 keys (key[e] of lane l at position e * 64 + l), descending.
 template <int E>
