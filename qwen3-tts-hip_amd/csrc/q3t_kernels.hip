@@ -1010,6 +1010,24 @@ __device__ __forceinline__ void split_bf16x8(const float *x, bf16x8_t &hi, bf16x
   }
 }
 
+// split_bf16x8 without contraction: the residual is taken from the rounded x even where x is
+// a product computed just before (otherwise the compiler may fuse that product into x - hi).
+__device__ __forceinline__ void split_bf16x8_nc(const float *x, bf16x8_t &hi, bf16x8_t &mid, bf16x8_t &lo) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const f32x2_t v = {x[e], x[e + 1]};
+    const bf16x2_t h = __builtin_convertvector(v, bf16x2_t);
+    const f32x2_t r1 = v - __builtin_convertvector(h, f32x2_t);
+    const bf16x2_t m = __builtin_convertvector(r1, bf16x2_t);
+    const f32x2_t r2 = r1 - __builtin_convertvector(m, f32x2_t);
+    const bf16x2_t l = __builtin_convertvector(r2, bf16x2_t);
+    hi[e] = h[0]; hi[e + 1] = h[1];
+    mid[e] = m[0]; mid[e + 1] = m[1];
+    lo[e] = l[0]; lo[e + 1] = l[1];
+  }
+}
+
 // Offset of X element (m, k) in the matrix-core GEMMs (k a multiple of 4 inside one 32-wide
 // k step, which never straddles an X segment).
 __device__ __forceinline__ size_t gemm_x_offset(const GemmArgs &a, int m, int k) {
@@ -1161,27 +1179,29 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
 // ---------------------------------------------------------------------------------------
 // ---------------------------------------------------------------------------------------
 // Prefill GEMM, LDS-tiled: Y[M][N] = f(X)[M][K] . W[N][K]^T for many rows.
-// Block tile 128 rows x 128 weight rows, k step 32; four waves, each 64 x 64 (4 x 4 tiles of
-// v_mfma_f32_16x16x32_bf16), two blocks per CU.  Global loads (a wave reads 8 rows x 128 B of
-// X or 16 rows x 64 B of W per instruction) go to registers while the matrix cores work on
-// the previous tile, then into the other LDS buffer (double buffering).  X is scaled by the row's
-// 1/rms and the gain on the way into LDS; its fp32 values become hi/mid/lo bf16 terms after
-// the LDS read, as in k_gemm_mfma.  SwiGLU blocks hold 64 gate rows and the matching 64 up
-// rows (64 outputs).  Requires K % 32 == 0 (and N % 64 == 0 for SwiGLU); a partial last block
-// of columns computes clamped weight rows and stores only columns below N.
+// Block tile 128 rows x 128 weight rows, k step 32; four waves, each 32 rows x 128 weight rows
+// (2 x 8 tiles of v_mfma_f32_16x16x32_bf16), two blocks per CU.  Each wave's X rows are its
+// own: it loads them from global memory in matrix-core fragment order, scales them by the
+// row's 1/rms and the gain, and splits them in registers into the hi/mid/lo bf16 terms of
+// k_gemm_mfma.  Only the weight tile, shared by the four waves, goes through LDS (double
+// buffered, in fragment order: conflict-free 16-byte reads).  Global loads of the next k step
+// are in flight while the matrix cores work on this one.  SwiGLU blocks hold 64 gate rows and
+// the matching 64 up rows (64 outputs).  Requires K % 32 == 0 (and N % 64 == 0 for SwiGLU); a
+// partial last block of columns computes clamped weight rows and stores only columns below N.
+// XS: bit 0 = GemmArgs::row_scale given, bit 1 = gamma given (compile-time, so that the k
+// loop is one basic block).
 // ---------------------------------------------------------------------------------------
-template <int EPI>
+template <int EPI, int XS>
 __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
   constexpr int BM = 128, BW = 128, BK = 32;
-  constexpr int PA = BK + 4;  // fp32 row stride (pads the LDS banks)
-  constexpr int PB = BK + 8;  // bf16 row stride
   constexpr bool SW = EPI == EPI_SWIGLU;
-  __shared__ float As[2][BM][PA];
-  __shared__ uint16_t Bs[2][BW][PB];
+  constexpr bool RS = XS & 1, GM = XS & 2;
+  // weight tile u (rows 16 u .. 16 u + 15 of the block) at Bs[buf][u]; lane li + 16 kb holds
+  // row 16 u + li, k = 8 kb .. 8 kb + 7
+  __shared__ bf16x8_t Bs[2][BW / 16][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
   const int li = lane & 15, kb = lane >> 4;
-  const int m0 = blockIdx.y * BM;
+  const int m0 = blockIdx.y * BM + wave * 32;  // this wave's rows m0 .. m0 + 31
   const int nb = blockIdx.x;
   // split z of gridDim.z: k tiles [kt0, kt1)
   const int KT = a.K / BK, nsplit = gridDim.z, z = blockIdx.z;
@@ -1193,115 +1213,139 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
     if constexpr (SW) return r < 64 ? nb * 64 + r : a.N + nb * 64 + (r - 64);
     else return min(nb * 128 + r, a.N - 1);
   };
-  // per thread and k step: 4 float4 of X (8 lanes x 16 B per 128-byte row), 2 uint4 of W
-  // (4 lanes x 16 B per 64-byte row)
-  constexpr int NA = BM * BK / 4 / 256, NB = BW * BK / 8 / 256, CA = BK / 4, CB = BK / 8;
-  float4 ra[NA];
-  float4 rg[NA];
-  uint4 rb[NB];
-  float rs[NA];
+  // X: lane (li, kb) reads rows m0 + 16 t + li, k = 8 kb .. 8 kb + 7 (two float4 per tile t).
+  // W: thread tid reads block rows (tid + 256 i) / 4, k = 8 ((tid + 256 i) % 4) .. + 7.
+  constexpr int NB = BW * BK / 8 / 256, CB = BK / 8;
+  const float *xp[2];
+  float rs[2];
 #pragma unroll
-  for (int i = 0; i < NA; ++i) {
-    const int row = (tid + 256 * i) / CA;
-    rs[i] = a.row_scale ? a.row_scale[min(m0 + row, a.M - 1)] : 1.0f;
+  for (int t = 0; t < 2; ++t) {
+    const int m = min(m0 + 16 * t + li, a.M - 1);
+    xp[t] = a.X + (size_t)m * a.ldx + 8 * kb;
+    rs[t] = RS ? a.row_scale[m] : 1.0f;
   }
+  const uint16_t *wp[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int idx = tid + 256 * i, row = idx / CB, c = idx % CB;
+    wp[i] = a.W + (size_t)wrow(row) * a.K + 8 * c;
+  }
+  const float *gp = GM ? a.gamma + 8 * kb : nullptr;
+  // X offset of the current k step and the k left in its segment (X rows in segments of
+  // xseg_len, xseg_stride apart; a 32-wide step never straddles two): advanced per step
+  int xk, xleft;
+  {
+    const int k = kt0 * BK;
+    if (a.xseg_len > 0) {
+      xk = (k / a.xseg_len) * a.xseg_stride + k % a.xseg_len;
+      xleft = a.xseg_len - k % a.xseg_len;
+    } else {
+      xk = k;
+      xleft = 1 << 30;
+    }
+  }
+  float4 rx[2][2];  // X of the loaded step, [tile][half]
+  float4 rg[2];     // gain of the loaded step
+  bf16x8_t rb[NB];  // a native vector (a uint4 struct copy stays a memcpy through scratch in the IR)
   auto gload = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < NA; ++i) {
-      const int idx = tid + 256 * i, row = idx / CA, c4 = idx % CA;
-      const int m = min(m0 + row, a.M - 1);
-      ra[i] = *reinterpret_cast<const float4 *>(a.X + gemm_x_offset(a, m, k0 + 4 * c4));
-      if (a.gamma) rg[i] = *reinterpret_cast<const float4 *>(a.gamma + k0 + 4 * c4);
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) rx[t][h] = *reinterpret_cast<const float4 *>(xp[t] + xk + 4 * h);
+    if constexpr (GM) {
+      rg[0] = *reinterpret_cast<const float4 *>(gp + k0);
+      rg[1] = *reinterpret_cast<const float4 *>(gp + k0 + 4);
     }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) rb[i] = *reinterpret_cast<const bf16x8_t *>(wp[i] + k0);
+    const bool wrap = xleft == BK;
+    xk += wrap ? BK + a.xseg_stride - a.xseg_len : BK;
+    xleft = wrap ? a.xseg_len : xleft - BK;
+  };
+  bf16x8_t aq[3][2];  // [lo, mid, hi][tile] of the step the matrix cores work on next
+  auto split = [&]() {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float xv[8] = {rx[t][0].x, rx[t][0].y, rx[t][0].z, rx[t][0].w,
+                     rx[t][1].x, rx[t][1].y, rx[t][1].z, rx[t][1].w};
+      if constexpr (RS) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[e] *= rs[t];
+      }
+      if constexpr (GM) {
+        const float gv[8] = {rg[0].x, rg[0].y, rg[0].z, rg[0].w, rg[1].x, rg[1].y, rg[1].z, rg[1].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[e] *= gv[e];
+      }
+      split_bf16x8_nc(xv, aq[2][t], aq[1][t], aq[0][t]);
+    }
+  };
+  auto bstore = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int idx = tid + 256 * i, row = idx / CB, c = idx % CB;
-      rb[i] = *reinterpret_cast<const uint4 *>(a.W + (size_t)wrow(row) * a.K + k0 + 8 * c);
+      Bs[buf][row >> 4][(row & 15) + 16 * c] = rb[i];
     }
-  };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < NA; ++i) {
-      const int idx = tid + 256 * i, row = idx / CA, c4 = idx % CA;
-      float4 v = ra[i];
-      if (a.row_scale) {
-        v.x *= rs[i]; v.y *= rs[i]; v.z *= rs[i]; v.w *= rs[i];
-      }
-      if (a.gamma) {
-        v.x *= rg[i].x; v.y *= rg[i].y; v.z *= rg[i].z; v.w *= rg[i].w;
-      }
-      *reinterpret_cast<float4 *>(&As[buf][row][4 * c4]) = v;
-    }
-#pragma unroll
-    for (int i = 0; i < NB; ++i) {
-      const int idx = tid + 256 * i, row = idx / CB, c = idx % CB;
-      *reinterpret_cast<uint4 *>(&Bs[buf][row][8 * c]) = rb[i];
-    }
-  };
-  // block weight row of the wave's B tile u
-  auto brow = [&](int u) -> int {
-    if constexpr (SW) return (u < 2 ? wn * 32 + u * 16 : 64 + wn * 32 + (u - 2) * 16);
-    else return wn * 64 + u * 16;
   };
 
-  f32x4_t acc[4][4];
+  f32x4_t acc[2][8];
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc[t][u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < 8; ++u) acc[t][u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto mma = [&](int buf) {
+    bf16x8_t bq[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) bq[u] = Bs[buf][u][lane];
+    // term-major: 16 independent accumulations between two that depend on each other;
+    // each accumulator still adds lo, mid, hi in that order.
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aq[q][t], bq[u], acc[t][u], 0, 0, 0);
+  };
 
   gload(kt0 * BK);
-  sstore(0);
+  split();
+  bstore(0);
   __syncthreads();
-  for (int kt = kt0; kt < kt1; ++kt) {
-    const int buf = (kt - kt0) & 1;
-    if (kt + 1 < kt1) gload((kt + 1) * BK);
-#pragma unroll
-    for (int ks = 0; ks < BK / 32; ++ks) {
-      bf16x8_t bq[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        bq[u] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4 *>(&Bs[buf][brow(u) + li][ks * 32 + 8 * kb]));
-      bf16x8_t aq[3][4];  // [lo, mid, hi][tile]
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const float *px = &As[buf][wm * 64 + t * 16 + li][ks * 32 + 8 * kb];
-        const float4 x0 = reinterpret_cast<const float4 *>(px)[0], x1 = reinterpret_cast<const float4 *>(px)[1];
-        const float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        split_bf16x8(xv, aq[2][t], aq[1][t], aq[0][t]);
-      }
-      // term-major: 16 independent accumulations between two that depend on each other;
-      // each accumulator still adds lo, mid, hi in that order.
-#pragma unroll
-      for (int q = 0; q < 3; ++q)
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-          for (int u = 0; u < 4; ++u)
-            acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aq[q][t], bq[u], acc[t][u], 0, 0, 0);
-    }
-    if (kt + 1 < kt1) sstore(buf ^ 1);
+  // all but the last k step: load the next step's operands, multiply this one, split and store
+  // the next
+  int buf = 0;
+  for (int kt = kt0; kt < kt1 - 1; ++kt) {
+    // without the fences the scheduler sinks the loads among the MFMAs and waits for them there
+    gload((kt + 1) * BK);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(buf);
+    __builtin_amdgcn_sched_barrier(0);
+    split();
+    bstore(buf ^ 1);
     __syncthreads();
+    buf ^= 1;
   }
+  mma(buf);
 
   // C[i][j] of a tile sits in lane j + 16 (i / 4), element i % 4.
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int m = m0 + wm * 64 + t * 16 + 4 * kb + e;
+      const int m = m0 + t * 16 + 4 * kb + e;
       if (m >= a.M) continue;
       if constexpr (SW) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int n = nb * 64 + wn * 32 + u * 16 + li;
-          const float g = acc[t][u][e], up = acc[t][u + 2][e];
+        for (int u = 0; u < 4; ++u) {
+          const int n = nb * 64 + u * 16 + li;
+          const float g = acc[t][u][e], up = acc[t][u + 4][e];
           a.Y[(size_t)m * a.ldy + n] = g / (1.0f + expf(-g)) * up;
         }
       } else {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int n = nb * 128 + wn * 64 + u * 16 + li;
+        for (int u = 0; u < 8; ++u) {
+          const int n = nb * 128 + u * 16 + li;
           if (n >= a.N) continue;
           if (nsplit > 1) a.split_ws[((size_t)z * a.M + m) * a.N + n] = acc[t][u][e];
           else a.Y[(size_t)m * a.ldy + n] = gemm_epilogue<EPI>(a, m, n, acc[t][u][e]);
@@ -2721,7 +2765,14 @@ static hipError_t gemm_epi(const GemmArgs &a, hipStream_t s) {
     path = 2;
   }
   grid.z = gemm_splits(a, (int)(grid.x * grid.y), EPI == EPI_SWIGLU);
-  if (path == 0) hipLaunchKernelGGL((k_gemm_lds<EPI>), grid, dim3(256), 0, s, a);
+  if (path == 0) {
+    switch ((a.row_scale ? 1 : 0) | (a.gamma ? 2 : 0)) {
+      case 0: hipLaunchKernelGGL((k_gemm_lds<EPI, 0>), grid, dim3(256), 0, s, a); break;
+      case 1: hipLaunchKernelGGL((k_gemm_lds<EPI, 1>), grid, dim3(256), 0, s, a); break;
+      case 2: hipLaunchKernelGGL((k_gemm_lds<EPI, 2>), grid, dim3(256), 0, s, a); break;
+      default: hipLaunchKernelGGL((k_gemm_lds<EPI, 3>), grid, dim3(256), 0, s, a); break;
+    }
+  }
   else if (path == 1) hipLaunchKernelGGL((k_gemm_mfma<EPI, 1, NB>), grid, dim3(256), 0, s, a);
   else hipLaunchKernelGGL((k_gemm_mfma<EPI, 2, NB>), grid, dim3(256), 0, s, a);
   if constexpr (EPI != EPI_SWIGLU) {
