@@ -1196,13 +1196,27 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
   constexpr int BM = 128, BW = 128, BK = 32;
   constexpr bool SW = EPI == EPI_SWIGLU;
   constexpr bool RS = XS & 1, GM = XS & 2;
-  // weight tile u (rows 16 u .. 16 u + 15 of the block) at Bs[buf][u]; lane li + 16 kb holds
-  // row 16 u + li, k = 8 kb .. 8 kb + 7
+  // weight tile u (rows 16 u .. 16 u + 15 of the block) at Bs[buf][u]; lane li + 16 kb reads
+  // row 16 u + li, k = 8 kb .. 8 kb + 7, from entry 16 kb + (li ^ 4 kb).  The xor spreads the
+  // stores (four lanes of one row, k = 0 .. 31, see below) over distinct banks while every 16
+  // lanes of a read still cover all 16 bank groups.
   __shared__ bf16x8_t Bs[2][BW / 16][64];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, kb = lane >> 4;
-  const int m0 = blockIdx.y * BM + wave * 32;  // this wave's rows m0 .. m0 + 31
-  const int nb = blockIdx.x;
+  // Block tile (mb, nb).  Workgroups go to the 8 XCDs round robin (linear id % 8), each with its
+  // own L2.  With few column blocks (gridDim.x <= 8) that would send every row block of one
+  // column block to the same XCD, which would then read all of X; instead each XCD takes a
+  // contiguous range of row-major tiles (all column blocks of its row blocks), so its L2 reads
+  // only its own X rows, once for all column blocks.
+  int mb = blockIdx.y, nb = blockIdx.x;
+  if (gridDim.x <= 8) {
+    const int total = gridDim.x * gridDim.y, L = blockIdx.y * gridDim.x + blockIdx.x;
+    const int xcd = L % 8, local = L / 8, C = (total + 7) / 8, r = total % 8;
+    const int t = (r == 0 || xcd < r) ? xcd * C + local : r * C + (xcd - r) * (C - 1) + local;
+    mb = t / gridDim.x;
+    nb = t % gridDim.x;
+  }
+  const int m0 = mb * BM + wave * 32;  // this wave's rows m0 .. m0 + 31
   // split z of gridDim.z: k tiles [kt0, kt1)
   const int KT = a.K / BK, nsplit = gridDim.z, z = blockIdx.z;
   const int kt0 = (int)((int64_t)KT * z / nsplit), kt1 = (int)((int64_t)KT * (z + 1) / nsplit);
@@ -1214,7 +1228,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
     else return min(nb * 128 + r, a.N - 1);
   };
   // X: lane (li, kb) reads rows m0 + 16 t + li, k = 8 kb .. 8 kb + 7 (two float4 per tile t).
-  // W: thread tid reads block rows (tid + 256 i) / 4, k = 8 ((tid + 256 i) % 4) .. + 7.
+  // W: thread tid reads block rows (tid + 256 i) / 4, k = 8 ((tid + 256 i) % 4) .. + 7 (four
+  // consecutive lanes read one row's 64 contiguous bytes).
   constexpr int NB = BW * BK / 8 / 256, CB = BK / 8;
   const float *xp[2];
   float rs[2];
@@ -1284,7 +1299,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int idx = tid + 256 * i, row = idx / CB, c = idx % CB;
-      Bs[buf][row >> 4][(row & 15) + 16 * c] = rb[i];
+      Bs[buf][row >> 4][16 * c + ((row & 15) ^ (4 * c))] = rb[i];
     }
   };
 
@@ -1296,7 +1311,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
   auto mma = [&](int buf) {
     bf16x8_t bq[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) bq[u] = Bs[buf][u][lane];
+    for (int u = 0; u < 8; ++u) bq[u] = Bs[buf][u][16 * kb + (li ^ (4 * kb))];
     // term-major: 16 independent accumulations between two that depend on each other;
     // each accumulator still adds lo, mid, hi in that order.
 #pragma unroll
