@@ -248,6 +248,22 @@ struct PrefillAttnArgs {
   const int32_t *row_on;
 };
 
+// The prompt prefill attention of several streams in one launch (segment s = one stream's
+// P[s] prompt rows, rows row0[s] .. row0[s] + P[s] - 1 of qkv / out, positions 0 .. P[s] - 1
+// of its caches).  unit0[s] = first attention unit of segment s (units per segment:
+// ceil(P / 16) * q_heads), unit0[nseg] = all units.
+constexpr int kMaxPrefillSegs = 16;
+struct PrefillBatchArgs {
+  float *qkv;            // [M][ldq] raw projections (q normalised + rotated in place)
+  const float *gq, *gk;  // q_norm / k_norm gains
+  const float2 *rope;    // [cap][d/2]
+  float *out;            // [M][ldo] attention output
+  int32_t M, ldq, ldo, q_heads, kv_heads, cap, nseg, kv_bf16;
+  float eps, scale;
+  int32_t row0[kMaxPrefillSegs], P[kMaxPrefillSegs], unit0[kMaxPrefillSegs + 1];
+  void *kcache[kMaxPrefillSegs], *vcache[kMaxPrefillSegs];  // [kv_heads][cap][d] of the layer
+};
+
 struct SelectTalkerArgs {
   const float *logits;      // [V] raw codec-head logits
   const float *x;           // [H] Talker output before the final norm

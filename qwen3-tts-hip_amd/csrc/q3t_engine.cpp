@@ -422,9 +422,9 @@ struct Engine {
   }
 
   // Talker prompt prefill on the matrix cores: every layer runs over the prompt rows of all
-  // segments at once (decode.rs:845-880, 1077-1298); attention runs per segment against
-  // that stream's own cache.  The prompt rows are in pools.px; each segment's last row's
-  // output lands in its slot's x_t.
+  // segments at once (decode.rs:845-880, 1077-1298), and so does attention, each segment
+  // against its stream's own cache.  The prompt rows are in pools.px; each segment's last
+  // row's output lands in its slot's x_t.
   void prefill_segments(const std::vector<PrefillSeg> &segs, int M, hipStream_t s) {
     const Dims &d = td;
     Pools &p = pools;
@@ -440,13 +440,20 @@ struct Engine {
       g.W = L.qkv; g.Y = p.pqkv; g.ldy = Q; g.M = M; g.N = Q; g.K = H;
       g.split_ws = split_ws; g.split_cap = kSplitFloats;
       hip_check(launch_gemm(EPI_STORE, g, s), "launch_gemm(qkv)");
-      for (const PrefillSeg &sg : segs) {
-        const Slot &sl = slots[sg.slot];
-        PrefillAttnArgs pa{p.pqkv + (size_t)sg.row0 * Q, L.gq, L.gk, talker.rope, sl.t_k + l * cache_layer,
-                           sl.t_v + l * cache_layer, p.pattn + (size_t)sg.row0 * O, sg.P, 0, Q, O, d.q_heads,
-                           d.kv_heads, talker.cap, d.eps, 1.0f / std::sqrt((float)d.head_dim), kv_bf16};
-        hip_check(launch_prefill_attention(pa, s), "launch_prefill_attention");
+      PrefillBatchArgs pa{};
+      pa.qkv = p.pqkv; pa.gq = L.gq; pa.gk = L.gk; pa.rope = talker.rope; pa.out = p.pattn;
+      pa.M = M; pa.ldq = Q; pa.ldo = O; pa.q_heads = d.q_heads; pa.kv_heads = d.kv_heads; pa.cap = talker.cap;
+      pa.nseg = (int)segs.size(); pa.kv_bf16 = kv_bf16; pa.eps = d.eps;
+      pa.scale = 1.0f / std::sqrt((float)d.head_dim);
+      for (int i = 0; i < pa.nseg; ++i) {
+        const Slot &sl = slots[segs[i].slot];
+        pa.row0[i] = segs[i].row0;
+        pa.P[i] = segs[i].P;
+        pa.unit0[i + 1] = pa.unit0[i] + (segs[i].P + 15) / 16 * d.q_heads;
+        pa.kcache[i] = sl.t_k + l * cache_layer;
+        pa.vcache[i] = sl.t_v + l * cache_layer;
       }
+      hip_check(launch_prefill_attention(pa, s), "launch_prefill_attention");
       g = GemmArgs{};
       g.X = p.pattn; g.ldx = O; g.W = L.o; g.res = p.px; g.ldr = H; g.Y = p.px; g.ldy = H;
       g.M = M; g.N = H; g.K = O;

@@ -85,7 +85,7 @@ hipError_t launch_text_assemble(const float *Y, int H, int M, const int32_t *cod
 hipError_t launch_bf16_to_f32(const uint16_t *src, float *dst, size_t n, hipStream_t stream);
 
 // Prefill attention: q/k norm + RoPE + KV store for P rows, then causal attention.
-hipError_t launch_prefill_attention(const PrefillAttnArgs &a, hipStream_t stream);
+hipError_t launch_prefill_attention(const PrefillBatchArgs &a, hipStream_t stream);
 // The same for P = 2 rows at positions 0 and 1 (the CodePredictor's prefix) in one launch.
 // With a.wo set, the output projection is fused in as in launch_attn_oproj: row p's per-KV-head
 // shares go to a.opart + p * a.opart_row (a.out unused).

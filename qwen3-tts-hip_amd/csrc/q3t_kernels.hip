@@ -1556,23 +1556,32 @@ __global__ __launch_bounds__(256) void k_row_rms(const float *X, int ldx, int M,
 }
 
 // ---------------------------------------------------------------------------------------
-// Prompt prefill attention, rows at positions 0..P-1 (decode.rs:1077-1298 with the cache
-// written first and read back, the same values the decode steps read).
+// Prompt prefill attention over every stream's prompt rows at once, rows at positions
+// 0..P-1 of their stream (decode.rs:1077-1298 with the cache written first and read back, the
+// same values the decode steps read).  Segment s holds rows row0[s] .. row0[s] + P[s] - 1.
 //   k_prefill_qkv: per (row, head vector): q/k head RMSNorm + RoPE at the row's position
-//     (q written back in place), K and V stored into the cache row.  One wave per vector.
-//   k_attn_prefill: per (KV head, row): causal attention of the row's G query heads over
-//     cache rows 0..p with an online softmax over 64-row chunks.
+//     (q written back in place), K and V stored into the row's stream cache.  One wave per
+//     vector.
+//   k_attn_prefill: per (stream, query head, 16-row query block): causal attention over
+//     the stream's cache rows on the fp32 matrix cores, one wave per unit.
 // ---------------------------------------------------------------------------------------
+__device__ __forceinline__ int prefill_segment(const PrefillBatchArgs &a, int row) {
+  int s = 0;
+  while (s + 1 < a.nseg && row >= a.row0[s + 1]) ++s;
+  return s;
+}
+
 template <typename KVT>
-__global__ __launch_bounds__(256) void k_prefill_qkv(PrefillAttnArgs a) {
+__global__ __launch_bounds__(256) void k_prefill_qkv(PrefillBatchArgs a) {
   constexpr int D = 128;
   const int lane = threadIdx.x & 63;
   const int vec = blockIdx.x * 4 + (threadIdx.x >> 6);  // q heads, then k heads, then v heads
-  const int p = blockIdx.y;
+  const int r = blockIdx.y;
   const int nvec = a.q_heads + 2 * a.kv_heads;
-  if (vec >= nvec || p >= a.P) return;
-  const int pos = a.pos0 + p;
-  float *row = a.qkv + (size_t)p * a.ldq;
+  if (vec >= nvec || r >= a.M) return;
+  const int sg = prefill_segment(a, r);
+  const int pos = r - a.row0[sg];
+  float *row = a.qkv + (size_t)r * a.ldq;
   float *v = row + vec * D;
   float x0 = v[lane], x1 = v[lane + 64];
   if (vec < a.q_heads + a.kv_heads) {
@@ -1592,7 +1601,7 @@ __global__ __launch_bounds__(256) void k_prefill_qkv(PrefillAttnArgs a) {
   } else {
     const bool is_k = vec < a.q_heads + a.kv_heads;
     const int h = is_k ? vec - a.q_heads : vec - a.q_heads - a.kv_heads;
-    KVT *cache = reinterpret_cast<KVT *>(is_k ? a.kcache : a.vcache) + ((size_t)h * a.cap + pos) * D;
+    KVT *cache = reinterpret_cast<KVT *>(is_k ? a.kcache[sg] : a.vcache[sg]) + ((size_t)h * a.cap + pos) * D;
     KvIo<KVT>::store(cache + lane, x0);
     KvIo<KVT>::store(cache + lane + 64, x1);
   }
@@ -1738,95 +1747,100 @@ __global__ __launch_bounds__(256) void k_attn_prefix(PrefillAttnArgs a) {
   }
 }
 
-template <int G, typename KVT>
-__global__ __launch_bounds__(256) void k_attn_prefill(PrefillAttnArgs a) {
-  constexpr int D = 128, CH = 64;
-  const int h = blockIdx.x;
-  const int p = blockIdx.y;
-  if (p >= a.P) return;
-  const int L = a.pos0 + p + 1;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int sub = lane & 15, grp = lane >> 4;
-  const KVT *kb = reinterpret_cast<const KVT *>(a.kcache) + (size_t)h * a.cap * D;
-  const KVT *vb = reinterpret_cast<const KVT *>(a.vcache) + (size_t)h * a.cap * D;
-  __shared__ float qs[G * D];
-  __shared__ float sc[G][CH];
-  __shared__ float red[4][G][D];
-  __shared__ float mstat[G];
-  const float *row = a.qkv + (size_t)p * a.ldq;
-  for (int i = threadIdx.x; i < G * D; i += 256) qs[i] = row[h * G * D + i];
-  float m_run[G], l_run[G], acc[G][2];
+// One wave per unit (stream s, query head hq, query rows q0 .. q0 + 15), units in
+// PrefillBatchArgs::unit0 order: per stream, the last query block first (the longest causal
+// range).  v_mfma_f32_16x16x4_f32 (fp32 products and sums):
+//   S^T = K Q^T per 16-key tile: lane (li, kk) supplies key row li and query row li, dims
+//     32 kk + s at step s (32 steps: the four lane groups cover the 128 dims in quarters), and
+//     holds scores of keys 4 kk + e (e = 0..3) for query li.
+//   O^T += V^T P^T: step s' takes keys 4 kk + s' (lane group kk), so each lane's own score
+//     e = s' is its B operand; A row i of output tile t is dim 8 i + t, so a lane reads 8
+//     consecutive floats of a value row and ends up holding dims 32 kk .. 32 kk + 31 of query li.
+//   Online softmax per query over 16-key tiles: the tile max over the four lane groups by lane
+//     exchanges, per-lane partial sums of p (added across the groups at the end).
+template <typename KVT>
+__global__ __launch_bounds__(256) void k_attn_prefill(PrefillBatchArgs a) {
+  constexpr int D = 128;
+  const int lane = threadIdx.x & 63, li = lane & 15, kk = lane >> 4;
+  const int u = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (u >= a.unit0[a.nseg]) return;
+  int sg = 0;
+  while (sg + 1 < a.nseg && u >= a.unit0[sg + 1]) ++sg;
+  const int P = a.P[sg], local = u - a.unit0[sg];
+  const int nqb = (P + 15) / 16;
+  const int hq = local % a.q_heads, q0 = 16 * (nqb - 1 - local / a.q_heads);
+  const int kvh = hq / (a.q_heads / a.kv_heads);
+  const float *qkv = a.qkv + (size_t)a.row0[sg] * a.ldq;
+  const KVT *kb = reinterpret_cast<const KVT *>(a.kcache[sg]) + (size_t)kvh * a.cap * D;
+  const KVT *vb = reinterpret_cast<const KVT *>(a.vcache[sg]) + (size_t)kvh * a.cap * D;
+
+  float q[32];
+  {
+    const float *qp = qkv + (size_t)min(q0 + li, P - 1) * a.ldq + hq * D + 32 * kk;
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m_run[g] = -FLT_MAX;
-    l_run[g] = 0.f;
-    acc[g][0] = acc[g][1] = 0.f;
+    for (int c = 0; c < 4; ++c) {
+      const float4 x0 = reinterpret_cast<const float4 *>(qp + 8 * c)[0];
+      const float4 x1 = reinterpret_cast<const float4 *>(qp + 8 * c)[1];
+      q[8 * c] = x0.x; q[8 * c + 1] = x0.y; q[8 * c + 2] = x0.z; q[8 * c + 3] = x0.w;
+      q[8 * c + 4] = x1.x; q[8 * c + 5] = x1.y; q[8 * c + 6] = x1.z; q[8 * c + 7] = x1.w;
+    }
   }
-  __syncthreads();
-  for (int t0 = 0; t0 < L; t0 += CH) {
-    const int t1 = min(L, t0 + CH);
-    for (int base = t0 + wave * 4; base < t1; base += 16) {
-      const int t = base + grp;
-      float kv[8];
-      KvIo<KVT>::load8(kb + (size_t)min(t, L - 1) * D + sub * 8, kv);
+  f32x4_t o[8];
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float sacc = 0.f;
+  for (int t = 0; t < 8; ++t) o[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m_run = -FLT_MAX, l_part = 0.f;
+  const int qrow = q0 + li;                      // this lane's query (rows >= P are not stored)
+  const int nkt = (min(q0 + 16, P) + 15) / 16;   // key tiles up to the block's last row
+  for (int kt = 0; kt < nkt; ++kt) {
+    float kv[32];
+    {
+      const KVT *kp = kb + (size_t)min(16 * kt + li, P - 1) * D + 32 * kk;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) sacc = fmaf(qs[g * D + sub * 8 + j], kv[j], sacc);
-        sacc = row16_sum(sacc);
-        if (sub == 0 && t < t1) sc[g][t - t0] = sacc * a.scale;
-      }
+      for (int c = 0; c < 4; ++c) KvIo<KVT>::load8(kp + 8 * c, kv + 8 * c);
     }
-    __syncthreads();
-    const int n = t1 - t0;
-    if (wave < G) {
-      const float sv = lane < n ? sc[wave][lane] : -FLT_MAX;
-      const float mc = wave_max(sv);
-      if (lane == 0) mstat[wave] = mc;
-    }
-    __syncthreads();
-    float scale_old[G];
+    float vv[4][8];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float m_new = fmaxf(m_run[g], mstat[g]);
-      scale_old[g] = expf(m_run[g] - m_new);
-      m_run[g] = m_new;
-    }
-    __syncthreads();
-    if (wave < G && lane < n) sc[wave][lane] = expf(sc[wave][lane] - m_run[wave]);
-    __syncthreads();
+    for (int s2 = 0; s2 < 4; ++s2) KvIo<KVT>::load8(vb + (size_t)min(16 * kt + 4 * kk + s2, P - 1) * D + 8 * li, vv[s2]);
+    f32x4_t st = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float ls = 0.f;
-      for (int i = 0; i < n; ++i) ls += sc[g][i];
-      l_run[g] = l_run[g] * scale_old[g] + ls;
-      acc[g][0] *= scale_old[g];
-      acc[g][1] *= scale_old[g];
-    }
-    for (int t = t0 + wave; t < t1; t += 4) {
-      const float2 v = KvIo<KVT>::load2(vb + (size_t)t * D + 2 * lane);
+    for (int s1 = 0; s1 < 32; ++s1) st = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[s1], q[s1], st, 0, 0, 0);
+    float p[4], mt = -FLT_MAX;
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float pr = sc[g][t - t0];
-        acc[g][0] = fmaf(pr, v.x, acc[g][0]);
-        acc[g][1] = fmaf(pr, v.y, acc[g][1]);
-      }
+    for (int e = 0; e < 4; ++e) {
+      const int key = 16 * kt + 4 * kk + e;
+      p[e] = (key <= qrow && key < P) ? st[e] * a.scale : -FLT_MAX;
+      mt = fmaxf(mt, p[e]);
     }
-    __syncthreads();
+    mt = fmaxf(mt, __builtin_bit_cast(float, lane_xor_u32<16>(__builtin_bit_cast(uint32_t, mt))));
+    mt = fmaxf(mt, __builtin_bit_cast(float, lane_xor_u32<32>(__builtin_bit_cast(uint32_t, mt))));
+    const float m_new = fmaxf(m_run, mt);
+    const float corr = expf(m_run - m_new);
+    float ps = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      p[e] = p[e] == -FLT_MAX ? 0.f : expf(p[e] - m_new);
+      ps += p[e];
+    }
+    l_part = l_part * corr + ps;
+    m_run = m_new;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) o[t] *= corr;
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[s2][t], p[s2], o[t], 0, 0, 0);
   }
+  float l = l_part;
+  l += __builtin_bit_cast(float, lane_xor_u32<16>(__builtin_bit_cast(uint32_t, l)));
+  l += __builtin_bit_cast(float, lane_xor_u32<32>(__builtin_bit_cast(uint32_t, l)));
+  if (qrow >= P) return;
+  const float inv = 1.0f / l;
+  float *op = a.out + (size_t)(a.row0[sg] + qrow) * a.ldo + hq * D + 32 * kk;
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    red[wave][g][2 * lane] = acc[g][0];
-    red[wave][g][2 * lane + 1] = acc[g][1];
+  for (int e = 0; e < 4; ++e) {
+    reinterpret_cast<float4 *>(op + 8 * e)[0] = make_float4(o[0][e] * inv, o[1][e] * inv, o[2][e] * inv, o[3][e] * inv);
+    reinterpret_cast<float4 *>(op + 8 * e)[1] = make_float4(o[4][e] * inv, o[5][e] * inv, o[6][e] * inv, o[7][e] * inv);
   }
-  __syncthreads();
-  const int o = threadIdx.x;
-  if (o >= G * D) return;
-  const int g_o = o / D, d_o = o % D;
-  const float v_o = ((red[0][g_o][d_o] + red[1][g_o][d_o]) + red[2][g_o][d_o]) + red[3][g_o][d_o];
-  a.out[(size_t)p * a.ldo + (h * G + g_o) * D + d_o] = v_o / l_run[g_o];
 }
 
 // ---------------------------------------------------------------------------------------
@@ -3016,20 +3030,25 @@ hipError_t launch_prefix_attention_rows(const PrefillAttnArgs &a, int rows, hipS
   return hipGetLastError();
 }
 
-hipError_t launch_prefill_attention(const PrefillAttnArgs &a, hipStream_t s) {
-  if (a.P <= 0 || a.kv_heads <= 0 || a.q_heads % a.kv_heads || a.pos0 < 0 || a.pos0 + a.P > a.cap)
+hipError_t launch_prefill_attention(const PrefillBatchArgs &a, hipStream_t s) {
+  if (a.nseg < 1 || a.nseg > kMaxPrefillSegs || a.kv_heads <= 0 || a.q_heads % a.kv_heads || a.ldq % 4 ||
+      a.ldo % 4 || a.unit0[0] != 0)
     return hipErrorInvalidValue;
-  const int G = a.q_heads / a.kv_heads;
-  if (G != 1 && G != 2) return hipErrorInvalidValue;
-  const dim3 g1((a.q_heads + 2 * a.kv_heads + 3) / 4, a.P), g2(a.kv_heads, a.P), block(256);
+  int rows = 0;
+  for (int i = 0; i < a.nseg; ++i) {
+    if (a.P[i] < 1 || a.P[i] > a.cap || a.row0[i] != rows || !a.kcache[i] || !a.vcache[i] ||
+        a.unit0[i + 1] != a.unit0[i] + (a.P[i] + 15) / 16 * a.q_heads)
+      return hipErrorInvalidValue;
+    rows += a.P[i];
+  }
+  if (rows != a.M) return hipErrorInvalidValue;
+  const dim3 g1((a.q_heads + 2 * a.kv_heads + 3) / 4, a.M), g2((a.unit0[a.nseg] + 3) / 4), block(256);
   if (a.kv_bf16) {
     hipLaunchKernelGGL(k_prefill_qkv<uint16_t>, g1, block, 0, s, a);
-    if (G == 1) hipLaunchKernelGGL((k_attn_prefill<1, uint16_t>), g2, block, 0, s, a);
-    else hipLaunchKernelGGL((k_attn_prefill<2, uint16_t>), g2, block, 0, s, a);
+    hipLaunchKernelGGL(k_attn_prefill<uint16_t>, g2, block, 0, s, a);
   } else {
     hipLaunchKernelGGL(k_prefill_qkv<float>, g1, block, 0, s, a);
-    if (G == 1) hipLaunchKernelGGL((k_attn_prefill<1, float>), g2, block, 0, s, a);
-    else hipLaunchKernelGGL((k_attn_prefill<2, float>), g2, block, 0, s, a);
+    hipLaunchKernelGGL(k_attn_prefill<float>, g2, block, 0, s, a);
   }
   return hipGetLastError();
 }
