@@ -203,9 +203,10 @@ struct GemmArgs {
   // largest order key (value, lowest column) at keys_out[m * keys_row + blockIdx.x].
   uint64_t *keys_out;
   int64_t keys_row;
-  // matrix-core GEMMs (not SwiGLU): a launch of few workgroups may split K over grid z, each
-  // split storing its raw sums to split_ws[z][M][N] (split_cap floats available); a second
-  // kernel adds the splits in order and applies the epilogue.  Null: never split.
+  // matrix-core GEMMs: a launch of few workgroups may split K over grid z, each split storing
+  // its raw sums to split_ws[z][M][N] (SwiGLU: [z][M][2N], the up sums at N + n; split_cap
+  // floats available); a second kernel adds the splits in order and applies the epilogue.
+  // Null: never split.
   float *split_ws;
   int64_t split_cap;
   // skinny GEMM, EPI_RESIDUAL, T16 Y: K split in two halves over grid y.  Each half adds its

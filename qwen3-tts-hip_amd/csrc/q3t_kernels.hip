@@ -1157,6 +1157,12 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
         float v = acc[i][j][e];
         if constexpr (EPI == EPI_SWIGLU) {
           const float u = acc[i][j + NTILE][e];
+          if (nsplit > 1) {  // raw gate and up sums: [split][M][2N], up at N + n
+            float *w = a.split_ws + ((size_t)z * a.M + m) * 2 * a.N;
+            w[n] = v;
+            w[a.N + n] = u;
+            continue;
+          }
           v = v / (1.0f + expf(-v)) * u;
         } else {
           if (nsplit > 1) {
@@ -1355,7 +1361,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
         for (int u = 0; u < 4; ++u) {
           const int n = nb * 64 + u * 16 + li;
           const float g = acc[t][u][e], up = acc[t][u + 4][e];
-          a.Y[(size_t)m * a.ldy + n] = g / (1.0f + expf(-g)) * up;
+          if (nsplit > 1) {  // raw gate and up sums: [split][M][2N], up at N + n
+            float *w = a.split_ws + ((size_t)z * a.M + m) * 2 * a.N;
+            w[n] = g;
+            w[a.N + n] = up;
+          } else {
+            a.Y[(size_t)m * a.ldy + n] = g / (1.0f + expf(-g)) * up;
+          }
         }
       } else {
 #pragma unroll
@@ -2752,24 +2764,36 @@ hipError_t launch_attn_oproj(const AttnArgs &a, int head_dim, hipStream_t s, con
   return hipGetLastError();
 }
 
-// Sum of the K splits in split order, then the epilogue: Y[m][n] = f(sum_z ws[z][m][n]).
+// Sum of the K splits in split order, then the epilogue: Y[m][n] = f(sum_z ws[z][m][n])
+// (SwiGLU: silu(sum_z gate) * sum_z up).
 template <int EPI>
 __global__ __launch_bounds__(256) void k_gemm_split_reduce(GemmArgs a, int nsplit) {
   const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   const size_t mn = (size_t)a.M * a.N;
   if (i >= mn) return;
+  const int m = (int)(i / a.N), n = (int)(i % a.N);
+  if constexpr (EPI == EPI_SWIGLU) {  // gate and up sums, each added in split order
+    const size_t gi = (size_t)m * 2 * a.N + n;
+    float g = a.split_ws[gi], u = a.split_ws[gi + a.N];
+    for (int z = 1; z < nsplit; ++z) {
+      g += a.split_ws[(size_t)z * 2 * mn + gi];
+      u += a.split_ws[(size_t)z * 2 * mn + gi + a.N];
+    }
+    a.Y[(size_t)m * a.ldy + n] = g / (1.0f + expf(-g)) * u;
+    return;
+  }
   float v = a.split_ws[i];
   for (int z = 1; z < nsplit; ++z) v += a.split_ws[(size_t)z * mn + i];
-  const int m = (int)(i / a.N), n = (int)(i % a.N);
   a.Y[(size_t)m * a.ldy + n] = gemm_epilogue<EPI>(a, m, n, v);
 }
 
 // K splits for a launch of `blocks` workgroups: enough to reach ~256 workgroups, at least
 // 4 k steps of 32 per split, at most 16 splits, within the workspace.
 static int gemm_splits(const GemmArgs &a, int blocks, bool swiglu) {
-  if (!a.split_ws || swiglu || blocks >= 128) return 1;
+  if (!a.split_ws || blocks >= 128) return 1;
   int sp = std::min(std::min((256 + blocks - 1) / blocks, a.K / 32 / 4), 16);
-  while (sp > 1 && (int64_t)sp * a.M * a.N > a.split_cap) --sp;
+  // SwiGLU keeps the gate and the up sums apart until the reduction
+  while (sp > 1 && (int64_t)sp * a.M * a.N * (swiglu ? 2 : 1) > a.split_cap) --sp;
   return std::max(sp, 1);
 }
 
@@ -2804,12 +2828,10 @@ static hipError_t gemm_epi(const GemmArgs &a, hipStream_t s) {
   }
   else if (path == 1) hipLaunchKernelGGL((k_gemm_mfma<EPI, 1, NB>), grid, dim3(256), 0, s, a);
   else hipLaunchKernelGGL((k_gemm_mfma<EPI, 2, NB>), grid, dim3(256), 0, s, a);
-  if constexpr (EPI != EPI_SWIGLU) {
-    if (grid.z > 1) {
-      const size_t mn = (size_t)a.M * a.N;
-      hipLaunchKernelGGL((k_gemm_split_reduce<EPI>), dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, a,
-                         (int)grid.z);
-    }
+  if (grid.z > 1) {
+    const size_t mn = (size_t)a.M * a.N;
+    hipLaunchKernelGGL((k_gemm_split_reduce<EPI>), dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, s, a,
+                       (int)grid.z);
   }
   return hipGetLastError();
 }
