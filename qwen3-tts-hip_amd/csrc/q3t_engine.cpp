@@ -463,6 +463,7 @@ struct Engine {
       g = GemmArgs{};
       g.X = p.px; g.ldx = H; g.row_scale = p.pinv; g.gamma = L.g_post;
       g.W = L.gu; g.Y = p.pact; g.ldy = I; g.M = M; g.N = I; g.K = H;
+      g.split_ws = split_ws; g.split_cap = kSplitFloats;
       hip_check(launch_gemm(EPI_SWIGLU, g, s), "launch_gemm(gate_up)");
       g = GemmArgs{};
       g.X = p.pact; g.ldx = I; g.W = L.down; g.res = p.px; g.ldr = H; g.Y = p.px; g.ldy = H;
