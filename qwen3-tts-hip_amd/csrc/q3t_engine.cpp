@@ -219,6 +219,7 @@ struct Pools {
   int prefill_rows = 0;                                 // n * cap
   float *px = nullptr, *pqkv = nullptr, *pattn = nullptr, *pact = nullptr, *pinv = nullptr;
   SlotState *h_states = nullptr;                        // pinned [n]
+  int32_t *h_codes = nullptr;                           // pinned [n][codes_row], mirrors codes
   int32_t *h_row_on = nullptr;                          // pinned [n]
   hipStream_t stream = nullptr;                         // batched work
   hipGraphExec_t graph = nullptr;                       // batched frame, keyed by (rows, traced, fused)
@@ -1008,6 +1009,7 @@ void alloc_pools(Engine &e, int n) {
   p.pact = dev_alloc<float>((size_t)p.prefill_rows * td.intermediate, t);
   p.pinv = dev_alloc<float>((size_t)p.prefill_rows, t);
   HIPC(hipHostMalloc((void **)&p.h_states, sizeof(SlotState) * n, hipHostMallocDefault));
+  HIPC(hipHostMalloc((void **)&p.h_codes, (size_t)p.codes_row * n * 4, hipHostMallocDefault));
   HIPC(hipHostMalloc((void **)&p.h_row_on, sizeof(int32_t) * n, hipHostMallocDefault));
   std::memset(p.h_row_on, 0, sizeof(int32_t) * n);
   HIPC(hipStreamCreateWithFlags(&p.stream, hipStreamNonBlocking));
@@ -1063,6 +1065,7 @@ void free_pools(Engine &e) {
   for (void *q : ptrs)
     if (q) (void)hipFree(q);
   if (p.h_states) (void)hipHostFree(p.h_states);
+  if (p.h_codes) (void)hipHostFree(p.h_codes);
   if (p.h_row_on) (void)hipHostFree(p.h_row_on);
   p = Pools();
 }
@@ -2077,6 +2080,17 @@ int q3t_streams_next_codes(q3t_engine *e, q3t_stream *const *streams, int32_t n,
     for (int slot : on) fused = fused && e->slots[slot].cp_greedy;
     // Streams that need fewer frames than nrun reach max_frames on the device and stop there.
     run_rows_frames(*e, rows, nrun, fused);
+    // Every row's frames [lo, hi) (a window covering each listed stream's frames; the rest is
+    // never read) and the states in one round trip, instead of one synchronous copy per stream.
+    int lo = INT32_MAX, hi = 0;
+    for (int j = 0; j < n; ++j)
+      if (want[j]) {
+        lo = std::min(lo, streams[j]->host_frame);
+        hi = std::max(hi, streams[j]->host_frame + want[j]);
+      }
+    const size_t pitch = (size_t)p.codes_row * 4;
+    HIPC(hipMemcpy2DAsync(p.h_codes + (size_t)lo * e->groups, pitch, p.codes + (size_t)lo * e->groups, pitch,
+                          (size_t)(hi - lo) * e->groups * 4, rows, hipMemcpyDeviceToHost, p.stream));
     HIPC(hipMemcpyAsync(p.h_states, p.st, sizeof(SlotState) * rows, hipMemcpyDeviceToHost, p.stream));
     HIPC(hipStreamSynchronize(p.stream));
     for (int j = 0; j < n; ++j) {
@@ -2086,9 +2100,9 @@ int q3t_streams_next_codes(q3t_engine *e, q3t_stream *const *streams, int32_t n,
       const int produced = hs.frame - sp->host_frame;
       if (produced < 0 || produced > want[j]) fail(Q3T_ERR_HIP, "device loop state is inconsistent");
       if (produced > 0)
-        HIPC(hipMemcpy(codes + (size_t)j * max_chunk * e->groups,
-                       e->slots[sp->slot].codes + (size_t)sp->host_frame * e->groups,
-                       (size_t)produced * e->groups * 4, hipMemcpyDeviceToHost));
+        std::memcpy(codes + (size_t)j * max_chunk * e->groups,
+                    p.h_codes + (size_t)sp->slot * p.codes_row + (size_t)sp->host_frame * e->groups,
+                    (size_t)produced * e->groups * 4);
       sp->host_frame += produced;
       sp->done = hs.done;
       info[j].frames = produced;
@@ -2154,12 +2168,14 @@ void ensure_phase_graphs(Engine &e, Slot &s) {
 void collect_frames(q3t_stream *sp, int n, int32_t *codes, q3t_chunk_info *info) {
   Engine &e = *sp->engine;
   Slot &s = e.slots[sp->slot];
+  // The state and the n frames' codes (those not produced are never read) in one round trip.
+  int32_t *h = e.pools.h_codes + (size_t)sp->slot * e.pools.codes_row + (size_t)sp->host_frame * e.groups;
+  HIPC(hipMemcpyAsync(h, s.codes + (size_t)sp->host_frame * e.groups, (size_t)n * e.groups * 4,
+                      hipMemcpyDeviceToHost, s.stream));
   sync_state(s);
   const int produced = s.h_state->frame - sp->host_frame;
   if (produced < 0 || produced > n) fail(Q3T_ERR_HIP, "device loop state is inconsistent");
-  if (produced > 0)
-    HIPC(hipMemcpy(codes, s.codes + (size_t)sp->host_frame * e.groups, (size_t)produced * e.groups * 4,
-                   hipMemcpyDeviceToHost));
+  if (produced > 0) std::memcpy(codes, h, (size_t)produced * e.groups * 4);
   sp->host_frame += produced;
   sp->done = s.h_state->done;
   info->frames = produced;
