@@ -117,6 +117,18 @@ struct GemvArgs {
   float *x_store;
   // rows = 2 with parts: row 1's parts at parts + ldp_r, its sum stored at x_store + ldxs_r
   int32_t ldp_r, ldxs_r;
+  // Input = the next Talker input, assembled from the last CodePredictor group's greedy
+  // hand-off when tin.keys is set (one stream; EPI_STORE with RMSNorm, streamed weights,
+  // K = tin.emb_width): tok = the token of the largest of tin.keys[0 .. n_keys), e =
+  // tin.emb[tok], s = tin.sum + e and x = (tin_codec_emb[st->semantic] + s) +
+  // tin_trailing[min(st->frame, st->trailing_rows)], what the selection kernel would store.
+  // Workgroup 0 stores x to tin_x and tok to tin.codes[st->frame * tin.groups + tin.code]
+  // unless the stream has ended, before the launch's own skip check.  tin.sum and tin.cur
+  // are not written (nothing reads them after the last group).
+  TokenHandoff tin;
+  const uint16_t *tin_codec_emb;  // [V][K] bf16
+  const float *tin_trailing;      // [rows][K]
+  float *tin_x;                   // [K]
 };
 
 // Most workgroups a hand-off producer may have (keys per group).

@@ -323,9 +323,11 @@ struct Engine {
   // handoff: layer 0 takes its raw q/k/v row from qkv_table (row = the handed-off token) in its
   // attention kernel and runs no QKV GEMV; `in` is then the row that kernel stores
   // (handoff->cur).
+  // tin (the Talker after a greedy CodePredictor): layer 0's QKV GEMV assembles its input from
+  // the last group's hand-off (GemvArgs::tin) and stores it to `in`.
   void stack_step(const StackW &w, char *kc, char *vc, const float *in, float *x, Slot &sl, int pos_mode,
                   int pos_const, int skip, hipStream_t s, const TokenHandoff *handoff = nullptr,
-                  const float *qkv_table = nullptr) {
+                  const float *qkv_table = nullptr, const GemvArgs *tin = nullptr) {
     const Dims &d = w.d;
     const bool nt = &w == &talker;
     const bool fuse_o = oproj_ok(w);
@@ -334,7 +336,12 @@ struct Engine {
       const LayerW &L = w.layers[l];
       const float *src = l == 0 ? in : x;
       const bool table = l == 0 && handoff;
-      if (!table)
+      if (l == 0 && tin) {
+        GemvArgs a = *tin;
+        a.W = L.qkv; a.x = nullptr; a.gamma = L.g_in; a.out = sl.qkv; a.N = d.qkv_rows(); a.K = d.hidden;
+        a.eps = d.eps; a.skip = skip; a.st = sl.st; a.tin_x = const_cast<float *>(in);
+        hip_check(launch_gemv(EPI_STORE, true, nt, a, s), "launch_gemv(qkv, Talker input hand-off)");
+      } else if (!table)
         gemv(EPI_STORE, true, L.qkv, src, L.g_in, d.eps, nullptr, nullptr, sl.qkv, d.qkv_rows(), d.hidden, skip,
              sl.st, s, nt);
       if (fuse_o) {
@@ -489,12 +496,38 @@ struct Engine {
   // Everything one frame does after its semantic token is known (generation.rs:697-741):
   // CodePredictor groups 0..14, the next Talker step, token selection, frame bookkeeping.
   void enqueue_frame(Slot &sl, hipStream_t s) {
-    enqueue_code_predictor(sl, s);
-    enqueue_talker_decode(sl, s);
+    const bool fold = fold_last_group(sl);
+    enqueue_code_predictor(sl, s, fold);
+    enqueue_talker_decode(sl, s, fold);
   }
 
-  void enqueue_talker_decode(Slot &sl, hipStream_t s) {
-    stack_step(talker, sl.t_k, sl.t_v, sl.t_in, sl.x_t, sl, POS_TALKER_FRAME, 0, SKIP_TALKER, s);
+  // A greedy CodePredictor hands its last group's token to the Talker step that follows
+  // (the Talker's layer-0 QKV GEMV assembles its own input: GemvArgs::tin) instead of
+  // running a selection kernel.  Both halves of the frame must agree on it.
+  bool fold_last_group(const Slot &sl) const {
+    return sl.cp_greedy && cp_qkv_table &&
+           (talker_hidden == 512 || talker_hidden == 1024 || talker_hidden == 2048);
+  }
+
+  void enqueue_talker_decode(Slot &sl, hipStream_t s, bool fold = false) {
+    if (fold) {
+      const int Vc = cd.vocab, nac = groups - 1;
+      GemvArgs tin{};
+      tin.tin.keys = sl.cp_keys + (size_t)(nac - 1) * kHandoffKeys;
+      tin.tin.n_keys = gemv_grid_for(Vc, cd.hidden);
+      tin.tin.emb = cp_emb + (size_t)(nac - 1) * Vc * talker_hidden;
+      tin.tin.emb_width = talker_hidden;
+      tin.tin.sum = sl.emb_sum;
+      tin.tin.codes = sl.codes;
+      tin.tin.code = groups - 1;
+      tin.tin.groups = groups;
+      tin.tin_codec_emb = codec_emb;
+      tin.tin_trailing = sl.trailing;
+      stack_step(talker, sl.t_k, sl.t_v, sl.t_in, sl.x_t, sl, POS_TALKER_FRAME, 0, SKIP_TALKER, s, nullptr, nullptr,
+                 &tin);
+    } else {
+      stack_step(talker, sl.t_k, sl.t_v, sl.t_in, sl.x_t, sl, POS_TALKER_FRAME, 0, SKIP_TALKER, s);
+    }
     gemv(EPI_STORE, true, codec_head, sl.x_t, t_norm, td.eps, nullptr, nullptr, sl.logits_t, td.vocab, td.hidden,
          SKIP_TALKER, sl.st, s, true);
     select_talker(sl, 1, s);  // + frame bookkeeping
@@ -563,7 +596,10 @@ struct Engine {
     return x2 + H;
   }
 
-  void enqueue_code_predictor(Slot &sl, hipStream_t s) {
+  // fold (fold_last_group): the last group's LM head stores hand-off keys for the Talker step
+  // that follows instead of running a selection kernel; codes[frame][groups - 1] and the next
+  // Talker input are then stored by that step.
+  void enqueue_code_predictor(Slot &sl, hipStream_t s, bool fold = false) {
     const int Ht = talker_hidden, Hc = cd.hidden, Vc = cd.vocab, nac = groups - 1;
     const float *in = sl.cp_prefix;
     int ldin = Ht;
@@ -621,7 +657,7 @@ struct Engine {
       }
       GemvArgs a{lm_heads + (size_t)g * Vc * Hc, g == 0 ? x_pos1 : sl.x_c, c_norm, nullptr, nullptr, sl.logits_c,
                  Vc, Hc, cd.eps, SKIP_DONE, sl.st};
-      if (fused && g < nac - 1) {
+      if (fused && (g < nac - 1 || fold)) {
         a.keys_out = sl.cp_keys + (size_t)g * kHandoffKeys;
         if (trace) {
           a.trace = sl.trace_c + (size_t)g * Vc;
@@ -2148,8 +2184,8 @@ void ensure_phase_graphs(Engine &e, Slot &s) {
     hipGraph_t g = nullptr;
     HIPC(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal));
     try {
-      if (ph == 0) e.enqueue_code_predictor(s, s.stream);
-      else e.enqueue_talker_decode(s, s.stream);
+      if (ph == 0) e.enqueue_code_predictor(s, s.stream, e.fold_last_group(s));
+      else e.enqueue_talker_decode(s, s.stream, e.fold_last_group(s));
     } catch (...) {
       (void)hipStreamEndCapture(s.stream, &g);
       if (g) (void)hipGraphDestroy(g);
@@ -2217,9 +2253,9 @@ int q3t_stream_next_codes_profiled(q3t_stream *sp, int32_t max_chunk, int32_t *c
     // the stream is not run, so that it adds no time.
     while (ran < n && !s.h_state->done) {
       HIPC(hipEventRecord(ev.ev[0], s.stream));
-      e.enqueue_code_predictor(s, s.stream);
+      e.enqueue_code_predictor(s, s.stream, e.fold_last_group(s));
       HIPC(hipEventRecord(ev.ev[1], s.stream));
-      e.enqueue_talker_decode(s, s.stream);
+      e.enqueue_talker_decode(s, s.stream, e.fold_last_group(s));
       HIPC(hipEventRecord(ev.ev[2], s.stream));
       sync_state(s);
       prof->code_predictor_seconds += ev.seconds(0, 1);
@@ -2247,10 +2283,10 @@ int q3t_debug_phase_times(q3t_stream *sp, int32_t max_chunk, int32_t *codes, q3t
     while (ran < n && !s.h_state->done) {
       HIPC(hipEventRecord(ev.ev[0], s.stream));
       if (e.use_graph) HIPC(hipGraphLaunch(s.phase_graph[0], s.stream));
-      else e.enqueue_code_predictor(s, s.stream);
+      else e.enqueue_code_predictor(s, s.stream, e.fold_last_group(s));
       HIPC(hipEventRecord(ev.ev[1], s.stream));
       if (e.use_graph) HIPC(hipGraphLaunch(s.phase_graph[1], s.stream));
-      else e.enqueue_talker_decode(s, s.stream);
+      else e.enqueue_talker_decode(s, s.stream, e.fold_last_group(s));
       HIPC(hipEventRecord(ev.ev[2], s.stream));
       sync_state(s);
       cp_us[ran] = (float)(1e6 * ev.seconds(0, 1));

@@ -248,8 +248,9 @@ constexpr int kMaxParts = 8;
 
 // The input vector of k_gemv: IN_X = x; IN_ATTN = the merge of attention partials (see
 // merge_attention); IN_PARTS = x plus the per-head partials of the fused attention + O
-// projection (GemvArgs::parts), summed through LDS.
-constexpr int IN_X = 0, IN_ATTN = 1, IN_PARTS = 2;
+// projection (GemvArgs::parts), summed through LDS; IN_TALKER = the next Talker input from
+// the last CodePredictor group's hand-off (GemvArgs::tin), assembled through LDS.
+constexpr int IN_X = 0, IN_ATTN = 1, IN_PARTS = 2, IN_TALKER = 3;
 
 // Waves per workgroup of the IN_PARTS form: every workgroup sums the partials into LDS, so
 // it runs the launch's waves in fewer, larger workgroups (the partials are read from L2 once
@@ -263,16 +264,19 @@ template <int EPI, bool NORM, int KC, int RW, bool NT, int IN = IN_X, int MR = 1
 __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gemv(GemvArgs a) {
   constexpr bool ATTN = IN == IN_ATTN;
   constexpr bool PARTS = IN == IN_PARTS;
+  constexpr bool TIN = IN == IN_TALKER;
   constexpr int WPB = PARTS ? kPartsWaves : 4;
   static_assert(!ATTN || MR == 1, "the attention merge feeds one row");
   static_assert(!PARTS || (KC == 1 || KC == 2), "the partial sum feeds rows of K <= 1024");
   static_assert(!HO || (MR == 1 && IN == IN_X && EPI == EPI_STORE), "the hand-off producer stores one row");
+  static_assert(!TIN || (MR == 1 && EPI == EPI_STORE && NORM && (KC == 1 || KC == 2 || KC == 4)),
+                "the Talker input feeds one normed row of K 512, 1024 or 2048");
   constexpr int K = KC * 512;
   constexpr int NR = (EPI == EPI_SWIGLU) ? 2 * RW : RW;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int unit0 = (blockIdx.x * WPB + wave) * RW;
-  __shared__ float xs[PARTS ? MR : 1][(ATTN || PARTS) ? K : 1];
+  __shared__ float xs[PARTS ? MR : 1][(ATTN || PARTS || TIN) ? K : 1];
   __shared__ uint64_t wkeys[HO ? 4 : 1];
   // IN_PARTS: thread t sums elements 4t .. 4t+3 of x and of every part (K <= 1024), for each
   // input row m (x + m * ldx_r, parts + m * ldp_r).
@@ -292,6 +296,20 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
     }
   }
 
+  // IN_TALKER: thread t covers elements 4t .. 4t+3 and 1024 + 4t .. (K <= 2048); the hand-off
+  // keys (four per lane, every wave reduces them all) and the running sum are loaded first.
+  uint64_t tkey[TIN ? 4 : 1];
+  float4 tsum[TIN ? 2 : 1];
+  if constexpr (TIN) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tkey[j] = a.tin.keys[min(lane + 64 * j, a.tin.n_keys - 1)];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = 4 * (int)threadIdx.x + 1024 * j;
+      tsum[j] = i < K ? *reinterpret_cast<const float4 *>(a.tin.sum + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+
   // Load order: activations (and the norm gain), then every weight row of this wave, then
   // nothing else until the arithmetic.  The norm then only waits for the small activation
   // loads while the whole launch's weights are in flight (one DRAM round trip per launch).
@@ -306,7 +324,7 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
   }
 #pragma unroll
   for (int c = 0; c < KC; ++c) {
-    if constexpr (ATTN || PARTS) break;
+    if constexpr (ATTN || PARTS || TIN) break;
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       const float4 *px = reinterpret_cast<const float4 *>(a.x + m * a.ldx_r + c * 512 + lane * 8);
@@ -348,10 +366,51 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
     for (int c = 0; c < KC; ++c) w[r][c] = load_w<NT>(pw + c * 64);
   }
   __builtin_amdgcn_sched_barrier(0);
-  // The stream-state check comes after the loads (every address above is valid whatever the
-  // state), so its round trip overlaps theirs instead of preceding them.  Nothing is stored
-  // before it.
-  if (skip_work(a.st, a.skip)) return;
+  if constexpr (TIN) {
+    // The last group's token and the Talker input (the selection kernel's arithmetic, in its
+    // order), stored by workgroup 0 unless the stream has ended; then the launch's own skip
+    // check (after the last frame the Talker step does not run, the stores above do).
+    if (a.st->done) return;
+    const int tok = key_token(wave_max_u64(umax64(umax64(tkey[0], tkey[1]), umax64(tkey[2], tkey[3]))));
+    const int frame = a.st->frame, sem = a.st->semantic;
+    const int trow = min(frame, a.st->trailing_rows);
+    float4 te[2], tc[2], tt[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = 4 * (int)threadIdx.x + 1024 * j;
+      if (i < K) {
+        const uint2 we = *reinterpret_cast<const uint2 *>(a.tin.emb + (size_t)tok * K + i);
+        const uint2 wc = *reinterpret_cast<const uint2 *>(a.tin_codec_emb + (size_t)sem * K + i);
+        te[j] = make_float4(bf_lo(we.x), bf_hi(we.x), bf_lo(we.y), bf_hi(we.y));
+        tc[j] = make_float4(bf_lo(wc.x), bf_hi(wc.x), bf_lo(wc.y), bf_hi(wc.y));
+        tt[j] = *reinterpret_cast<const float4 *>(a.tin_trailing + (size_t)trow * K + i);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = 4 * (int)threadIdx.x + 1024 * j;
+      if (i < K) {
+        const float4 sm = make_float4(tsum[j].x + te[j].x, tsum[j].y + te[j].y, tsum[j].z + te[j].z,
+                                      tsum[j].w + te[j].w);
+        const float4 v = make_float4((tc[j].x + sm.x) + tt[j].x, (tc[j].y + sm.y) + tt[j].y,
+                                     (tc[j].z + sm.z) + tt[j].z, (tc[j].w + sm.w) + tt[j].w);
+        *reinterpret_cast<float4 *>(&xs[0][i]) = v;
+        if (blockIdx.x == 0) *reinterpret_cast<float4 *>(a.tin_x + i) = v;
+      }
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) a.tin.codes[(size_t)frame * a.tin.groups + a.tin.code] = tok;
+    __syncthreads();
+    if (skip_work(a.st, a.skip)) return;
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xv[0][c][j] = xs[0][c * 512 + lane * 8 + j];
+  } else {
+    // The stream-state check comes after the loads (every address above is valid whatever
+    // the state), so its round trip overlaps theirs instead of preceding them.  Nothing is
+    // stored before it.
+    if (skip_work(a.st, a.skip)) return;
+  }
   if constexpr (PARTS) {
     const int i = 4 * (int)threadIdx.x;
     if (i < K) {
@@ -2541,6 +2600,13 @@ static void gemv_launch(const GemvArgs &a, hipStream_t s, const LaunchTiming *t)
       return;
     }
   }
+  // The Talker's layer-0 QKV GEMV taking its input from the last CodePredictor group.
+  if constexpr (EPI == EPI_STORE && NORM && NT && (KC == 1 || KC == 2 || KC == 4)) {
+    if (a.tin.keys) {
+      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_TALKER>, grid, dim3(256), 0, s, t, a);
+      return;
+    }
+  }
   if constexpr (EPI == EPI_RESIDUAL && !NORM && KC <= 8) {
     if (a.attn_part) {
       launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_ATTN>, grid, dim3(256), 0, s, t, a);
@@ -2642,6 +2708,15 @@ hipError_t launch_gemv(int epi, bool norm, bool streaming, const GemvArgs &a, hi
   if (a.parts && a.rows == 2 && (a.ldp_r % 4 || a.ldp_r < a.n_parts * a.ld_parts || (a.x_store && a.ldxs_r < a.K) ||
                                  a.ldxs_r % 4))
     return hipErrorInvalidValue;
+  if (a.tin.keys) {
+    const TokenHandoff &h = a.tin;
+    const bool ok = epi == EPI_STORE && norm && streaming && a.rows <= 1 && !a.attn_part && !a.parts &&
+                    !a.keys_out && (a.K == 512 || a.K == 1024 || a.K == 2048) && h.emb_width == a.K &&
+                    h.n_keys >= 1 && h.n_keys <= kHandoffKeys && h.emb && h.sum && h.codes && h.groups > 1 &&
+                    h.code >= 1 && h.code < h.groups && a.tin_codec_emb && a.tin_trailing && a.tin_x && a.st &&
+                    a.skip != SKIP_NEVER;
+    if (!ok) return hipErrorInvalidValue;
+  }
   if (a.parts && (epi != EPI_SWIGLU || !norm || a.attn_part || a.keys_out ||
                   (a.K != 512 && a.K != 1024) || a.n_parts < 1 || a.n_parts > kMaxParts ||
                   a.ld_parts < a.K || a.ld_parts % 4 || !a.x))
