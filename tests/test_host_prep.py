@@ -56,8 +56,9 @@ def test_safetensors_round_trip(tmp_path):
     np.testing.assert_array_equal(t.view(torch.int16).numpy().view(np.uint16), m.tensors["talker.codec_head.weight"])
 
 
-def test_inventory_sizes_match_the_survey():
-    """0.6B Talker stack 440,466,432 params; CP stack 78,654,720 (+ 2 x 1024 norms)."""
+def test_inventory_sizes_match_the_0_6b_stacks():
+    """0.6B Talker stack 440,466,432 params; CP stack 78,654,720 (+ 2 x 1024 norms): 28 and 5
+    layers of hidden 1024, 16 q / 8 kv heads of 128, intermediate 3072, with q/k norms."""
     inv = {n: int(np.prod(s)) for n, s, _ in synth.tensor_inventory(synth.SPECS["0.6b"])}
     talker = sum(v for k, v in inv.items() if k.startswith("talker.model.layers."))
     cp = sum(v for k, v in inv.items() if k.startswith("talker.code_predictor.model.layers."))
