@@ -58,6 +58,7 @@ struct Codec {
   } up[2];
   uint16_t *init_w = nullptr;  // [1536][7][1024]
   float *init_b = nullptr;
+  // Snake tables (a*: exp(alpha), b*: exp(beta) + 1e-9, per channel; launch_codec_snake).
   struct Unit {
     float *a1a, *a1b, *a2a, *a2b, *b1, *b2;
     uint16_t *w1, *w2;  // [co][7][co], [co][co]
@@ -102,6 +103,13 @@ Codec *codec_load(const std::string &model_dir, int64_t *device_bytes) {
     };
     auto f32 = [&](const std::string &n, int64_t len) { return st.f32(n, {len}); };
     auto up_f32 = [&](const std::string &n, int64_t len) { return c->upload(f32(n, len)); };
+    // A Snake's alpha / beta (prefix + "alpha" / "beta"), turned into the per-channel tables
+    // launch_codec_snake reads (exp(alpha), exp(beta) + 1e-9) on the device.
+    auto up_snake = [&](const std::string &prefix, int64_t len, float *&a, float *&b) {
+      a = up_f32(prefix + "alpha", len);
+      b = up_f32(prefix + "beta", len);
+      hip_check(launch_codec_snake_prep(a, b, (int)len, nullptr), "launch_codec_snake_prep");
+    };
     // [O][C][K] -> [O][K][C]
     auto taps_last_to_first = [](const std::vector<uint16_t> &w, int O, int C, int K) {
       std::vector<uint16_t> r((size_t)O * C * K);
@@ -207,8 +215,7 @@ Codec *codec_load(const std::string &model_dir, int64_t *device_bytes) {
       const auto [ci, co, s] = kBlocks[b];
       const std::string p = "decoder.decoder." + std::to_string(b + 1) + ".block";
       Codec::Block &B = c->blocks[b];
-      B.snake_a = up_f32(p + ".0.alpha", ci);
-      B.snake_b = up_f32(p + ".0.beta", ci);
+      up_snake(p + ".0.", ci, B.snake_a, B.snake_b);
       const auto tw = bf16(p + ".1.conv.weight", {ci, co, 2 * s});  // [in][out][2s]
       std::vector<uint16_t> w((size_t)s * co * 2 * ci);
       for (int ph = 0; ph < s; ++ph)
@@ -226,18 +233,16 @@ Codec *codec_load(const std::string &model_dir, int64_t *device_bytes) {
       for (int u = 0; u < 3; ++u) {
         const std::string r = p + "." + std::to_string(u + 2);
         Codec::Unit &Un = B.u[u];
-        Un.a1a = up_f32(r + ".act1.alpha", co);
-        Un.a1b = up_f32(r + ".act1.beta", co);
-        Un.a2a = up_f32(r + ".act2.alpha", co);
-        Un.a2b = up_f32(r + ".act2.beta", co);
+        up_snake(r + ".act1.", co, Un.a1a, Un.a1b);
+        up_snake(r + ".act2.", co, Un.a2a, Un.a2b);
         Un.w1 = c->upload(taps_last_to_first(bf16(r + ".conv1.conv.weight", {co, co, 7}), co, co, 7));
         Un.b1 = up_f32(r + ".conv1.conv.bias", co);
         Un.w2 = c->upload(bf16(r + ".conv2.conv.weight", {co, co, 1}));
         Un.b2 = up_f32(r + ".conv2.conv.bias", co);
       }
     }
-    c->fin_a = up_f32("decoder.decoder.5.alpha", kFinal);
-    c->fin_b = up_f32("decoder.decoder.5.beta", kFinal);
+    up_snake("decoder.decoder.5.", kFinal, c->fin_a, c->fin_b);
+    HIPC(hipStreamSynchronize(nullptr));
     {
       const std::vector<float> w = st.f32("decoder.decoder.6.conv.weight", {1, kFinal, 7});
       std::vector<float> r((size_t)7 * kFinal);

@@ -28,8 +28,12 @@ float *codec_samples_buffer(Codec &c, size_t n);
 // Kernels (q3t_codec.hip).
 hipError_t launch_codec_rvq(const int32_t *codes, int frames, int groups, const float *first, const float *rest,
                             int V, int D, float *E, hipStream_t s);
-hipError_t launch_codec_snake(const float *x, const float *alpha, const float *beta, int C, size_t n, float *out,
+// Snake over [n / C][C]: out = x + sin(x * ea[c])^2 / eb[c], with the per-channel tables
+// ea = exp(alpha), eb = exp(beta) + 1e-9 that launch_codec_snake_prep makes in place from the
+// checkpoint's alpha / beta (snake_beta_f32, kernels.rs).
+hipError_t launch_codec_snake(const float *x, const float *ea, const float *eb, int C, size_t n, float *out,
                               hipStream_t s);
+hipError_t launch_codec_snake_prep(float *alpha, float *beta, int C, hipStream_t s);
 hipError_t launch_codec_dwconv(const float *xin, const float *w, const float *b, int T, int C, int K, float *out,
                                hipStream_t s);
 hipError_t launch_codec_layernorm(const float *x, const float *g, const float *b, int T, int C, float eps, float *out,

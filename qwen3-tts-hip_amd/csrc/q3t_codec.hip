@@ -32,13 +32,35 @@ __global__ void k_codec_rvq(const int32_t *codes, int groups, const float *first
 }
 
 // out[t][c] = x + sin(x e^alpha[c])^2 / (e^beta[c] + 1e-9) (codec_snake_beta_f32, kernels.rs:692-710).
-__global__ void k_codec_snake(const float *x, const float *alpha, const float *beta, int C, size_t n, float *out) {
+// alpha := exp(alpha), beta := exp(beta) + 1e-9 (once, at load): the per-channel factors of
+// every Snake launch, computed by the same device expf the per-element form used.
+__global__ void k_codec_snake_prep(float *alpha, float *beta, int C) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  alpha[c] = expf(alpha[c]);
+  beta[c] = expf(beta[c]) + 1.0e-9f;
+}
+
+__device__ __forceinline__ float snake1(float v, float ea, float eb) {
+  const float s = sinf(v * ea);
+  return v + (s * s) / eb;
+}
+
+// Four channels per thread (C % 4 == 0, 16-byte aligned rows): n4 = n / 4 quads, c4 = C / 4.
+__global__ void k_codec_snake4(const float4 *x, const float4 *ea, const float4 *eb, uint32_t c4, uint32_t n4,
+                               float4 *out) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n4) return;
+  const uint32_t c = i % c4;
+  const float4 v = x[i], a = ea[c], b = eb[c];
+  out[i] = make_float4(snake1(v.x, a.x, b.x), snake1(v.y, a.y, b.y), snake1(v.z, a.z, b.z), snake1(v.w, a.w, b.w));
+}
+
+__global__ void k_codec_snake(const float *x, const float *ea, const float *eb, int C, size_t n, float *out) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int c = (int)(i % C);
-  const float v = x[i];
-  const float s = sinf(v * expf(alpha[c]));
-  out[i] = v + (s * s) / (expf(beta[c]) + 1.0e-9f);
+  out[i] = snake1(x[i], ea[c], eb[c]);
 }
 
 // Depthwise causal conv, kernel K: out[t][c] = b[c] + sum_j xin[t + j][c] w[c][j], where xin
@@ -155,11 +177,25 @@ hipError_t launch_codec_rvq(const int32_t *codes, int frames, int groups, const 
   return hipGetLastError();
 }
 
-hipError_t launch_codec_snake(const float *x, const float *alpha, const float *beta, int C, size_t n, float *out,
+hipError_t launch_codec_snake(const float *x, const float *ea, const float *eb, int C, size_t n, float *out,
                               hipStream_t s) {
   if (C <= 0 || n % C) return hipErrorInvalidValue;
   if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_codec_snake, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, alpha, beta, C, n, out);
+  auto aligned = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  if (C % 4 == 0 && n / 4 < (size_t)UINT32_MAX && aligned(x) && aligned(ea) && aligned(eb) && aligned(out)) {
+    const size_t n4 = n / 4;
+    hipLaunchKernelGGL(k_codec_snake4, dim3(blocks_for(n4, 256)), dim3(256), 0, s, reinterpret_cast<const float4 *>(x),
+                       reinterpret_cast<const float4 *>(ea), reinterpret_cast<const float4 *>(eb), (uint32_t)(C / 4),
+                       (uint32_t)n4, reinterpret_cast<float4 *>(out));
+  } else {
+    hipLaunchKernelGGL(k_codec_snake, dim3(blocks_for(n, 256)), dim3(256), 0, s, x, ea, eb, C, n, out);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_codec_snake_prep(float *alpha, float *beta, int C, hipStream_t s) {
+  if (C <= 0 || !alpha || !beta) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_codec_snake_prep, dim3((C + 255) / 256), dim3(256), 0, s, alpha, beta, C);
   return hipGetLastError();
 }
 
