@@ -145,24 +145,32 @@ __global__ __launch_bounds__(64) void k_codec_attention(const float *qkv, int T,
 // Last convolution to one channel + clamp to [-1, 1]: out[t] = clamp(b + sum_{j, c}
 // xin[t + j][c] w[j][c]) with xin row 0 = time -(K-1) (kernels.rs:742-770, 903-918).  A
 // workgroup stages the kFinalTile + K - 1 input rows its kFinalTile outputs read in LDS
-// (unit-stride loads), then each thread sums its K * C products in (j, c) order.
+// (unit-stride loads), rows C + 1 floats apart so that the 64 lanes of a wave, which read
+// rows t .. t + 63 at one channel, fall in different banks (at a pitch of C = 96 every lane
+// hit the same bank); each thread then sums its K * C products in (j, c) order.
 constexpr int kFinalTile = 128, kFinalMaxC = 96, kFinalMaxK = 7;
 
 __global__ __launch_bounds__(kFinalTile) void k_codec_final(const float *xin, const float *w, const float *b, int T,
                                                             int C, int K, float *out) {
-  __shared__ float xs[(kFinalTile + kFinalMaxK - 1) * kFinalMaxC];
+  __shared__ float xs[(kFinalTile + kFinalMaxK - 1) * (kFinalMaxC + 1)];
   __shared__ float ws[kFinalMaxK * kFinalMaxC];
   const int t0 = blockIdx.x * kFinalTile;
   const int rows = min(kFinalTile, T - t0) + K - 1;
+  const int pitch = C + 1;
   const float *src = xin + (size_t)t0 * C;
-  for (int i = threadIdx.x; i < rows * C; i += kFinalTile) xs[i] = src[i];
+  for (int i = threadIdx.x; i < rows * C; i += kFinalTile) {
+    const int r = i / C;
+    xs[r * pitch + (i - r * C)] = src[i];
+  }
   for (int i = threadIdx.x; i < K * C; i += kFinalTile) ws[i] = w[i];
   __syncthreads();
   const int t = t0 + (int)threadIdx.x;
   if (t >= T) return;
   float s = b[0];
-  for (int j = 0; j < K; ++j)
-    for (int c = 0; c < C; ++c) s += xs[(threadIdx.x + j) * C + c] * ws[j * C + c];
+  for (int j = 0; j < K; ++j) {
+    const float *xr = xs + (threadIdx.x + j) * pitch;
+    for (int c = 0; c < C; ++c) s += xr[c] * ws[j * C + c];
+  }
   out[t] = fminf(fmaxf(s, -1.0f), 1.0f);
 }
 
