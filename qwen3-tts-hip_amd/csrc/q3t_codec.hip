@@ -123,10 +123,19 @@ __global__ __launch_bounds__(64) void k_codec_attention(const float *qkv, int T,
   const int Q = heads * 64;
   const float q = qkv[(size_t)t * ld + h * 64 + lane];
   float m = -FLT_MAX;
-  for (int u = 0; u <= t; ++u) {
-    const float s = wave_sum64(q * qkv[(size_t)u * ld + Q + h * 64 + lane]) * scale;
-    if (lane == 0) sc[u] = s;
-    m = fmaxf(m, s);
+  // Key rows in batches of 8, every load of a batch issued before its reductions.
+  constexpr int KB = 8;
+  for (int u0 = 0; u0 <= t; u0 += KB) {
+    float kv[KB];
+#pragma unroll
+    for (int j = 0; j < KB; ++j) kv[j] = qkv[(size_t)min(u0 + j, t) * ld + Q + h * 64 + lane];
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      if (u0 + j > t) break;
+      const float s = wave_sum64(q * kv[j]) * scale;
+      if (lane == 0) sc[u0 + j] = s;
+      m = fmaxf(m, s);
+    }
   }
   __syncthreads();
   float l = 0.f;
@@ -138,7 +147,16 @@ __global__ __launch_bounds__(64) void k_codec_attention(const float *qkv, int T,
   l = wave_sum64(l);
   __syncthreads();
   float acc = 0.f;
-  for (int u = 0; u <= t; ++u) acc = fmaf(sc[u], qkv[(size_t)u * ld + 2 * Q + h * 64 + lane], acc);
+  for (int u0 = 0; u0 <= t; u0 += KB) {
+    float vv[KB];
+#pragma unroll
+    for (int j = 0; j < KB; ++j) vv[j] = qkv[(size_t)min(u0 + j, t) * ld + 2 * Q + h * 64 + lane];
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      if (u0 + j > t) break;
+      acc = fmaf(sc[u0 + j], vv[j], acc);
+    }
+  }
   out[(size_t)t * ldo + h * 64 + lane] = acc / l;
 }
 
