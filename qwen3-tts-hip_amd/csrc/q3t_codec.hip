@@ -113,39 +113,52 @@ __global__ void k_codec_rope(float *qkv, int T, int ld, int heads, const float2 
   v[i + 32] = b * cs.x + a * cs.y;
 }
 
-// Causal attention over rows 0..t for query row t and head h (one wave): scores scaled by
-// `scale`, softmax, weighted sum of V (attention_scores_causal_f32 + masked softmax +
-// apply_value, kernels.rs:980-1040).  qkv rows: [q heads | k heads | v heads] x 64 dims.
-__global__ __launch_bounds__(64) void k_codec_attention(const float *qkv, int T, int ld, int heads, float scale,
-                                                        float *out, int ldo) {
+// Causal attention over rows 0..t for query row t and head h: scores scaled by `scale`,
+// softmax, weighted sum of V (attention_scores_causal_f32 + masked softmax + apply_value,
+// kernels.rs:980-1040).  qkv rows: [q heads | k heads | v heads] x 64 dims.  The four waves
+// score interleaved batches of 8 keys (each score one wave sum, the same in every lane and
+// whichever wave computes it); wave 0 then forms the probabilities with the scores' maximum
+// and sums V in key order.
+__global__ __launch_bounds__(256) void k_codec_attention(const float *qkv, int T, int ld, int heads, float scale,
+                                                         float *out, int ldo) {
   extern __shared__ float sc[];  // [T]
-  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+  __shared__ float mw[4];
+  const int h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int Q = heads * 64;
   const float q = qkv[(size_t)t * ld + h * 64 + lane];
   float m = -FLT_MAX;
   // Key rows in batches of 8, every load of a batch issued before its reductions.
   constexpr int KB = 8;
-  for (int u0 = 0; u0 <= t; u0 += KB) {
+  for (int u0 = wave * KB; u0 <= t; u0 += 4 * KB) {
     float kv[KB];
 #pragma unroll
     for (int j = 0; j < KB; ++j) kv[j] = qkv[(size_t)min(u0 + j, t) * ld + Q + h * 64 + lane];
 #pragma unroll
     for (int j = 0; j < KB; ++j) {
+      // A rounded product, not contracted into the butterfly's first add (which would add
+      // each lane's own exact product to its partner's rounded one): every lane then holds
+      // the same score.
+#pragma clang fp contract(off)
       if (u0 + j > t) break;
       const float s = wave_sum64(q * kv[j]) * scale;
       if (lane == 0) sc[u0 + j] = s;
       m = fmaxf(m, s);
     }
   }
+  if (lane == 0) mw[wave] = m;
   __syncthreads();
+  m = fmaxf(fmaxf(mw[0], mw[1]), fmaxf(mw[2], mw[3]));
   float l = 0.f;
-  for (int u = lane; u <= t; u += 64) {
-    const float p = expf(sc[u] - m);
-    sc[u] = p;
-    l += p;
+  if (wave == 0) {
+    for (int u = lane; u <= t; u += 64) {
+      const float p = expf(sc[u] - m);
+      sc[u] = p;
+      l += p;
+    }
+    l = wave_sum64(l);
   }
-  l = wave_sum64(l);
   __syncthreads();
+  if (wave != 0) return;
   float acc = 0.f;
   for (int u0 = 0; u0 <= t; u0 += KB) {
     float vv[KB];
@@ -249,7 +262,7 @@ hipError_t launch_codec_attention(const float *qkv, int T, int ld, int heads, fl
                                   hipStream_t s) {
   if (T <= 0 || T > kCodecMaxAttnRows || heads <= 0 || ld < 3 * heads * 64 || ldo < heads * 64)
     return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_codec_attention, dim3(heads, T), dim3(64), (size_t)T * sizeof(float), s, qkv, T, ld, heads,
+  hipLaunchKernelGGL(k_codec_attention, dim3(heads, T), dim3(256), (size_t)T * sizeof(float), s, qkv, T, ld, heads,
                      scale, out, ldo);
   return hipGetLastError();
 }
