@@ -205,6 +205,41 @@ __global__ __launch_bounds__(kFinalTile) void k_codec_final(const float *xin, co
   out[t] = fminf(fmaxf(s, -1.0f), 1.0f);
 }
 
+// The same for C % 4 == 0: rows C + 4 floats apart (16-byte aligned; the 16 lanes of a
+// 128-bit LDS read start in distinct banks), x and w read four channels at a time, the
+// products still added one by one in (j, c) order.
+__global__ __launch_bounds__(kFinalTile) void k_codec_final4(const float *xin, const float *w, const float *b, int T,
+                                                             int C, int K, float *out) {
+  __shared__ float4 xs4[(kFinalTile + kFinalMaxK - 1) * (kFinalMaxC + 4) / 4];
+  __shared__ float4 ws4[kFinalMaxK * kFinalMaxC / 4];
+  const int t0 = blockIdx.x * kFinalTile;
+  const int rows = min(kFinalTile, T - t0) + K - 1;
+  const int c4 = C / 4, pitch4 = c4 + 1;
+  const float4 *src = reinterpret_cast<const float4 *>(xin + (size_t)t0 * C);
+  for (int i = threadIdx.x; i < rows * c4; i += kFinalTile) {
+    const int r = i / c4;
+    xs4[r * pitch4 + (i - r * c4)] = src[i];
+  }
+  for (int i = threadIdx.x; i < K * c4; i += kFinalTile) ws4[i] = reinterpret_cast<const float4 *>(w)[i];
+  __syncthreads();
+  const int t = t0 + (int)threadIdx.x;
+  if (t >= T) return;
+  float s = b[0];
+  for (int j = 0; j < K; ++j) {
+    const float4 *xr = xs4 + (threadIdx.x + j) * pitch4;
+    const float4 *wr = ws4 + j * c4;
+#pragma unroll 4
+    for (int c = 0; c < c4; ++c) {
+      const float4 x = xr[c], v = wr[c];
+      s += x.x * v.x;
+      s += x.y * v.y;
+      s += x.z * v.z;
+      s += x.w * v.w;
+    }
+  }
+  out[t] = fminf(fmaxf(s, -1.0f), 1.0f);
+}
+
 unsigned blocks_for(size_t n, unsigned threads) { return (unsigned)((n + threads - 1) / threads); }
 
 }  // namespace
@@ -270,7 +305,12 @@ hipError_t launch_codec_attention(const float *qkv, int T, int ld, int heads, fl
 hipError_t launch_codec_final(const float *xin, const float *w, const float *b, int T, int C, int K, float *out,
                               hipStream_t s) {
   if (T <= 0 || C <= 0 || K <= 0 || C > kFinalMaxC || K > kFinalMaxK) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_codec_final, dim3(blocks_for(T, kFinalTile)), dim3(kFinalTile), 0, s, xin, w, b, T, C, K, out);
+  auto aligned = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  if (C % 4 == 0 && aligned(xin) && aligned(w))
+    hipLaunchKernelGGL(k_codec_final4, dim3(blocks_for(T, kFinalTile)), dim3(kFinalTile), 0, s, xin, w, b, T, C, K,
+                       out);
+  else
+    hipLaunchKernelGGL(k_codec_final, dim3(blocks_for(T, kFinalTile)), dim3(kFinalTile), 0, s, xin, w, b, T, C, K, out);
   return hipGetLastError();
 }
 
