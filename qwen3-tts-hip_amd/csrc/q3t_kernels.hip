@@ -1254,12 +1254,16 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
 // the matching 64 up rows (64 outputs).  Requires K % 32 == 0 (and N % 64 == 0 for SwiGLU); a
 // partial last block of columns computes clamped weight rows and stores only columns below N.
 // XS: bit 0 = GemmArgs::row_scale given, bit 1 = gamma given (compile-time, so that the k
-// loop is one basic block).
+// loop is one basic block).  BW = 96 (not SwiGLU): 96-column blocks, for N a multiple of 96
+// but not of 128 (the codec's 96- and 192-channel convolutions), where 128-column blocks
+// would leave a quarter of the matrix-core work on padding columns.
 // ---------------------------------------------------------------------------------------
-template <int EPI, int XS>
+template <int EPI, int XS, int BW = 128>
 __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
-  constexpr int BM = 128, BW = 128, BK = 32;
+  constexpr int BM = 128, BK = 32;
   constexpr bool SW = EPI == EPI_SWIGLU;
+  static_assert(BW == 128 || (BW == 96 && !SW), "column block");
+  constexpr int NU = BW / 16;  // 16-column tiles per block
   constexpr bool RS = XS & 1, GM = XS & 2;
   // weight tile u (rows 16 u .. 16 u + 15 of the block) at Bs[buf][u]; lane li + 16 kb reads
   // row 16 u + li, k = 8 kb .. 8 kb + 7, from entry 16 kb + (li ^ 4 kb).  The xor spreads the
@@ -1290,12 +1294,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
   // its columns are not stored)
   auto wrow = [&](int r) -> int {
     if constexpr (SW) return r < 64 ? nb * 64 + r : a.N + nb * 64 + (r - 64);
-    else return min(nb * 128 + r, a.N - 1);
+    else return min(nb * BW + r, a.N - 1);
   };
   // X: lane (li, kb) reads rows m0 + 16 t + li, k = 8 kb .. 8 kb + 7 (two float4 per tile t).
   // W: thread tid reads block rows (tid + 256 i) / 4, k = 8 ((tid + 256 i) % 4) .. + 7 (four
   // consecutive lanes read one row's 64 contiguous bytes).
-  constexpr int NB = BW * BK / 8 / 256, CB = BK / 8;
+  // NCH 16-byte weight chunks per k step, NB per thread (the last one partial for BW = 96)
+  constexpr int NCH = BW * BK / 8, NB = (NCH + 255) / 256, CB = BK / 8;
   const float *xp[2];
   float rs[2];
 #pragma unroll
@@ -1337,7 +1342,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
       rg[1] = *reinterpret_cast<const float4 *>(gp + k0 + 4);
     }
 #pragma unroll
-    for (int i = 0; i < NB; ++i) rb[i] = *reinterpret_cast<const bf16x8_t *>(wp[i] + k0);
+    for (int i = 0; i < NB; ++i)
+      if (NCH % 256 == 0 || tid + 256 * i < NCH) rb[i] = *reinterpret_cast<const bf16x8_t *>(wp[i] + k0);
     const bool wrap = xleft == BK;
     xk += wrap ? BK + a.xseg_stride - a.xseg_len : BK;
     xleft = wrap ? a.xseg_len : xleft - BK;
@@ -1364,19 +1370,19 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int idx = tid + 256 * i, row = idx / CB, c = idx % CB;
-      Bs[buf][row >> 4][16 * c + ((row & 15) ^ (4 * c))] = rb[i];
+      if (NCH % 256 == 0 || idx < NCH) Bs[buf][row >> 4][16 * c + ((row & 15) ^ (4 * c))] = rb[i];
     }
   };
 
-  f32x4_t acc[2][8];
+  f32x4_t acc[2][NU];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc[t][u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < NU; ++u) acc[t][u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   auto mma = [&](int buf) {
-    bf16x8_t bq[8];
+    bf16x8_t bq[NU];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) bq[u] = Bs[buf][u][16 * kb + (li ^ (4 * kb))];
+    for (int u = 0; u < NU; ++u) bq[u] = Bs[buf][u][16 * kb + (li ^ (4 * kb))];
     // term-major: 16 independent accumulations between two that depend on each other;
     // each accumulator still adds lo, mid, hi in that order.
 #pragma unroll
@@ -1384,7 +1390,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
+        for (int u = 0; u < NU; ++u)
           acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aq[q][t], bq[u], acc[t][u], 0, 0, 0);
   };
 
@@ -1430,8 +1436,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
         }
       } else {
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          const int n = nb * 128 + u * 16 + li;
+        for (int u = 0; u < NU; ++u) {
+          const int n = nb * BW + u * 16 + li;
           if (n >= a.N) continue;
           if (nsplit > 1) a.split_ws[((size_t)z * a.M + m) * a.N + n] = acc[t][u][e];
           else a.Y[(size_t)m * a.ldy + n] = gemm_epilogue<EPI>(a, m, n, acc[t][u][e]);
@@ -2881,8 +2887,10 @@ static hipError_t gemm_epi(const GemmArgs &a, hipStream_t s) {
   const int cols_per_wg = 4 * 16 * NT;
   dim3 grid;
   int path;
+  // 96-column blocks where N is a multiple of 96 but not of 128
+  const bool bw96 = EPI != EPI_SWIGLU && a.N % 128 != 0 && a.N % 96 == 0;
   if (a.M >= 128 && a.K % 32 == 0 && (EPI != EPI_SWIGLU || a.N % 64 == 0) && a.ldx % 4 == 0) {
-    const int nout = EPI == EPI_SWIGLU ? 64 : 128;
+    const int nout = EPI == EPI_SWIGLU ? 64 : (bw96 ? 96 : 128);
     grid = dim3((a.N + nout - 1) / nout, (a.M + 127) / 128);
     path = 0;
   } else if (a.M <= 16) {
@@ -2894,11 +2902,26 @@ static hipError_t gemm_epi(const GemmArgs &a, hipStream_t s) {
   }
   grid.z = gemm_splits(a, (int)(grid.x * grid.y), EPI == EPI_SWIGLU);
   if (path == 0) {
-    switch ((a.row_scale ? 1 : 0) | (a.gamma ? 2 : 0)) {
-      case 0: hipLaunchKernelGGL((k_gemm_lds<EPI, 0>), grid, dim3(256), 0, s, a); break;
-      case 1: hipLaunchKernelGGL((k_gemm_lds<EPI, 1>), grid, dim3(256), 0, s, a); break;
-      case 2: hipLaunchKernelGGL((k_gemm_lds<EPI, 2>), grid, dim3(256), 0, s, a); break;
-      default: hipLaunchKernelGGL((k_gemm_lds<EPI, 3>), grid, dim3(256), 0, s, a); break;
+    const int xs = (a.row_scale ? 1 : 0) | (a.gamma ? 2 : 0);
+    bool launched = false;
+    if constexpr (EPI != EPI_SWIGLU) {
+      if (bw96) {
+        switch (xs) {
+          case 0: hipLaunchKernelGGL((k_gemm_lds<EPI, 0, 96>), grid, dim3(256), 0, s, a); break;
+          case 1: hipLaunchKernelGGL((k_gemm_lds<EPI, 1, 96>), grid, dim3(256), 0, s, a); break;
+          case 2: hipLaunchKernelGGL((k_gemm_lds<EPI, 2, 96>), grid, dim3(256), 0, s, a); break;
+          default: hipLaunchKernelGGL((k_gemm_lds<EPI, 3, 96>), grid, dim3(256), 0, s, a); break;
+        }
+        launched = true;
+      }
+    }
+    if (!launched) {
+      switch (xs) {
+        case 0: hipLaunchKernelGGL((k_gemm_lds<EPI, 0>), grid, dim3(256), 0, s, a); break;
+        case 1: hipLaunchKernelGGL((k_gemm_lds<EPI, 1>), grid, dim3(256), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((k_gemm_lds<EPI, 2>), grid, dim3(256), 0, s, a); break;
+        default: hipLaunchKernelGGL((k_gemm_lds<EPI, 3>), grid, dim3(256), 0, s, a); break;
+      }
     }
   }
   else if (path == 1) hipLaunchKernelGGL((k_gemm_mfma<EPI, 1, NB>), grid, dim3(256), 0, s, a);

@@ -36,7 +36,7 @@ def _close(got, want):
 
 @pytest.mark.parametrize("M,N,K", [(1, 64, 32), (16, 1024, 1024), (17, 300, 64), (73, 4096, 1024),
                                    (521, 1024, 3072), (5, 2048, 2048), (16, 1024, 3072), (1, 3072, 1024),
-                                   (9, 100, 6144)])
+                                   (9, 100, 6144), (521, 96, 1024), (300, 192, 672), (130, 288, 384)])
 def test_store(eng, M, N, K):
     print(f"[gpu] gemm store M={M} N={N} K={K}", flush=True)
     rng = np.random.default_rng(M * 7 + N)
@@ -64,6 +64,25 @@ def test_epilogues_and_norm(eng):
     # SwiGLU over gate rows [0, N) and up rows [N, 2N)
     gate, up = Xn @ W[:N].T, Xn @ W[N:].T
     _close(eng.debug_gemm(2, X, Wb, N, gamma=g), gate / (1 + np.exp(-gate)) * up)
+
+
+@pytest.mark.parametrize("N", [96, 192])
+def test_epilogues_96_column_blocks(eng, N):
+    """M >= 128 with N a multiple of 96 but not of 128 (the codec's 96- and 192-channel
+    convolutions) runs the LDS-tiled kernel in 96-column blocks: bias, and residual with the
+    RMSNorm prologue."""
+    M, K = 200, 672
+    print(f"[gpu] gemm 96-column blocks M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(N)
+    X = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    Xn = X.astype(np.float64) / np.sqrt((X.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6) * g
+    Wb = _weights(N, K, N + 1)
+    W = synth.bf16_bits_to_f32(Wb).astype(np.float64)
+    res = rng.standard_normal((M, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    _close(eng.debug_gemm(3, X, Wb, N, bias=bias), X.astype(np.float64) @ W.T + bias)
+    _close(eng.debug_gemm(1, X, Wb, N, gamma=g, res=res), res + Xn @ W.T)
 
 
 @pytest.mark.parametrize("M", [16, 40])
