@@ -1113,6 +1113,24 @@ __device__ __forceinline__ float gemm_epilogue(const GemmArgs &a, int m, int n, 
   return v;
 }
 
+// gemm_epilogue with its operands loaded beforehand: r = res[m][n], b = bias[n] (when
+// given), c = scale[n] (when given); the same arithmetic in the same order.
+template <int EPI>
+__device__ __forceinline__ float gemm_epilogue_ops(const GemmArgs &a, float v, float r, float b, float c) {
+  if constexpr (EPI == EPI_RESIDUAL) v = r + v;
+  if constexpr (EPI == EPI_BIAS) v = v + b;
+  if constexpr (EPI == EPI_AFFINE_RES) {
+    if (a.bias) v = v + b;
+    if (a.scale) v = v * c;
+    v = r + v;
+  }
+  if constexpr (EPI == EPI_BIAS_GELU) {
+    v = v + b;
+    v = 0.5f * v * (1.0f + erff(v * 0.7071067811865476f));
+  }
+  return v;
+}
+
 template <int EPI, int MB, int NB>
 __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
   const int lane = threadIdx.x & 63;
@@ -1434,16 +1452,55 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
             a.Y[(size_t)m * a.ldy + n] = g / (1.0f + expf(-g)) * up;
           }
         }
-      } else {
+      } else if (nsplit > 1) {
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+          const int n = nb * BW + u * 16 + li;
+          if (n < a.N) a.split_ws[((size_t)z * a.M + m) * a.N + n] = acc[t][u][e];
+        }
+      }
+    }
+  if constexpr (!SW) {
+    if (nsplit > 1) return;
+    // Every epilogue operand is loaded before the first store: Y may be the residual itself
+    // (each element read and written by this lane only), and a load after a store that may
+    // alias it would wait for that store, one memory round trip per element.
+    constexpr bool RES = EPI == EPI_RESIDUAL || EPI == EPI_AFFINE_RES;
+    constexpr bool BIAS = EPI == EPI_BIAS || EPI == EPI_AFFINE_RES || EPI == EPI_BIAS_GELU;
+    float rv[2][4][RES ? NU : 1], bv[BIAS ? NU : 1], cv[EPI == EPI_AFFINE_RES ? NU : 1];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+      const int nc = min(nb * BW + u * 16 + li, a.N - 1);
+      if constexpr (BIAS) bv[u] = (EPI != EPI_AFFINE_RES || a.bias) ? a.bias[nc] : 0.f;
+      if constexpr (EPI == EPI_AFFINE_RES) cv[u] = a.scale ? a.scale[nc] : 1.f;
+    }
+    if constexpr (RES) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+          for (int u = 0; u < NU; ++u) {
+            const int mc = min(m0 + t * 16 + 4 * kb + e, a.M - 1), nc = min(nb * BW + u * 16 + li, a.N - 1);
+            rv[t][e][u] = a.res[(size_t)mc * a.ldr + nc];
+          }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + t * 16 + 4 * kb + e;
+        if (m >= a.M) continue;
 #pragma unroll
         for (int u = 0; u < NU; ++u) {
           const int n = nb * BW + u * 16 + li;
           if (n >= a.N) continue;
-          if (nsplit > 1) a.split_ws[((size_t)z * a.M + m) * a.N + n] = acc[t][u][e];
-          else a.Y[(size_t)m * a.ldy + n] = gemm_epilogue<EPI>(a, m, n, acc[t][u][e]);
+          a.Y[(size_t)m * a.ldy + n] = gemm_epilogue_ops<EPI>(a, acc[t][u][e], RES ? rv[t][e][RES ? u : 0] : 0.f,
+                                                              BIAS ? bv[BIAS ? u : 0] : 0.f,
+                                                              EPI == EPI_AFFINE_RES ? cv[EPI == EPI_AFFINE_RES ? u : 0] : 1.f);
         }
       }
-    }
+  }
 }
 
 // KEYS (EPI_STORE): store per-row argmax keys (GemmArgs::keys_out) instead of Y.  XT16: X is
