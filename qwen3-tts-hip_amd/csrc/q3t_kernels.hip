@@ -1222,6 +1222,27 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
   }
 
   // epilogue: lane holds C[4 * kb + e][li] of every tile
+  // The epilogue's operands are loaded before the first store (Y may be the residual itself:
+  // a load after a store that may alias it would wait for that store).
+  constexpr bool RES = EPI == EPI_RESIDUAL || EPI == EPI_AFFINE_RES;
+  constexpr bool BIAS = EPI == EPI_BIAS || EPI == EPI_AFFINE_RES || EPI == EPI_BIAS_GELU;
+  constexpr bool OPS = RES || BIAS;
+  float rv[OPS ? MB : 1][OPS ? NTILE : 1][4], bv[OPS ? NTILE : 1], cv[OPS ? NTILE : 1];
+  if constexpr (OPS) {
+    if (nsplit == 1) {
+#pragma unroll
+      for (int j = 0; j < NTILE; ++j) {
+        const int nc = min(n0 + 16 * j + li, a.N - 1);
+        bv[j] = (BIAS && (EPI != EPI_AFFINE_RES || a.bias)) ? a.bias[nc] : 0.f;
+        cv[j] = (EPI == EPI_AFFINE_RES && a.scale) ? a.scale[nc] : 1.f;
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            rv[i][j][e] = RES ? a.res[(size_t)min(m0 + 16 * i + 4 * kb + e, a.M - 1) * a.ldr + nc] : 0.f;
+      }
+    }
+  }
 #pragma unroll
   for (int i = 0; i < MB; ++i)
 #pragma unroll
@@ -1246,7 +1267,7 @@ __global__ __launch_bounds__(256) void k_gemm_mfma(GemmArgs a) {
             a.split_ws[((size_t)z * a.M + m) * a.N + n] = v;
             continue;
           }
-          v = gemm_epilogue<EPI>(a, m, n, v);
+          if constexpr (OPS) v = gemm_epilogue_ops<EPI>(a, v, rv[i][j][e], bv[j], cv[j]);
         }
         a.Y[(size_t)m * a.ldy + n] = v;
       }
