@@ -442,7 +442,8 @@ def main() -> int:
     active_mean = P + (per_gen - 1) / 2.0
     fb = frame_bytes(spec, active_mean, 2 if args.kv_bf16 else 4)
     frame_s = elapsed / frames
-    roofline = eng.dominant_kernel_roofline(HBM_PEAK_GBPS)
+    # --eager captures no graph anywhere (the form profiled under rocprofv3's kernel tracer)
+    roofline = eng.dominant_kernel_roofline(HBM_PEAK_GBPS, graph=not args.eager)
     roofline["traffic"] = measured_traffic(w.name, roofline["kernel"])
     with eng.start_stream(inputs, opts) as st_steps:
         steps_line = per_step(st_steps, spec, P, w.chunk_frames, 2 if args.kv_bf16 else 4)

@@ -285,6 +285,10 @@ struct Engine {
   // except between a layer's O GEMM, which accumulates into it, and its down GEMM, which
   // reads it as the residual and zeroes it again.
   float *bmid = nullptr;
+  size_t bmid_floats = 0;
+  // Set when batched frames stopped with an error, possibly between a split O GEMM and its
+  // down GEMM (bmid then holds partial sums): the next batched call zeroes bmid first.
+  bool bmid_dirty = false;
   // The two-block prefix pass's q/k/v rows: [2 positions][16 rows][qkv_rows] (row-major).
   float *bqkv2 = nullptr;
   std::vector<Slot> slots;
@@ -1200,7 +1204,8 @@ void alloc_rows(Engine &e) {
   e.battn = zeroed((size_t)16 * std::max(td.q_out(), 2 * cd.q_out()));
   e.bact = zeroed((size_t)16 * std::max(td.intermediate, 2 * cd.intermediate));
   e.bcp_in = zeroed((size_t)3 * 16 * Hc);
-  e.bmid = zeroed((size_t)16 * std::max(Ht, 2 * Hc));
+  e.bmid_floats = (size_t)16 * std::max(Ht, 2 * Hc);
+  e.bmid = zeroed(e.bmid_floats);
   e.bqkv2 = zeroed((size_t)32 * cd.qkv_rows());
 }
 
@@ -1270,7 +1275,7 @@ void run_frames(Engine &e, Slot &s, int n) {
 }
 
 // n batched frames over stream rows 0..rows-1 (pools.row_on already on the device).
-void run_rows_frames(Engine &e, int rows, int n, bool fused) {
+void run_rows_frames_impl(Engine &e, int rows, int n, bool fused) {
   Pools &p = e.pools;
   if (e.use_graph) {
     if (!p.graph || p.graph_rows != rows || p.graph_traced != (bool)e.trace || p.graph_fused != fused) {
@@ -1298,6 +1303,23 @@ void run_rows_frames(Engine &e, int rows, int n, bool fused) {
     for (int i = 0; i < n; ++i) HIPC(hipGraphLaunch(p.graph, p.stream));
   } else {
     for (int i = 0; i < n; ++i) e.enqueue_rows_frame(rows, fused, p.stream);
+  }
+}
+
+// The split O / down GEMMs keep bmid all zeros between layers (each zeroes what it read).
+// An error can stop a frame between the two, so after any error the next call first
+// restores the zeros (outside any captured graph), and later frames never add onto stale sums.
+void run_rows_frames(Engine &e, int rows, int n, bool fused) {
+  Pools &p = e.pools;
+  if (e.bmid_dirty && e.bmid) {
+    HIPC(hipMemsetAsync(e.bmid, 0, e.bmid_floats * sizeof(float), p.stream));
+    e.bmid_dirty = false;
+  }
+  try {
+    run_rows_frames_impl(e, rows, n, fused);
+  } catch (...) {
+    e.bmid_dirty = true;
+    throw;
   }
 }
 

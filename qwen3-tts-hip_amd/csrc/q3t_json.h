@@ -42,6 +42,10 @@ struct Value {
 
 class Parser {
  public:
+  // Nesting deeper than this is rejected: value() -> object() / array() recurse, so an
+  // unbounded depth would let a crafted header overflow the host stack.
+  static constexpr int kMaxDepth = 64;
+
   explicit Parser(const std::string &text) : s_(text) {}
   Value parse() {
     Value v = value();
@@ -53,6 +57,16 @@ class Parser {
  private:
   const std::string &s_;
   size_t i_ = 0;
+  int depth_ = 0;
+
+  // Counts one level of object / array nesting for the lifetime of the guard.
+  struct Nest {
+    Parser &p;
+    explicit Nest(Parser &parser) : p(parser) {
+      if (++p.depth_ > kMaxDepth) p.fail("nesting too deep");
+    }
+    ~Nest() { --p.depth_; }
+  };
 
   [[noreturn]] void fail(const char *what) {
     throw std::runtime_error(std::string("json: ") + what + " at offset " + std::to_string(i_));
@@ -99,6 +113,7 @@ class Parser {
     return number();
   }
   Value object() {
+    Nest nest(*this);
     Value v;
     v.kind = Value::Object;
     expect('{');
@@ -119,6 +134,7 @@ class Parser {
     return v;
   }
   Value array() {
+    Nest nest(*this);
     Value v;
     v.kind = Value::Array;
     expect('[');

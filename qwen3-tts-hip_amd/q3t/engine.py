@@ -487,23 +487,29 @@ class HipTtsEngine:
         _check(_lib.q3t_bench_kernel_timed(self._h, int(kernel), int(iters), ctypes.byref(us), ctypes.byref(b)))
         return us.value, b.value
 
-    def dominant_kernel_roofline(self, peak_gbps: float, kernel: int = 2, iters: int = 1030) -> dict:
+    def dominant_kernel_roofline(self, peak_gbps: float, kernel: int = 2, iters: int = 1030,
+                                 graph: bool = True) -> dict:
         """Roofline entry for the kernel class that dominates a frame's time (the gate/up GEMV).
 
         ``achieved`` divides the algorithmic bytes of a launch by the kernel's own duration: the
         1030 launches of one frame order are issued eagerly, each timed by its dispatch's start
         and stop events (the per-dispatch duration rocprofv3's kernel trace reports for the same
         command).  ``graph_us_per_launch`` is the same sequence replayed as one graph, timed as a
-        whole (the dependent-launch gap included): the cost a frame sees."""
+        whole (the dependent-launch gap included): the cost a frame sees.  ``graph=False``
+        captures no graph at all (commands run under a kernel tracer): that leg is then null."""
         self.bench_kernel_timed(kernel, 103)   # warm
         us, b = self.bench_kernel_timed(kernel, iters)
-        self.bench_kernel(kernel, 103)
-        gus, _ = self.bench_kernel(kernel, iters)
+        gus = None
+        if graph:
+            self.bench_kernel(kernel, 103)
+            gus, _ = self.bench_kernel(kernel, iters)
         achieved = b / (us * 1e-6) / 1e9
         return {"kernel": self.KERNELS[kernel], "bound": "hbm", "achieved": round(achieved, 1),
                 "peak": peak_gbps, "unit": "GB/s", "frac": round(achieved / peak_gbps, 4), "traffic": None,
                 "avg_launch_us": round(us, 3), "timing": "eager launches, per-dispatch start/stop events",
-                "graph_us_per_launch": round(gus, 3), "graph_frac_gap_included": round(b / (gus * 1e-6) / 1e9 / peak_gbps, 4),
+                "graph_us_per_launch": round(gus, 3) if gus is not None else None,
+                "graph_frac_gap_included": (round(b / (gus * 1e-6) / 1e9 / peak_gbps, 4)
+                                            if gus is not None else None),
                 "algorithmic_bytes_per_launch": int(b), "launches_timed": iters}
 
     def debug_gemm(self, epi: int, X: np.ndarray, W_bits: np.ndarray, N: int, gamma=None, eps: float = 1e-6,

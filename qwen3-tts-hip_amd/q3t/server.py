@@ -464,7 +464,7 @@ class TtsServer:
             ("X-TTS-Left-Context-Frames", str(g.stream_options.left_context_frames)),
             ("X-TTS-Voice-Clone", _bool(g.use_voice_clone)),
         ]
-        return Response(200, "OK", headers, chunks=pcm(), on_done=done)
+        return Response(200, "OK", headers, chunks=_StreamChunks(pcm(), st), on_done=done)
 
     # -- GET / -----------------------------------------------------------------------------
     def index_html(self) -> str:
@@ -499,6 +499,13 @@ class TtsServer:
             except Exception as err:  # headers already sent: the connection just ends
                 self.log(f"request failed: {err}")
                 return
+            finally:
+                # A client that went away leaves the generator suspended mid-stream: close it
+                # here, so its engine stream (and the slot it holds) is released now rather
+                # than whenever the generator is garbage-collected.
+                close = getattr(resp.chunks, "close", None)
+                if close is not None:
+                    close()
             if resp.on_done:
                 resp.on_done()
 
@@ -515,6 +522,25 @@ class TtsServer:
                 continue
             self.serve_connection(conn)
             served += 1
+
+
+class _StreamChunks:
+    """The PCM chunks of an engine stream.  ``close()`` ends the generator and closes the
+    stream even when the generator never started (the response head could not be sent):
+    the stream was started before the head, so its slot must not wait for the garbage
+    collector."""
+
+    def __init__(self, gen: Iterator[bytes], stream) -> None:
+        self._gen, self._stream = gen, stream
+
+    def __iter__(self) -> Iterator[bytes]:
+        return self._gen
+
+    def close(self) -> None:
+        try:
+            self._gen.close()
+        finally:
+            self._stream.close()
 
 
 def _send_all(conn: socket.socket, data: bytes) -> None:

@@ -144,3 +144,41 @@ def test_malformed_weights_header_rejected_before_any_gpu_call(tmp_path, header,
     _weights_file(tmp_path, {"__metadata__": {"format": "pt"}, **header}, hlen=hlen)
     with pytest.raises(E.InvalidInputError, match=match):
         E.HipTtsEngine(d)
+
+
+def _raw_weights_file(tmp_path, text: bytes):
+    import struct
+    (tmp_path / "model.safetensors").write_bytes(struct.pack("<Q", len(text)) + text + b"\0" * 64)
+
+
+@pytest.mark.parametrize("text,match", [
+    (b'{"a": ' + b"[" * 100000 + b"]" * 100000 + b"}", "nesting too deep"),
+    (b'{"a": ' + b'{"b": ' * 65 + b"1" + b"}" * 65 + b"}", "nesting too deep"),
+    (b'{"a": {"dtype": "F32", "shape": [4], "data_offsets": [0, 16', "unexpected end|expected"),
+    (b'{"a": {"dtype": "F32", "shape": [4], "data_off', "unterminated string"),
+])
+def test_deep_or_truncated_weights_header_rejected(tmp_path, text, match):
+    """A safetensors header nested past the parser's depth limit, or cut off mid-value, is
+    an InvalidInputError from q3t_engine_create (not a host stack overflow), before any
+    device call."""
+    d = _config_dir(tmp_path)
+    _raw_weights_file(tmp_path, text)
+    with pytest.raises(E.InvalidInputError, match=match):
+        E.HipTtsEngine(d)
+
+
+def test_header_nesting_at_the_limit_parses(tmp_path):
+    """64 levels of nesting are accepted (the limit is not off by one): the file then fails
+    later, on its missing tensors, not in the parser."""
+    d = _config_dir(tmp_path)
+    _raw_weights_file(tmp_path, b'{"__metadata__": ' + b"[" * 63 + b"]" * 63 + b"}")
+    with pytest.raises(E.Q3tError) as ei:
+        E.HipTtsEngine(d)
+    assert "nesting" not in str(ei.value)
+
+
+def test_deeply_nested_config_json_rejected(tmp_path):
+    """config.json goes through the same parser: deep nesting is an InvalidInputError."""
+    (tmp_path / "config.json").write_text('{"x": ' + "[" * 50000 + "]" * 50000 + "}")
+    with pytest.raises(E.InvalidInputError, match="nesting too deep"):
+        E.HipTtsEngine(str(tmp_path))

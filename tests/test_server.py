@@ -349,3 +349,52 @@ def test_live_socket_round_trip(live):
         while chunk := raw.recv(4096):
             got += chunk
     assert got.startswith(b"HTTP/1.1 500 Internal Server Error\r\n") and got.endswith(b"request body is too large")
+
+
+class _DroppingConn:
+    """A connection whose client goes away after `ok_sends` sendall calls."""
+
+    def __init__(self, request: bytes, ok_sends: int):
+        self.request, self.ok_sends, self.sent = request, ok_sends, []
+
+    def recv(self, n):
+        data, self.request = self.request[:n], self.request[n:]
+        return data
+
+    def sendall(self, data):
+        if len(self.sent) >= self.ok_sends:
+            raise BrokenPipeError("client went away")
+        self.sent.append(data)
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        return False
+
+
+@pytest.mark.parametrize("ok_sends", [0, 1, 2])
+def test_stream_closed_when_client_disconnects(ok_sends):
+    """A client that disconnects mid-stream (sendall raises after the head, after one chunk,
+    ...) must not leave the engine stream open until garbage collection: the server closes
+    the PCM generator, which closes the stream (its slot is free for the next request)."""
+    srv, logs = _srv()
+    body = b"text=abc&stream_chunk_frames=2"
+    raw = (b"POST /api/stream HTTP/1.1\r\nHost: x\r\nContent-Type: " + S.FORM_TYPE.encode() +
+           b"\r\nContent-Length: " + str(len(body)).encode() + b"\r\n\r\n" + body)
+    conn = _DroppingConn(raw, ok_sends)
+    keep = []  # a lingering reference to the generator must not keep the stream open
+    orig = srv.handle
+
+    def handle(req):
+        r = orig(req)
+        keep.append(r.chunks)
+        return r
+    srv.handle = handle
+    srv.serve_connection(conn)
+    assert len(conn.sent) == ok_sends
+    assert any(l.startswith("request failed:") for l in logs)
+    # the stream starts before the head is sent (start errors are answered with a status):
+    # it must be closed now, also when no chunk was ever pulled (ok_sends = 0)
+    assert len(srv.engine.streams) == 1 and srv.engine.streams[0].closed
+    assert not any(l.startswith("streamed:") for l in logs)
