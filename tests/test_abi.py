@@ -156,7 +156,7 @@ def _raw_weights_file(tmp_path, text: bytes):
     (b'{"a": ' + b'{"b": ' * 65 + b"1" + b"}" * 65 + b"}", "nesting too deep"),
     (b'{"a": {"dtype": "F32", "shape": [4], "data_offsets": [0, 16', "unexpected end|expected"),
     (b'{"a": {"dtype": "F32", "shape": [4], "data_off', "unterminated string"),
-])
+], ids=["arrays-100000-deep", "objects-66-deep", "truncated-number", "truncated-key"])
 def test_deep_or_truncated_weights_header_rejected(tmp_path, text, match):
     """A safetensors header nested past the parser's depth limit, or cut off mid-value, is
     an InvalidInputError from q3t_engine_create (not a host stack overflow), before any
