@@ -318,10 +318,12 @@ int q3t_engine_synchronize(q3t_engine *engine);
  *          6: greedy CodePredictor selection     7: Talker attention at half the cache
  *          8: CodePredictor LM-head GEMV
  *          9: CodePredictor attention with the O projection fused (when the model has it)
- * Classes 1 and 2 run as frames do: where the model splits an O projection by KV head (the
- * 0.6B Talker's), class 1 is that per-head projection and class 2 (gate/up) sums its shares;
- * class 2 also sums the CodePredictor's fused projection shares. Slot 0 must not hold a
- * stream. */
+ *         10: Talker attention at half the cache with the O projection fused (when the model
+ *             has it: the 0.6B Talker)
+ * Class 1 is the O GEMV merging split-attention partials (Talker layers); a Talker with
+ * the fused attention + O projection (the 0.6B's) runs class 10 in frames instead.  Class 2
+ * (gate/up) sums the per-head shares of the Talker's and the CodePredictor's fused
+ * projections as frames do. Slot 0 must not hold a stream. */
 int q3t_bench_kernel(q3t_engine *engine, int32_t kernel, int32_t iters, double *avg_us,
                      double *bytes_per_launch);
 

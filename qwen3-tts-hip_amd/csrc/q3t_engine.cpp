@@ -313,14 +313,16 @@ struct Engine {
            (d.hidden == 512 || d.hidden == 1024);
   }
 
-  // The Talker's split attention (partials) feeds an O projection split by KV head
-  // (launch_oproj_heads) whose shares the gate/up GEMV sums into the residual, when its
-  // hidden size takes the partial-sum GEMV (512 or 1024: the 0.6B Talker).  Each O workgroup
-  // then merges one head's partials instead of all of them.
+  // The Talker's attention runs with its O projection fused in, split by KV head
+  // (launch_attn_oproj_full), the shares summed into the residual by the gate/up GEMV, when
+  // its hidden size takes the partial-sum GEMV (512 or 1024: the 0.6B Talker) and the cache
+  // fits the fused kernel (33 .. 1024 rows).  Otherwise the split attention's partials are
+  // merged by the O GEMV.
   bool talker_heads_o(const StackW &w) const {
     const Dims &d = w.d;
+    const int rows = attn_oproj_full_rows(d.q_heads, d.kv_heads);
     return &w == &talker && attn_chunks(w.cap) > 1 && attn_chunks(w.cap) <= kAttnGemvMergeChunks &&
-           d.kv_heads <= 8 && (d.hidden == 512 || d.hidden == 1024);
+           d.kv_heads <= 8 && (d.hidden == 512 || d.hidden == 1024) && rows > 0 && d.hidden % rows == 0;
   }
 
   // One decoder-stack step for one position (decode.rs:951-1001 / 1300-1475).
@@ -373,6 +375,26 @@ struct Engine {
              sl.st, s, nt);
         continue;
       }
+      if (talker_heads_o(w)) {
+        // Attention and the O projection (K split by KV head) in one launch; the gate/up GEMV
+        // sums the residual and the per-head shares, and stores that sum (x_mid) for down.
+        AttnArgs aa{sl.qkv,   L.gq,      L.gk,       w.rope,  kc + l * cache_layer, vc + l * cache_layer,
+                    nullptr,  d.q_heads, d.kv_heads, w.cap,   d.eps, 1.0f / std::sqrt((float)d.head_dim),
+                    pos_mode, pos_const, skip,       kv_bf16, sl.st, nullptr, 0, attn_chunk_len(w.cap), 0};
+        aa.wo = L.o;
+        aa.wo_rows = d.hidden;
+        aa.opart = sl.opart;
+        hip_check(launch_attn_oproj_full(aa, d.head_dim, s), "launch_attn_oproj_full");
+        GemvArgs gu{L.gu, src, L.g_post, nullptr, nullptr, sl.act, d.intermediate, d.hidden, d.eps, skip, sl.st};
+        gu.parts = sl.opart;
+        gu.n_parts = d.kv_heads;
+        gu.ld_parts = d.hidden;
+        gu.x_store = sl.x_mid;
+        hip_check(launch_gemv(EPI_SWIGLU, true, nt, gu, s), "launch_gemv(gate/up, partial sum)");
+        gemv(EPI_RESIDUAL, false, L.down, sl.act, nullptr, 0.f, sl.x_mid, nullptr, x, d.hidden, d.intermediate, skip,
+             sl.st, s, nt);
+        continue;
+      }
       // The Talker's attention spans many chunks: partials, merged by the O projection.  The
       // CodePredictor's 16-row cache is one chunk: direct output.
       const int partial = attn_chunks(w.cap) > 1 ? 1 : 0;
@@ -386,26 +408,6 @@ struct Engine {
         aa.ld_table = d.qkv_rows();
       }
       hip_check(launch_attn_decode(aa, d.head_dim, s), "launch_attn_decode");
-      if (talker_heads_o(w)) {
-        GemvArgs og{L.o, nullptr, nullptr, nullptr, nullptr, sl.opart, d.hidden, d.q_out(), 0.f, skip, sl.st};
-        og.attn_part = sl.attn_part;
-        og.attn_part_chunks = sl.attn_part_chunks;
-        og.attn_chunk = attn_chunk_len(w.cap);
-        og.attn_pos_mode = pos_mode;
-        og.attn_pos_const = pos_const;
-        og.attn_q_heads = d.q_heads;
-        og.attn_kv_heads = d.kv_heads;
-        hip_check(launch_oproj_heads(og, s), "launch_oproj_heads");
-        GemvArgs gu{L.gu, src, L.g_post, nullptr, nullptr, sl.act, d.intermediate, d.hidden, d.eps, skip, sl.st};
-        gu.parts = sl.opart;
-        gu.n_parts = d.kv_heads;
-        gu.ld_parts = d.hidden;
-        gu.x_store = sl.x_mid;
-        hip_check(launch_gemv(EPI_SWIGLU, true, nt, gu, s), "launch_gemv(gate/up, partial sum)");
-        gemv(EPI_RESIDUAL, false, L.down, sl.act, nullptr, 0.f, sl.x_mid, nullptr, x, d.hidden, d.intermediate, skip,
-             sl.st, s, nt);
-        continue;
-      }
       // Up to kAttnGemvMergeChunks partials are merged inside the O projection; more (caches
       // past 1024 rows) by the merge kernel first.
       const bool merge_in_o = partial && attn_chunks(w.cap) <= kAttnGemvMergeChunks;
@@ -2518,8 +2520,10 @@ int bench_kernel_impl(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_
     using namespace q3t;
     if (!e || !avg_us || !bytes) fail(Q3T_ERR_INVALID, "null argument");
     if (iters <= 0 || iters > 8192) fail(Q3T_ERR_INVALID, "iters must be in 1..8192");
-    if (kernel < 0 || kernel > 9) fail(Q3T_ERR_INVALID, "unknown kernel class %d", kernel);
+    if (kernel < 0 || kernel > 10) fail(Q3T_ERR_INVALID, "unknown kernel class %d", kernel);
     if (kernel == 9 && !e->oproj_ok(e->cp)) fail(Q3T_ERR_INVALID, "the model's CodePredictor has no fused O projection");
+    if (kernel == 10 && !e->talker_heads_o(e->talker))
+      fail(Q3T_ERR_INVALID, "the model's Talker has no fused attention + O projection");
     Slot &s = e->slots[0];
     if (s.in_use) fail(Q3T_ERR_BUSY, "stream slot 0 is in use");
     HIPC(hipSetDevice(e->device));
@@ -2568,25 +2572,9 @@ int bench_kernel_impl(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_
                   SKIP_NEVER, s.st, s.stream, nt, lt);
           b = 2.0 * d.qkv_rows() * d.hidden + 4.0 * (d.hidden * 2 + d.qkv_rows());
           break;
-        case 1: {  // O projection + residual (Talker layers merge attention partials first; split
-                   // by KV head into per-head shares where frames run it that way)
+        case 1: {  // O projection + residual (Talker layers merge split-attention partials first;
+                   // frames of a Talker with the fused attention + O run class 10 instead)
           GemvArgs og{W.o, s.attn, nullptr, s.act, nullptr, s.act, d.hidden, d.q_out(), 0.f, SKIP_NEVER, s.st};
-          if (e->talker_heads_o(*l.w)) {
-            og.x = nullptr;
-            og.res = nullptr;
-            og.out = s.opart;
-            og.attn_part = s.attn_part;
-            og.attn_part_chunks = s.attn_part_chunks;
-            og.attn_chunk = attn_chunk_len(l.w->cap);
-            og.attn_pos_mode = POS_CONST;
-            og.attn_pos_const = l.w->cap / 2;
-            og.attn_q_heads = d.q_heads;
-            og.attn_kv_heads = d.kv_heads;
-            hip_check(launch_oproj_heads(og, s.stream, lt), "launch_oproj_heads");
-            b = 2.0 * d.hidden * d.q_out() + 4.0 * (d.kv_heads * d.hidden) +
-                4.0 * d.q_heads * (d.head_dim + 2) * std::min(attn_chunks(l.w->cap), (l.w->cap / 2) / attn_chunk_len(l.w->cap) + 1);
-            break;
-          }
           if (nt && attn_chunks(l.w->cap) <= kAttnGemvMergeChunks) {
             og.x = nullptr;
             og.attn_part = s.attn_part;
@@ -2674,6 +2662,21 @@ int bench_kernel_impl(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_
           aa.wo_rows = d.hidden;
           aa.opart = s.opart;
           hip_check(launch_attn_oproj(aa, d.head_dim, s.stream, lt), "launch_attn_oproj");
+          b = 2.0 * esz * d.kv_heads * d.head_dim * (pos + 1) + 4.0 * d.qkv_rows() + 2.0 * d.hidden * d.q_out() +
+              4.0 * d.kv_heads * d.hidden;
+          break;
+        }
+        case 10: {  // Talker attention with the O projection fused (per-head shares), half the cache
+          const size_t esz = e->kv_bf16 ? 2 : 4;
+          const size_t layer_bytes = (size_t)d.kv_heads * l.w->cap * d.head_dim * esz;
+          const int pos = l.w->cap / 2;
+          AttnArgs aa{s.qkv, W.gq, W.gk, l.w->rope, s.t_k + layer_bytes * l.layer, s.t_v + layer_bytes * l.layer,
+                      nullptr, d.q_heads, d.kv_heads, l.w->cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
+                      POS_CONST, pos, SKIP_NEVER, e->kv_bf16, s.st, nullptr, 0, attn_chunk_len(l.w->cap), 0};
+          aa.wo = W.o;
+          aa.wo_rows = d.hidden;
+          aa.opart = s.opart;
+          hip_check(launch_attn_oproj_full(aa, d.head_dim, s.stream, lt), "launch_attn_oproj_full");
           b = 2.0 * esz * d.kv_heads * d.head_dim * (pos + 1) + 4.0 * d.qkv_rows() + 2.0 * d.hidden * d.q_out() +
               4.0 * d.kv_heads * d.hidden;
           break;

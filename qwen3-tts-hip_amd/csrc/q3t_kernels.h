@@ -38,12 +38,16 @@ hipError_t launch_attn_merge(const AttnMergeArgs &a, int rows, hipStream_t strea
 // or 2 query heads per KV head.
 hipError_t launch_attn_oproj(const AttnArgs &a, int head_dim, hipStream_t stream,
                              const LaunchTiming *timing = nullptr);
-// The O projection of one stream's split attention with its K split by KV head: a.out[h][r]
-// (a.out + h * a.N + r) = KV head h's share of (a.W * attn)[r], attn being the merge of the
-// partials a.attn_part (GemvArgs attention-merge fields; at most kAttnGemvMergeChunks
-// chunks).  a.W is [a.N][a.K] bf16 with a.K = q_heads * 128 and a.N a multiple of 32; the
-// weights are streamed.  The gate/up GEMV adds the shares to the residual (GemvArgs::parts).
-hipError_t launch_oproj_heads(const GemvArgs &a, hipStream_t stream, const LaunchTiming *timing = nullptr);
+// The Talker's decode attention (one stream) and its O projection in one launch, with the
+// projection's K split by KV head: a.opart[h][r] = KV head h's share of (a.wo * attn)[r] for
+// r < a.wo_rows, the shares the gate/up GEMV adds to the residual (GemvArgs::parts).  Every
+// workgroup runs its head's whole attention (no partials): a.cap <= 1024, position from the
+// stream state (POS_TALKER_FRAME) or the launch; a.wo_rows a multiple of
+// attn_oproj_full_rows(q_heads, kv_heads); at most 8 KV heads and 1 or 2 query heads per KV
+// head; a.kcache / a.vcache are the layer's caches of one stream.
+hipError_t launch_attn_oproj_full(const AttnArgs &a, int head_dim, hipStream_t stream,
+                                  const LaunchTiming *timing = nullptr);
+int attn_oproj_full_rows(int q_heads, int kv_heads);
 // Most attention chunks the O-projection GEMV merges itself (caches up to 8 x 128 rows); the
 // partials of a longer cache are merged by launch_attn_merge first.
 constexpr int kAttnGemvMergeChunks = 8;

@@ -542,6 +542,15 @@ struct KvIo<float> {
     o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
   }
   __device__ static float2 load2(const float *p) { return *reinterpret_cast<const float2 *>(p); }
+  // Elements 4 sub .. 4 sub + 3 and 64 + 4 sub .. 64 + 4 sub + 3 of a 128-element row: 16 lanes
+  // then read the row as two contiguous 256-byte halves; split_dim(sub, j) is element j's index.
+  __device__ static void load8_split(const float *row, int sub, float *o) {
+    const float4 a = *reinterpret_cast<const float4 *>(row + 4 * sub);
+    const float4 b = *reinterpret_cast<const float4 *>(row + 64 + 4 * sub);
+    o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+    o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+  }
+  __device__ static constexpr int split_dim(int sub, int j) { return j < 4 ? 4 * sub + j : 60 + 4 * sub + j; }
 };
 
 template <>
@@ -562,6 +571,10 @@ struct KvIo<uint16_t> {
     const uint32_t w = *reinterpret_cast<const uint32_t *>(p);
     return make_float2(bf_lo(w), bf_hi(w));
   }
+  // bf16 rows: one 16-byte load of 8 consecutive elements already covers 256 contiguous bytes
+  // per row over 16 lanes.
+  __device__ static void load8_split(const uint16_t *row, int sub, float *o) { load8(row + 8 * sub, o); }
+  __device__ static constexpr int split_dim(int sub, int j) { return 8 * sub + j; }
 };
 
 // ---------------------------------------------------------------------------------------
@@ -918,73 +931,227 @@ __device__ void merge_attention(const GemvArgs &a, float *xs) {
   }
 }
 
-// The Talker's O projection with its K split by KV head (one stream): workgroup (h, b)
-// merges the split-attention partials of KV head h's G query heads (chunk order, the same
-// arithmetic as merge_finish), then multiplies the merged head outputs by head h's G * D
-// columns of W (a.W, [N][K]) for output rows kOprojRows * b ..: out[h][r] = that share of
-// (W attn)[r].  The gate/up GEMV adds the kv_heads shares to the residual
-// (GemvArgs::parts).  Every load (partials of every chunk slot, the weight slice) is issued
-// before the stream state is read.
-template <int G>
-__global__ __launch_bounds__(256) void k_oproj_heads(GemvArgs a) {
-  constexpr int D = 128;
-  constexpr int LPR = G * D / 8;  // lanes per weight row slice
-  constexpr int RPL = 64 / LPR;   // rows per 16-byte load
-  constexpr int NWO = kOprojRows / 4 / RPL;
+// The Talker's decode attention with its O projection fused in, one stream (no partials, no
+// merge, no second launch).  Grid (kv_heads, N / ROWS), 16 waves.  Workgroup (h, b) runs KV
+// head h's whole attention over key rows [0, pos] and multiplies its G query heads' outputs by
+// head h's G * D columns of W_o for output rows ROWS * b ..: out[h][r] = that share of
+// (W_o attn)[r], summed into the residual by the gate/up GEMV (GemvArgs::parts).
+//   - Block id = h + kv_heads * b, and workgroup i runs on XCD i mod 8: with 8 KV heads every
+//     workgroup of head h is on XCD h, so the head's K/V rows come from HBM once and from
+//     that XCD's L2 for the other workgroups.
+//   - Loads before the state: the W_o slice (streamed), the q/k/v head vectors and the norm
+//     gains.  After it: the RoPE row and the first kFusedRows key rows' K and V (one round
+//     trip); longer caches take one more round trip per further kFusedRows rows.
+//   - Only b = 0 stores the K/V row at `pos`; every workgroup computes it (same arithmetic).
+//   - Scores of every row go to LDS (wave w: rows 4w + (lane >> 4) + 64 i, 16 lanes x 8 dims
+//     per row), then one softmax over all rows (wave g: query head g), then P.V (wave w: rows
+//     w + 16 i, lane: dims 2 lane, 2 lane + 1) summed over the 16 waves in wave order.
+constexpr int kFusedWaves = 16;
+constexpr int kFusedRows = 256;      // key rows per register pass
+constexpr int kFusedMaxCap = 1024;   // longest cache (score rows in LDS)
+
+template <int G, typename KVT>
+__global__ __launch_bounds__(64 * kFusedWaves) void k_attn_oproj_full(AttnArgs a) {
+  constexpr int D = 128, NW = kFusedWaves, BL = kFusedRows;
+  constexpr int KI = BL / (NW * 4);  // K rows per lane per pass
+  constexpr int VI = BL / NW;        // V rows per wave per pass
+  constexpr int LPR = G * D / 8;     // lanes per W_o row slice
+  constexpr int RPL = 64 / LPR;      // W_o rows per wave load
+  constexpr int ROWS = NW * RPL;     // W_o rows per workgroup
+  static_assert(G >= 1 && G <= 2, "query heads per KV head");
   const int h = blockIdx.x, rb = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane & 15, grp = lane >> 4;
+  const int q_out = a.q_heads * D, kv_out = a.kv_heads * D;
+  KVT *kcache = reinterpret_cast<KVT *>(a.kcache);
+  KVT *vcache = reinterpret_cast<KVT *>(a.vcache);
+  const KVT *kbase = kcache + (size_t)h * a.cap * D;
+  const KVT *vbase = vcache + (size_t)h * a.cap * D;
+
+  __shared__ float qs[G * D];
+  __shared__ __align__(16) float ks[D], vs[D];
+  __shared__ float sc[G][kFusedMaxCap];
+  __shared__ float red[NW][G][D];
+  __shared__ float stat[G][2];
   __shared__ float ao[G * D];
-  // thread t < G * D: element d of query head g of KV head h
-  const int t = threadIdx.x, g = t / D, d = t % D;
-  const bool has = t < G * D;
-  float mv[kAttnGemvMergeChunks], lv[kAttnGemvMergeChunks], av[kAttnGemvMergeChunks];
-  const float *p0 = a.attn_part + (((size_t)h * a.attn_part_chunks) * G + (has ? g : 0)) * (D + 2);
-  const size_t stride = (size_t)G * (D + 2);
-#pragma unroll
-  for (int c = 0; c < kAttnGemvMergeChunks; ++c) {
-    const float *pc = p0 + min(c, a.attn_part_chunks - 1) * stride;
-    mv[c] = pc[0];
-    lv[c] = pc[1];
-    av[c] = pc[2 + d];
-  }
-  uint4 wo[NWO];
-#pragma unroll
-  for (int i = 0; i < NWO; ++i) {
-    const int r = rb * kOprojRows + wave * (kOprojRows / 4) + i * RPL + lane / LPR;
-    wo[i] = load_w<true>(reinterpret_cast<const u32x4 *>(a.W + (size_t)r * a.K + h * G * D + (lane % LPR) * 8));
+
+  // 1. Everything that does not depend on the position.
+  const int orow = rb * ROWS + wave * RPL + lane / LPR;
+  const uint4 wo = load_w<true>(reinterpret_cast<const u32x4 *>(a.wo + (size_t)orow * q_out + h * G * D +
+                                                                  (lane % LPR) * 8));
+  const int vec = wave;  // waves 0..G-1: q heads; G: k; G+1: v
+  const bool has_vec = wave < G + 2;
+  const float *gain = vec < G ? a.gq : (vec == G ? a.gk : nullptr);
+  const int vec_off = vec < G ? (h * G + vec) * D : (vec == G ? q_out + h * D : q_out + kv_out + h * D);
+  float x0 = 0.f, x1 = 0.f, g0 = 0.f, g1 = 0.f;
+  if (has_vec) {
+    x0 = a.qkv[vec_off + lane];
+    x1 = a.qkv[vec_off + lane + 64];
+    if (gain) {
+      g0 = gain[lane];
+      g1 = gain[lane + 64];
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
-  if (skip_work(a.st, a.skip)) return;
-  const int pos = (a.attn_pos_mode == POS_TALKER_FRAME) ? a.st->prefill_steps + a.st->frame : a.attn_pos_const;
-  const int nchunks = (pos + a.attn_chunk) / a.attn_chunk;  // ceil((pos + 1) / chunk)
-  if (has) {
-    float M = -FLT_MAX;
+
+  // 2. The position (stream state, or the launch's), then the first pass's K/V rows.
+  int pos = a.pos_const;
+  if (a.pos_mode == POS_TALKER_FRAME) {
+    const SlotState sv = *a.st;
+    if (skip_state(sv, a.skip)) return;
+    pos = sv.prefill_steps + sv.frame;
+  } else if (skip_work(a.st, a.skip)) {
+    return;
+  }
+  if (pos < 0 || pos >= a.cap) return;  // host validates; never index outside the cache
+  const int L = pos + 1;
+  const int tmax = max(pos - 1, 0);
+  float2 cs = make_float2(0.f, 0.f);
+  if (has_vec && gain) cs = a.rope[(size_t)pos * (D / 2) + lane];
+  // fp32 caches: only the row groups that hold rows below L are loaded (wave-uniform tests):
+  // every load instruction costs the CU the same load-path time, used or not, and a short
+  // cache needs a fraction of them.  bf16 caches load every group (clamped): there the tests
+  // measured slower from half the cache on.  Each lane of an fp32 K row takes dims 4 sub ..
+  // 4 sub + 3 and 64 + 4 sub .. (KvIo::load8_split), so one instruction covers 256
+  // contiguous bytes per row.
+  constexpr bool GUARD = sizeof(KVT) == 4;
+  float kreg[KI][8];
+  float2 vreg[VI];
+  auto load_k = [&](int p0) {
 #pragma unroll
-    for (int c = 0; c < kAttnGemvMergeChunks; ++c)
-      if (c < nchunks) M = fmaxf(M, mv[c]);
-    float den = 0.f, num = 0.f;
+    for (int i = 0; i < KI; ++i) {
+      if (GUARD && p0 + wave * 4 + 64 * i >= L) break;
+      const int t = min(p0 + wave * 4 + grp + 64 * i, tmax);
+      KvIo<KVT>::load8_split(kbase + (size_t)t * D, sub, kreg[i]);
+    }
+  };
+  auto load_v = [&](int p0) {
 #pragma unroll
-    for (int c = 0; c < kAttnGemvMergeChunks; ++c)
-      if (c < nchunks) {
-        const float w = expf(mv[c] - M);
-        den = fmaf(w, lv[c], den);
-        num = fmaf(w, av[c], num);
+    for (int i = 0; i < VI; ++i) {
+      if (GUARD && p0 + wave + NW * i >= L) break;
+      const int t = min(p0 + wave + NW * i, tmax);
+      vreg[i] = KvIo<KVT>::load2(vbase + (size_t)t * D + 2 * lane);
+    }
+  };
+  load_k(0);
+  load_v(0);
+
+  // 3. q heads (waves 0..G-1), k and v (waves G, G+1): norm, RoPE, the row at `pos`.
+  if (has_vec) {
+    if (gain) {
+      const float ss = wave_sum(fmaf(x0, x0, x1 * x1));
+      const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+      x0 = (x0 * inv) * g0;
+      x1 = (x1 * inv) * g1;
+      const float r0 = x0 * cs.x - x1 * cs.y;
+      const float r1 = x1 * cs.x + x0 * cs.y;
+      x0 = r0;
+      x1 = r1;
+    }
+    if (vec < G) {
+      qs[vec * D + lane] = x0;
+      qs[vec * D + lane + 64] = x1;
+    } else {
+      KVT *cache = (vec == G) ? kcache : vcache;
+      float *keep = (vec == G) ? ks : vs;
+      const size_t r = ((size_t)h * a.cap + pos) * D;
+      if (rb == 0) {
+        keep[lane] = KvIo<KVT>::store(cache + r + lane, x0);
+        keep[lane + 64] = KvIo<KVT>::store(cache + r + lane + 64, x1);
+      } else {
+        keep[lane] = KvIo<KVT>::round(x0);
+        keep[lane + 64] = KvIo<KVT>::round(x1);
       }
-    ao[t] = num / den;
+    }
   }
   __syncthreads();
-  // the rows' sums first, then the stores (one basic block: the chains interleave)
-  float sum[NWO];
-#pragma unroll
-  for (int i = 0; i < NWO; ++i) {
-    sum[i] = row16_sum(dot8(wo[i], ao + (lane % LPR) * 8));
-    if constexpr (LPR == 32) sum[i] += dpp_f<0x142, 0xa>(sum[i], 0.f);
+
+  // 4. Scores of every row [0, L) (the dims of load8_split).
+  float kown[8];
+  {
+    const float4 a0 = *reinterpret_cast<const float4 *>(&ks[KvIo<KVT>::split_dim(sub, 0)]);
+    const float4 a1 = *reinterpret_cast<const float4 *>(&ks[KvIo<KVT>::split_dim(sub, 4)]);
+    kown[0] = a0.x; kown[1] = a0.y; kown[2] = a0.z; kown[3] = a0.w;
+    kown[4] = a1.x; kown[5] = a1.y; kown[6] = a1.z; kown[7] = a1.w;
   }
-  if (lane % LPR == LPR - 1) {
+  for (int p0 = 0; p0 < L; p0 += BL) {
+    if (p0 > 0) load_k(p0);
 #pragma unroll
-    for (int i = 0; i < NWO; ++i)
-      a.out[(size_t)h * a.N + rb * kOprojRows + wave * (kOprojRows / 4) + i * RPL + lane / LPR] = sum[i];
+    for (int i = 0; i < KI; ++i) {
+      const int t = p0 + wave * 4 + grp + 64 * i;
+      if (p0 + wave * 4 + 64 * i >= L) break;  // wave-uniform
+      float kv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) kv[j] = (t < pos) ? kreg[i][j] : ((t == pos) ? kown[j] : 0.f);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float sacc = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sacc = fmaf(qs[g * D + KvIo<KVT>::split_dim(sub, j)], kv[j], sacc);
+        sacc = row16_sum(sacc);
+        if (sub == 0 && t < L) sc[g][t] = sacc * a.scale;
+      }
+    }
   }
+  __syncthreads();
+
+  // 5. Softmax over all rows (wave g: query head g).
+  if (wave < G) {
+    float m = -FLT_MAX;
+    for (int i = lane; i < L; i += 64) m = fmaxf(m, sc[wave][i]);
+    m = wave_max(m);
+    float l = 0.f;
+    for (int i = lane; i < L; i += 64) {
+      const float p = expf(sc[wave][i] - m);
+      sc[wave][i] = p;
+      l += p;
+    }
+    l = wave_sum(l);
+    if (lane == 0) {
+      stat[wave][0] = m;
+      stat[wave][1] = l;
+    }
+  }
+  __syncthreads();
+
+  // 6. P.V, per wave, then the 16 waves' sums in wave order.
+  float acc[G][2];
+#pragma unroll
+  for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.f;
+  for (int p0 = 0; p0 < L; p0 += BL) {
+    if (p0 > 0) load_v(p0);
+#pragma unroll
+    for (int i = 0; i < VI; ++i) {
+      const int t = p0 + wave + NW * i;
+      if (t >= L) break;  // wave-uniform
+      const float2 v = (t < pos) ? vreg[i] : make_float2(vs[2 * lane], vs[2 * lane + 1]);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float p = sc[g][t];
+        acc[g][0] = fmaf(p, v.x, acc[g][0]);
+        acc[g][1] = fmaf(p, v.y, acc[g][1]);
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    red[wave][g][2 * lane] = acc[g][0];
+    red[wave][g][2 * lane + 1] = acc[g][1];
+  }
+  __syncthreads();
+  if (threadIdx.x < G * D) {
+    const int g_o = threadIdx.x / D, d_o = threadIdx.x % D;
+    float v_o = red[0][g_o][d_o];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v_o += red[w][g_o][d_o];
+    ao[threadIdx.x] = v_o / stat[g_o][1];
+  }
+  __syncthreads();
+
+  // 7. This workgroup's rows of head h's share of W_o attn.
+  float sum = row16_sum(dot8(wo, ao + (lane % LPR) * 8));
+  if constexpr (LPR == 32) sum += dpp_f<0x142, 0xa>(sum, 0.f);
+  if (lane % LPR == LPR - 1) a.opart[(size_t)h * a.wo_rows + orow] = sum;
 }
 
 // Stream-row form of merge_attention for the batched frame: workgroup (h, r) merges KV head
@@ -2873,20 +3040,30 @@ hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t s, co
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_oproj_heads(const GemvArgs &a, hipStream_t s, const LaunchTiming *t) {
-  constexpr int D = 128;
-  if (!a.W || !a.out || !a.attn_part || !a.st || a.attn_kv_heads <= 0 || a.attn_kv_heads > kMaxParts ||
-      a.attn_q_heads % a.attn_kv_heads || a.K != a.attn_q_heads * D || a.N <= 0 || a.N % kOprojRows ||
-      a.attn_part_chunks < 1 || a.attn_part_chunks > kAttnGemvMergeChunks || a.attn_chunk <= 0 ||
-      (a.attn_pos_mode != POS_TALKER_FRAME && a.attn_pos_mode != POS_CONST))
+hipError_t launch_attn_oproj_full(const AttnArgs &a, int head_dim, hipStream_t s, const LaunchTiming *t) {
+  if (head_dim != 128 || a.kv_heads <= 0 || a.kv_heads > kMaxParts || a.q_heads % a.kv_heads) return hipErrorInvalidValue;
+  const int G = a.q_heads / a.kv_heads;
+  const int rows = kFusedWaves * (64 / (G * 16));  // W_o rows per workgroup
+  if (G < 1 || G > 2 || a.cap < 1 || a.cap > kFusedMaxCap || a.row_on || a.h.keys || a.h.tok_in ||
+      (a.pos_mode != POS_TALKER_FRAME && a.pos_mode != POS_CONST) || !a.wo || !a.opart || !a.st ||
+      a.wo_rows <= 0 || a.wo_rows % rows)
     return hipErrorInvalidValue;
-  const int G = a.attn_q_heads / a.attn_kv_heads;
-  const dim3 grid(a.attn_kv_heads, a.N / kOprojRows);
-  if (G == 1) launch_timed(k_oproj_heads<1>, grid, dim3(256), 0, s, t, a);
-  else if (G == 2) launch_timed(k_oproj_heads<2>, grid, dim3(256), 0, s, t, a);
-  else return hipErrorInvalidValue;
+  const dim3 grid(a.kv_heads, a.wo_rows / rows, 1), block(64 * kFusedWaves);
+  if (a.kv_bf16) {
+    if (G == 1) launch_timed(k_attn_oproj_full<1, uint16_t>, grid, block, 0, s, t, a);
+    else launch_timed(k_attn_oproj_full<2, uint16_t>, grid, block, 0, s, t, a);
+  } else {
+    if (G == 1) launch_timed(k_attn_oproj_full<1, float>, grid, block, 0, s, t, a);
+    else launch_timed(k_attn_oproj_full<2, float>, grid, block, 0, s, t, a);
+  }
   return hipGetLastError();
 }
+
+int attn_oproj_full_rows(int q_heads, int kv_heads) {
+  const int G = kv_heads > 0 ? q_heads / kv_heads : 0;
+  return (G == 1 || G == 2) ? kFusedWaves * (64 / (G * 16)) : 0;
+}
+
 
 hipError_t launch_attn_oproj(const AttnArgs &a, int head_dim, hipStream_t s, const LaunchTiming *t) {
   if (head_dim != 128 || a.kv_heads <= 0 || a.q_heads % a.kv_heads || a.kv_heads > kMaxParts) return hipErrorInvalidValue;

@@ -472,7 +472,8 @@ class HipTtsEngine:
 
     KERNELS = {0: "gemv_qkv_rmsnorm", 1: "gemv_o_residual", 2: "gemv_gate_up_swiglu", 3: "gemv_down_residual",
                4: "attention_decode_full_cache", 5: "attention_codepredictor", 6: "select_cp_greedy",
-               7: "attention_talker_half_cache", 8: "gemv_lm_head", 9: "attention_oproj_codepredictor"}
+               7: "attention_talker_half_cache", 8: "gemv_lm_head", 9: "attention_oproj_codepredictor",
+               10: "attention_oproj_talker_half_cache"}
 
     def bench_kernel(self, kernel: int, iters: int = 1030):
         """(average launch microseconds, algorithmic bytes per launch) of one kernel class."""

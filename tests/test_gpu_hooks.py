@@ -108,4 +108,4 @@ def test_kernel_timing_hook_covers_every_class(models):
         _, b2 = eng.bench_kernel(2, 103)
         assert b2 > 2 * 2 * 3072 * 1024
         with pytest.raises(E.Q3tError):
-            eng.bench_kernel(10, 8)
+            eng.bench_kernel(11, 8)
