@@ -1777,6 +1777,10 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
     __builtin_amdgcn_sched_barrier(0);
 
     if constexpr (NORM) {  // single pass: this wave holds its whole k range of every row
+      // RMSNorm(x) W^T = r (x * g) W^T with r = 1 / rms(x) one scalar per row: the products
+      // take x * g, and r multiplies the sums in the epilogue.  Each wave leaves its rows'
+      // sums of squares in ssq; the reduction's barrier then covers them too, so no wave
+      // waits for the others' activation loads before its matrix-core work.
 #pragma unroll
       for (int b = 0; b < MB; ++b) {
         float ss = 0.f;
@@ -1787,20 +1791,10 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
         ss = pair16_sum(ss);  // the four lanes of a row (kb = 0..3)
         ss = pair32_sum(ss);
         if (kb == 0) ssq[wave][b * 16 + li] = ss;
-      }
-      __syncthreads();
-      // every lane sums its row's 16 wave shares itself (the same order for all): one
-      // barrier instead of a second one behind 16 threads
-#pragma unroll
-      for (int b = 0; b < MB; ++b) {
-        float tot = 0.f;
-#pragma unroll
-        for (int w = 0; w < 16; ++w) tot += ssq[w][b * 16 + li];
-        const float r = 1.0f / sqrtf(tot / (float)a.K + a.eps);
 #pragma unroll
         for (int st = 0; st < KP; ++st)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) xa[b][st][e] = (xa[b][st][e] * r) * ga[st][e];
+          for (int e = 0; e < 8; ++e) xa[b][st][e] = xa[b][st][e] * ga[st][e];
       }
     }
 
@@ -1835,6 +1829,14 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
 #pragma unroll
     for (int w = 1; w < 16; ++w) sacc += part[w][ob * T + t][ol][oe];
     v[t] = sacc;
+  }
+  if constexpr (NORM) {  // the row's 1 / rms from the 16 waves' sums of squares, in wave order
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < 16; ++w) tot += ssq[w][ob * 16 + cm];
+    const float r = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+#pragma unroll
+    for (int t = 0; t < T; ++t) v[t] *= r;
   }
   if constexpr (KEYS) {
     // The 16 columns of row om sit in lanes oe + 4c (c = 0..15) of one wave: their largest
