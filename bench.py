@@ -13,6 +13,8 @@ Prints one JSON line.  Besides the contract fields it carries:
   frame_algorithmic_GBps         bytes one frame must move (weights + KV) / frame time
   roofline                       the dominant kernel, timed live with HIP events
   per_step                       Talker-step and CodePredictor-pass rooflines (phases timed as graphs)
+  kv_bf16, per_step_kv_bf16      the headline workload again on the bf16 KV cache: frames/s, per-step
+                                 rooflines (bf16 KV bytes), leading frames equal to the fp32 run's codes
   multistream                    BASELINE config 5 (16 streams together) on the same model, with
                                  the batched frame's roofline
   multistream_kv_bf16            the same on the bf16 KV cache
@@ -228,10 +230,17 @@ def multistream(eng_cls, model_dir: str, name: str, steps: int, warmup: int, use
     # workload); a live stream at prefill P reads P + f + 2 Talker KV rows (P + f + 1 read, 1
     # written) and its CodePredictor rows
     n_batched = max(budgets)
-    kv = sum(sum(kv_t * (9 + n + f + 2) for f in range(fr - 1)) + fr * cp_kv for n, fr in zip(lengths, budgets))
+
+    def kv_bytes(kv_t, cp_kv):
+        return sum(sum(kv_t * (9 + n + f + 2) for f in range(fr - 1)) + fr * cp_kv for n, fr in zip(lengths, budgets))
+    kv = kv_bytes(kv_t, cp_kv)
     alg_bytes = n_batched * weights + kv
     decode_s = (el - prefill_s) / steps
     gbps = alg_bytes / decode_s / 1e9
+    # the per-frame algorithmic-byte definition counts KV rows at bf16 width whatever the cache type
+    _, _, kv_t2, kv_c2 = step_bytes(spec, 2)
+    alg_bytes_8d = n_batched * weights + kv_bytes(kv_t2, kv_c2 * (sum(range(2, groups + 2)) + 2))
+    gbps_8d = alg_bytes_8d / decode_s / 1e9
     return {"workload": name, "streams": w.streams, "value": round(frames / el, 2), "unit": "frames/s (all streams)",
             "steps": steps, "warmup": warmup, "ms_per_step": round(1000 * el / steps, 3),
             "frames_per_step": frames // steps, "prefill_rows": sum(9 + n for n in lengths),
@@ -243,8 +252,12 @@ def multistream(eng_cls, model_dir: str, name: str, steps: int, warmup: int, use
                          "frac": round(gbps / HBM_PEAK_GBPS, 4), "batched_frames": n_batched,
                          "algorithmic_bytes_per_step": int(alg_bytes),
                          "batched_frame_ms": round(1000 * decode_s / n_batched, 4),
-                         "note": "every weight once per batched frame + each live stream's KV rows, over "
-                                 "the step time without the prefill"}}
+                         "kv_bytes_counted": "bf16" if kv_bf16 else "fp32",
+                         "frac_bf16_kv_bytes": round(gbps_8d / HBM_PEAK_GBPS, 4),
+                         "note": "every weight once per batched frame + each live stream's KV rows at the "
+                                 "cache's own width (frac) or at bf16 width, the width of the per-frame "
+                                 "byte definition (frac_bf16_kv_bytes), over the step time without the "
+                                 "prefill"}}
 
 
 def big_model_line(E, synth, w, use_graph: bool) -> dict:
@@ -284,6 +297,67 @@ def big_model_line(E, synth, w, use_graph: bool) -> dict:
             "rtf": round(el / (n * FRAME_SECONDS), 5), "frame_ms": round(1000 * el / n, 4),
             "frame_algorithmic_GBps": round(fb / (el / n) / 1e9, 1), "prefill_steps": inputs.prefill_steps,
             "kv_capacity": w.max_cache_steps, "per_step": steps}
+
+
+def batch1_kv_bf16(E, model_dir, w, inputs, opts, spec, P, args, fp32_codes) -> dict:
+    """The headline workload on a bf16 KV cache (engine option kv_dtype = 1): frames/s over the
+    same steps after one warmup, the per-step rooflines with bf16 KV bytes, and how many
+    leading frames equal the fp32-cache run's codes (the bf16 cache rounds K/V once at the
+    store, so greedy codes part from the fp32 run after some frames)."""
+    import numpy as np
+    eng = E.HipTtsEngine(model_dir, E.EngineOptions(max_cache_steps=w.max_cache_steps, use_graph=not args.eager,
+                                                    kv_bf16=True))
+    codes = []
+
+    def one():
+        with eng.start_stream(inputs, opts) as st:
+            got = []
+            while (c := st.next_codes_chunk(w.chunk_frames)) is not None:
+                got.append(c.codes)
+        codes[:] = got
+        return sum(g.shape[0] for g in got)
+    for _ in range(args.warmup):
+        one()
+    eng.synchronize()
+    t0 = time.perf_counter()
+    frames = 0
+    for _ in range(args.steps):
+        frames += one()
+    eng.synchronize()
+    el = time.perf_counter() - t0
+    with eng.start_stream(inputs, opts) as st:
+        steps_line = per_step(st, spec, P, w.chunk_frames, 2)
+    eng.close()
+    a, b = np.concatenate(codes), np.concatenate(fp32_codes)
+    n = min(len(a), len(b))
+    same = np.all(a[:n] == b[:n], axis=1)
+    lead = int(n if same.all() else np.argmin(same))
+    frame_s = el / frames
+    fb = frame_bytes(spec, P + (frames / max(args.steps, 1) - 1) / 2.0, 2)
+    return {"kv_cache": "bf16", "value": round(frames / el, 2), "unit": "frames/s", "steps": args.steps,
+            "rtf": round(frame_s / FRAME_SECONDS, 5), "frame_ms": round(1000 * frame_s, 4),
+            "frame_algorithmic_GBps": round(fb / frame_s / 1e9, 1),
+            "frames_equal_to_fp32_cache_codes": lead, "frames_per_step": frames // max(args.steps, 1),
+            "per_step_kv_bf16": steps_line}
+
+
+def copy_calibration(nbytes: int = 256 << 20) -> int:
+    """One device-to-device copy of `nbytes` through the HIP runtime (its copy kernel), the
+    known-size reference for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE counters.  No torch
+    import, no engine: the copy is the only kernel of the process."""
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so")
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    n = ctypes.c_size_t(nbytes)
+    for rc in (hip.hipMalloc(ctypes.byref(a), n), hip.hipMalloc(ctypes.byref(b), n), hip.hipMemset(a, 1, n),
+               hip.hipMemcpy(b, a, n, 3), hip.hipDeviceSynchronize()):  # 3 = hipMemcpyDeviceToDevice
+        if rc != 0:
+            print(json.dumps({"copy_calibration": "failed", "hip_error": rc}))
+            return 1
+    hip.hipFree(a)
+    hip.hipFree(b)
+    print(json.dumps({"copy_calibration_bytes": nbytes, "kernel": "the runtime's device-to-device copy"}))
+    return 0
 
 
 def codec_decode_only(E, synth, frames: int, steps: int) -> int:
@@ -335,9 +409,15 @@ def main() -> int:
                          "traces for profiles/) and exit")
     ap.add_argument("--no-multistream-bf16", action="store_true",
                     help="skip the config-5 run on the bf16 KV cache")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy 256 MiB device to device (the PMC traffic counters' calibration) and exit")
+    ap.add_argument("--no-kv-bf16", action="store_true",
+                    help="skip the headline workload's second run on the bf16 KV cache")
     ap.add_argument("--kernel-classes", action="store_true",
                     help="graph-time every kernel class of q3t_bench_kernel on the workload's model and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "streams shard across GPUs by data parallelism with no exchange step, so N GPUs = N x one GPU.",
@@ -447,6 +527,9 @@ def main() -> int:
     roofline["traffic"] = measured_traffic(w.name, roofline["kernel"])
     with eng.start_stream(inputs, opts) as st_steps:
         steps_line = per_step(st_steps, spec, P, w.chunk_frames, 2 if args.kv_bf16 else 4)
+    kv_bf16_line = None
+    if not args.kv_bf16 and not args.no_kv_bf16:
+        kv_bf16_line = batch1_kv_bf16(E, tmp, w, inputs, opts, spec, P, args, last_codes)
     text_prep = None
     if with_text:
         # Prompt preparation of the same prompt on the device (q3t_prepare_text, host copies
@@ -553,6 +636,9 @@ def main() -> int:
         "roofline": roofline,
         "per_step": steps_line,
     }
+    if kv_bf16_line is not None:
+        out["kv_bf16"] = kv_bf16_line
+        out["per_step_kv_bf16"] = kv_bf16_line["per_step_kv_bf16"]
     if multi is not None:
         out["multistream"] = multi
     if multi_bf16 is not None:

@@ -323,7 +323,9 @@ int q3t_engine_synchronize(q3t_engine *engine);
  * Class 1 is the O GEMV merging split-attention partials (Talker layers); a Talker with
  * the fused attention + O projection (the 0.6B's) runs class 10 in frames instead.  Class 2
  * (gate/up) sums the per-head shares of the Talker's and the CodePredictor's fused
- * projections as frames do. Slot 0 must not hold a stream. */
+ * projections as frames do. Slot 0 must not hold a stream.  An engine created with
+ * use_graph = 0 captures no graph anywhere: there this call fails with Q3T_ERR_INVALID (the
+ * timed variant below launches eagerly). */
 int q3t_bench_kernel(q3t_engine *engine, int32_t kernel, int32_t iters, double *avg_us,
                      double *bytes_per_launch);
 

@@ -139,31 +139,51 @@ class CodecOracle:
         n = rmsnorm(h, t[f"{p}.norm.weight"], 1e-5)
         return n @ t[f"{p}.output_proj.weight"].T + t[f"{p}.output_proj.bias"]
 
+    def convnext(self, y: np.ndarray, i: int) -> np.ndarray:
+        """The ConvNeXt block of upsample stage i on the transposed conv's output y
+        (codec_hip.rs:700-800): depthwise causal conv k 7, LayerNorm eps 1e-6, pointwise 4C +
+        GELU(erf), pointwise back to C, times gamma, plus y."""
+        t, p = self.t, f"decoder.upsample.{i}.1"
+        dw = y.shape[1]
+        w = t[f"{p}.dwconv.conv.weight"][:, 0, :]               # [C, 7]
+        yp = np.concatenate([np.zeros((6, dw)), y], axis=0)
+        d = t[f"{p}.dwconv.conv.bias"] + sum(yp[j:j + y.shape[0]] * w[:, j] for j in range(7))
+        n = layernorm(d, t[f"{p}.norm.weight"], t[f"{p}.norm.bias"], 1e-6)
+        a = gelu(n @ t[f"{p}.pwconv1.weight"].T + t[f"{p}.pwconv1.bias"])
+        u = a @ t[f"{p}.pwconv2.weight"].T + t[f"{p}.pwconv2.bias"]
+        return y + u * t[f"{p}.gamma"]
+
     def upsample(self, x: np.ndarray, i: int) -> np.ndarray:
+        """Upsample stage i (codec_hip.rs:656-800): transposed conv k = stride = 2, then the
+        ConvNeXt block."""
         t, p = self.t, f"decoder.upsample.{i}"
         y = transposed_conv(x, t[f"{p}.0.conv.weight"], t[f"{p}.0.conv.bias"], 2)
-        dw = y.shape[1]
-        w = t[f"{p}.1.dwconv.conv.weight"][:, 0, :]               # [C, 7]
-        yp = np.concatenate([np.zeros((6, dw)), y], axis=0)
-        d = t[f"{p}.1.dwconv.conv.bias"] + sum(yp[j:j + y.shape[0]] * w[:, j] for j in range(7))
-        n = layernorm(d, t[f"{p}.1.norm.weight"], t[f"{p}.1.norm.bias"], 1e-6)
-        a = gelu(n @ t[f"{p}.1.pwconv1.weight"].T + t[f"{p}.1.pwconv1.bias"])
-        u = a @ t[f"{p}.1.pwconv2.weight"].T + t[f"{p}.1.pwconv2.bias"]
-        return y + u * t[f"{p}.1.gamma"]
+        return self.convnext(y, i)
+
+    def residual_unit(self, h: np.ndarray, b: int, u: int) -> np.ndarray:
+        """Residual unit u (dilation 1, 3, 9) of decoder block b (codec_hip.rs:1253-1368):
+        h + conv k 1(Snake(conv k 7, dilated(Snake(h))))."""
+        t, r, dil = self.t, f"decoder.decoder.{b + 1}.block.{u + 2}", (1, 3, 9)[u]
+        a = snake(h, t[f"{r}.act1.alpha"], t[f"{r}.act1.beta"])
+        a = causal_conv(a, t[f"{r}.conv1.conv.weight"], t[f"{r}.conv1.conv.bias"], dil)
+        a = snake(a, t[f"{r}.act2.alpha"], t[f"{r}.act2.beta"])
+        return h + causal_conv(a, t[f"{r}.conv2.conv.weight"], t[f"{r}.conv2.conv.bias"])
+
+    def decoder_block(self, h: np.ndarray, b: int) -> np.ndarray:
+        """Decoder block b (codec_hip.rs:802-1072): Snake, the right-trimmed transposed conv
+        (kernel 2 x stride), then the three residual units."""
+        t, p = self.t, f"decoder.decoder.{b + 1}.block"
+        h = snake(h, t[f"{p}.0.alpha"], t[f"{p}.0.beta"])
+        h = transposed_conv(h, t[f"{p}.1.conv.weight"], t[f"{p}.1.conv.bias"], BLOCKS[b][2])
+        for u in range(3):
+            h = self.residual_unit(h, b, u)
+        return h
 
     def decoder(self, x: np.ndarray) -> np.ndarray:
         t = self.t
         h = causal_conv(x, t["decoder.decoder.0.conv.weight"], t["decoder.decoder.0.conv.bias"])
-        for b, (_, _, stride) in enumerate(BLOCKS):
-            p = f"decoder.decoder.{b + 1}.block"
-            h = snake(h, t[f"{p}.0.alpha"], t[f"{p}.0.beta"])
-            h = transposed_conv(h, t[f"{p}.1.conv.weight"], t[f"{p}.1.conv.bias"], stride)
-            for u, dil in enumerate((1, 3, 9)):
-                r = f"{p}.{u + 2}"
-                a = snake(h, t[f"{r}.act1.alpha"], t[f"{r}.act1.beta"])
-                a = causal_conv(a, t[f"{r}.conv1.conv.weight"], t[f"{r}.conv1.conv.bias"], dil)
-                a = snake(a, t[f"{r}.act2.alpha"], t[f"{r}.act2.beta"])
-                h = h + causal_conv(a, t[f"{r}.conv2.conv.weight"], t[f"{r}.conv2.conv.bias"])
+        for b in range(len(BLOCKS)):
+            h = self.decoder_block(h, b)
         h = snake(h, t["decoder.decoder.5.alpha"], t["decoder.decoder.5.beta"])
         return causal_conv(h, t["decoder.decoder.6.conv.weight"], t["decoder.decoder.6.conv.bias"])[:, 0]
 

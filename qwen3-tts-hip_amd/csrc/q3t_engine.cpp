@@ -2557,6 +2557,9 @@ int bench_kernel_impl(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_
       HIPC(hipMemcpy(s.prm, &pr, sizeof pr, hipMemcpyHostToDevice));
     }
     if (timed && kernel == 6) fail(Q3T_ERR_INVALID, "kernel class 6 has no timed launch");
+    if (!timed && !e->use_graph)
+      fail(Q3T_ERR_INVALID, "the engine runs without graphs (use_graph = 0); q3t_bench_kernel captures one: "
+                            "use q3t_bench_kernel_timed");
     double total_bytes = 0.0;
     const LaunchTiming *lt = nullptr;  // set per launch in the timed mode
     auto enqueue = [&](int i, bool count) {

@@ -109,3 +109,17 @@ def test_kernel_timing_hook_covers_every_class(models):
         assert b2 > 2 * 2 * 3072 * 1024
         with pytest.raises(E.Q3tError):
             eng.bench_kernel(11, 8)
+
+
+def test_eager_engine_captures_no_graph(models):
+    """An engine created with use_graph = False (the form profiled under a kernel tracer)
+    refuses the graph-timed kernel hook and still runs the eagerly timed one."""
+    w = WORKLOADS["cfg2_0.6b_greedy"]
+    _, d = models.get(w.spec, w.weight_seed)
+    with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=w.max_cache_steps, use_graph=False)) as eng:
+        with pytest.raises(E.InvalidInputError, match="without graphs"):
+            eng.bench_kernel(2, 8)
+        us, b = eng.bench_kernel_timed(2, 8)
+        assert us > 0 and b > 0
+        r = eng.dominant_kernel_roofline(8000.0, iters=8, graph=False)
+        assert r["graph_us_per_launch"] is None and r["avg_launch_us"] > 0
