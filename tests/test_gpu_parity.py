@@ -236,6 +236,38 @@ def test_eos_ends_stream_like_the_reference(models, tmp_path):
     assert r["eos"] and r["chunks"][-1].ended_by_eos
 
 
+@pytest.mark.parametrize("spec,n_ids,cap,frames,kv_bf16", [
+    ("tiny", 291, 512, 8, False),      # positions 300-307: two 256-row passes
+    ("tiny", 240, 320, 16, False),     # positions 249-264: the second pass starts mid-stream
+    ("tiny-g1", 240, 320, 16, False),  # one query head per KV head
+    ("tiny", 1000, 1024, 10, False),   # positions 1009-1018: four passes, the longest cache
+    ("tiny", 291, 512, 8, True),       # bf16 cache (every row group loaded)
+])
+def test_fused_talker_attention_long_caches_match_oracle(models, spec, n_ids, cap, frames, kv_bf16):
+    """The Talker's fused attention + O projection (hidden 512 / 1024, caches of 33 .. 1024
+    rows) runs its key rows in passes of 256: caches past one pass, across the pass boundary,
+    and at the 1024-row limit, against the oracle's rollout of the same prompt."""
+    model, d = models.get(spec)
+    prompt = np.random.default_rng(n_ids + cap).integers(0, 151643, n_ids)
+    from q3t import textprep
+    inputs = textprep.TextPrep(model).prepare(prompt)
+    assert inputs.prefill_steps == n_ids + 9
+    opts = E.GenerateOptions.greedy(frames)
+    print(f"[gpu] fused attention spec={spec} P={inputs.prefill_steps} cap={cap} kv_bf16={kv_bf16}", flush=True)
+    with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=cap, kv_bf16=kv_bf16)) as eng:
+        eng.set_trace(True)
+        with eng.start_stream(inputs, opts) as st:
+            chunks = []
+            while (c := st.next_codes_chunk(4)) is not None:
+                chunks.append(c)
+            tl, eos = st.talker_logits(), st.ended_by_eos
+    codes = np.concatenate([c.codes for c in chunks])
+    fx = _as_fixture(_oracle_rollout(model, inputs, opts, cap, kv_bf16=kv_bf16))
+    same = (check_codes_near_tie if kv_bf16 else check_codes)(codes, eos, fx)
+    err = check_talker_logits(tl, fx, same)
+    print(f"{spec} P={inputs.prefill_steps} cap={cap}: {same} frames identical, talker logit err {err:.2e}")
+
+
 def test_cache_past_1024_rows_matches_oracle(models):
     """A 1,109-row prompt in a 1,152-row cache: the Talker's attention spans 9 chunks of 128
     rows, more than the O projection merges itself, so the merge kernel runs first."""
