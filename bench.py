@@ -46,8 +46,11 @@ def frame_bytes(spec, active_steps_mean: float, kv_elem: int) -> float:
     t, c = spec.talker, spec.code_predictor
 
     def stack_params(s):
+        # per layer: q/k/v, o, gate/up and down matrices, plus the four norm gains (input,
+        # post-attention, q head, k head)
         q, kv = s.q_heads * s.head_dim, s.kv_heads * s.head_dim
-        return s.layers * ((q + 2 * kv) * s.hidden + s.hidden * q + 3 * s.intermediate * s.hidden)
+        return s.layers * ((q + 2 * kv) * s.hidden + s.hidden * q + 3 * s.intermediate * s.hidden +
+                           2 * s.hidden + 2 * s.head_dim)
 
     talker = 2 * (stack_params(t) + t.vocab * t.hidden + t.hidden)
     proj = c.hidden * t.hidden if spec.has_projection else 0
@@ -66,8 +69,11 @@ def step_bytes(spec, kv_elem: int):
     t, c = spec.talker, spec.code_predictor
 
     def stack_params(s):
+        # per layer: q/k/v, o, gate/up and down matrices, plus the four norm gains (input,
+        # post-attention, q head, k head)
         q, kv = s.q_heads * s.head_dim, s.kv_heads * s.head_dim
-        return s.layers * ((q + 2 * kv) * s.hidden + s.hidden * q + 3 * s.intermediate * s.hidden)
+        return s.layers * ((q + 2 * kv) * s.hidden + s.hidden * q + 3 * s.intermediate * s.hidden +
+                           2 * s.hidden + 2 * s.head_dim)
 
     talker = 2 * (stack_params(t) + t.vocab * t.hidden + t.hidden)
     proj = c.hidden * t.hidden if spec.has_projection else 0
@@ -75,6 +81,21 @@ def step_bytes(spec, kv_elem: int):
     kv_t = t.layers * 2 * t.kv_heads * t.head_dim * kv_elem
     kv_c = c.layers * 2 * c.kv_heads * c.head_dim * kv_elem
     return talker, cp_pass, kv_t, kv_c
+
+
+def batched_bytes(spec, prefill_steps, frames, kv_elem: int) -> int:
+    """Algorithmic bytes of a multi-stream generation run as batched frames: every weight once
+    per batched frame (as many batched frames as the longest stream has frames), plus each
+    live stream's KV rows.  In batched frame f a stream with more than f frames is live (no
+    EOS); at prefill P it runs the Talker step after frame f at position P + f, which reads
+    P + f + 1 rows and writes one (none after its last frame), and its frame's CodePredictor
+    passes.  kv_elem: bytes per cached element (4 fp32, 2 bf16)."""
+    talker_w, cp_w, kv_t, kv_c = step_bytes(spec, kv_elem)
+    groups = spec.num_code_groups - 1
+    weights = talker_w + groups * cp_w
+    cp_kv = kv_c * (sum(range(2, groups + 2)) + 2)
+    kv = sum(sum(kv_t * (p + f + 2) for f in range(fr - 1)) + fr * cp_kv for p, fr in zip(prefill_steps, frames))
+    return int(max(frames) * weights + kv)
 
 
 def per_step(st, spec, prefill_steps: int, chunk: int, kv_elem: int) -> dict:
@@ -222,24 +243,12 @@ def multistream(eng_cls, model_dir: str, name: str, steps: int, warmup: int, use
     if frames_cap > 0:
         budgets = [min(f, frames_cap) for f in budgets]
     spec = synth.SPECS[w.spec]
-    talker_w, cp_w, kv_t, kv_c = step_bytes(spec, 2 if kv_bf16 else 4)
-    groups = spec.num_code_groups - 1
-    weights = talker_w + groups * cp_w
-    cp_kv = kv_c * (sum(range(2, groups + 2)) + 2)
-    # batched frame f: every stream with more than f frames is live (no EOS in this greedy
-    # workload); a live stream at prefill P reads P + f + 2 Talker KV rows (P + f + 1 read, 1
-    # written) and its CodePredictor rows
     n_batched = max(budgets)
-
-    def kv_bytes(kv_t, cp_kv):
-        return sum(sum(kv_t * (9 + n + f + 2) for f in range(fr - 1)) + fr * cp_kv for n, fr in zip(lengths, budgets))
-    kv = kv_bytes(kv_t, cp_kv)
-    alg_bytes = n_batched * weights + kv
+    alg_bytes = batched_bytes(spec, [9 + n for n in lengths], budgets, 2 if kv_bf16 else 4)
     decode_s = (el - prefill_s) / steps
     gbps = alg_bytes / decode_s / 1e9
     # the per-frame algorithmic-byte definition counts KV rows at bf16 width whatever the cache type
-    _, _, kv_t2, kv_c2 = step_bytes(spec, 2)
-    alg_bytes_8d = n_batched * weights + kv_bytes(kv_t2, kv_c2 * (sum(range(2, groups + 2)) + 2))
+    alg_bytes_8d = batched_bytes(spec, [9 + n for n in lengths], budgets, 2)
     gbps_8d = alg_bytes_8d / decode_s / 1e9
     return {"workload": name, "streams": w.streams, "value": round(frames / el, 2), "unit": "frames/s (all streams)",
             "steps": steps, "warmup": warmup, "ms_per_step": round(1000 * el / steps, 3),
