@@ -39,29 +39,6 @@ HBM_PEAK_GBPS = 8000.0
 FRAME_SECONDS = 0.080
 
 
-def frame_bytes(spec, active_steps_mean: float, kv_elem: int) -> float:
-    """Algorithmic bytes of one frame: every bf16 weight the frame reads once per pass
-    (Talker stack + codec head + final norm, then 15 CodePredictor passes of stack + one
-    LM head (+ projection)), plus the KV cache rows attention reads and writes."""
-    t, c = spec.talker, spec.code_predictor
-
-    def stack_params(s):
-        # per layer: q/k/v, o, gate/up and down matrices, plus the four norm gains (input,
-        # post-attention, q head, k head)
-        q, kv = s.q_heads * s.head_dim, s.kv_heads * s.head_dim
-        return s.layers * ((q + 2 * kv) * s.hidden + s.hidden * q + 3 * s.intermediate * s.hidden +
-                           2 * s.hidden + 2 * s.head_dim)
-
-    talker = 2 * (stack_params(t) + t.vocab * t.hidden + t.hidden)
-    proj = c.hidden * t.hidden if spec.has_projection else 0
-    cp_pass = 2 * (stack_params(c) + c.vocab * c.hidden + c.hidden + proj)
-    groups = spec.num_code_groups - 1
-    kv_row_t = t.layers * 2 * t.kv_heads * t.head_dim * kv_elem
-    kv_row_c = c.layers * 2 * c.kv_heads * c.head_dim * kv_elem
-    kv = kv_row_t * active_steps_mean + kv_row_c * sum(range(1, spec.num_code_groups + 1))
-    return talker + groups * cp_pass + kv
-
-
 def step_bytes(spec, kv_elem: int):
     """Algorithmic bytes of one Talker step (stack + codec head + final norm, bf16) and of one
     CodePredictor pass (stack + one LM head + final norm (+ projection)), without KV, and the
@@ -81,6 +58,16 @@ def step_bytes(spec, kv_elem: int):
     kv_t = t.layers * 2 * t.kv_heads * t.head_dim * kv_elem
     kv_c = c.layers * 2 * c.kv_heads * c.head_dim * kv_elem
     return talker, cp_pass, kv_t, kv_c
+
+
+def frame_bytes(spec, active_steps_mean: float, kv_elem: int) -> float:
+    """Algorithmic bytes of one frame: every bf16 weight the frame reads once per pass (the
+    Talker step, then 15 CodePredictor passes), plus the KV cache rows attention reads and
+    writes: the Talker's at the mean active length, the CodePredictor's 1 .. 16 rows."""
+    talker, cp_pass, kv_t, kv_c = step_bytes(spec, kv_elem)
+    groups = spec.num_code_groups - 1
+    kv = kv_t * active_steps_mean + kv_c * sum(range(1, spec.num_code_groups + 1))
+    return talker + groups * cp_pass + kv
 
 
 def batched_bytes(spec, prefill_steps, frames, kv_elem: int) -> int:
