@@ -142,7 +142,9 @@ int q3t_streams_start(q3t_engine *engine, int32_t n, const q3t_stream_input *inp
  * the weights (ragged positions, per-stream KV caches and options), until each has produced
  * max_chunk_frames frames or ended.  Stream j's codes go to codes + j * max_chunk_frames *
  * num_code_groups and its chunk to info[j] (frames = 0: nothing left, the reference's None).
- * Streams not listed are untouched. */
+ * Streams not listed are untouched.  When exactly one listed stream has frames left it runs
+ * the single-stream frame (q3t_stream_next_codes), which is faster for one row; both compute
+ * the same frame to float32 rounding. */
 int q3t_streams_next_codes(q3t_engine *engine, q3t_stream *const *streams, int32_t n,
                            int32_t max_chunk_frames, int32_t *codes, q3t_chunk_info *info);
 

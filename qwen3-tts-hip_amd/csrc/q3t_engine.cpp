@@ -1921,6 +1921,25 @@ q3t_stream *start_text_stream(Engine *e, const TextPlan &p, const q3t_generate_o
   return out;
 }
 
+// The frames a single-stream run just produced: codes, state and the stream's counters.
+void collect_frames(q3t_stream *sp, int n, int32_t *codes, q3t_chunk_info *info) {
+  Engine &e = *sp->engine;
+  Slot &s = e.slots[sp->slot];
+  // The state and the n frames' codes (those not produced are never read) in one round trip.
+  int32_t *h = e.pools.h_codes + (size_t)sp->slot * e.pools.codes_row + (size_t)sp->host_frame * e.groups;
+  HIPC(hipMemcpyAsync(h, s.codes + (size_t)sp->host_frame * e.groups, (size_t)n * e.groups * 4,
+                      hipMemcpyDeviceToHost, s.stream));
+  sync_state(s);
+  const int produced = s.h_state->frame - sp->host_frame;
+  if (produced < 0 || produced > n) fail(Q3T_ERR_HIP, "device loop state is inconsistent");
+  if (produced > 0) std::memcpy(codes, h, (size_t)produced * e.groups * 4);
+  sp->host_frame += produced;
+  sp->done = s.h_state->done;
+  info->frames = produced;
+  info->total_frames = sp->host_frame;
+  info->ended_by_eos = sp->done == 1;
+}
+
 }  // namespace
 }  // namespace q3t
 
@@ -2134,6 +2153,19 @@ int q3t_streams_next_codes(q3t_engine *e, q3t_stream *const *streams, int32_t n,
     }
     if (nrun == 0) return;
     HIPC(hipSetDevice(e->device));
+    if (on.size() == 1) {
+      // One stream to run (the tail of a ragged batch, once the others have ended): the
+      // single-stream frame (GEMV kernels, 1.7 ms for the 0.6B shape) instead of a batched
+      // frame, which costs about the same at 1 live row as at 16 (2.7 ms).  Both read and
+      // write the same per-slot state (caches, loop state, codes, the next pass's inputs) at
+      // frame boundaries, so a stream may take either path at any frame.
+      for (int j = 0; j < n; ++j)
+        if (want[j]) {
+          run_frames(*e, e->slots[streams[j]->slot], want[j]);
+          collect_frames(streams[j], want[j], codes + (size_t)j * max_chunk * e->groups, &info[j]);
+        }
+      return;
+    }
     Pools &p = e->pools;
     const int rows = set_rows(*e, on, p.stream);
     bool fused = e->rows_handoff_ok();
@@ -2225,23 +2257,6 @@ void ensure_phase_graphs(Engine &e, Slot &s) {
 }
 
 // After up to n frames ran: the new codes to the caller, the host's view of the stream.
-void collect_frames(q3t_stream *sp, int n, int32_t *codes, q3t_chunk_info *info) {
-  Engine &e = *sp->engine;
-  Slot &s = e.slots[sp->slot];
-  // The state and the n frames' codes (those not produced are never read) in one round trip.
-  int32_t *h = e.pools.h_codes + (size_t)sp->slot * e.pools.codes_row + (size_t)sp->host_frame * e.groups;
-  HIPC(hipMemcpyAsync(h, s.codes + (size_t)sp->host_frame * e.groups, (size_t)n * e.groups * 4,
-                      hipMemcpyDeviceToHost, s.stream));
-  sync_state(s);
-  const int produced = s.h_state->frame - sp->host_frame;
-  if (produced < 0 || produced > n) fail(Q3T_ERR_HIP, "device loop state is inconsistent");
-  if (produced > 0) std::memcpy(codes, h, (size_t)produced * e.groups * 4);
-  sp->host_frame += produced;
-  sp->done = s.h_state->done;
-  info->frames = produced;
-  info->total_frames = sp->host_frame;
-  info->ended_by_eos = sp->done == 1;
-}
 
 
 }  // namespace
