@@ -222,10 +222,19 @@ struct Pools {
   int32_t *h_codes = nullptr;                           // pinned [n][codes_row], mirrors codes
   int32_t *h_row_on = nullptr;                          // pinned [n]
   hipStream_t stream = nullptr;                         // batched work
-  hipGraphExec_t graph = nullptr;                       // batched frame, keyed by (rows, traced, fused)
-  int graph_rows = 0;
-  bool graph_traced = false;
-  bool graph_fused = false;
+  // The batched frame's graphs, one per (rows, fused), all captured with the trace setting
+  // graphs_traced: a ragged batch changes its row count as streams end, and each count keeps
+  // its graph instead of capturing again in every generation.
+  hipGraphExec_t graphs[kMaxRows + 1][2] = {};
+  bool graphs_traced = false;
+  void drop_graphs() {
+    for (auto &byrows : graphs)
+      for (hipGraphExec_t &g : byrows)
+        if (g) {
+          (void)hipGraphExecDestroy(g);
+          g = nullptr;
+        }
+  }
 };
 
 constexpr int kRowsAttnChunk = 32;
@@ -1098,7 +1107,7 @@ void free_pools(Engine &e) {
   }
   e.slots.clear();
   Pools &p = e.pools;
-  if (p.graph) (void)hipGraphExecDestroy(p.graph);
+  p.drop_graphs();
   if (p.stream) (void)hipStreamDestroy(p.stream);
   void *ptrs[] = {p.t_k,      p.t_v,     p.c_k,   p.c_v,      p.x_t,      p.t_in,    p.qkv,  p.attn,
                   p.act,      p.logits_t, p.logits_c, p.x_c,  p.cp_prefix, p.cp_in,  p.cur,  p.emb_sum,
@@ -1279,12 +1288,14 @@ void run_frames(Engine &e, Slot &s, int n) {
 // n batched frames over stream rows 0..rows-1 (pools.row_on already on the device).
 void run_rows_frames_impl(Engine &e, int rows, int n, bool fused) {
   Pools &p = e.pools;
+  if (rows < 1 || rows > kMaxRows) fail(Q3T_ERR_INVALID, "batched frame of %d rows", rows);
   if (e.use_graph) {
-    if (!p.graph || p.graph_rows != rows || p.graph_traced != (bool)e.trace || p.graph_fused != fused) {
-      if (p.graph) {
-        HIPC(hipGraphExecDestroy(p.graph));
-        p.graph = nullptr;
-      }
+    if (p.graphs_traced != (bool)e.trace) {
+      p.drop_graphs();
+      p.graphs_traced = (bool)e.trace;
+    }
+    hipGraphExec_t &graph = p.graphs[rows][fused ? 1 : 0];
+    if (!graph) {
       hipGraph_t g;
       HIPC(hipStreamBeginCapture(p.stream, hipStreamCaptureModeThreadLocal));
       try {
@@ -1295,14 +1306,12 @@ void run_rows_frames_impl(Engine &e, int rows, int n, bool fused) {
         throw;
       }
       HIPC(hipStreamEndCapture(p.stream, &g));
-      const hipError_t err = hipGraphInstantiate(&p.graph, g, nullptr, nullptr, 0);
+      const hipError_t err = hipGraphInstantiate(&graph, g, nullptr, nullptr, 0);
       (void)hipGraphDestroy(g);
+      if (err != hipSuccess) graph = nullptr;
       hip_check(err, "hipGraphInstantiate");
-      p.graph_rows = rows;
-      p.graph_traced = (bool)e.trace;
-      p.graph_fused = fused;
     }
-    for (int i = 0; i < n; ++i) HIPC(hipGraphLaunch(p.graph, p.stream));
+    for (int i = 0; i < n; ++i) HIPC(hipGraphLaunch(graph, p.stream));
   } else {
     for (int i = 0; i < n; ++i) e.enqueue_rows_frame(rows, fused, p.stream);
   }
