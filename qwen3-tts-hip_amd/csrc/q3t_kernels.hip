@@ -2670,28 +2670,60 @@ __global__ __launch_bounds__(1024) void k_select_talker(SelectTalkerArgs a) {
   if (a.end_frame && tid == 0) end_frame(a.st, a.prm, a.after_frame);
 }
 
+// Loads first, in two dependent steps: the logits and the row's running embedding sum (their
+// addresses need no state), then the state and, for the last group, the semantic token's
+// codec embedding row and the trailing text row.  Only the chosen token's embedding row waits
+// for the selection.  Vc <= kMaxVocab and Ht <= 2048 (launch_select_cp).
 __global__ __launch_bounds__(1024) void k_select_cp(SelectCpArgs a) {
+  constexpr int LV = kMaxVocab / 1024;
   const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const float *logits = a.logits + (size_t)row * a.Vc;
+  float *emb_sum = a.emb_sum + (size_t)row * a.Ht;
+  float lv[LV], es[2];
+#pragma unroll
+  for (int j = 0; j < LV; ++j) {
+    const int i = tid + 1024 * j;
+    lv[j] = i < a.Vc ? logits[i] : 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int i = tid + 1024 * j;
+    es[j] = (a.group > 0 && i < a.Ht) ? emb_sum[i] : 0.f;
+  }
   if (a.row_on && !a.row_on[row]) return;
   a.st += row;
   a.prm += row;
   if (skip_work(a.st, SKIP_DONE)) return;
-  a.logits += (size_t)row * a.Vc;
   a.cur += (size_t)row * a.Ht;
-  a.emb_sum += (size_t)row * a.Ht;
   a.talker_in += (size_t)row * a.Ht;
   a.codes += row * a.codes_row;
   a.trailing += row * a.trailing_row;
   if (a.trace) a.trace += row * a.trace_row;
   __shared__ SelectShared sh;
-  const int tid = threadIdx.x;
   const SlotParams prm = *a.prm;
   const int frame = a.st->frame;
   const int semantic = a.st->semantic;
-  for (int i = tid; i < a.Vc; i += 1024) {
-    const float l = a.logits[i];
-    if (a.trace) a.trace[((size_t)frame * (a.groups - 1) + a.group) * a.Vc + i] = l;
-    sh.lg[i] = l;
+  const bool last = a.group == a.groups - 2;
+  float ce[2] = {0.f, 0.f}, tr[2] = {0.f, 0.f};
+  if (last) {
+    const int trow = min(frame, a.st->trailing_rows);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = tid + 1024 * j;
+      if (i < a.Ht) {
+        ce[j] = bf16_to_f32(a.codec_emb[(size_t)semantic * a.Ht + i]);
+        tr[j] = a.trailing[(size_t)trow * a.Ht + i];
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < LV; ++j) {
+    const int i = tid + 1024 * j;
+    if (i < a.Vc) {
+      if (a.trace) a.trace[((size_t)frame * (a.groups - 1) + a.group) * a.Vc + i] = lv[j];
+      sh.lg[i] = lv[j];
+    }
   }
   __syncthreads();
   const int tok = prm.cp.do_sample ? block_sample(sh, a.Vc, prm.cp, sampler_uniform(prm, frame, 1 + a.group))
@@ -2701,15 +2733,16 @@ __global__ __launch_bounds__(1024) void k_select_cp(SelectCpArgs a) {
     if (a.group == 0) a.codes[(size_t)frame * a.groups] = semantic;
     if (a.tok_out) *a.tok_out = tok;
   }
-  const bool last = a.group == a.groups - 2;
-  const int trow = min(frame, a.st->trailing_rows);
-  for (int i = tid; i < a.Ht; i += 1024) {
-    const float e = bf16_to_f32(a.emb[(size_t)tok * a.Ht + i]);
-    a.cur[i] = e;
-    const float s = (a.group == 0) ? e : a.emb_sum[i] + e;
-    a.emb_sum[i] = s;
-    if (last)
-      a.talker_in[i] = (bf16_to_f32(a.codec_emb[(size_t)semantic * a.Ht + i]) + s) + a.trailing[(size_t)trow * a.Ht + i];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int i = tid + 1024 * j;
+    if (i < a.Ht) {
+      const float e = bf16_to_f32(a.emb[(size_t)tok * a.Ht + i]);
+      a.cur[i] = e;
+      const float sum = (a.group == 0) ? e : es[j] + e;
+      emb_sum[i] = sum;
+      if (last) a.talker_in[i] = (ce[j] + sum) + tr[j];
+    }
   }
 }
 
@@ -3452,7 +3485,7 @@ hipError_t launch_select_talker(const SelectTalkerArgs &a, hipStream_t s, int ro
 }
 
 hipError_t launch_select_cp(const SelectCpArgs &a, hipStream_t s, int rows) {
-  if (a.Vc > kMaxVocab) return hipErrorInvalidValue;
+  if (a.Vc < 1 || a.Vc > kMaxVocab || a.Ht < 1 || a.Ht > 2048) return hipErrorInvalidValue;
   if (rows < 1 || rows > kMaxRows ||
       (rows > 1 && (!a.row_on || a.codes_row <= 0 || a.trailing_row <= 0 || (a.trace && a.trace_row <= 0) ||
                     a.tok_out)))
