@@ -177,11 +177,12 @@ struct Slot {
   float *trace_t = nullptr, *trace_c = nullptr;
   hipStream_t stream = nullptr;
   hipGraphExec_t graph = nullptr;
+  hipGraphExec_t graph_long = nullptr;  // the same frame with the split Talker attention
   bool graph_traced = false;
   bool graph_cp_greedy = false;
-  // The frame as two graphs, the CodePredictor and the Talker step (q3t_debug_phase_times),
-  // keyed like `graph`.
-  hipGraphExec_t phase_graph[2] = {nullptr, nullptr};
+  // The frame as separate graphs (q3t_debug_phase_times), keyed like `graph`: the
+  // CodePredictor, the Talker step, and the Talker step with the split attention.
+  hipGraphExec_t phase_graph[3] = {nullptr, nullptr, nullptr};
   bool phase_traced = false, phase_cp_greedy = false;
   SlotState *h_state = nullptr;  // pinned host mirror
   // Greedy CodePredictor (the stream's subtalker does not sample): each LM head hands its
@@ -303,6 +304,12 @@ struct Engine {
   std::vector<Slot> slots;
   Pools pools;
   bool rows_ok = false;  // the batched frame's fused-norm GEMMs support both hidden sizes
+  // Talker positions below this run the fused attention + O kernel (talker_heads_o), from it
+  // the split attention and the merging O GEMV: each fused workgroup reads its head's whole
+  // cache, and per layer (graph-timed, the gap included) the fused kernel took 6.0 µs at
+  // position 128 against 3.6 + 2.6 for the pair, 9.0 against 4.9 + 2.5 at 256 and 13.7
+  // against 7.4 + 2.6 at 512.  q3t_engine_set_fused_attention_rows changes it.
+  int fused_attn_rows = 256;
   int64_t device_bytes = 0;
 
   // nt: stream the weights with non-temporal loads (Talker weights are read once per frame).
@@ -342,7 +349,7 @@ struct Engine {
   // the last group's hand-off (GemvArgs::tin) and stores it to `in`.
   void stack_step(const StackW &w, char *kc, char *vc, const float *in, float *x, Slot &sl, int pos_mode,
                   int pos_const, int skip, hipStream_t s, const TokenHandoff *handoff = nullptr,
-                  const float *qkv_table = nullptr, const GemvArgs *tin = nullptr) {
+                  const float *qkv_table = nullptr, const GemvArgs *tin = nullptr, bool split_attn = false) {
     const Dims &d = w.d;
     const bool nt = &w == &talker;
     const bool fuse_o = oproj_ok(w);
@@ -384,7 +391,7 @@ struct Engine {
              sl.st, s, nt);
         continue;
       }
-      if (talker_heads_o(w)) {
+      if (!split_attn && talker_heads_o(w)) {
         // Attention and the O projection (K split by KV head) in one launch; the gate/up GEMV
         // sums the residual and the per-head shares, and stores that sum (x_mid) for down.
         AttnArgs aa{sl.qkv,   L.gq,      L.gk,       w.rope,  kc + l * cache_layer, vc + l * cache_layer,
@@ -510,10 +517,10 @@ struct Engine {
 
   // Everything one frame does after its semantic token is known (generation.rs:697-741):
   // CodePredictor groups 0..14, the next Talker step, token selection, frame bookkeeping.
-  void enqueue_frame(Slot &sl, hipStream_t s) {
+  void enqueue_frame(Slot &sl, hipStream_t s, bool split_attn = false) {
     const bool fold = fold_last_group(sl);
     enqueue_code_predictor(sl, s, fold);
-    enqueue_talker_decode(sl, s, fold);
+    enqueue_talker_decode(sl, s, fold, split_attn);
   }
 
   // A greedy CodePredictor hands its last group's token to the Talker step that follows
@@ -524,7 +531,7 @@ struct Engine {
            (talker_hidden == 512 || talker_hidden == 1024 || talker_hidden == 2048);
   }
 
-  void enqueue_talker_decode(Slot &sl, hipStream_t s, bool fold = false) {
+  void enqueue_talker_decode(Slot &sl, hipStream_t s, bool fold = false, bool split_attn = false) {
     if (fold) {
       const int Vc = cd.vocab, nac = groups - 1;
       GemvArgs tin{};
@@ -539,9 +546,10 @@ struct Engine {
       tin.tin_codec_emb = codec_emb;
       tin.tin_trailing = sl.trailing;
       stack_step(talker, sl.t_k, sl.t_v, sl.t_in, sl.x_t, sl, POS_TALKER_FRAME, 0, SKIP_TALKER, s, nullptr, nullptr,
-                 &tin);
+                 &tin, split_attn);
     } else {
-      stack_step(talker, sl.t_k, sl.t_v, sl.t_in, sl.x_t, sl, POS_TALKER_FRAME, 0, SKIP_TALKER, s);
+      stack_step(talker, sl.t_k, sl.t_v, sl.t_in, sl.x_t, sl, POS_TALKER_FRAME, 0, SKIP_TALKER, s, nullptr, nullptr,
+                 nullptr, split_attn);
     }
     gemv(EPI_STORE, true, codec_head, sl.x_t, t_norm, td.eps, nullptr, nullptr, sl.logits_t, td.vocab, td.hidden,
          SKIP_TALKER, sl.st, s, true);
@@ -1101,6 +1109,7 @@ void alloc_pools(Engine &e, int n) {
 void free_pools(Engine &e) {
   for (Slot &sl : e.slots) {
     if (sl.graph) (void)hipGraphExecDestroy(sl.graph);
+    if (sl.graph_long) (void)hipGraphExecDestroy(sl.graph_long);
     for (hipGraphExec_t g : sl.phase_graph)
       if (g) (void)hipGraphExecDestroy(g);
     if (sl.stream) (void)hipStreamDestroy(sl.stream);
@@ -1256,32 +1265,52 @@ void sync_state(Slot &s) {
   HIPC(hipStreamSynchronize(s.stream));
 }
 
+// The slot's frames in the next call whose Talker step attends with the fused attention + O
+// kernel: those at positions below Engine::fused_attn_rows.  The host mirror holds the state
+// after the last synchronised call, and a frame advances the position by one (frames after
+// the stream's end run nothing), so frame i of the call is at position P + frame + i at most.
+int fused_frames(const Engine &e, const Slot &s, int n) {
+  if (!e.talker_heads_o(e.talker)) return n;  // one variant only
+  const int pos = s.h_state->prefill_steps + s.h_state->frame;
+  return std::clamp(e.fused_attn_rows - pos, 0, n);
+}
+
 void run_frames(Engine &e, Slot &s, int n) {
+  const int nf = fused_frames(e, s, n);
   if (e.use_graph) {
-    if (!s.graph || s.graph_traced != (bool)e.trace || s.graph_cp_greedy != s.cp_greedy) {
-      if (s.graph) {
-        HIPC(hipGraphExecDestroy(s.graph));
-        s.graph = nullptr;
-      }
-      hipGraph_t g;
-      HIPC(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal));
-      try {
-        e.enqueue_frame(s, s.stream);
-      } catch (...) {
-        (void)hipStreamEndCapture(s.stream, &g);
-        if (g) (void)hipGraphDestroy(g);
-        throw;
-      }
-      HIPC(hipStreamEndCapture(s.stream, &g));
-      const hipError_t err = hipGraphInstantiate(&s.graph, g, nullptr, nullptr, 0);
-      (void)hipGraphDestroy(g);
-      hip_check(err, "hipGraphInstantiate");
+    if (s.graph_traced != (bool)e.trace || s.graph_cp_greedy != s.cp_greedy) {
+      for (hipGraphExec_t *gp : {&s.graph, &s.graph_long})
+        if (*gp) {
+          HIPC(hipGraphExecDestroy(*gp));
+          *gp = nullptr;
+        }
       s.graph_traced = (bool)e.trace;
       s.graph_cp_greedy = s.cp_greedy;
     }
-    for (int i = 0; i < n; ++i) HIPC(hipGraphLaunch(s.graph, s.stream));
+    for (const bool lc : {false, true}) {
+      const int count = lc ? n - nf : nf;
+      hipGraphExec_t &graph = lc ? s.graph_long : s.graph;
+      if (count == 0) continue;
+      if (!graph) {
+        hipGraph_t g;
+        HIPC(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal));
+        try {
+          e.enqueue_frame(s, s.stream, lc);
+        } catch (...) {
+          (void)hipStreamEndCapture(s.stream, &g);
+          if (g) (void)hipGraphDestroy(g);
+          throw;
+        }
+        HIPC(hipStreamEndCapture(s.stream, &g));
+        const hipError_t err = hipGraphInstantiate(&graph, g, nullptr, nullptr, 0);
+        (void)hipGraphDestroy(g);
+        if (err != hipSuccess) graph = nullptr;
+        hip_check(err, "hipGraphInstantiate");
+      }
+      for (int i = 0; i < count; ++i) HIPC(hipGraphLaunch(graph, s.stream));
+    }
   } else {
-    for (int i = 0; i < n; ++i) e.enqueue_frame(s, s.stream);
+    for (int i = 0; i < n; ++i) e.enqueue_frame(s, s.stream, i >= nf);
   }
 }
 
@@ -1558,6 +1587,14 @@ int q3t_engine_set_trace(q3t_engine *e, int32_t enabled) {
   return guarded([&] {
     if (!e) fail(Q3T_ERR_INVALID, "null engine");
     e->trace = enabled ? 1 : 0;
+  });
+}
+
+int q3t_engine_set_fused_attention_rows(q3t_engine *e, int32_t rows) {
+  return guarded([&] {
+    if (!e) fail(Q3T_ERR_INVALID, "null engine");
+    if (rows < 0) fail(Q3T_ERR_INVALID, "fused attention rows must not be negative");
+    e->fused_attn_rows = rows;
   });
 }
 
@@ -2245,12 +2282,12 @@ void ensure_phase_graphs(Engine &e, Slot &s) {
       HIPC(hipGraphExecDestroy(g));
       g = nullptr;
     }
-  for (int ph = 0; ph < 2; ++ph) {
+  for (int ph = 0; ph < 3; ++ph) {
     hipGraph_t g = nullptr;
     HIPC(hipStreamBeginCapture(s.stream, hipStreamCaptureModeThreadLocal));
     try {
       if (ph == 0) e.enqueue_code_predictor(s, s.stream, e.fold_last_group(s));
-      else e.enqueue_talker_decode(s, s.stream, e.fold_last_group(s));
+      else e.enqueue_talker_decode(s, s.stream, e.fold_last_group(s), ph == 2);
     } catch (...) {
       (void)hipStreamEndCapture(s.stream, &g);
       if (g) (void)hipGraphDestroy(g);
@@ -2300,10 +2337,11 @@ int q3t_stream_next_codes_profiled(q3t_stream *sp, int32_t max_chunk, int32_t *c
     // One frame at a time (rollout_profiled, generation.rs:751-874): a frame after the end of
     // the stream is not run, so that it adds no time.
     while (ran < n && !s.h_state->done) {
+      const bool split = fused_frames(e, s, 1) == 0;
       HIPC(hipEventRecord(ev.ev[0], s.stream));
       e.enqueue_code_predictor(s, s.stream, e.fold_last_group(s));
       HIPC(hipEventRecord(ev.ev[1], s.stream));
-      e.enqueue_talker_decode(s, s.stream, e.fold_last_group(s));
+      e.enqueue_talker_decode(s, s.stream, e.fold_last_group(s), split);
       HIPC(hipEventRecord(ev.ev[2], s.stream));
       sync_state(s);
       prof->code_predictor_seconds += ev.seconds(0, 1);
@@ -2329,12 +2367,13 @@ int q3t_debug_phase_times(q3t_stream *sp, int32_t max_chunk, int32_t *codes, q3t
     Events ev(3);
     int ran = 0;
     while (ran < n && !s.h_state->done) {
+      const bool split = fused_frames(e, s, 1) == 0;
       HIPC(hipEventRecord(ev.ev[0], s.stream));
       if (e.use_graph) HIPC(hipGraphLaunch(s.phase_graph[0], s.stream));
       else e.enqueue_code_predictor(s, s.stream, e.fold_last_group(s));
       HIPC(hipEventRecord(ev.ev[1], s.stream));
-      if (e.use_graph) HIPC(hipGraphLaunch(s.phase_graph[1], s.stream));
-      else e.enqueue_talker_decode(s, s.stream, e.fold_last_group(s));
+      if (e.use_graph) HIPC(hipGraphLaunch(s.phase_graph[split ? 2 : 1], s.stream));
+      else e.enqueue_talker_decode(s, s.stream, e.fold_last_group(s), split);
       HIPC(hipEventRecord(ev.ev[2], s.stream));
       sync_state(s);
       cp_us[ran] = (float)(1e6 * ev.seconds(0, 1));

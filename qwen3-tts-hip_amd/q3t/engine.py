@@ -173,6 +173,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
         "q3t_engine_destroy": (ctypes.c_int, [ctypes.c_void_p]),
         "q3t_engine_get_info": (ctypes.c_int, [ctypes.c_void_p, P(_EngineInfo)]),
         "q3t_engine_set_trace": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32]),
+        "q3t_engine_set_fused_attention_rows": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32]),
         "q3t_stream_start": (ctypes.c_int, [ctypes.c_void_p, f32p, ctypes.c_int32, f32p, ctypes.c_int32,
                                             f32p, P(_GenerateOptions), P(ctypes.c_void_p)]),
         "q3t_stream_next_codes": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int32, i32p, P(_ChunkInfo)]),
@@ -466,6 +467,11 @@ class HipTtsEngine:
     def set_trace(self, enabled: bool) -> None:
         """Record raw logits of every step (parity checks)."""
         _check(_lib.q3t_engine_set_trace(self._h, int(bool(enabled))))
+
+    def set_fused_attention_rows(self, rows: int) -> None:
+        """Talker positions below `rows` run the fused attention + O kernel (default 256),
+        later ones the split attention and the merging O projection."""
+        _check(_lib.q3t_engine_set_fused_attention_rows(self._h, int(rows)))
 
     def synchronize(self) -> None:
         _check(_lib.q3t_engine_synchronize(self._h))

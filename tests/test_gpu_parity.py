@@ -236,25 +236,35 @@ def test_eos_ends_stream_like_the_reference(models, tmp_path):
     assert r["eos"] and r["chunks"][-1].ended_by_eos
 
 
-@pytest.mark.parametrize("spec,n_ids,cap,frames,kv_bf16", [
-    ("tiny", 291, 512, 8, False),      # positions 300-307: two 256-row passes
-    ("tiny", 240, 320, 16, False),     # positions 249-264: the second pass starts mid-stream
-    ("tiny-g1", 240, 320, 16, False),  # one query head per KV head
-    ("tiny", 1000, 1024, 10, False),   # positions 1009-1018: four passes, the longest cache
-    ("tiny", 291, 512, 8, True),       # bf16 cache (every row group loaded)
+@pytest.mark.parametrize("spec,n_ids,cap,frames,kv_bf16,fused_rows", [
+    ("tiny", 291, 512, 8, False, 512),      # positions 300-307: two 256-row passes
+    ("tiny", 240, 320, 16, False, 320),     # positions 249-264: the second pass starts mid-stream
+    ("tiny-g1", 240, 320, 16, False, 320),  # one query head per KV head
+    ("tiny", 1000, 1024, 10, False, 1024),  # positions 1009-1018: four passes, the longest cache
+    ("tiny", 291, 512, 8, True, 512),       # bf16 cache (every row group loaded)
+    # the engine's default: fused below position 256, split attention + merging O from it
+    # (calls of 4 frames: one call runs both graphs of the slot)
+    ("tiny", 240, 320, 16, False, None),
+    ("tiny", 1000, 1024, 10, False, None),
+    ("tiny", 240, 320, 16, True, None),
 ])
-def test_fused_talker_attention_long_caches_match_oracle(models, spec, n_ids, cap, frames, kv_bf16):
+def test_fused_talker_attention_long_caches_match_oracle(models, spec, n_ids, cap, frames, kv_bf16, fused_rows):
     """The Talker's fused attention + O projection (hidden 512 / 1024, caches of 33 .. 1024
     rows) runs its key rows in passes of 256: caches past one pass, across the pass boundary,
-    and at the 1024-row limit, against the oracle's rollout of the same prompt."""
+    and at the 1024-row limit (q3t_engine_set_fused_attention_rows at the capacity keeps it at
+    every position), against the oracle's rollout of the same prompt; and the engine's
+    default, which moves long positions to the split attention mid-stream."""
     model, d = models.get(spec)
     prompt = np.random.default_rng(n_ids + cap).integers(0, 151643, n_ids)
     from q3t import textprep
     inputs = textprep.TextPrep(model).prepare(prompt)
     assert inputs.prefill_steps == n_ids + 9
     opts = E.GenerateOptions.greedy(frames)
-    print(f"[gpu] fused attention spec={spec} P={inputs.prefill_steps} cap={cap} kv_bf16={kv_bf16}", flush=True)
+    print(f"[gpu] fused attention spec={spec} P={inputs.prefill_steps} cap={cap} kv_bf16={kv_bf16} "
+          f"fused_rows={fused_rows}", flush=True)
     with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=cap, kv_bf16=kv_bf16)) as eng:
+        if fused_rows is not None:
+            eng.set_fused_attention_rows(fused_rows)
         eng.set_trace(True)
         with eng.start_stream(inputs, opts) as st:
             chunks = []
