@@ -144,6 +144,28 @@ def test_unlisted_stream_is_untouched(models, name):
         np.testing.assert_array_equal(got[j], ref[j], err_msg=f"stream {j}")
 
 
+@pytest.mark.parametrize("name", ["tiny_multistream", "tinyg1_multistream"])
+def test_lone_stream_switches_paths_mid_stream(models, name):
+    """q3t_streams_next_codes runs a call with one stream left on the single-stream frame: a
+    stream that alternates between batched calls and calls where it runs alone must still
+    reproduce its single-stream rollout (the two frames share every piece of per-slot state)."""
+    w = MULTI_WORKLOADS[name]
+    model, d = models.get(w.spec, w.weight_seed)
+    inputs = w.inputs(model)[:2]
+    opts = [E.GenerateOptions(**kw) for kw in w.options_kwargs()[:2]]
+    ref = [run_single(models, name, j).codes for j in range(2)]
+    print(f"[gpu] lone stream path switches {name}", flush=True)
+    with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=w.max_cache_steps, max_streams=3)) as eng:
+        s = eng.start_streams(inputs, opts, E.StreamOptions(text_lookahead_tokens=1 << 30))
+        for step in range(64):
+            listed = [s[0]] if step % 3 == 1 else ([s[1]] if step % 3 == 2 else list(s))
+            if all(c is None for c in eng.next_codes_chunks(listed, 2)) and step % 3 == 0:
+                break
+        got = [x.finish_codes().codes for x in s]
+    for j in range(2):
+        np.testing.assert_array_equal(got[j], ref[j], err_msg=f"stream {j}")
+
+
 def test_streams_start_reports_busy_and_capacity(models):
     w = MULTI_WORKLOADS["tiny_multistream"]
     model, d = models.get(w.spec, w.weight_seed)
