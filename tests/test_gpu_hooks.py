@@ -123,3 +123,36 @@ def test_eager_engine_captures_no_graph(models):
         assert us > 0 and b > 0
         r = eng.dominant_kernel_roofline(8000.0, iters=8, graph=False)
         assert r["graph_us_per_launch"] is None and r["avg_launch_us"] > 0
+
+
+def test_phase_timing_and_profiled_rollout_take_the_split_attention(models):
+    """Talker steps at positions from 256 on take the split attention + merging O projection
+    (q3t_engine_set_fused_attention_rows), also when each frame's phases are timed as their own
+    graphs (q3t_debug_phase_times) and in the profiled rollout: a prompt of 254 rows crosses
+    that position in its third frame, and every path yields the same codes."""
+    model, d = models.get("tiny")
+    prompt = np.random.default_rng(3).integers(0, 151643, 245)
+    from q3t import textprep
+    inputs = textprep.TextPrep(model).prepare(prompt)
+    assert inputs.prefill_steps == 254
+    opts = E.GenerateOptions.greedy(8)
+    print("[gpu] split attention in phase timing and profiled rollout", flush=True)
+    with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=320)) as eng:
+        with pytest.raises(E.InvalidInputError):
+            eng.set_fused_attention_rows(-1)
+        ref = eng.generate_codes(inputs, opts).codes
+        with eng.start_stream(inputs, opts) as st:
+            timed = []
+            while True:
+                c, cp_us, tk_us = st.next_codes_chunk_timed(3)
+                if c is None:
+                    break
+                assert len(cp_us) == len(tk_us) == c.frames and (tk_us > 0).all()
+                timed.append(c.codes)
+        prof = eng.generate_codes_profiled(inputs, opts)
+        eng.set_fused_attention_rows(1 << 20)  # fused at every position
+        fused = eng.generate_codes(inputs, opts).codes
+    np.testing.assert_array_equal(np.concatenate(timed), ref)
+    np.testing.assert_array_equal(prof.codes.codes, ref)
+    np.testing.assert_array_equal(fused, ref)
+
