@@ -306,10 +306,11 @@ struct Engine {
   bool rows_ok = false;  // the batched frame's fused-norm GEMMs support both hidden sizes
   // Talker positions below this run the fused attention + O kernel (talker_heads_o), from it
   // the split attention and the merging O GEMV: each fused workgroup reads its head's whole
-  // cache, and per layer (graph-timed, the gap included) the fused kernel took 6.0 µs at
-  // position 128 against 3.6 + 2.6 for the pair, 9.0 against 4.9 + 2.5 at 256 and 13.7
-  // against 7.4 + 2.6 at 512.  q3t_engine_set_fused_attention_rows changes it.
-  int fused_attn_rows = 256;
+  // cache.  Whole 0.6B frames (ms, every frame split / fused) cross near 190 rows: positions
+  // 16-255 1.720 / 1.691, 129-248 1.729 / 1.731, 256-375 1.841 / 1.899, 509-628 1.934 /
+  // 2.088; config 2 at limits 256 / 224 / 192 / 160 ran 589.5 / 590.7 / 590.8 / 590.5
+  // frames/s.  q3t_engine_set_fused_attention_rows changes it.
+  int fused_attn_rows = 192;
   int64_t device_bytes = 0;
 
   // nt: stream the weights with non-temporal loads (Talker weights are read once per frame).

@@ -126,15 +126,15 @@ def test_eager_engine_captures_no_graph(models):
 
 
 def test_phase_timing_and_profiled_rollout_take_the_split_attention(models):
-    """Talker steps at positions from 256 on take the split attention + merging O projection
+    """Talker steps at positions from 192 on take the split attention + merging O projection
     (q3t_engine_set_fused_attention_rows), also when each frame's phases are timed as their own
-    graphs (q3t_debug_phase_times) and in the profiled rollout: a prompt of 254 rows crosses
+    graphs (q3t_debug_phase_times) and in the profiled rollout: a prompt of 190 rows crosses
     that position in its third frame, and every path yields the same codes."""
     model, d = models.get("tiny")
-    prompt = np.random.default_rng(3).integers(0, 151643, 245)
+    prompt = np.random.default_rng(3).integers(0, 151643, 181)
     from q3t import textprep
     inputs = textprep.TextPrep(model).prepare(prompt)
-    assert inputs.prefill_steps == 254
+    assert inputs.prefill_steps == 190
     opts = E.GenerateOptions.greedy(8)
     print("[gpu] split attention in phase timing and profiled rollout", flush=True)
     with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=320)) as eng:
