@@ -305,10 +305,11 @@ int q3t_debug_talker_step(q3t_engine *engine, const float *input, int32_t offset
 int q3t_debug_code_predictor(q3t_engine *engine, const float *talker_hidden,
                              const float *semantic_embed, int32_t *tokens, float *embedding_sum);
 
-/* Talker positions below `rows` (default 192) run the 0.6B Talker's fused attention + O
- * projection kernel, later positions the split attention and the O projection that merges its
- * partials (the fused kernel's workgroups each read their head's whole cache, which costs more
- * than the extra launch from ~190 rows on).  0 never fuses; a value at or above the KV capacity
+/* Talker positions below `rows` (default 192 with an fp32 KV cache, 256 with bf16) run the
+ * 0.6B Talker's fused attention + O projection kernel, later positions the split attention and
+ * the O projection that merges its partials (the fused kernel's workgroups each read their
+ * head's whole cache, which costs more than the extra launch from ~190 fp32 / ~265 bf16 rows
+ * on).  0 never fuses; a value at or above the KV capacity
  * always does.  Both compute the same step to float32 rounding.  Takes effect from the next
  * call that runs frames.  No counterpart in the reference (a tuning and test hook). */
 int q3t_engine_set_fused_attention_rows(q3t_engine *engine, int32_t rows);

@@ -306,11 +306,14 @@ struct Engine {
   bool rows_ok = false;  // the batched frame's fused-norm GEMMs support both hidden sizes
   // Talker positions below this run the fused attention + O kernel (talker_heads_o), from it
   // the split attention and the merging O GEMV: each fused workgroup reads its head's whole
-  // cache.  Whole 0.6B frames (ms, every frame split / fused) cross near 190 rows: positions
-  // 16-255 1.720 / 1.691, 129-248 1.729 / 1.731, 256-375 1.841 / 1.899, 509-628 1.934 /
-  // 2.088; config 2 at limits 256 / 224 / 192 / 160 ran 589.5 / 590.7 / 590.8 / 590.5
-  // frames/s.  q3t_engine_set_fused_attention_rows changes it.
-  int fused_attn_rows = 192;
+  // cache.  Whole 0.6B frames (ms, every frame split / fused), fp32 cache: positions 16-255
+  // 1.720 / 1.691, 129-248 1.729 / 1.731, 256-375 1.841 / 1.899, 509-628 1.934 / 2.088, so
+  // they cross near 190 rows (config 2 at limits 256 / 224 / 192 / 160: 589.5 / 590.7 /
+  // 590.8 / 590.5 frames/s); bf16 cache (half the bytes per row): 1.703 / 1.655, 1.709 /
+  // 1.678, 1.733 / 1.753, 1.820 / 1.918, crossing near 265.  Set at engine creation by the
+  // cache's type; q3t_engine_set_fused_attention_rows changes it.
+  static constexpr int kFusedAttnRowsF32 = 192, kFusedAttnRowsBf16 = 256;
+  int fused_attn_rows = kFusedAttnRowsF32;
   int64_t device_bytes = 0;
 
   // nt: stream the weights with non-temporal loads (Talker weights are read once per frame).
@@ -1425,6 +1428,7 @@ int q3t_engine_create(const q3t_engine_options *opts, q3t_engine **out) {
     e->use_graph = opts->use_graph;
     if (opts->kv_dtype != 0 && opts->kv_dtype != 1) fail(Q3T_ERR_INVALID, "kv_dtype must be 0 (fp32) or 1 (bf16)");
     e->kv_bf16 = opts->kv_dtype;
+    e->fused_attn_rows = e->kv_bf16 ? Engine::kFusedAttnRowsBf16 : Engine::kFusedAttnRowsF32;
     const int nslots = opts->max_streams > 0 ? opts->max_streams : 1;
     if (nslots > kMaxRows) fail(Q3T_ERR_INVALID, "max_streams %d exceeds %d", nslots, kMaxRows);
     const std::string dir = opts->model_dir;

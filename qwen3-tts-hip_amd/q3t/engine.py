@@ -469,8 +469,9 @@ class HipTtsEngine:
         _check(_lib.q3t_engine_set_trace(self._h, int(bool(enabled))))
 
     def set_fused_attention_rows(self, rows: int) -> None:
-        """Talker positions below `rows` run the fused attention + O kernel (default 192),
-        later ones the split attention and the merging O projection."""
+        """Talker positions below `rows` run the fused attention + O kernel (default 192 with
+        an fp32 KV cache, 256 with bf16), later ones the split attention and the merging O
+        projection."""
         _check(_lib.q3t_engine_set_fused_attention_rows(self._h, int(rows)))
 
     def synchronize(self) -> None:

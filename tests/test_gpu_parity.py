@@ -242,11 +242,12 @@ def test_eos_ends_stream_like_the_reference(models, tmp_path):
     ("tiny-g1", 240, 320, 16, False, 320),  # one query head per KV head
     ("tiny", 1000, 1024, 10, False, 1024),  # positions 1009-1018: four passes, the longest cache
     ("tiny", 291, 512, 8, True, 512),       # bf16 cache (every row group loaded)
-    # the engine's default: fused below position 192, split attention + merging O from it
-    # (positions 189-204 in calls of 4 frames: one call runs both graphs of the slot)
+    # the engine's default: fused below position 192 (fp32 cache) or 256 (bf16), the split
+    # attention + merging O from there (positions 189-204 and 254-269 in calls of 4 frames:
+    # one call runs both graphs of the slot)
     ("tiny", 180, 320, 16, False, None),
     ("tiny", 1000, 1024, 10, False, None),
-    ("tiny", 180, 320, 16, True, None),
+    ("tiny", 245, 320, 16, True, None),
 ])
 def test_fused_talker_attention_long_caches_match_oracle(models, spec, n_ids, cap, frames, kv_bf16, fused_rows):
     """The Talker's fused attention + O projection (hidden 512 / 1024, caches of 33 .. 1024
