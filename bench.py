@@ -134,7 +134,7 @@ def measured_traffic(workload: str, kernel: str):
 
 
 def cpu_baseline(runs: int = 3) -> dict:
-    """BASELINE config 1 on the host CPU, as BASELINE.md section 3 sets it: the float32 oracle,
+    """BASELINE config 1 on the host CPU, the reported CPU baseline: the float32 oracle,
     0.6B shape, 32-token prompt (non-streaming, P = 41), greedy, 40 frames; one warmup
     generation, then `runs` measured ones.  frames/s and ms/frame count the frames only (the
     prefill is reported beside them), as the reference's GenerationProfile splits them."""
