@@ -38,7 +38,7 @@ typedef struct q3t_stream q3t_stream;
 typedef struct {
   const char *model_dir;   /* holds config.json + model.safetensors */
   int32_t device;          /* HIP device ordinal */
-  int32_t max_cache_steps; /* Talker KV capacity per stream (default 512) */
+  int32_t max_cache_steps; /* Talker KV capacity per stream (default 512, at most 8192) */
   int32_t max_streams;     /* stream slots (KV caches) to allocate (default 1, at most 16) */
   int32_t use_graph;       /* 1 = replay each frame as one captured hipGraph (default) */
   int32_t kv_dtype;        /* KV cache element: 0 = fp32 (default, as the reference),

@@ -203,8 +203,9 @@ struct Pools {
   int s_qkv = 0, s_attn = 0, s_act = 0;
   int part_chunks = 0;
   // The batched frame splits the Talker's attention into shorter chunks (more workgroups,
-  // fewer bytes each) than one stream can: its partials are merged by k_attn_merge.
-  int rows_chunk = 0, rows_part_chunks = 0;
+  // fewer bytes each) than one stream can: its partials are merged by k_attn_merge
+  // (attn_rows_chunk_len: 32 rows up to a 2,048-row cache, longer chunks beyond).
+  int rows_part_chunks = 0;
   int64_t part_row = 0, trailing_row = 0, codes_row = 0, trace_t_row = 0, trace_c_row = 0, s_opart = 0;
   char *t_k = nullptr, *t_v = nullptr, *c_k = nullptr, *c_v = nullptr;
   float *x_t = nullptr, *t_in = nullptr, *qkv = nullptr, *attn = nullptr, *act = nullptr, *logits_t = nullptr,
@@ -237,8 +238,6 @@ struct Pools {
         }
   }
 };
-
-constexpr int kRowsAttnChunk = 32;
 
 // One stream's rows in a (possibly multi-stream) prompt prefill.
 struct PrefillSeg {
@@ -757,7 +756,7 @@ struct Engine {
     Pools &p = pools;
     const int H = d.hidden;
     const size_t cache_layer = (size_t)d.kv_heads * w.cap * d.head_dim * (kv_bf16 ? 2 : 4);
-    const int chunk = p.rows_chunk;
+    const int chunk = attn_rows_chunk_len(w.cap);  // the CodePredictor's short cache: one 32-row chunk
     const int nch = (w.cap + chunk - 1) / chunk;
     const int partial = nch > 1 ? 1 : 0;
     const Act none{nullptr, 0};
@@ -1025,8 +1024,7 @@ void alloc_pools(Engine &e, int n) {
   p.s_attn = std::max(td.q_out(), cd.q_out());
   p.s_act = std::max(td.intermediate, cd.intermediate);
   p.part_chunks = std::max(attn_chunks(e.cap), attn_chunks(e.cp.cap));
-  p.rows_chunk = kRowsAttnChunk;
-  p.rows_part_chunks = (e.cap + p.rows_chunk - 1) / p.rows_chunk;
+  p.rows_part_chunks = (e.cap + attn_rows_chunk_len(e.cap) - 1) / attn_rows_chunk_len(e.cap);
   const int kvh = std::max(td.kv_heads, cd.kv_heads);
   const int gq = std::max(td.q_heads / td.kv_heads, cd.q_heads / cd.kv_heads);
   p.part_row = (int64_t)kvh * std::max(p.part_chunks, p.rows_part_chunks) * gq * (td.head_dim + 2);

@@ -51,11 +51,16 @@ int attn_oproj_full_rows(int q_heads, int kv_heads);
 // Most attention chunks the O-projection GEMV merges itself (caches up to 8 x 128 rows); the
 // partials of a longer cache are merged by launch_attn_merge first.
 constexpr int kAttnGemvMergeChunks = 8;
+// Most chunk partials launch_attn_merge merges per (KV head, stream row).
+constexpr int kAttnMergeMaxChunks = 64;
 int attn_max_cache_steps(int q_heads, int kv_heads);
 // Key rows per attention workgroup for a cache of `cap` rows, and the resulting number of
 // chunks (partials the workspace must hold per head).
 int attn_chunk_len(int cap);
 int attn_chunks(int cap);
+// Key rows per workgroup of the stream-row (batched) attention, whose partials
+// launch_attn_merge merges: 32 up to a 2,048-row cache, then 64 and 128.
+int attn_rows_chunk_len(int cap);
 
 // Matrix-core GEMM (bf16 weights, fp32 activations split into three bf16 terms, fp32 accumulate)
 // for many rows: prompt prefill and batched decode.  Requires K % 32 == 0.

@@ -3019,10 +3019,16 @@ int attn_chunk_len(int cap) {
 
 int attn_chunks(int cap) { return (cap + attn_chunk_len(cap) - 1) / attn_chunk_len(cap); }
 
+int attn_rows_chunk_len(int cap) {
+  int c = 32;
+  while (c < kAttnMaxChunk && c * kAttnMergeMaxChunks < cap) c *= 2;
+  return c;
+}
+
 int attn_max_cache_steps(int q_heads, int kv_heads) {
   (void)q_heads;
   (void)kv_heads;
-  return kAttnMaxChunk * 64;  // at most 64 partial chunks per head
+  return kAttnMaxChunk * kAttnMergeMaxChunks;  // the merge's most partials, of the longest chunks
 }
 
 hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t s, const LaunchTiming *t, int rows) {
@@ -3467,7 +3473,7 @@ hipError_t launch_attn_merge(const AttnMergeArgs &a, int rows, hipStream_t s) {
   if (rows < 1 || rows > kMaxRows || a.kv_heads <= 0 || a.q_heads % a.kv_heads || a.chunk <= 0 ||
       a.part_chunks <= 0 || a.q_heads * 128 > a.ld_out || (rows > 1 && (!a.row_on || a.part_row <= 0)))
     return hipErrorInvalidValue;
-  if ((a.q_heads / a.kv_heads) * 128 > 256 || a.part_chunks > 64) return hipErrorInvalidValue;
+  if ((a.q_heads / a.kv_heads) * 128 > 256 || a.part_chunks > kAttnMergeMaxChunks) return hipErrorInvalidValue;
   const dim3 grid(a.kv_heads, rows), block(256);
   if (a.part_chunks <= 8) hipLaunchKernelGGL(k_attn_merge<8>, grid, block, 0, s, a);
   else if (a.part_chunks <= 16) hipLaunchKernelGGL(k_attn_merge<16>, grid, block, 0, s, a);

@@ -277,3 +277,35 @@ def test_batched_bf16_kv_tracks_single_stream(models):
         print(f"stream {j}: first differing frame {first} of {n}, logits over {rows} rows max diff {err:.2e}")
         assert err <= LOGIT_TOL
         assert first >= min(4, n)
+
+
+@pytest.mark.parametrize("cap,n_ids", [(2304, (2100, 2190)), (4224, (3990, 4098))])
+def test_batched_caches_past_2048_rows_match_oracle(models, cap, n_ids):
+    """Stream rows in caches longer than 64 chunks of 32 rows: the batched Talker attention
+    takes 64-row chunks (2,304-row cache, 36 partials) or 128-row chunks (4,224 rows, 33),
+    since k_attn_merge merges at most 64, while the CodePredictor keeps its one 32-row chunk.
+    Two greedy streams of 5 and 7 frames (the longer one ends alone, on the single-stream
+    frame) each reproduce their float64 oracle rollout."""
+    from oracle.model import GenerateOptions as OracleOptions
+    from oracle.model import Oracle
+    from q3t import textprep
+    model, d = models.get("tiny", 0)
+    prep = textprep.TextPrep(model)
+    inputs = [prep.prepare(np.random.default_rng(30 + j).integers(0, 151643, n)) for j, n in enumerate(n_ids)]
+    opts = [E.GenerateOptions.greedy(5), E.GenerateOptions.greedy(7)]
+    print(f"[gpu] batched long caches cap={cap}", flush=True)
+    with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=cap, max_streams=2)) as eng:
+        streams = eng.start_streams(inputs, opts, E.StreamOptions(text_lookahead_tokens=1 << 30))
+        live = list(streams)
+        while live:
+            chunks = eng.next_codes_chunks(live, 3)
+            live = [s for s, c in zip(live, chunks) if c is not None]
+        out = [s.finish_codes() for s in streams]
+    for j in range(2):
+        o = Oracle(model.tensors, model.config(), max_cache_steps=cap)
+        oo = OracleOptions(**{k: getattr(opts[j], k) for k in OracleOptions.__dataclass_fields__})
+        tr = o.rollout(inputs[j].prefill, inputs[j].trailing_text, inputs[j].tts_pad_embed, oo)
+        fx = dict(codes=tr.codes, talker_margins=tr.talker_margins, cp_margins=tr.cp_margins,
+                  meta=dict(ended_by_eos=tr.ended_by_eos))
+        same = check_codes(out[j].codes, out[j].ended_by_eos, fx)
+        print(f"stream {j} (prefill {inputs[j].prefill_steps} rows): {same} frames identical")

@@ -313,6 +313,26 @@ def test_cache_of_33_chunks_matches_oracle(models):
     print(f"4224-row cache: {same} frames identical, talker logit err {err:.2e}")
 
 
+def test_largest_cache_matches_oracle_to_its_last_row(models):
+    """The largest cache the attention kernels take (64 key chunks of 128 rows, 8,192 rows):
+    an 8,186-row prompt and 6 frames, so the last frame's Talker row is row 8,191.  One row
+    more is refused when the engine is created, before any kernel runs."""
+    w = WORKLOADS["tiny_greedy"]
+    model, d = models.get(w.spec)
+    with pytest.raises(E.InvalidInputError):
+        E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=8193))
+    prompt = np.random.default_rng(23).integers(0, 151643, 8177)
+    from q3t import textprep
+    inputs = textprep.TextPrep(model).prepare(prompt)
+    assert inputs.prefill_steps == 8186
+    opts = E.GenerateOptions.greedy(6)
+    r = run(models, "tiny_greedy", options=opts, inputs=inputs, cap=8192)
+    fx = _as_fixture(_oracle_rollout(model, inputs, opts, 8192))
+    same = check_codes(r["codes"], r["eos"], fx)
+    err = check_talker_logits(r["talker_logits"], fx, same)
+    print(f"8192-row cache: {same} frames identical, talker logit err {err:.2e}")
+
+
 def test_capacity_busy_and_exhausted_streams(models):
     w = WORKLOADS["tiny_greedy"]
     model, d = models.get(w.spec)
