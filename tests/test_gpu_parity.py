@@ -333,6 +333,22 @@ def test_largest_cache_matches_oracle_to_its_last_row(models):
     print(f"8192-row cache: {same} frames identical, talker logit err {err:.2e}")
 
 
+@pytest.mark.parametrize("frames", [1, 2])
+def test_shortest_streams_match_oracle(models, frames):
+    """One frame (the prefill's logits give its semantic token and the frame's last Talker
+    decode is skipped) and two frames, on the graph and the eager path."""
+    w = WORKLOADS["tiny_greedy"]
+    model, _ = models.get(w.spec)
+    inputs = w.inputs(model)
+    opts = E.GenerateOptions.greedy(frames)
+    fx = _as_fixture(_oracle_rollout(model, inputs, opts, w.max_cache_steps))
+    for use_graph in (True, False):
+        r = run(models, "tiny_greedy", options=opts, inputs=inputs, use_graph=use_graph)
+        assert len(r["codes"]) == frames
+        same = check_codes(r["codes"], r["eos"], fx)
+        check_talker_logits(r["talker_logits"], fx, same)
+
+
 def test_capacity_busy_and_exhausted_streams(models):
     w = WORKLOADS["tiny_greedy"]
     model, d = models.get(w.spec)

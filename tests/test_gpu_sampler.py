@@ -37,6 +37,7 @@ def _logits(V, seed):
     (2048, 50, 1.0, 0.9),     # config 3 CodePredictor
     (3072, 0, 0.8, 1.0),      # nucleus only
     (2048, 20, 0.7, 0.6),
+    (2048, 2048, 1.0, 1.3),   # top_k = V keeps every candidate
 ])
 def test_draws_follow_closed_form(eng, V, top_k, top_p, T):
     logits = _logits(V, V + top_k)
@@ -71,6 +72,15 @@ def test_greedy_is_lowest_index_argmax(eng):
     logits[100] = logits[2000] = logits.max() + 1.0
     out = eng.sampler_draw(logits, 4, do_sample=False)
     assert out.tolist() == [100] * 4
+
+
+@pytest.mark.parametrize("V,top_k,top_p,T", [(3072, 1, 1.0, 0.9), (2048, 0, 1e-6, 1.0), (3072, 50, 1e-6, 0.7)])
+def test_degenerate_settings_draw_the_argmax(eng, V, top_k, top_p, T):
+    """top_k = 1, or a nucleus smaller than the top candidate's probability, leaves one
+    candidate: every draw is the argmax."""
+    logits = _logits(V, 17 + top_k)
+    draws = eng.sampler_draw(logits, 500, True, top_k, top_p, T, seed=7)
+    assert set(draws.tolist()) == {int(np.argmax(logits))}
 
 
 def test_masked_logits_never_drawn(eng):

@@ -46,12 +46,16 @@ def test_prepare_text_matches_oracle(tiny_text, n, look, speaker, language):
     assert err <= TOL
 
 
-def test_stream_from_ids_matches_oracle(tiny_text):
+@pytest.mark.parametrize("n,steps", [(32, 15), (0, 9)])
+def test_stream_from_ids_matches_oracle(tiny_text, n, steps):
+    """A stream started from content ids (lookahead 6), including empty content: the 9-row
+    role prefix alone, then tts_eos as the only trailing text row."""
     model, oracle, eng = tiny_text
-    ids = textprep.random_prompt(32, 1)
+    ids = textprep.random_prompt(n, 1)
     opts = E.GenerateOptions.greedy(16)
+    print(f"[gpu] stream from {n} content ids", flush=True)
     st = eng.start_stream_text(ids, opts, E.StreamOptions(text_lookahead_tokens=6))
-    assert st.prefill_steps == 15
+    assert st.prefill_steps == steps
     chunks = []
     while (c := st.next_codes_chunk(5)) is not None:
         chunks.append(c.codes)
