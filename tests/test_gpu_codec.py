@@ -1,7 +1,8 @@
 """Codec decoder on the GPU (q3t_decode_codes, q3t_stream_next_audio) against the float64 CPU
 oracle of the reference's decoder (oracle/codec.py), on the synthetic speech-tokenizer
 checkpoint.  Frame counts 3 and 10 put the decoder stages on both matrix-core GEMM paths
-(fewer and more than 128 rows)."""
+(fewer and more than 128 rows); 70 frames take the pre-transformer attention past one pass of
+its four waves' 32-key stride and its 64-key softmax loop."""
 import numpy as np
 import pytest
 
@@ -24,7 +25,7 @@ def codec_case(models):
     eng.close()
 
 
-@pytest.mark.parametrize("frames", [3, 10])
+@pytest.mark.parametrize("frames", [3, 10, 70])
 def test_decode_matches_oracle(codec_case, frames):
     eng, oracle = codec_case
     assert eng.has_codec and eng.info["samples_per_frame"] == C.SAMPLES_PER_FRAME
