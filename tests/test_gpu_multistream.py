@@ -309,3 +309,35 @@ def test_batched_caches_past_2048_rows_match_oracle(models, cap, n_ids):
                   meta=dict(ended_by_eos=tr.ended_by_eos))
         same = check_codes(out[j].codes, out[j].ended_by_eos, fx)
         print(f"stream {j} (prefill {inputs[j].prefill_steps} rows): {same} frames identical")
+
+
+def test_batched_1p7b_streams_match_fixture_and_single_stream(models):
+    """The 1.7B Talker on the batched frame (hidden 2048 and intermediate 6144 in the skinny
+    GEMMs, the CodePredictor input projected to 1024): config 4's stream next to two others
+    (40, 25 and 33 frames, so config 4's stream ends alone on the single-stream frame).  Its
+    codes repeat the first 40 frames of its float64 fixture; the others repeat their
+    single-stream rollouts.  The model stays cached for config 4's parity test."""
+    from q3t import textprep
+    from q3t.workloads import WORKLOADS
+    fx = load_fixture("cfg4_1.7b_greedy")
+    w = WORKLOADS["cfg4_1.7b_greedy"]
+    model, d = models.get(w.spec, w.weight_seed)
+    assert model.checksum() == fx["meta"]["checksum"]
+    prep = textprep.TextPrep(model)
+    inputs = [w.inputs(model)] + [prep.prepare(textprep.random_prompt(n, 40 + n)) for n in (30, 90)]
+    opts = [E.GenerateOptions.greedy(40), E.GenerateOptions.greedy(25), E.GenerateOptions.greedy(33)]
+    print("[gpu] batched 1.7B streams", flush=True)
+    with E.HipTtsEngine(d, E.EngineOptions(max_cache_steps=w.max_cache_steps, max_streams=3)) as eng:
+        streams = eng.start_streams(inputs, opts)
+        live = list(streams)
+        while live:
+            chunks = eng.next_codes_chunks(live, 6)
+            live = [s for s, c in zip(live, chunks) if c is not None]
+        got = [s.finish_codes().codes for s in streams]
+        for s in streams:
+            s.close()
+        refs = [eng.generate_codes(inputs[j], opts[j]).codes for j in (1, 2)]
+    np.testing.assert_array_equal(got[0], fx["codes"][:40])
+    for j in (1, 2):
+        np.testing.assert_array_equal(got[j], refs[j - 1], err_msg=f"stream {j}")
+    print(f"1.7B batched: {[len(g) for g in got]} frames, config 4's stream equal to its fixture")
