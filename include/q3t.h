@@ -102,6 +102,7 @@ int q3t_generate_options_validate(const q3t_generate_options *opts);
 /* HipTtsEngine::load_with_options (generation.rs:255-315). */
 int q3t_engine_create(const q3t_engine_options *opts, q3t_engine **out);
 int q3t_engine_destroy(q3t_engine *engine);
+/* The loaded shapes (q3t_engine_info) and the engine's capacity, memory and codec figures. */
 int q3t_engine_get_info(const q3t_engine *engine, q3t_engine_info *out);
 
 /* HipTtsEngine::start_stream_with_inputs (generation.rs:513-567): validates options
