@@ -80,8 +80,9 @@ struct TokenHandoff {
   // sum + r * sum_row, cur + r * cur_row, codes + r * codes_row (all 0 for one stream).
   int64_t keys_row, sum_row, cur_row, codes_row;
   // One stream, token chosen by a selection kernel (sampled groups): the token is read from
-  // tok_in instead of reduced from keys, and the selection kernel has done the stores above
-  // (only the table row is taken).
+  // tok_in instead of reduced from keys.  With emb null the selection kernel has done the
+  // stores above (only the table row is taken); with emb set (and cur, sum, codes, first,
+  // code, groups) workgroup (0, 0) does them, as for keys.
   const int32_t *tok_in;
 };
 
@@ -318,6 +319,9 @@ struct SelectCpArgs {
   int64_t codes_row, trace_row, trailing_row;
   const int32_t *row_on;
   int32_t *tok_out;           // one stream: the chosen token is also stored here (or null)
+  // tok_out set, not the last group: only the token and its code are stored; the next
+  // group's hand-off attention (TokenHandoff::tok_in with emb) stores cur and emb_sum.
+  int32_t token_only;
 };
 
 }  // namespace q3t

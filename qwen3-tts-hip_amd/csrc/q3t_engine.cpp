@@ -666,10 +666,20 @@ struct Engine {
           stack_step(cp, sl.c_k, sl.c_v, in, sl.x_c, sl, POS_CONST, g + 1, SKIP_DONE, s, &t,
                      cp_qkv_table + (size_t)(g - 1) * Vc * cd.qkv_rows());
         } else if (sampled_tables) {
-          // the previous group's selection kernel chose the token (tok_cur) and stored its
-          // embedding row (cur): layer 0 takes the token's q/k/v table row
+          // the previous group's selection kernel chose the token (tok_cur): layer 0 takes the
+          // token's q/k/v table row, and its workgroup (0, 0) stores the token's embedding row
+          // (cur, the layer's residual input) and the running sum, off the selection kernel's
+          // critical path
           TokenHandoff t{};
           t.tok_in = sl.tok_cur;
+          t.emb = cp_emb + (size_t)(g - 1) * Vc * Ht;
+          t.emb_width = Ht;
+          t.cur = sl.cur;
+          t.sum = sl.emb_sum;
+          t.codes = sl.codes;
+          t.first = g == 1;
+          t.code = g;
+          t.groups = groups;
           stack_step(cp, sl.c_k, sl.c_v, in, sl.x_c, sl, POS_CONST, g + 1, SKIP_DONE, s, &t,
                      cp_qkv_table + (size_t)(g - 1) * Vc * cd.qkv_rows());
         } else {
@@ -697,6 +707,7 @@ struct Engine {
                       trace ? sl.trace_c : nullptr, sl.t_in, codec_emb, sl.trailing, sl.st, sl.prm, Vc, Ht, groups,
                       g};
       sa.tok_out = sl.tok_cur;
+      sa.token_only = sampled_tables && g < nac - 1;
       hip_check(launch_select_cp(sa, s), "launch_select_cp");
     }
   }

@@ -769,7 +769,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
       x0 = src[lane];
       x1 = src[lane + 64];
     }
-    if (h == 0 && c == 0 && rb == 0 && !a.h.tok_in) handoff_load(a.h, row, tok, side_e, side_s, side_c);
+    if (h == 0 && c == 0 && rb == 0 && a.h.emb) handoff_load(a.h, row, tok, side_e, side_s, side_c);
   }
 
   // 1: q heads (waves 0..G-1); k and v (waves G, G+1) only where row `pos` is stored.
@@ -873,7 +873,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   __syncthreads();
 
   if constexpr (HO) {
-    if (h == 0 && c == 0 && rb == 0 && !a.h.tok_in) handoff_store(a.h, row, tok, st, side_e, side_s, side_c);
+    if (h == 0 && c == 0 && rb == 0 && a.h.emb) handoff_store(a.h, row, tok, st, side_e, side_s, side_c);
   }
 
   if constexpr (OPROJ) {
@@ -2733,6 +2733,7 @@ __global__ __launch_bounds__(1024) void k_select_cp(SelectCpArgs a) {
     if (a.group == 0) a.codes[(size_t)frame * a.groups] = semantic;
     if (a.tok_out) *a.tok_out = tok;
   }
+  if (a.token_only) return;  // the next group's hand-off attention stores the rows
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int i = tid + 1024 * j;
@@ -3117,9 +3118,11 @@ hipError_t launch_attn_oproj(const AttnArgs &a, int head_dim, hipStream_t s, con
     const int qkv_rows = (a.q_heads + 2 * a.kv_heads) * head_dim;
     const TokenHandoff &h = a.h;
     if (!a.qkv_table || a.ld_table < qkv_rows) return hipErrorInvalidValue;
-    // tok_in: the token's table row only (the caller validates the token's range: the
-    // selection kernel that stores it draws from the table's vocabulary)
-    if (h.tok_in ? (h.keys != nullptr || h.cur_table != nullptr)
+    // tok_in: the token's table row (the caller validates the token's range: the selection
+    // kernel that stores it draws from the table's vocabulary), and with emb the stores
+    const bool stores_ok = h.emb && h.emb_width > 0 && h.emb_width <= 2048 && h.emb_width % 8 == 0 && h.cur &&
+                           h.sum && h.codes && h.code >= 1 && h.code < h.groups;
+    if (h.tok_in ? (h.keys != nullptr || h.cur_table != nullptr || (h.emb && !stores_ok))
                  : (!handoff_ok(h) || h.emb_width > 2048 || h.emb_width % 4 || (h.cur_table && h.cur_width > 2048)))
       return hipErrorInvalidValue;
     if (a.kv_bf16) {
@@ -3492,6 +3495,7 @@ hipError_t launch_select_talker(const SelectTalkerArgs &a, hipStream_t s, int ro
 
 hipError_t launch_select_cp(const SelectCpArgs &a, hipStream_t s, int rows) {
   if (a.Vc < 1 || a.Vc > kMaxVocab || a.Ht < 1 || a.Ht > 2048) return hipErrorInvalidValue;
+  if (a.token_only && (rows != 1 || !a.tok_out || a.group >= a.groups - 2)) return hipErrorInvalidValue;
   if (rows < 1 || rows > kMaxRows ||
       (rows > 1 && (!a.row_on || a.codes_row <= 0 || a.trailing_row <= 0 || (a.trace && a.trace_row <= 0) ||
                     a.tok_out)))
