@@ -1157,7 +1157,7 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_attn_oproj_full(AttnArgs a
 // Stream-row form of merge_attention for the batched frame: workgroup (h, r) merges KV head
 // h's G query heads of row r (thread = one output element), in chunk order as in
 // merge_attention.
-// NC = chunk slots loaded (a power of two >= part_chunks): every partial of every slot is
+// NC = chunk slots loaded (a multiple of 8 >= part_chunks): every partial of every slot is
 // loaded before the stream state is read, so the merge waits on one memory round trip.
 template <int NC>
 __global__ __launch_bounds__(256) void k_attn_merge(AttnMergeArgs a) {
@@ -1173,8 +1173,9 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnMergeArgs a) {
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const float *pc = p0 + min(c, a.part_chunks - 1) * stride;
-    mv[c] = pc[0];
-    lv[c] = pc[1];
+    const float2 ml = *reinterpret_cast<const float2 *>(pc);  // (m, l): 8-byte aligned, D + 2 even
+    mv[c] = ml.x;
+    lv[c] = ml.y;
     av[c] = pc[2 + d];
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -3477,10 +3478,13 @@ hipError_t launch_attn_merge(const AttnMergeArgs &a, int rows, hipStream_t s) {
       a.part_chunks <= 0 || a.q_heads * 128 > a.ld_out || (rows > 1 && (!a.row_on || a.part_row <= 0)))
     return hipErrorInvalidValue;
   if ((a.q_heads / a.kv_heads) * 128 > 256 || a.part_chunks > kAttnMergeMaxChunks) return hipErrorInvalidValue;
+  if ((a.part_row & 1) || (reinterpret_cast<uintptr_t>(a.part) & 7)) return hipErrorInvalidValue;  // (m, l) pairs
   const dim3 grid(a.kv_heads, rows), block(256);
   if (a.part_chunks <= 8) hipLaunchKernelGGL(k_attn_merge<8>, grid, block, 0, s, a);
   else if (a.part_chunks <= 16) hipLaunchKernelGGL(k_attn_merge<16>, grid, block, 0, s, a);
+  else if (a.part_chunks <= 24) hipLaunchKernelGGL(k_attn_merge<24>, grid, block, 0, s, a);
   else if (a.part_chunks <= 32) hipLaunchKernelGGL(k_attn_merge<32>, grid, block, 0, s, a);
+  else if (a.part_chunks <= 48) hipLaunchKernelGGL(k_attn_merge<48>, grid, block, 0, s, a);
   else hipLaunchKernelGGL(k_attn_merge<64>, grid, block, 0, s, a);
   return hipGetLastError();
 }
