@@ -542,6 +542,7 @@ struct KvIo<float> {
     o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
   }
   __device__ static float2 load2(const float *p) { return *reinterpret_cast<const float2 *>(p); }
+  __device__ static float4 load4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
   // Elements 4 sub .. 4 sub + 3 and 64 + 4 sub .. 64 + 4 sub + 3 of a 128-element row: 16 lanes
   // then read the row as two contiguous 256-byte halves; split_dim(sub, j) is element j's index.
   __device__ static void load8_split(const float *row, int sub, float *o) {
@@ -570,6 +571,10 @@ struct KvIo<uint16_t> {
   __device__ static float2 load2(const uint16_t *p) {
     const uint32_t w = *reinterpret_cast<const uint32_t *>(p);
     return make_float2(bf_lo(w), bf_hi(w));
+  }
+  __device__ static float4 load4(const uint16_t *p) {
+    const uint2 w = *reinterpret_cast<const uint2 *>(p);
+    return make_float4(bf_lo(w.x), bf_hi(w.x), bf_lo(w.y), bf_hi(w.y));
   }
   // bf16 rows: one 16-byte load of 8 consecutive elements already covers 256 contiguous bytes
   // per row over 16 lanes.
@@ -733,11 +738,14 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
     const int t = min(t0 + wave * 4 + grp + 16 * i, tmax);
     KvIo<KVT>::load8(kbase + (size_t)t * D + sub * 8, kpre[i]);
   }
-  float2 vpre[CH / 4];
+  // V rows two per load instruction: half-wave hf of wave w takes row t0 + 8 i + 2 w + hf,
+  // lane q = lane % 32 of it dims 4q .. 4q + 3.
+  const int hf = lane >> 5, q4 = (lane & 31) * 4;
+  float4 vpre[CH / 8];
 #pragma unroll
-  for (int i = 0; i < CH / 4; ++i) {
-    const int t = min(t0 + wave + 4 * i, tmax);
-    vpre[i] = KvIo<KVT>::load2(vbase + (size_t)t * D + 2 * lane);
+  for (int i = 0; i < CH / 8; ++i) {
+    const int t = min(t0 + 8 * i + 2 * wave + hf, tmax);
+    vpre[i] = KvIo<KVT>::load4(vbase + (size_t)t * D + q4);
   }
   // The fused projection's weights: wave w takes rows rb * kOprojRows + w * kOprojRows / 4 ..;
   // a row's G * D bf16 of head h are LPR lanes x 8, so one 16-byte load per lane covers RPL
@@ -849,26 +857,34 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   }
   __syncthreads();
 
-  // 2c: acc = sum_t p_t V_t.  Wave w takes rows t0 + w (mod 4); lane owns dims 2l, 2l+1.
-  float acc[G][2];
+  // 2c: acc = sum_t p_t V_t over the rows of the loads above (value g * 4 + k: query head g,
+  // dim 4q + k).  The two half-waves' sums are then folded by one lane swap per pair of
+  // values: lanes 0-31 keep values 0 .. 2G - 1, lanes 32-63 values 2G .. 4G - 1.
+  constexpr int NV = 4 * G;
+  float acc[NV];
 #pragma unroll
-  for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.f;
+  for (int v = 0; v < NV; ++v) acc[v] = 0.f;
+  const float4 vown = *reinterpret_cast<const float4 *>(&vs[q4]);
 #pragma unroll
-  for (int i = 0; i < CH / 4; ++i) {
-    const int t = t0 + wave + 4 * i;
-    if (t >= t1) break;  // wave-uniform
-    const float2 v = (t < tpast) ? vpre[i] : make_float2(vs[2 * lane], vs[2 * lane + 1]);
+  for (int i = 0; i < CH / 8; ++i) {
+    if (t0 + 8 * i + 2 * wave >= t1) break;  // wave-uniform
+    const int t = t0 + 8 * i + 2 * wave + hf;
+    const float4 v = (t < tpast) ? vpre[i] : ((t == pos) ? vown : make_float4(0.f, 0.f, 0.f, 0.f));
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float p = sc[g][t - t0];
-      acc[g][0] = fmaf(p, v.x, acc[g][0]);
-      acc[g][1] = fmaf(p, v.y, acc[g][1]);
+      const float p = (t < t1) ? sc[g][min(t - t0, CH - 1)] : 0.f;
+      acc[g * 4 + 0] = fmaf(p, v.x, acc[g * 4 + 0]);
+      acc[g * 4 + 1] = fmaf(p, v.y, acc[g * 4 + 1]);
+      acc[g * 4 + 2] = fmaf(p, v.z, acc[g * 4 + 2]);
+      acc[g * 4 + 3] = fmaf(p, v.w, acc[g * 4 + 3]);
     }
   }
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    red[wave][g][2 * lane] = acc[g][0];
-    red[wave][g][2 * lane + 1] = acc[g][1];
+  for (int k = 0; k < NV / 2; ++k) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[k]), __float_as_uint(acc[k + NV / 2]),
+                                                    false, false);
+    const int v = hf * (NV / 2) + k;
+    red[wave][v / 4][q4 + v % 4] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
   __syncthreads();
 
