@@ -1171,28 +1171,29 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_attn_oproj_full(AttnArgs a
 }
 
 // Stream-row form of merge_attention for the batched frame: workgroup (h, r) merges KV head
-// h's G query heads of row r (thread = one output element), in chunk order as in
+// h's G query heads of row r (thread = two adjacent output elements), in chunk order as in
 // merge_attention.
 // NC = chunk slots loaded (a multiple of 8 >= part_chunks): every partial of every slot is
 // loaded before the stream state is read, so the merge waits on one memory round trip.
 template <int NC>
-__global__ __launch_bounds__(256) void k_attn_merge(AttnMergeArgs a) {
+__global__ __launch_bounds__(128) void k_attn_merge(AttnMergeArgs a) {
   constexpr int D = 128;
   const int h = blockIdx.x;
   const int row = blockIdx.y;
   const int G = a.q_heads / a.kv_heads;
-  if ((int)threadIdx.x >= G * D) return;
-  const int g = threadIdx.x / D, d = threadIdx.x % D;
+  if (2 * (int)threadIdx.x >= G * D) return;
+  const int g = 2 * threadIdx.x / D, d = 2 * threadIdx.x % D;  // two output elements per thread
   const float *p0 = a.part + row * a.part_row + (((size_t)h * a.part_chunks) * G + g) * (D + 2);
   const size_t stride = (size_t)G * (D + 2);
-  float mv[NC], lv[NC], av[NC];
+  float mv[NC], lv[NC];
+  float2 av[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const float *pc = p0 + min(c, a.part_chunks - 1) * stride;
-    const float2 ml = *reinterpret_cast<const float2 *>(pc);  // (m, l): 8-byte aligned, D + 2 even
+    const float2 ml = *reinterpret_cast<const float2 *>(pc);  // records of D + 2 floats: 8-byte aligned
     mv[c] = ml.x;
     lv[c] = ml.y;
-    av[c] = pc[2 + d];
+    av[c] = *reinterpret_cast<const float2 *>(pc + 2 + d);
   }
   __builtin_amdgcn_sched_barrier(0);
   if (a.row_on && !a.row_on[row]) return;
@@ -1205,16 +1206,18 @@ __global__ __launch_bounds__(256) void k_attn_merge(AttnMergeArgs a) {
 #pragma unroll
   for (int c = 0; c < NC; ++c)
     if (c < nchunks) M = fmaxf(M, mv[c]);
-  float den = 0.f, num = 0.f;
+  float den = 0.f, num0 = 0.f, num1 = 0.f;
 #pragma unroll
   for (int c = 0; c < NC; ++c)
     if (c < nchunks) {
       const float w = expf(mv[c] - M);
       den = fmaf(w, lv[c], den);
-      num = fmaf(w, av[c], num);
+      num0 = fmaf(w, av[c].x, num0);
+      num1 = fmaf(w, av[c].y, num1);
     }
-  const int k = (h * G + g) * D + d;
-  a.out[a.out_t16 ? t16_index(row, k) : (size_t)row * a.ld_out + k] = num / den;
+  const int k = (h * G + g) * D + d;  // even: k, k + 1 adjacent in both layouts
+  *reinterpret_cast<float2 *>(a.out + (a.out_t16 ? t16_index(row, k) : (size_t)row * a.ld_out + k)) =
+      make_float2(num0 / den, num1 / den);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -3494,8 +3497,11 @@ hipError_t launch_attn_merge(const AttnMergeArgs &a, int rows, hipStream_t s) {
       a.part_chunks <= 0 || a.q_heads * 128 > a.ld_out || (rows > 1 && (!a.row_on || a.part_row <= 0)))
     return hipErrorInvalidValue;
   if ((a.q_heads / a.kv_heads) * 128 > 256 || a.part_chunks > kAttnMergeMaxChunks) return hipErrorInvalidValue;
-  if ((a.part_row & 1) || (reinterpret_cast<uintptr_t>(a.part) & 7)) return hipErrorInvalidValue;  // (m, l) pairs
-  const dim3 grid(a.kv_heads, rows), block(256);
+  // (m, l) and output pairs: 8-byte aligned records and rows
+  if ((a.part_row & 1) || (reinterpret_cast<uintptr_t>(a.part) & 7) || (reinterpret_cast<uintptr_t>(a.out) & 7) ||
+      (!a.out_t16 && (a.ld_out & 1)))
+    return hipErrorInvalidValue;
+  const dim3 grid(a.kv_heads, rows), block(128);
   if (a.part_chunks <= 8) hipLaunchKernelGGL(k_attn_merge<8>, grid, block, 0, s, a);
   else if (a.part_chunks <= 16) hipLaunchKernelGGL(k_attn_merge<16>, grid, block, 0, s, a);
   else if (a.part_chunks <= 24) hipLaunchKernelGGL(k_attn_merge<24>, grid, block, 0, s, a);
