@@ -960,13 +960,16 @@ __device__ void merge_attention(const GemvArgs &a, float *xs) {
 //     trip); longer caches take one more round trip per further kFusedRows rows.
 //   - Only b = 0 stores the K/V row at `pos`; every workgroup computes it (same arithmetic).
 //   - Scores of every row go to LDS (wave w: rows 4w + (lane >> 4) + 64 i, 16 lanes x 8 dims
-//     per row), then one softmax over all rows (wave g: query head g), then P.V (wave w: rows
-//     w + 16 i, lane: dims 2 lane, 2 lane + 1) summed over the 16 waves in wave order.
+//     per row), then one softmax over all rows (wave g: query head g), then P.V summed over
+//     the 16 waves in wave order: fp32 caches (V4) load V rows two per 16-byte load (half-wave
+//     h of wave w: row 2 (16 i + w) + h, lane: 4 dims), the half-waves' sums folded by
+//     v_permlane32_swap; bf16 caches one row per load (wave w: rows w + 16 i, lane: dims
+//     2 lane, 2 lane + 1), which measured faster for them.
 constexpr int kFusedWaves = 16;
 constexpr int kFusedRows = 256;      // key rows per register pass
 constexpr int kFusedMaxCap = 1024;   // longest cache (score rows in LDS)
 
-template <int G, typename KVT>
+template <int G, typename KVT, bool V4 = sizeof(KVT) == 4>
 __global__ __launch_bounds__(64 * kFusedWaves) void k_attn_oproj_full(AttnArgs a) {
   constexpr int D = 128, NW = kFusedWaves, BL = kFusedRows;
   constexpr int KI = BL / (NW * 4);  // K rows per lane per pass
@@ -1032,7 +1035,11 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_attn_oproj_full(AttnArgs a
   // contiguous bytes per row.
   constexpr bool GUARD = sizeof(KVT) == 4;
   float kreg[KI][8];
-  float2 vreg[VI];
+  float2 vreg[V4 ? 1 : VI];
+  // V4: V rows two per 16-byte load, half-wave hf of wave w taking row p0 + 2 (NW i + w) + hf,
+  // lane q = lane % 32 dims 4q .. 4q + 3
+  const int hf = lane >> 5, q4 = (lane & 31) * 4;
+  float4 vreg4[V4 ? VI / 2 : 1];
   auto load_k = [&](int p0) {
 #pragma unroll
     for (int i = 0; i < KI; ++i) {
@@ -1042,6 +1049,15 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_attn_oproj_full(AttnArgs a
     }
   };
   auto load_v = [&](int p0) {
+    if constexpr (V4) {
+#pragma unroll
+      for (int i = 0; i < VI / 2; ++i) {
+        if (GUARD && p0 + 2 * (NW * i + wave) >= L) break;
+        const int t = min(p0 + 2 * (NW * i + wave) + hf, tmax);
+        vreg4[i] = KvIo<KVT>::load4(vbase + (size_t)t * D + q4);
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < VI; ++i) {
       if (GUARD && p0 + wave + NW * i >= L) break;
@@ -1131,28 +1147,62 @@ __global__ __launch_bounds__(64 * kFusedWaves) void k_attn_oproj_full(AttnArgs a
   __syncthreads();
 
   // 6. P.V, per wave, then the 16 waves' sums in wave order.
-  float acc[G][2];
+  if constexpr (V4) {
+    // value g * 4 + k: query head g, dim 4q + k; the half-waves' sums folded by one lane swap
+    // per pair of values (lanes 0-31 keep values 0 .. 2G - 1, lanes 32-63 the rest)
+    constexpr int NV = 4 * G;
+    float acc[NV];
 #pragma unroll
-  for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.f;
-  for (int p0 = 0; p0 < L; p0 += BL) {
-    if (p0 > 0) load_v(p0);
+    for (int v = 0; v < NV; ++v) acc[v] = 0.f;
+    const float4 vown = *reinterpret_cast<const float4 *>(&vs[q4]);
+    for (int p0 = 0; p0 < L; p0 += BL) {
+      if (p0 > 0) load_v(p0);
 #pragma unroll
-    for (int i = 0; i < VI; ++i) {
-      const int t = p0 + wave + NW * i;
-      if (t >= L) break;  // wave-uniform
-      const float2 v = (t < pos) ? vreg[i] : make_float2(vs[2 * lane], vs[2 * lane + 1]);
+      for (int i = 0; i < VI / 2; ++i) {
+        if (p0 + 2 * (NW * i + wave) >= L) break;  // wave-uniform
+        const int t = p0 + 2 * (NW * i + wave) + hf;
+        const float4 v = (t < pos) ? vreg4[i] : ((t == pos) ? vown : make_float4(0.f, 0.f, 0.f, 0.f));
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float p = sc[g][t];
-        acc[g][0] = fmaf(p, v.x, acc[g][0]);
-        acc[g][1] = fmaf(p, v.y, acc[g][1]);
+        for (int g = 0; g < G; ++g) {
+          const float p = (t < L) ? sc[g][min(t, L - 1)] : 0.f;
+          acc[g * 4 + 0] = fmaf(p, v.x, acc[g * 4 + 0]);
+          acc[g * 4 + 1] = fmaf(p, v.y, acc[g * 4 + 1]);
+          acc[g * 4 + 2] = fmaf(p, v.z, acc[g * 4 + 2]);
+          acc[g * 4 + 3] = fmaf(p, v.w, acc[g * 4 + 3]);
+        }
       }
     }
-  }
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    red[wave][g][2 * lane] = acc[g][0];
-    red[wave][g][2 * lane + 1] = acc[g][1];
+    for (int k = 0; k < NV / 2; ++k) {
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[k]), __float_as_uint(acc[k + NV / 2]),
+                                                      false, false);
+      const int v = hf * (NV / 2) + k;
+      red[wave][v / 4][q4 + v % 4] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+  } else {
+    float acc[G][2];
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.f;
+    for (int p0 = 0; p0 < L; p0 += BL) {
+      if (p0 > 0) load_v(p0);
+#pragma unroll
+      for (int i = 0; i < VI; ++i) {
+        const int t = p0 + wave + NW * i;
+        if (t >= L) break;  // wave-uniform
+        const float2 v = (t < pos) ? vreg[i] : make_float2(vs[2 * lane], vs[2 * lane + 1]);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float p = sc[g][t];
+          acc[g][0] = fmaf(p, v.x, acc[g][0]);
+          acc[g][1] = fmaf(p, v.y, acc[g][1]);
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      red[wave][g][2 * lane] = acc[g][0];
+      red[wave][g][2 * lane + 1] = acc[g][1];
+    }
   }
   __syncthreads();
   if (threadIdx.x < G * D) {
