@@ -323,12 +323,12 @@ struct Engine {
     hip_check(launch_gemv(epi, norm, nt, a, s, timing), "launch_gemv");
   }
 
-  // The CodePredictor's attention fits one 32-row chunk, so its O projection can be fused
+  // The CodePredictor's attention fits one chunk (16 rows), so its O projection can be fused
   // into the attention kernel (launch_attn_oproj) with the residual summed by the gate/up
   // GEMV: one launch fewer per layer.
   bool oproj_ok(const StackW &w) const {
     const Dims &d = w.d;
-    return &w == &cp && w.cap <= 32 && attn_chunk_len(w.cap) == 32 && d.kv_heads <= 8 &&
+    return &w == &cp && w.cap <= 32 && d.kv_heads <= 8 &&
            (d.hidden == 512 || d.hidden == 1024);
   }
 
@@ -374,7 +374,7 @@ struct Engine {
         // sum in the gate/up GEMV, which also stores it (x_mid) for the down GEMV.
         AttnArgs aa{sl.qkv,   L.gq,      L.gk,       w.rope,  kc + l * cache_layer, vc + l * cache_layer,
                     nullptr,  d.q_heads, d.kv_heads, w.cap,   d.eps, 1.0f / std::sqrt((float)d.head_dim),
-                    pos_mode, pos_const, skip,       kv_bf16, sl.st, nullptr, 0, 32, 0};
+                    pos_mode, pos_const, skip,       kv_bf16, sl.st, nullptr, 0, attn_chunk_len(w.cap), 0};
         if (table) {
           aa.h = *handoff;
           aa.qkv_table = qkv_table;
@@ -767,7 +767,7 @@ struct Engine {
     Pools &p = pools;
     const int H = d.hidden;
     const size_t cache_layer = (size_t)d.kv_heads * w.cap * d.head_dim * (kv_bf16 ? 2 : 4);
-    const int chunk = attn_rows_chunk_len(w.cap);  // the CodePredictor's short cache: one 32-row chunk
+    const int chunk = attn_rows_chunk_len(w.cap);  // the CodePredictor's short cache: one 16-row chunk
     const int nch = (w.cap + chunk - 1) / chunk;
     const int partial = nch > 1 ? 1 : 0;
     const Act none{nullptr, 0};
@@ -2737,7 +2737,7 @@ int bench_kernel_impl(q3t_engine *e, int32_t kernel, int32_t iters, double *avg_
           const int pos = (i / d.layers) % e->groups;
           AttnArgs aa{s.qkv, W.gq, W.gk, l.w->rope, s.c_k + layer_bytes * l.layer, s.c_v + layer_bytes * l.layer,
                       nullptr, d.q_heads, d.kv_heads, l.w->cap, d.eps, 1.0f / std::sqrt((float)d.head_dim),
-                      POS_CONST, pos, SKIP_NEVER, e->kv_bf16, s.st, nullptr, 0, 32, 0};
+                      POS_CONST, pos, SKIP_NEVER, e->kv_bf16, s.st, nullptr, 0, attn_chunk_len(l.w->cap), 0};
           aa.wo = W.o;
           aa.wo_rows = d.hidden;
           aa.opart = s.opart;

@@ -31,8 +31,8 @@ constexpr int kMaxRows = 16;
 hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t stream,
                               const LaunchTiming *timing = nullptr, int rows = 1);
 hipError_t launch_attn_merge(const AttnMergeArgs &a, int rows, hipStream_t stream);
-// The same attention for one stream and one 32-row chunk (cap <= 32, position from the
-// launch), with the output projection fused in: a.opart[h][r] = KV head h's share of
+// The same attention for one stream and one chunk (cap <= 32, chunk attn_chunk_len(cap),
+// position from the launch), with the output projection fused in: a.opart[h][r] = KV head h's share of
 // (a.wo * attn)[r] for r < a.wo_rows (a multiple of 32).  The gate/up GEMV adds the shares
 // to the residual (GemvArgs::parts, hidden 512 or 1024).  Requires at most 8 KV heads and 1
 // or 2 query heads per KV head.

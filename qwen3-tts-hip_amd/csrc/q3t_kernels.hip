@@ -653,7 +653,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   static_assert(D == 128, "lane layout assumes head_dim 128");
   static_assert(G >= 1 && G <= 2, "query heads per KV head");
   static_assert(CH % 16 == 0 && CH <= kAttnMaxChunk, "chunk length");
-  static_assert(!OPROJ || CH == 32, "the fused projection covers one 32-row chunk");
+  static_assert(!OPROJ || CH <= 32, "the fused projection covers one chunk of at most 32 rows");
   const int row = blockIdx.z;
   const SlotState *st = a.st + row;
   // A position given by the launch needs no state: the row mask and the stream state are
@@ -3082,7 +3082,9 @@ hipError_t launch_gemv(int epi, bool norm, bool streaming, const GemvArgs &a, hi
 }
 
 int attn_chunk_len(int cap) {
-  // 32, 64 or 128 rows: at most kAttnMaxChunks chunks up to a 1024-row cache
+  // 16 rows for a cache of at most 16 (the CodePredictor's), else 32, 64 or 128: at most
+  // kAttnMaxChunks chunks up to a 1024-row cache
+  if (cap <= 16) return 16;
   int c = 32;
   while (c < kAttnMaxChunk && c * kAttnMaxChunks < cap) c *= 2;
   return c;
@@ -3091,6 +3093,7 @@ int attn_chunk_len(int cap) {
 int attn_chunks(int cap) { return (cap + attn_chunk_len(cap) - 1) / attn_chunk_len(cap); }
 
 int attn_rows_chunk_len(int cap) {
+  if (cap <= 16) return 16;
   int c = 32;
   while (c < kAttnMaxChunk && c * kAttnMergeMaxChunks < cap) c *= 2;
   return c;
@@ -3110,30 +3113,31 @@ hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t s, co
   // chunk: attn_chunk_len(cap) for one stream (the O GEMV merges at most kAttnMaxChunks
   // partials); any of 32 / 64 / 128 for stream rows (merged by k_attn_merge).
   if (a.cap > attn_max_cache_steps(a.q_heads, a.kv_heads)) return hipErrorInvalidValue;
-  if (rows == 1 ? a.chunk != attn_chunk_len(a.cap) : (a.chunk != 32 && a.chunk != 64 && a.chunk != 128))
+  if (rows == 1 ? a.chunk != attn_chunk_len(a.cap) : a.chunk != attn_rows_chunk_len(a.cap))
     return hipErrorInvalidValue;
   const int nch = (a.cap + a.chunk - 1) / a.chunk;
   if (a.partial_out ? a.part_chunks < nch : nch != 1) return hipErrorInvalidValue;
   const dim3 grid(a.kv_heads, nch, rows), block(256);
   if (a.h.keys) {
-    // the hand-off: one chunk of 32 rows, a position given by the launch; stream rows store
+    // the hand-off: one chunk (16 or 32 rows), a position given by the launch; stream rows store
     // through their own slices (no overlap between rows)
     const int qkv_rows = (a.q_heads + 2 * a.kv_heads) * head_dim;
     const TokenHandoff &h = a.h;
     const bool rows_ok = rows == 1 || (h.keys_row >= h.n_keys && h.sum_row >= h.emb_width &&
                                        h.cur_row >= (h.cur_table ? h.cur_width : h.emb_width) &&
                                        h.codes_row >= h.groups);
-    if (!rows_ok || a.partial_out || a.chunk != 32 || a.pos_mode != POS_CONST || !a.qkv_table ||
+    if (!rows_ok || a.partial_out || (a.chunk != 16 && a.chunk != 32) || a.pos_mode != POS_CONST || !a.qkv_table ||
         a.ld_table < qkv_rows || !handoff_ok(h) || h.emb_width > 2048 || h.emb_width % 4 ||
         (h.cur_table && h.cur_width > 2048) || !a.st)
       return hipErrorInvalidValue;
+#define Q3T_HO_CASE(GG, TT, CC) \
+  if (G == GG && a.chunk == CC) launch_timed(k_attn_split<128, GG, TT, CC, true>, grid, block, 0, s, t, a);
     if (a.kv_bf16) {
-      if (G == 1) launch_timed(k_attn_split<128, 1, uint16_t, 32, true>, grid, block, 0, s, t, a);
-      else launch_timed(k_attn_split<128, 2, uint16_t, 32, true>, grid, block, 0, s, t, a);
+      Q3T_HO_CASE(1, uint16_t, 16) Q3T_HO_CASE(2, uint16_t, 16) Q3T_HO_CASE(1, uint16_t, 32) Q3T_HO_CASE(2, uint16_t, 32)
     } else {
-      if (G == 1) launch_timed(k_attn_split<128, 1, float, 32, true>, grid, block, 0, s, t, a);
-      else launch_timed(k_attn_split<128, 2, float, 32, true>, grid, block, 0, s, t, a);
+      Q3T_HO_CASE(1, float, 16) Q3T_HO_CASE(2, float, 16) Q3T_HO_CASE(1, float, 32) Q3T_HO_CASE(2, float, 32)
     }
+#undef Q3T_HO_CASE
     return hipGetLastError();
   }
 #define Q3T_ATTN_CASE(GG, TT, CC) \
@@ -3142,11 +3146,13 @@ hipError_t launch_attn_decode(const AttnArgs &a, int head_dim, hipStream_t s, co
     return hipGetLastError();     \
   }
   if (a.kv_bf16) {
-    Q3T_ATTN_CASE(1, uint16_t, 32) Q3T_ATTN_CASE(1, uint16_t, 64) Q3T_ATTN_CASE(1, uint16_t, 128)
-    Q3T_ATTN_CASE(2, uint16_t, 32) Q3T_ATTN_CASE(2, uint16_t, 64) Q3T_ATTN_CASE(2, uint16_t, 128)
+    Q3T_ATTN_CASE(1, uint16_t, 16) Q3T_ATTN_CASE(1, uint16_t, 32) Q3T_ATTN_CASE(1, uint16_t, 64)
+    Q3T_ATTN_CASE(1, uint16_t, 128)
+    Q3T_ATTN_CASE(2, uint16_t, 16) Q3T_ATTN_CASE(2, uint16_t, 32) Q3T_ATTN_CASE(2, uint16_t, 64)
+    Q3T_ATTN_CASE(2, uint16_t, 128)
   } else {
-    Q3T_ATTN_CASE(1, float, 32) Q3T_ATTN_CASE(1, float, 64) Q3T_ATTN_CASE(1, float, 128)
-    Q3T_ATTN_CASE(2, float, 32) Q3T_ATTN_CASE(2, float, 64) Q3T_ATTN_CASE(2, float, 128)
+    Q3T_ATTN_CASE(1, float, 16) Q3T_ATTN_CASE(1, float, 32) Q3T_ATTN_CASE(1, float, 64) Q3T_ATTN_CASE(1, float, 128)
+    Q3T_ATTN_CASE(2, float, 16) Q3T_ATTN_CASE(2, float, 32) Q3T_ATTN_CASE(2, float, 64) Q3T_ATTN_CASE(2, float, 128)
   }
 #undef Q3T_ATTN_CASE
   return hipErrorInvalidValue;
@@ -3180,7 +3186,7 @@ int attn_oproj_full_rows(int q_heads, int kv_heads) {
 hipError_t launch_attn_oproj(const AttnArgs &a, int head_dim, hipStream_t s, const LaunchTiming *t) {
   if (head_dim != 128 || a.kv_heads <= 0 || a.q_heads % a.kv_heads || a.kv_heads > kMaxParts) return hipErrorInvalidValue;
   const int G = a.q_heads / a.kv_heads;
-  if (G < 1 || G > 2 || a.cap < 1 || a.cap > 32 || a.chunk != 32 || a.partial_out || a.row_on ||
+  if (G < 1 || G > 2 || a.cap < 1 || a.cap > 32 || a.chunk != attn_chunk_len(a.cap) || a.partial_out || a.row_on ||
       a.pos_mode != POS_CONST || !a.wo || !a.opart || a.wo_rows <= 0 || a.wo_rows % kOprojRows || !a.st)
     return hipErrorInvalidValue;
   const dim3 grid(a.kv_heads, a.wo_rows / kOprojRows, 1), block(256);
@@ -3195,22 +3201,25 @@ hipError_t launch_attn_oproj(const AttnArgs &a, int head_dim, hipStream_t s, con
     if (h.tok_in ? (h.keys != nullptr || h.cur_table != nullptr || (h.emb && !stores_ok))
                  : (!handoff_ok(h) || h.emb_width > 2048 || h.emb_width % 4 || (h.cur_table && h.cur_width > 2048)))
       return hipErrorInvalidValue;
+#define Q3T_OP_CASE(GG, TT, CC, HH) \
+  if (G == GG && a.chunk == CC) launch_timed(k_attn_split<128, GG, TT, CC, HH, true>, grid, block, 0, s, t, a);
     if (a.kv_bf16) {
-      if (G == 1) launch_timed(k_attn_split<128, 1, uint16_t, 32, true, true>, grid, block, 0, s, t, a);
-      else launch_timed(k_attn_split<128, 2, uint16_t, 32, true, true>, grid, block, 0, s, t, a);
+      Q3T_OP_CASE(1, uint16_t, 16, true) Q3T_OP_CASE(2, uint16_t, 16, true)
+      Q3T_OP_CASE(1, uint16_t, 32, true) Q3T_OP_CASE(2, uint16_t, 32, true)
     } else {
-      if (G == 1) launch_timed(k_attn_split<128, 1, float, 32, true, true>, grid, block, 0, s, t, a);
-      else launch_timed(k_attn_split<128, 2, float, 32, true, true>, grid, block, 0, s, t, a);
+      Q3T_OP_CASE(1, float, 16, true) Q3T_OP_CASE(2, float, 16, true)
+      Q3T_OP_CASE(1, float, 32, true) Q3T_OP_CASE(2, float, 32, true)
     }
     return hipGetLastError();
   }
   if (a.kv_bf16) {
-    if (G == 1) launch_timed(k_attn_split<128, 1, uint16_t, 32, false, true>, grid, block, 0, s, t, a);
-    else launch_timed(k_attn_split<128, 2, uint16_t, 32, false, true>, grid, block, 0, s, t, a);
+    Q3T_OP_CASE(1, uint16_t, 16, false) Q3T_OP_CASE(2, uint16_t, 16, false)
+    Q3T_OP_CASE(1, uint16_t, 32, false) Q3T_OP_CASE(2, uint16_t, 32, false)
   } else {
-    if (G == 1) launch_timed(k_attn_split<128, 1, float, 32, false, true>, grid, block, 0, s, t, a);
-    else launch_timed(k_attn_split<128, 2, float, 32, false, true>, grid, block, 0, s, t, a);
+    Q3T_OP_CASE(1, float, 16, false) Q3T_OP_CASE(2, float, 16, false)
+    Q3T_OP_CASE(1, float, 32, false) Q3T_OP_CASE(2, float, 32, false)
   }
+#undef Q3T_OP_CASE
   return hipGetLastError();
 }
 
