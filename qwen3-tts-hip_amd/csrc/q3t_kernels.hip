@@ -250,7 +250,7 @@ constexpr int kMaxParts = 8;
 // merge_attention); IN_PARTS = x plus the per-head partials of the fused attention + O
 // projection (GemvArgs::parts), summed through LDS; IN_TALKER = the next Talker input from
 // the last CodePredictor group's hand-off (GemvArgs::tin), assembled through LDS.
-constexpr int IN_X = 0, IN_ATTN = 1, IN_PARTS = 2, IN_TALKER = 3;
+constexpr int IN_X = 0, IN_ATTN = 1, IN_PARTS = 2, IN_TALKER = 3, IN_XLDS = 4;
 
 // Waves per workgroup of the IN_PARTS form: every workgroup sums the partials into LDS, so
 // it runs the launch's waves in fewer, larger workgroups (the partials are read from L2 once
@@ -265,10 +265,16 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
   constexpr bool ATTN = IN == IN_ATTN;
   constexpr bool PARTS = IN == IN_PARTS;
   constexpr bool TIN = IN == IN_TALKER;
+  // IN_XLDS: x (and the norm gain) loaded once per workgroup, one float4 per thread and pass,
+  // and read by every wave from LDS: each lane otherwise loads the whole vector (2 KC loads,
+  // and 2 KC more for the gain), more load instructions than its weight rows take.
+  constexpr bool XLDS = IN == IN_XLDS;
+  static_assert(!XLDS || MR == 1, "x through LDS: one row");
   constexpr int WPB = PARTS ? kPartsWaves : 4;
   static_assert(!ATTN || MR == 1, "the attention merge feeds one row");
   static_assert(!PARTS || (KC == 1 || KC == 2), "the partial sum feeds rows of K <= 1024");
-  static_assert(!HO || (MR == 1 && IN == IN_X && EPI == EPI_STORE), "the hand-off producer stores one row");
+  static_assert(!HO || (MR == 1 && (IN == IN_X || IN == IN_XLDS) && EPI == EPI_STORE),
+                "the hand-off producer stores one row");
   static_assert(!TIN || (MR == 1 && EPI == EPI_STORE && NORM && (KC == 1 || KC == 2 || KC == 4)),
                 "the Talker input feeds one normed row of K 512, 1024 or 2048");
   constexpr int K = KC * 512;
@@ -276,7 +282,8 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int unit0 = (blockIdx.x * WPB + wave) * RW;
-  __shared__ float xs[PARTS ? MR : 1][(ATTN || PARTS || TIN) ? K : 1];
+  __shared__ float xs[PARTS ? MR : 1][(ATTN || PARTS || TIN || XLDS) ? K : 1];
+  __shared__ float gsh[(XLDS && NORM) ? K : 1];
   __shared__ uint64_t wkeys[HO ? 4 : 1];
   // IN_PARTS: thread t sums elements 4t .. 4t+3 of x and of every part (K <= 1024), for each
   // input row m (x + m * ldx_r, parts + m * ldp_r).
@@ -322,9 +329,20 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
   if constexpr (ATTN_EARLY) {
     if (threadIdx.x * 8 < K) merge_load(a, threadIdx.x * 8, mregs);
   }
+  constexpr int XQ = XLDS ? (K + 1023) / 1024 : 1;
+  float4 xq[XQ], gq[(XLDS && NORM) ? XQ : 1];
+  if constexpr (XLDS) {
+#pragma unroll
+    for (int j = 0; j < XQ; ++j) {
+      const int i = 4 * (int)threadIdx.x + 1024 * j;
+      xq[j] = i < K ? *reinterpret_cast<const float4 *>(a.x + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+      if constexpr (NORM)
+        gq[j] = i < K ? *reinterpret_cast<const float4 *>(a.gamma + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
 #pragma unroll
   for (int c = 0; c < KC; ++c) {
-    if constexpr (ATTN || PARTS || TIN) break;
+    if constexpr (ATTN || PARTS || TIN || XLDS) break;
 #pragma unroll
     for (int m = 0; m < MR; ++m) {
       const float4 *px = reinterpret_cast<const float4 *>(a.x + m * a.ldx_r + c * 512 + lane * 8);
@@ -333,7 +351,7 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
       xv[m][c][4] = p1.x; xv[m][c][5] = p1.y; xv[m][c][6] = p1.z; xv[m][c][7] = p1.w;
     }
   }
-  if constexpr (NORM) {
+  if constexpr (NORM && !XLDS) {
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
       const float4 *pg = reinterpret_cast<const float4 *>(a.gamma + c * 512 + lane * 8);
@@ -436,6 +454,24 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
       for (int c = 0; c < KC; ++c)
 #pragma unroll
         for (int j = 0; j < 8; ++j) xv[m][c][j] = xs[m][c * 512 + lane * 8 + j];
+  }
+  if constexpr (XLDS) {
+#pragma unroll
+    for (int j = 0; j < XQ; ++j) {
+      const int i = 4 * (int)threadIdx.x + 1024 * j;
+      if (i < K) {
+        *reinterpret_cast<float4 *>(&xs[0][i]) = xq[j];
+        if constexpr (NORM) *reinterpret_cast<float4 *>(&gsh[i]) = gq[j];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < KC; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        xv[0][c][j] = xs[0][c * 512 + lane * 8 + j];
+        if constexpr (NORM) gv[c][j] = gsh[c * 512 + lane * 8 + j];
+      }
   }
   if constexpr (ATTN_EARLY) {
     if (threadIdx.x * 8 < K) merge_finish(a, threadIdx.x * 8, mregs, xs[0]);
@@ -2953,7 +2989,7 @@ static void gemv_launch(const GemvArgs &a, hipStream_t s, const LaunchTiming *t)
   if constexpr (!NT && KC <= 4 && KC != 3 && EPI == EPI_STORE && NORM) {
     if (a.keys_out) {
       if (grid.x > (unsigned)kHandoffKeys) return;  // launch_gemv checked the grid
-      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_X, 1, true>, grid, dim3(256), 0, s, t, a);
+      launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_XLDS, 1, true>, grid, dim3(256), 0, s, t, a);
       return;
     }
   }
@@ -2991,7 +3027,7 @@ static void gemv_launch(const GemvArgs &a, hipStream_t s, const LaunchTiming *t)
       return;
     }
   }
-  launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_X>, grid, dim3(256), 0, s, t, a);
+  launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_XLDS>, grid, dim3(256), 0, s, t, a);
 }
 
 template <int EPI, bool NORM, int KC, bool NT>
