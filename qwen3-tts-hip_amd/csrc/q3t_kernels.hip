@@ -283,7 +283,9 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
   const int wave = threadIdx.x >> 6;
   const int unit0 = (blockIdx.x * WPB + wave) * RW;
   __shared__ float xs[PARTS ? MR : 1][(ATTN || PARTS || TIN || XLDS) ? K : 1];
-  __shared__ float gsh[(XLDS && NORM) ? K : 1];
+  // The norm gain goes through LDS with the input wherever the input does (GLDS).
+  constexpr bool GLDS = NORM && (XLDS || PARTS || TIN);
+  __shared__ float gsh[GLDS ? K : 1];
   __shared__ uint64_t wkeys[HO ? 4 : 1];
   // IN_PARTS: thread t sums elements 4t .. 4t+3 of x and of every part (K <= 1024), for each
   // input row m (x + m * ldx_r, parts + m * ldp_r).
@@ -330,16 +332,41 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
     if (threadIdx.x * 8 < K) merge_load(a, threadIdx.x * 8, mregs);
   }
   constexpr int XQ = XLDS ? (K + 1023) / 1024 : 1;
-  float4 xq[XQ], gq[(XLDS && NORM) ? XQ : 1];
+  float4 xq[XQ];
   if constexpr (XLDS) {
 #pragma unroll
     for (int j = 0; j < XQ; ++j) {
       const int i = 4 * (int)threadIdx.x + 1024 * j;
       xq[j] = i < K ? *reinterpret_cast<const float4 *>(a.x + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-      if constexpr (NORM)
-        gq[j] = i < K ? *reinterpret_cast<const float4 *>(a.gamma + i) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
+  constexpr int GQ = GLDS ? (K + 1023) / 1024 : 1;
+  float4 gq[GQ];
+  if constexpr (GLDS) {
+#pragma unroll
+    for (int j = 0; j < GQ; ++j) {
+      const int i = 4 * (int)threadIdx.x + 1024 * j;
+      gq[j] = i < K ? *reinterpret_cast<const float4 *>(a.gamma + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  // the gain's LDS stores (before the input's barrier) and the lane's reads (after it)
+  auto gain_store = [&] {
+    if constexpr (GLDS) {
+#pragma unroll
+      for (int j = 0; j < GQ; ++j) {
+        const int i = 4 * (int)threadIdx.x + 1024 * j;
+        if (i < K) *reinterpret_cast<float4 *>(&gsh[i]) = gq[j];
+      }
+    }
+  };
+  auto gain_read = [&] {
+    if constexpr (GLDS) {
+#pragma unroll
+      for (int c = 0; c < KC; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) gv[c][j] = gsh[c * 512 + lane * 8 + j];
+    }
+  };
 #pragma unroll
   for (int c = 0; c < KC; ++c) {
     if constexpr (ATTN || PARTS || TIN || XLDS) break;
@@ -351,7 +378,7 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
       xv[m][c][4] = p1.x; xv[m][c][5] = p1.y; xv[m][c][6] = p1.z; xv[m][c][7] = p1.w;
     }
   }
-  if constexpr (NORM && !XLDS) {
+  if constexpr (NORM && !GLDS) {
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
       const float4 *pg = reinterpret_cast<const float4 *>(a.gamma + c * 512 + lane * 8);
@@ -417,8 +444,10 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
       }
     }
     if (blockIdx.x == 0 && threadIdx.x == 0) a.tin.codes[(size_t)frame * a.tin.groups + a.tin.code] = tok;
+    gain_store();
     __syncthreads();
     if (skip_work(a.st, a.skip)) return;
+    gain_read();
 #pragma unroll
     for (int c = 0; c < KC; ++c)
 #pragma unroll
@@ -447,7 +476,9 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
         if (a.x_store && blockIdx.x == 0) *reinterpret_cast<float4 *>(a.x_store + m * a.ldxs_r + i) = v;
       }
     }
+    gain_store();
     __syncthreads();
+    gain_read();
 #pragma unroll
     for (int m = 0; m < PR; ++m)
 #pragma unroll
@@ -459,19 +490,15 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
 #pragma unroll
     for (int j = 0; j < XQ; ++j) {
       const int i = 4 * (int)threadIdx.x + 1024 * j;
-      if (i < K) {
-        *reinterpret_cast<float4 *>(&xs[0][i]) = xq[j];
-        if constexpr (NORM) *reinterpret_cast<float4 *>(&gsh[i]) = gq[j];
-      }
+      if (i < K) *reinterpret_cast<float4 *>(&xs[0][i]) = xq[j];
     }
+    gain_store();
     __syncthreads();
+    gain_read();
 #pragma unroll
     for (int c = 0; c < KC; ++c)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        xv[0][c][j] = xs[0][c * 512 + lane * 8 + j];
-        if constexpr (NORM) gv[c][j] = gsh[c * 512 + lane * 8 + j];
-      }
+      for (int j = 0; j < 8; ++j) xv[0][c][j] = xs[0][c * 512 + lane * 8 + j];
   }
   if constexpr (ATTN_EARLY) {
     if (threadIdx.x * 8 < K) merge_finish(a, threadIdx.x * 8, mregs, xs[0]);
