@@ -246,10 +246,12 @@ __device__ void merge_attention(const GemvArgs &a, float *xs);
 // Most per-head partials a GEMV input sums (GemvArgs::parts): the KV heads of a layer.
 constexpr int kMaxParts = 8;
 
-// The input vector of k_gemv: IN_X = x; IN_ATTN = the merge of attention partials (see
-// merge_attention); IN_PARTS = x plus the per-head partials of the fused attention + O
-// projection (GemvArgs::parts), summed through LDS; IN_TALKER = the next Talker input from
-// the last CodePredictor group's hand-off (GemvArgs::tin), assembled through LDS.
+// The input vector of k_gemv: IN_X = x, loaded whole by every lane (the two-row form);
+// IN_XLDS = x loaded once per workgroup into LDS (the one-row form); IN_ATTN = the merge of
+// attention partials (see merge_attention); IN_PARTS = x plus the per-head partials of the
+// fused attention + O projection (GemvArgs::parts), summed through LDS; IN_TALKER = the next
+// Talker input from the last CodePredictor group's hand-off (GemvArgs::tin), assembled
+// through LDS.  With the RMSNorm prologue the LDS forms take the gain through LDS too.
 constexpr int IN_X = 0, IN_ATTN = 1, IN_PARTS = 2, IN_TALKER = 3, IN_XLDS = 4;
 
 // Waves per workgroup of the IN_PARTS form: every workgroup sums the partials into LDS, so
