@@ -1879,6 +1879,15 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
   for (int b = 0; b < MB; ++b)
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[b][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // The RMSNorm gain of this wave's k range (KW <= 128 values): one load per lane and 64
+  // values; each lane then takes its 8 values per k step by lane permutes (the 16 lanes of a
+  // row share them), not by two 16-byte loads per step.
+  constexpr int GL = NORM ? (KW + 63) / 64 : 1;
+  float gl[GL];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int j = 0; j < GL; ++j) gl[j] = (64 * j + lane < KW) ? a.gamma[kbase + 64 * j + lane] : 0.f;
+  }
 #pragma unroll
   for (int p0 = 0; p0 < KS; p0 += KP) {
     float xa[MB][KP][8];
@@ -1897,12 +1906,6 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
         xa[b][st][0] = x0.x; xa[b][st][1] = x0.y; xa[b][st][2] = x0.z; xa[b][st][3] = x0.w;
         xa[b][st][4] = x1.x; xa[b][st][5] = x1.y; xa[b][st][6] = x1.z; xa[b][st][7] = x1.w;
       }
-      if constexpr (NORM) {
-        const float4 *pg = reinterpret_cast<const float4 *>(a.gamma + k);
-        const float4 g0 = pg[0], g1 = pg[1];
-        ga[st][0] = g0.x; ga[st][1] = g0.y; ga[st][2] = g0.z; ga[st][3] = g0.w;
-        ga[st][4] = g1.x; ga[st][5] = g1.y; ga[st][6] = g1.z; ga[st][7] = g1.w;
-      }
 #pragma unroll
       for (int t = 0; t < T; ++t) {  // tile blockIdx.x (+ N / 16 for the up rows), k step k0 / 32
         const size_t tile = blockIdx.x + (size_t)t * (a.N >> 4);
@@ -1912,6 +1915,12 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
     __builtin_amdgcn_sched_barrier(0);
 
     if constexpr (NORM) {  // single pass: this wave holds its whole k range of every row
+#pragma unroll
+      for (int st = 0; st < KP; ++st) {
+        const int r = (p0 + st) * 32;  // this step's first value in the wave's range
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ga[st][e] = __shfl(gl[(r + 8 * kb + e) >> 6], (r + 8 * kb + e) & 63, 64);
+      }
       // RMSNorm(x) W^T = r (x * g) W^T with r = 1 / rms(x) one scalar per row: the products
       // take x * g, and r multiplies the sums in the epilogue.  Each wave leaves its rows'
       // sums of squares in ssq; the reduction's barrier then covers them too, so no wave
