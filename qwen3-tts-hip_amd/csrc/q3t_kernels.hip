@@ -2987,7 +2987,7 @@ static void launch_timed(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_
 
 // Weight loads in flight per lane are capped at kMaxLoads (4 VGPRs each) for streamed
 // weights, and at kMaxLoadsCached for cache-resident ones.
-constexpr int kMaxLoads = 24;
+constexpr int kMaxLoads = 8;
 constexpr int kMaxLoadsCached = 4;
 
 // Rows per wave: spread the matrix over ~256 workgroups (one per CU, one wave per SIMD)
@@ -2995,11 +2995,13 @@ constexpr int kMaxLoadsCached = 4;
 // cap per lane, use more workgroups instead.  The result is one of 1, 2, 3, 4, 6 that fits
 // the cap (or 1).
 // The cap depends on where the weights come from.  Streamed (non-temporal, read once per
-// frame from HBM) matrices keep up to 24 loads per lane.  The CodePredictor's matrices, reread
-// from the last-level cache 15 times per frame, do better with more workgroups and fewer
-// loads each: its gate/up GEMV at 3 workgroups per CU with 4 loads per lane instead of 1
-// with 12 took the 0.6B frame from 524 to 535 frames/s and the 1.7B frame from 435 to 448;
-// the same cap on the streamed Talker matrices cost the 1.7B frame 3%.
+// frame from HBM) matrices keep up to 8 loads per lane: since the input vector reaches the
+// waves through LDS once per workgroup, more workgroups with fewer rows each cost little
+// (the 1.7B gate/up at 1 row per wave instead of 3, its down at 1 instead of 2: config 4
+// 490.2 -> 497.7 frames/s; 24 was best while every lane loaded the whole vector).  The
+// CodePredictor's matrices, reread from the last-level cache 15 times per frame, keep 4:
+// its gate/up GEMV at 3 workgroups per CU with 4 loads per lane instead of 1 with 12 took
+// the 0.6B frame from 524 to 535 frames/s and the 1.7B frame from 435 to 448.
 static int gemv_rows_per_wave(int N, int KC, int epi, bool streaming) {
   const int pu = (epi == EPI_SWIGLU) ? 2 : 1;
   const int cap = streaming ? kMaxLoads : kMaxLoadsCached;
