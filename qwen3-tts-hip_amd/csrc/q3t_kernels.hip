@@ -258,12 +258,22 @@ constexpr int IN_X = 0, IN_ATTN = 1, IN_PARTS = 2, IN_TALKER = 3, IN_XLDS = 4;
 // it runs the launch's waves in fewer, larger workgroups (the partials are read from L2 once
 // per workgroup).
 constexpr int kPartsWaves = 12;
+// Waves per workgroup of the IN_XLDS form for K >= 512 * kXldsWideKC (the 1.7B Talker's down
+// projection, K = 6144): every workgroup loads the whole input (24 KB) into LDS, so 8-wave
+// workgroups halve the input bytes a launch pulls from L2.  Smaller K (inputs of 8-12 KB)
+// keeps 4 waves, which measured as fast or faster there.
+constexpr int kXldsWideKC = 12;
+constexpr int kXldsWideWaves = 8;
+template <int IN, int KC>
+constexpr int gemv_waves() {
+  return IN == IN_PARTS ? kPartsWaves : (IN == IN_XLDS && KC >= kXldsWideKC) ? kXldsWideWaves : 4;
+}
 
 // MR = input rows (1, or 2: row 1 at x + ldx_r, res + ldr_r, out + ldo_r) against the same
 // weight loads.
 // HO = greedy token hand-off producer (GemvArgs::keys_out).
 template <int EPI, bool NORM, int KC, int RW, bool NT, int IN = IN_X, int MR = 1, bool HO = false>
-__global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gemv(GemvArgs a) {
+__global__ __launch_bounds__((64 * gemv_waves<IN, KC>())) void k_gemv(GemvArgs a) {
   constexpr bool ATTN = IN == IN_ATTN;
   constexpr bool PARTS = IN == IN_PARTS;
   constexpr bool TIN = IN == IN_TALKER;
@@ -272,7 +282,8 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
   // and 2 KC more for the gain), more load instructions than its weight rows take.
   constexpr bool XLDS = IN == IN_XLDS;
   static_assert(!XLDS || MR == 1, "x through LDS: one row");
-  constexpr int WPB = PARTS ? kPartsWaves : 4;
+  constexpr int WPB = gemv_waves<IN, KC>();
+  constexpr int NTH = 64 * WPB;
   static_assert(!ATTN || MR == 1, "the attention merge feeds one row");
   static_assert(!PARTS || (KC == 1 || KC == 2), "the partial sum feeds rows of K <= 1024");
   static_assert(!HO || (MR == 1 && (IN == IN_X || IN == IN_XLDS) && EPI == EPI_STORE),
@@ -333,21 +344,21 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
   if constexpr (ATTN_EARLY) {
     if (threadIdx.x * 8 < K) merge_load(a, threadIdx.x * 8, mregs);
   }
-  constexpr int XQ = XLDS ? (K + 1023) / 1024 : 1;
+  constexpr int XQ = XLDS ? (K + 4 * NTH - 1) / (4 * NTH) : 1;
   float4 xq[XQ];
   if constexpr (XLDS) {
 #pragma unroll
     for (int j = 0; j < XQ; ++j) {
-      const int i = 4 * (int)threadIdx.x + 1024 * j;
+      const int i = 4 * (int)threadIdx.x + 4 * NTH * j;
       xq[j] = i < K ? *reinterpret_cast<const float4 *>(a.x + i) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
-  constexpr int GQ = GLDS ? (K + 1023) / 1024 : 1;
+  constexpr int GQ = GLDS ? (K + 4 * NTH - 1) / (4 * NTH) : 1;
   float4 gq[GQ];
   if constexpr (GLDS) {
 #pragma unroll
     for (int j = 0; j < GQ; ++j) {
-      const int i = 4 * (int)threadIdx.x + 1024 * j;
+      const int i = 4 * (int)threadIdx.x + 4 * NTH * j;
       gq[j] = i < K ? *reinterpret_cast<const float4 *>(a.gamma + i) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
@@ -356,7 +367,7 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
     if constexpr (GLDS) {
 #pragma unroll
       for (int j = 0; j < GQ; ++j) {
-        const int i = 4 * (int)threadIdx.x + 1024 * j;
+        const int i = 4 * (int)threadIdx.x + 4 * NTH * j;
         if (i < K) *reinterpret_cast<float4 *>(&gsh[i]) = gq[j];
       }
     }
@@ -491,7 +502,7 @@ __global__ __launch_bounds__(IN == IN_PARTS ? 64 * kPartsWaves : 256) void k_gem
   if constexpr (XLDS) {
 #pragma unroll
     for (int j = 0; j < XQ; ++j) {
-      const int i = 4 * (int)threadIdx.x + 1024 * j;
+      const int i = 4 * (int)threadIdx.x + 4 * NTH * j;
       if (i < K) *reinterpret_cast<float4 *>(&xs[0][i]) = xq[j];
     }
     gain_store();
@@ -3015,7 +3026,8 @@ static int gemv_rows_per_wave(int N, int KC, int epi, bool streaming) {
 }
 
 static int gemv_grid(int N, int K, int epi, bool streaming) {
-  const int units = 4 * gemv_rows_per_wave(N, K / 512, epi, streaming);
+  const int waves = K / 512 >= kXldsWideKC ? kXldsWideWaves : 4;  // the one-row forms' workgroups
+  const int units = waves * gemv_rows_per_wave(N, K / 512, epi, streaming);
   return (N + units - 1) / units;
 }
 
@@ -3067,7 +3079,9 @@ static void gemv_launch(const GemvArgs &a, hipStream_t s, const LaunchTiming *t)
       return;
     }
   }
-  launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_XLDS>, grid, dim3(256), 0, s, t, a);
+  constexpr int xw = gemv_waves<IN_XLDS, KC>();
+  const dim3 grid_x((a.N + xw * RW - 1) / (xw * RW));
+  launch_timed(k_gemv<EPI, NORM, KC, RW, NT, IN_XLDS>, grid_x, dim3(64 * xw), 0, s, t, a);
 }
 
 template <int EPI, bool NORM, int KC, bool NT>
