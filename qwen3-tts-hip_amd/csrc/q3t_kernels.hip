@@ -611,14 +611,31 @@ struct KvIo<float> {
   }
   __device__ static float round(float x) { return x; }
 
+  template <bool NT = false>
   __device__ static void load8(const float *p, float *o) {
-    const float4 a = reinterpret_cast<const float4 *>(p)[0];
-    const float4 b = reinterpret_cast<const float4 *>(p)[1];
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 *q = reinterpret_cast<const f4 *>(p);
+    f4 a, b;
+    if constexpr (NT) {
+      a = __builtin_nontemporal_load(q);
+      b = __builtin_nontemporal_load(q + 1);
+    } else {
+      a = q[0];
+      b = q[1];
+    }
     o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
     o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
   }
   __device__ static float2 load2(const float *p) { return *reinterpret_cast<const float2 *>(p); }
-  __device__ static float4 load4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+  template <bool NT = false>
+  __device__ static float4 load4(const float *p) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    if constexpr (NT) {
+      const f4 v = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(p));
+      return make_float4(v.x, v.y, v.z, v.w);
+    }
+    return *reinterpret_cast<const float4 *>(p);
+  }
   // Elements 4 sub .. 4 sub + 3 and 64 + 4 sub .. 64 + 4 sub + 3 of a 128-element row: 16 lanes
   // then read the row as two contiguous 256-byte halves; split_dim(sub, j) is element j's index.
   __device__ static void load8_split(const float *row, int sub, float *o) {
@@ -639,8 +656,14 @@ struct KvIo<uint16_t> {
   }
   __device__ static float round(float x) { return bf16_to_f32(f32_to_bf16(x)); }
 
+  template <bool NT = false>
   __device__ static void load8(const uint16_t *p, float *o) {
-    const uint4 w = *reinterpret_cast<const uint4 *>(p);
+    typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+    u4 w;
+    if constexpr (NT)
+      w = __builtin_nontemporal_load(reinterpret_cast<const u4 *>(p));
+    else
+      w = *reinterpret_cast<const u4 *>(p);
     o[0] = bf_lo(w.x); o[1] = bf_hi(w.x); o[2] = bf_lo(w.y); o[3] = bf_hi(w.y);
     o[4] = bf_lo(w.z); o[5] = bf_hi(w.z); o[6] = bf_lo(w.w); o[7] = bf_hi(w.w);
   }
@@ -648,8 +671,14 @@ struct KvIo<uint16_t> {
     const uint32_t w = *reinterpret_cast<const uint32_t *>(p);
     return make_float2(bf_lo(w), bf_hi(w));
   }
+  template <bool NT = false>
   __device__ static float4 load4(const uint16_t *p) {
-    const uint2 w = *reinterpret_cast<const uint2 *>(p);
+    typedef unsigned int u2 __attribute__((ext_vector_type(2)));
+    u2 w;
+    if constexpr (NT)
+      w = __builtin_nontemporal_load(reinterpret_cast<const u2 *>(p));
+    else
+      w = *reinterpret_cast<const u2 *>(p);
     return make_float4(bf_lo(w.x), bf_hi(w.x), bf_lo(w.y), bf_hi(w.y));
   }
   // bf16 rows: one 16-byte load of 8 consecutive elements already covers 256 contiguous bytes
@@ -730,6 +759,9 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
   static_assert(G >= 1 && G <= 2, "query heads per KV head");
   static_assert(CH % 16 == 0 && CH <= kAttnMaxChunk, "chunk length");
   static_assert(!OPROJ || CH <= 32, "the fused projection covers one chunk of at most 32 rows");
+  // The Talker's form (no fused projection) reads each K/V row once per step: non-temporal
+  // loads, as for the Talker's weights (the CodePredictor's form rereads its rows every group).
+  constexpr bool KV_NT = !OPROJ;
   const int row = blockIdx.z;
   const SlotState *st = a.st + row;
   // A position given by the launch needs no state: the row mask and the stream state are
@@ -812,7 +844,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < CH / 16; ++i) {
     const int t = min(t0 + wave * 4 + grp + 16 * i, tmax);
-    KvIo<KVT>::load8(kbase + (size_t)t * D + sub * 8, kpre[i]);
+    KvIo<KVT>::template load8<KV_NT>(kbase + (size_t)t * D + sub * 8, kpre[i]);
   }
   // V rows two per load instruction: half-wave hf of wave w takes row t0 + 8 i + 2 w + hf,
   // lane q = lane % 32 of it dims 4q .. 4q + 3.
@@ -821,7 +853,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < CH / 8; ++i) {
     const int t = min(t0 + 8 * i + 2 * wave + hf, tmax);
-    vpre[i] = KvIo<KVT>::load4(vbase + (size_t)t * D + q4);
+    vpre[i] = KvIo<KVT>::template load4<KV_NT>(vbase + (size_t)t * D + q4);
   }
   // The fused projection's weights: wave w takes rows rb * kOprojRows + w * kOprojRows / 4 ..;
   // a row's G * D bf16 of head h are LPR lanes x 8, so one 16-byte load per lane covers RPL
