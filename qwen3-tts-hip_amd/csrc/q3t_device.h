@@ -235,6 +235,9 @@ struct GemmArgs {
   // x_blk / r_blk / y_blk elements after.
   int32_t mb;
   int64_t x_blk, r_blk, y_blk;
+  // skinny GEMM: weights read with non-temporal loads (weights read once per step, e.g. the
+  // Talker's, so that they do not displace weights that are reread from the last-level cache).
+  int32_t w_nt;
 };
 
 // Prompt prefill attention over rows at positions pos0 .. pos0 + P - 1.

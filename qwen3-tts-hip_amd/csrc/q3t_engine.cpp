@@ -737,6 +737,11 @@ struct Engine {
   };
   static Act t16(const float *p) { return Act{p, -1}; }
 
+  // Set by rows_stack_step while it runs the Talker's layers, whose weights a batched frame
+  // reads once: rgemm and rgemm_split2 then load them non-temporally, so that they pass
+  // without displacing the CodePredictor's weights, which every group rereads, from the
+  // last-level cache.
+  bool rows_w_nt = false;
   // The batched frame's O and down GEMMs split K in two (rgemm_split2) when both can.
   bool split2_ok(const Dims &d) const {
     return bmid && gemm_skinny_split2_supports(d.q_out()) && gemm_skinny_split2_supports(d.intermediate);
@@ -754,6 +759,7 @@ struct Engine {
     g.Y = const_cast<float *>(Y.p); g.ldy = Y.ld < 0 ? N : Y.ld; g.y_t16 = Y.ld < 0;
     g.M = rows; g.N = N; g.K = K; g.row_on = pools.row_on;
     g.keys_out = keys_out; g.keys_row = keys_row;
+    g.w_nt = rows_w_nt;
     hip_check(launch_gemm_skinny(epi, norm, g, s), "launch_gemm_skinny");
   }
 
@@ -766,6 +772,11 @@ struct Engine {
     const Dims &d = w.d;
     Pools &p = pools;
     const int H = d.hidden;
+    struct WntScope {
+      bool &f;
+      WntScope(bool &flag, bool v) : f(flag) { f = v; }
+      ~WntScope() { f = false; }
+    } wnt_scope(rows_w_nt, &w == &talker);
     const size_t cache_layer = (size_t)d.kv_heads * w.cap * d.head_dim * (kv_bf16 ? 2 : 4);
     const int chunk = attn_rows_chunk_len(w.cap);  // the CodePredictor's short cache: one 16-row chunk
     const int nch = (w.cap + chunk - 1) / chunk;
@@ -830,6 +841,7 @@ struct Engine {
     g.Y = Y; g.ldy = N; g.y_t16 = 1;
     g.M = rows; g.N = N; g.K = K; g.row_on = pools.row_on;
     g.split2 = 1; g.res_zero = res_zero; g.mb = mb;
+    g.w_nt = mb == 1 && rows_w_nt;
     hip_check(launch_gemm_skinny(EPI_RESIDUAL, false, g, s), "launch_gemm_skinny(split2)");
   }
 

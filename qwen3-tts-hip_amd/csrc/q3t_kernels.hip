@@ -1880,7 +1880,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm_lds(GemmArgs a) {
 // same stream rows (row m of block b is stream row m, masked by row_on[m]).  T16 operands of
 // block b start 16 * K (X) or 16 * N (Y, res, res_zero) elements after block 0; row-major ones
 // x_blk / r_blk / y_blk elements after.
-template <int EPI, bool NORM, int KS, bool KEYS = false, bool XT16 = true, bool SPLIT = false, int MB = 1>
+template <int EPI, bool NORM, int KS, bool KEYS = false, bool XT16 = true, bool SPLIT = false, int MB = 1,
+          bool WNT = false>
 __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
   static_assert(!KEYS || EPI == EPI_STORE, "keys replace the plain store");
   static_assert(!SPLIT || (EPI == EPI_RESIDUAL && !NORM && XT16), "the split GEMM is the T16 residual form");
@@ -1952,7 +1953,7 @@ __global__ __launch_bounds__(1024) void k_gemm_skinny(GemmArgs a) {
 #pragma unroll
       for (int t = 0; t < T; ++t) {  // tile blockIdx.x (+ N / 16 for the up rows), k step k0 / 32
         const size_t tile = blockIdx.x + (size_t)t * (a.N >> 4);
-        wb[st][t] = *reinterpret_cast<const uint4 *>(a.W + ((tile * (a.K >> 5) + (k0 >> 5)) * 64 + lane) * 8);
+        wb[st][t] = load_w<WNT>(reinterpret_cast<const u32x4 *>(a.W + ((tile * (a.K >> 5) + (k0 >> 5)) * 64 + lane) * 8));
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -3434,25 +3435,25 @@ static hipError_t gemm_epi(const GemmArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int EPI, bool NORM, bool XT16>
+template <int EPI, bool NORM, bool XT16, bool WNT>
 static hipError_t skinny_ks(const GemmArgs &a, hipStream_t s) {
   const dim3 grid((a.N + 15) / 16), block(1024);
   switch (a.K / 512) {
-    case 1: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 1, false, XT16>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 2, false, XT16>), grid, block, 0, s, a); break;
-    case 3: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 3, false, XT16>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 4, false, XT16>), grid, block, 0, s, a); break;
+    case 1: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 1, false, XT16, false, 1, WNT>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 2, false, XT16, false, 1, WNT>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 3, false, XT16, false, 1, WNT>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 4, false, XT16, false, 1, WNT>), grid, block, 0, s, a); break;
     case 6:
       if constexpr (NORM) return hipErrorInvalidValue;
-      else hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 6, false, XT16>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 6, false, XT16, false, 1, WNT>), grid, block, 0, s, a);
       break;
     case 8:
       if constexpr (NORM) return hipErrorInvalidValue;
-      else hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 8, false, XT16>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 8, false, XT16, false, 1, WNT>), grid, block, 0, s, a);
       break;
     case 12:
       if constexpr (NORM) return hipErrorInvalidValue;
-      else hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 12, false, XT16>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((k_gemm_skinny<EPI, NORM, 12, false, XT16, false, 1, WNT>), grid, block, 0, s, a);
       break;
     default: return hipErrorInvalidValue;
   }
@@ -3461,19 +3462,20 @@ static hipError_t skinny_ks(const GemmArgs &a, hipStream_t s) {
 
 template <int EPI, bool NORM>
 static hipError_t skinny_ks(const GemmArgs &a, hipStream_t s) {
-  return a.x_t16 ? skinny_ks<EPI, NORM, true>(a, s) : skinny_ks<EPI, NORM, false>(a, s);
+  if (a.w_nt) return a.x_t16 ? skinny_ks<EPI, NORM, true, true>(a, s) : skinny_ks<EPI, NORM, false, true>(a, s);
+  return a.x_t16 ? skinny_ks<EPI, NORM, true, false>(a, s) : skinny_ks<EPI, NORM, false, false>(a, s);
 }
 
 // The K-split residual GEMM (GemmArgs::split2): 2 x N / 16 workgroups, each half of K.
-template <int MB>
+template <int MB, bool WNT = false>
 static hipError_t skinny_split2(const GemmArgs &a, hipStream_t s) {
   const dim3 grid((a.N + 15) / 16, 2), block(1024);
   switch (a.K / 1024) {
-    case 1: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 1, false, true, true, MB>), grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 2, false, true, true, MB>), grid, block, 0, s, a); break;
-    case 3: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 3, false, true, true, MB>), grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 4, false, true, true, MB>), grid, block, 0, s, a); break;
-    case 6: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 6, false, true, true, MB>), grid, block, 0, s, a); break;
+    case 1: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 1, false, true, true, MB, WNT>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 2, false, true, true, MB, WNT>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 3, false, true, true, MB, WNT>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 4, false, true, true, MB, WNT>), grid, block, 0, s, a); break;
+    case 6: hipLaunchKernelGGL((k_gemm_skinny<EPI_RESIDUAL, false, 6, false, true, true, MB, WNT>), grid, block, 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -3537,7 +3539,8 @@ hipError_t launch_gemm_skinny(int epi, bool norm, const GemmArgs &a, hipStream_t
   if (a.split2) {
     if (epi != EPI_RESIDUAL || norm || !a.x_t16 || !a.y_t16 || !a.res_zero || !gemm_skinny_split2_supports(a.K))
       return hipErrorInvalidValue;
-    return a.mb == 2 ? skinny_split2<2>(a, s) : skinny_split2<1>(a, s);
+    if (a.mb == 2) return skinny_split2<2>(a, s);
+    return a.w_nt ? skinny_split2<1, true>(a, s) : skinny_split2<1>(a, s);
   }
   if (a.mb == 2) return skinny_mb2(epi, norm, a, s);
   switch (epi) {
